@@ -1,0 +1,301 @@
+// extern "C" entry points of libictc_mi355x.so (declared in include/ictc_mi355x.h).
+#include <hipcub/hipcub.hpp>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/ictc_mi355x.h"
+#include "ictc_launch.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int check_hip(hipError_t err, const char* what) {
+  if (err == hipSuccess) return ICTC_OK;
+  return fail(ICTC_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(err));
+}
+
+// Natural-parity path count and output components (operators.py:206-207).
+bool tp_counts(int li, int le, int lo, int* P, int* NO) {
+  if (li < 0 || le < 0 || lo < 0 || li > 3 || le > 3 || lo > 3) return false;
+  int p = 0, no = 0;
+  for (int a = 0; a <= li; ++a)
+    for (int b = 0; b <= le; ++b)
+      for (int c = 0; c <= lo; ++c)
+        if (((a - b) <= c && (b - a) <= c) && c <= a + b && ((a + b + c) % 2 == 0)) {
+          ++p;
+          no += 2 * c + 1;
+        }
+  if (P) *P = p;
+  if (NO) *NO = no;
+  return p > 0;
+}
+
+int check_shape(int li, int le, int lo, int C) {
+  int P = 0;
+  if (!tp_counts(li, le, lo, &P, nullptr))
+    return fail(ICTC_ERR_UNSUPPORTED, "degrees (%d, %d, %d) are outside the compiled coverage (0..3, nonempty paths)",
+                li, le, lo);
+  if (C < 1 || ictc::channels_per_lane(C) == 0)
+    return fail(ICTC_ERR_UNSUPPORTED, "channels=%d outside the supported range 1..256", C);
+  return ICTC_OK;
+}
+
+ictc::Operands operands(const float* x, const float* sh, const float* g, const float* w, const float* mask,
+                        int64_t rows, int64_t edges, int C) {
+  ictc::Operands a;
+  a.x = x;
+  a.sh = sh;
+  a.gates = g;
+  a.weight = w;
+  a.mask = mask;
+  a.rows = rows;
+  a.edges = edges;
+  a.channels = C;
+  return a;
+}
+
+// ---- CSR build kernels ----------------------------------------------------
+__global__ void csr_keys_kernel(const int64_t* __restrict__ keys, int64_t E, int64_t N, int32_t* __restrict__ k32,
+                                int32_t* __restrict__ ids) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int64_t k = keys[e];
+  k32[e] = (k >= 0 && k < N) ? (int32_t)k : (int32_t)N;
+  ids[e] = (int32_t)e;
+}
+
+// ptr[n] = first position whose sorted key >= n, for n in [0, N]; ptr[N+1] = E.
+__global__ void csr_ptr_kernel(const int32_t* __restrict__ sorted, int64_t E, int64_t N, int32_t* __restrict__ ptr) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n > N + 1) return;
+  if (n == N + 1) {
+    ptr[n] = (int32_t)E;
+    return;
+  }
+  int64_t lo = 0, hi = E;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (sorted[mid] < n) lo = mid + 1;
+    else hi = mid;
+  }
+  ptr[n] = (int32_t)lo;
+}
+
+int key_bits(int64_t N) {
+  int bits = 1;
+  while (bits < 31 && (int64_t(1) << bits) <= N) ++bits;
+  return bits;
+}
+
+size_t sort_temp_bytes(int64_t E, int64_t N) {
+  size_t bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
+                                     (const int32_t*)nullptr, (int32_t*)nullptr, (int)E, 0, key_bits(N));
+  return bytes;
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Zero fill as a kernel (not hipMemsetAsync) so the call stays valid under
+// HIP graph capture.
+__global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+__global__ void fill_zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ictc_version(void) { return 100; }
+
+const char* ictc_last_error(void) { return g_error.c_str(); }
+
+int ictc_tp_shape(int input_lmax, int edge_lmax, int output_lmax, int* num_paths, int* out_components) {
+  if (!tp_counts(input_lmax, edge_lmax, output_lmax, num_paths, out_components))
+    return fail(ICTC_ERR_UNSUPPORTED, "degrees (%d, %d, %d) unsupported", input_lmax, edge_lmax, output_lmax);
+  return ICTC_OK;
+}
+
+int ictc_tp_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                int64_t E, float* out, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "edges must be nonnegative");
+  if (E == 0) return ICTC_OK;
+  if (!x || !sh || !g || !out) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_fwd: null operand");
+  const ictc::TpShape s{li, le, lo, C};
+  return check_hip(ictc::launch_edge_fwd(s, operands(x, sh, g, w, nullptr, E, E, C), out, (hipStream_t)stream),
+                   "ictc_tp_fwd launch");
+}
+
+int ictc_tp_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                const float* grad, int64_t E, float* dx, float* dsh, float* dg, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "edges must be nonnegative");
+  if (E == 0 || (!dx && !dsh && !dg)) return ICTC_OK;
+  if (!x || !sh || !g || !grad) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_bwd: null operand");
+  const ictc::TpShape s{li, le, lo, C};
+  return check_hip(ictc::launch_edge_bwd(s, operands(x, sh, g, w, nullptr, E, E, C), grad, dx, dsh, dg,
+                                         (hipStream_t)stream),
+                   "ictc_tp_bwd launch");
+}
+
+int64_t ictc_csr_workspace_bytes(int64_t E, int64_t N) {
+  if (E < 0 || N < 0 || E >= (int64_t(1) << 31) || N >= (int64_t(1) << 31) - 2) return -1;
+  return (int64_t)(3 * align256(sizeof(int32_t) * (size_t)(E > 0 ? E : 1)) + align256(sort_temp_bytes(E, N)));
+}
+
+int ictc_csr_build(const int64_t* keys, int64_t E, int64_t N, int32_t* ptr, int32_t* order, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  if (E < 0 || N < 0) return fail(ICTC_ERR_ARGUMENT, "csr: negative size");
+  if (E >= (int64_t(1) << 31) || N >= (int64_t(1) << 31) - 2)
+    return fail(ICTC_ERR_UNSUPPORTED, "csr: more than 2^31 edges or nodes");
+  if (!ptr) return fail(ICTC_ERR_ARGUMENT, "csr: null ptr");
+  hipStream_t st = (hipStream_t)stream;
+  if (E == 0) {
+    hipLaunchKernelGGL(fill_zero_i32_kernel, dim3((unsigned)((N + 2 + 255) / 256)), dim3(256), 0, st, ptr, N + 2);
+    return check_hip(hipGetLastError(), "csr fill");
+  }
+  if (!keys || !order || !workspace) return fail(ICTC_ERR_ARGUMENT, "csr: null operand");
+  const int64_t need = ictc_csr_workspace_bytes(E, N);
+  if (workspace_bytes < need)
+    return fail(ICTC_ERR_ARGUMENT, "csr: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)need);
+  char* ws = (char*)workspace;
+  const size_t slab = align256(sizeof(int32_t) * (size_t)E);
+  int32_t* k_in = (int32_t*)ws;
+  int32_t* k_out = (int32_t*)(ws + slab);
+  int32_t* ids = (int32_t*)(ws + 2 * slab);
+  void* temp = ws + 3 * slab;
+  size_t temp_bytes = sort_temp_bytes(E, N);
+  hipLaunchKernelGGL(csr_keys_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, st, keys, E, N, k_in, ids);
+  if (int rc = check_hip(hipGetLastError(), "csr keys")) return rc;
+  // Radix sort is stable: equal keys keep increasing edge order.
+  if (int rc = check_hip(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, k_in, k_out, ids, order, (int)E, 0,
+                                                            key_bits(N), st),
+                         "csr sort"))
+    return rc;
+  hipLaunchKernelGGL(csr_ptr_kernel, dim3((unsigned)((N + 2 + 255) / 256)), dim3(256), 0, st, k_out, E, N, ptr);
+  return check_hip(hipGetLastError(), "csr ptr");
+}
+
+int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                 const float* mask, const int64_t* src, int64_t N, int64_t E, const int32_t* dptr,
+                 const int32_t* dorder, float* out, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (N == 0) return ICTC_OK;
+  if (!x || !out || !dptr || (E > 0 && (!sh || !g || !src)))
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fwd: null operand");
+  const ictc::TpShape s{li, le, lo, C};
+  return check_hip(ictc::launch_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C), src, ictc::Csr{dptr, dorder}, out,
+                                        (hipStream_t)stream),
+                   "ictc_msg_fwd launch");
+}
+
+int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                 const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
+                 const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
+                 const float* grad, float* dx, float* dsh, float* dg, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (E == 0 && dx) {
+    const int64_t n = N * (int64_t)(C * (li + 1) * (li + 1));
+    if (n == 0) return ICTC_OK;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, dx, n);
+    return check_hip(hipGetLastError(), "dx fill");
+  }
+  if (N == 0 && E == 0) return ICTC_OK;
+  if (!x || !sh || !g || !src || !dst || !grad || !dptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: null operand");
+  if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: dfeatures needs the source CSR");
+  const ictc::TpShape s{li, le, lo, C};
+  return check_hip(ictc::launch_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder},
+                                        ictc::Csr{sptr, sorder}, grad, dx, dsh, dg, (hipStream_t)stream),
+                   "ictc_msg_bwd launch");
+}
+
+int ictc_sh_fwd(const float* n, int64_t E, int lmax, float* out, void* stream) {
+  if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "harmonics lmax=%d outside 0..3", lmax);
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (E == 0) return ICTC_OK;
+  if (!n || !out) return fail(ICTC_ERR_ARGUMENT, "ictc_sh_fwd: null operand");
+  const dim3 grid((unsigned)((E + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL(ictc::sh_fwd_kernel<0>, grid, dim3(256), 0, st, n, E, out); break;
+    case 1: hipLaunchKernelGGL(ictc::sh_fwd_kernel<1>, grid, dim3(256), 0, st, n, E, out); break;
+    case 2: hipLaunchKernelGGL(ictc::sh_fwd_kernel<2>, grid, dim3(256), 0, st, n, E, out); break;
+    default: hipLaunchKernelGGL(ictc::sh_fwd_kernel<3>, grid, dim3(256), 0, st, n, E, out); break;
+  }
+  return check_hip(hipGetLastError(), "ictc_sh_fwd launch");
+}
+
+int ictc_sh_bwd(const float* n, const float* grad, int64_t E, int lmax, float* dn, void* stream) {
+  if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "harmonics lmax=%d outside 0..3", lmax);
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (E == 0) return ICTC_OK;
+  if (!n || !grad || !dn) return fail(ICTC_ERR_ARGUMENT, "ictc_sh_bwd: null operand");
+  const dim3 grid((unsigned)((E + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL(ictc::sh_bwd_kernel<0>, grid, dim3(256), 0, st, n, grad, E, dn); break;
+    case 1: hipLaunchKernelGGL(ictc::sh_bwd_kernel<1>, grid, dim3(256), 0, st, n, grad, E, dn); break;
+    case 2: hipLaunchKernelGGL(ictc::sh_bwd_kernel<2>, grid, dim3(256), 0, st, n, grad, E, dn); break;
+    default: hipLaunchKernelGGL(ictc::sh_bwd_kernel<3>, grid, dim3(256), 0, st, n, grad, E, dn); break;
+  }
+  return check_hip(hipGetLastError(), "ictc_sh_bwd launch");
+}
+
+int ictc_sh_jvp(const float* n, const float* hn, int64_t E, int lmax, float* out, void* stream) {
+  if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "harmonics lmax=%d outside 0..3", lmax);
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (E == 0) return ICTC_OK;
+  if (!n || !hn || !out) return fail(ICTC_ERR_ARGUMENT, "ictc_sh_jvp: null operand");
+  const dim3 grid((unsigned)((E + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL(ictc::sh_jvp_kernel<0>, grid, dim3(256), 0, st, n, hn, E, out); break;
+    case 1: hipLaunchKernelGGL(ictc::sh_jvp_kernel<1>, grid, dim3(256), 0, st, n, hn, E, out); break;
+    case 2: hipLaunchKernelGGL(ictc::sh_jvp_kernel<2>, grid, dim3(256), 0, st, n, hn, E, out); break;
+    default: hipLaunchKernelGGL(ictc::sh_jvp_kernel<3>, grid, dim3(256), 0, st, n, hn, E, out); break;
+  }
+  return check_hip(hipGetLastError(), "ictc_sh_jvp launch");
+}
+
+int ictc_sh_hvp(const float* n, const float* grad, const float* hn, int64_t E, int lmax, float* out, void* stream) {
+  if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "harmonics lmax=%d outside 0..3", lmax);
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (E == 0) return ICTC_OK;
+  if (!n || !grad || !hn || !out) return fail(ICTC_ERR_ARGUMENT, "ictc_sh_hvp: null operand");
+  const dim3 grid((unsigned)((E + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL(ictc::sh_hvp_kernel<0>, grid, dim3(256), 0, st, n, grad, hn, E, out); break;
+    case 1: hipLaunchKernelGGL(ictc::sh_hvp_kernel<1>, grid, dim3(256), 0, st, n, grad, hn, E, out); break;
+    case 2: hipLaunchKernelGGL(ictc::sh_hvp_kernel<2>, grid, dim3(256), 0, st, n, grad, hn, E, out); break;
+    default: hipLaunchKernelGGL(ictc::sh_hvp_kernel<3>, grid, dim3(256), 0, st, n, grad, hn, E, out); break;
+  }
+  return check_hip(hipGetLastError(), "ictc_sh_hvp launch");
+}
+
+}  // extern "C"

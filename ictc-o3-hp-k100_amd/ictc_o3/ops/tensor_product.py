@@ -1,0 +1,288 @@
+"""Autograd Functions over the per-edge TP and the CSR graph message kernels.
+
+Both maps are multilinear in (features x, harmonics Y, gates g) and linear in
+the upstream cotangent go.  Writing F(x, Y, g) for the forward and
+A_x, A_Y, A_g for its first adjoints (each bilinear in the remaining operand
+and go), the mixed second derivatives needed for force-loss training follow
+from the same kernels with one operand swapped for its tangent
+(the algebra of the reference's _second_raw, ops/fused_message.py:677-729,
+and generated_message_second.py:78-204):
+
+  d go  = F(hx, Y, g) + F(x, hY, g) + F(x, Y, hg)
+  d x   = A_x(hY, g, go) + A_x(Y, hg, go)
+  d Y   = A_Y(hx, g, go) + A_Y(x, hg, go)
+  d g   = A_g(hx, Y, go) + A_g(x, hY, go)
+
+Every term is itself an autograd Function, so derivatives of any order stay
+on the HIP kernels (the reference recomputes third and higher orders through
+a differentiable torch path, operators.py:85-103).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from ictc_o3 import _native as nat
+
+
+@dataclass(frozen=True)
+class TpSpec:
+    """Static description of one natural-parity TP (degrees, channels, fixed weight)."""
+    li: int
+    le: int
+    lo: int
+    channels: int
+    num_paths: int
+    out_components: int
+    weight: Optional[torch.Tensor] = None   # [P, C] fixed coefficients, None = unit
+
+    @property
+    def nx(self):
+        return (self.li + 1) ** 2
+
+    @property
+    def ny(self):
+        return (self.le + 1) ** 2
+
+
+def make_spec(li, le, lo, channels, weight=None) -> TpSpec:
+    P, NO = nat.tp_shape(li, le, lo)
+    return TpSpec(li, le, lo, channels, P, NO, weight)
+
+
+def _w(spec):
+    return nat.ptr(spec.weight) if spec.weight is not None else None
+
+
+def _c(t):
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _add(a, b):
+    if a is None:
+        return b
+    if b is None:
+        return a
+    return a + b
+
+
+# ---------------------------------------------------------------------------
+# Per-edge TP
+# ---------------------------------------------------------------------------
+
+
+def _edge_fwd_raw(spec, x, sh, g):
+    E = x.shape[0]
+    out = x.new_empty(E, spec.out_components * spec.channels)
+    nat.call("ictc_tp_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+             _w(spec), E, nat.ptr(out), nat.stream_of(x))
+    return out
+
+
+def _edge_bwd_raw(spec, x, sh, g, go, need):
+    E = x.shape[0]
+    dx = torch.empty_like(x) if need[0] else None
+    dsh = torch.empty_like(sh) if need[1] else None
+    dg = torch.empty_like(g) if need[2] else None
+    nat.call("ictc_tp_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+             _w(spec), nat.ptr(go), E, nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.stream_of(x))
+    return dx, dsh, dg
+
+
+class EdgeTP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, sh, g, spec):
+        ctx.set_materialize_grads(False)
+        ctx.spec = spec
+        x, sh, g = _c(x), _c(sh), _c(g)
+        ctx.save_for_backward(x, sh, g)
+        return _edge_fwd_raw(spec, x, sh, g)
+
+    @staticmethod
+    def backward(ctx, go):
+        if go is None:
+            return None, None, None, None
+        x, sh, g = ctx.saved_tensors
+        need = tuple(ctx.needs_input_grad[:3])
+        if not any(need):
+            return None, None, None, None
+        dx, dsh, dg = EdgeTPAdjoint.apply(x, sh, g, _c(go), ctx.spec, need)
+        return dx, dsh, dg, None
+
+
+def edge_tp(x, sh, g, spec):
+    return EdgeTP.apply(x, sh, g, spec)
+
+
+def edge_adjoint(x, sh, g, go, spec, need):
+    return EdgeTPAdjoint.apply(x, sh, g, go, spec, need)
+
+
+class EdgeTPAdjoint(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, sh, g, go, spec, need):
+        ctx.set_materialize_grads(False)
+        ctx.spec = spec
+        x, sh, g, go = _c(x), _c(sh), _c(g), _c(go)
+        ctx.save_for_backward(x, sh, g, go)
+        return _edge_bwd_raw(spec, x, sh, g, go, need)
+
+    @staticmethod
+    def backward(ctx, hx, hsh, hg):
+        x, sh, g, go = ctx.saved_tensors
+        spec = ctx.spec
+        nx, nsh, ng, ngo = ctx.needs_input_grad[:4]
+        dx = dsh = dg = dgo = None
+        if ngo:
+            if hx is not None:
+                dgo = _add(dgo, edge_tp(hx, sh, g, spec))
+            if hsh is not None:
+                dgo = _add(dgo, edge_tp(x, hsh, g, spec))
+            if hg is not None:
+                dgo = _add(dgo, edge_tp(x, sh, hg, spec))
+        if nx:
+            if hsh is not None:
+                dx = _add(dx, edge_adjoint(x, hsh, g, go, spec, (True, False, False))[0])
+            if hg is not None:
+                dx = _add(dx, edge_adjoint(x, sh, hg, go, spec, (True, False, False))[0])
+        if nsh:
+            if hx is not None:
+                dsh = _add(dsh, edge_adjoint(hx, sh, g, go, spec, (False, True, False))[1])
+            if hg is not None:
+                dsh = _add(dsh, edge_adjoint(x, sh, hg, go, spec, (False, True, False))[1])
+        if ng:
+            if hx is not None:
+                dg = _add(dg, edge_adjoint(hx, sh, g, go, spec, (False, False, True))[2])
+            if hsh is not None:
+                dg = _add(dg, edge_adjoint(x, hsh, g, go, spec, (False, False, True))[2])
+        return dx, dsh, dg, dgo, None, None
+
+
+# ---------------------------------------------------------------------------
+# CSR topology and graph message
+# ---------------------------------------------------------------------------
+
+
+class Csr:
+    """Stable key-sorted CSR of an edge list (int32 ptr [N+2] and order [E])."""
+
+    def __init__(self, keys: torch.Tensor, nodes: int):
+        E = keys.numel()
+        self.nodes = nodes
+        self.ptr = torch.empty(nodes + 2, dtype=torch.int32, device=keys.device)
+        self.order = torch.empty(max(E, 1), dtype=torch.int32, device=keys.device)
+        ws_bytes = int(nat.lib().ictc_csr_workspace_bytes(E, nodes))
+        if ws_bytes < 0:
+            raise ValueError("graph too large for int32 CSR indices")
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=keys.device)
+        nat.call("ictc_csr_build", nat.ptr(keys), E, nodes, nat.ptr(self.ptr), nat.ptr(self.order),
+                 nat.ptr(ws), ws_bytes, nat.stream_of(keys))
+
+
+class Topology:
+    """Receiver-sorted CSR (forward, gate / harmonic adjoints) and source-sorted CSR (feature adjoint)."""
+
+    def __init__(self, src: torch.Tensor, dst: torch.Tensor, nodes: int):
+        self.src, self.dst, self.nodes = _c(src), _c(dst), nodes
+        self.by_dst = Csr(self.dst, nodes)
+        self._by_src = None
+
+    @property
+    def by_src(self):
+        if self._by_src is None:
+            self._by_src = Csr(self.src, self.nodes)
+        return self._by_src
+
+
+def _msg_fwd_raw(spec, topo, x, sh, g, mask):
+    N, E = x.shape[0], sh.shape[0]
+    out = x.new_empty(N, spec.out_components * spec.channels)
+    nat.call("ictc_msg_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+             _w(spec), nat.ptr(mask), nat.ptr(topo.src), N, E, nat.ptr(topo.by_dst.ptr),
+             nat.ptr(topo.by_dst.order), nat.ptr(out), nat.stream_of(x))
+    return out
+
+
+def _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need):
+    N, E = x.shape[0], sh.shape[0]
+    dx = torch.empty_like(x) if need[0] else None
+    dsh = torch.empty_like(sh) if need[1] else None
+    dg = torch.empty_like(g) if need[2] else None
+    sp = topo.by_src if need[0] else None
+    nat.call("ictc_msg_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+             _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
+             nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
+             nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(go),
+             nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.stream_of(x))
+    return dx, dsh, dg
+
+
+class Message(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, sh, g, spec, topo, mask):
+        ctx.set_materialize_grads(False)
+        ctx.spec, ctx.topo, ctx.mask = spec, topo, mask
+        x, sh, g = _c(x), _c(sh), _c(g)
+        ctx.save_for_backward(x, sh, g)
+        return _msg_fwd_raw(spec, topo, x, sh, g, mask)
+
+    @staticmethod
+    def backward(ctx, go):
+        if go is None:
+            return (None,) * 6
+        x, sh, g = ctx.saved_tensors
+        need = tuple(ctx.needs_input_grad[:3])
+        if not any(need):
+            return (None,) * 6
+        dx, dsh, dg = MessageAdjoint.apply(x, sh, g, _c(go), ctx.spec, ctx.topo, ctx.mask, need)
+        return dx, dsh, dg, None, None, None
+
+
+def message(x, sh, g, spec, topo, mask=None):
+    return Message.apply(x, sh, g, spec, topo, mask)
+
+
+def message_adjoint(x, sh, g, go, spec, topo, mask, need):
+    return MessageAdjoint.apply(x, sh, g, go, spec, topo, mask, need)
+
+
+class MessageAdjoint(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, sh, g, go, spec, topo, mask, need):
+        ctx.set_materialize_grads(False)
+        ctx.spec, ctx.topo, ctx.mask = spec, topo, mask
+        x, sh, g, go = _c(x), _c(sh), _c(g), _c(go)
+        ctx.save_for_backward(x, sh, g, go)
+        return _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need)
+
+    @staticmethod
+    def backward(ctx, hx, hsh, hg):
+        x, sh, g, go = ctx.saved_tensors
+        spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
+        nx, nsh, ng, ngo = ctx.needs_input_grad[:4]
+        dx = dsh = dg = dgo = None
+        if ngo:
+            if hx is not None:
+                dgo = _add(dgo, message(hx, sh, g, spec, topo, mask))
+            if hsh is not None:
+                dgo = _add(dgo, message(x, hsh, g, spec, topo, mask))
+            if hg is not None:
+                dgo = _add(dgo, message(x, sh, hg, spec, topo, mask))
+        if nx:
+            if hsh is not None:
+                dx = _add(dx, message_adjoint(x, hsh, g, go, spec, topo, mask, (True, False, False))[0])
+            if hg is not None:
+                dx = _add(dx, message_adjoint(x, sh, hg, go, spec, topo, mask, (True, False, False))[0])
+        if nsh:
+            if hx is not None:
+                dsh = _add(dsh, message_adjoint(hx, sh, g, go, spec, topo, mask, (False, True, False))[1])
+            if hg is not None:
+                dsh = _add(dsh, message_adjoint(x, sh, hg, go, spec, topo, mask, (False, True, False))[1])
+        if ng:
+            if hx is not None:
+                dg = _add(dg, message_adjoint(hx, sh, g, go, spec, topo, mask, (False, False, True))[2])
+            if hsh is not None:
+                dg = _add(dg, message_adjoint(x, hsh, g, go, spec, topo, mask, (False, False, True))[2])
+        return dx, dsh, dg, dgo, None, None, None, None

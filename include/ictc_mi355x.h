@@ -1,0 +1,126 @@
+/* C ABI of the MI355X (gfx950) ICTC-O3 equivariant-operator library.
+ *
+ * libictc_mi355x.so exports these entry points.  Every pointer is a device
+ * pointer (HBM) unless stated otherwise; every size is int64_t; `stream` is a
+ * hipStream_t passed as void* (nullptr = the null stream).  Calls only enqueue
+ * work on `stream` (no host synchronisation, no allocation) and return 0 on
+ * success or a negative code; ictc_last_error() then describes the failure
+ * (thread-local, valid until the next failing call on the same thread).
+ *
+ * Layouts (FP32, row-major, "component-major, channel-minor" = the reference's
+ * packed ir_mul layout, operators.py:283-308):
+ *   features [rows, C*(LI+1)^2]  degree l, component m at ((l*l+m)*C + c)
+ *   harmonics [E, (LE+1)^2]      degree l, component m at (l*l+m)
+ *   gates    [E, P*C]            path p (natural-parity order) at (p*C + c)
+ *   weight   [P, C] or NULL      fixed per-path coefficients (NULL = all ones)
+ *   output   [rows, C*NO]        degree-major, path slot, then [2l+1, C]
+ * Paths are the natural-parity triangle set of (LI, LE, LO) in the order of
+ * operators.py:206-207; supported degrees are 0..3 and channels 1..256.
+ */
+#ifndef ICTC_MI355X_H
+#define ICTC_MI355X_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ICTC_OK = 0,
+  ICTC_ERR_ARGUMENT = -1,    /* invalid shape / degree / channel count / null pointer */
+  ICTC_ERR_UNSUPPORTED = -2, /* configuration outside the compiled coverage */
+  ICTC_ERR_RUNTIME = -3      /* HIP launch / runtime failure */
+};
+
+/* Library version (major*10000 + minor*100 + patch). */
+int ictc_version(void);
+
+/* Description of the last failure on the calling thread. */
+const char* ictc_last_error(void);
+
+/* Number of paths and output components (units of C) of a natural-parity TP;
+ * returns a negative code for unsupported degrees.  Host-only. */
+int ictc_tp_shape(int input_lmax, int edge_lmax, int output_lmax, int* num_paths, int* out_components);
+
+/* ---- Per-edge tensor product -------------------------------------------
+ * Replaces the generated_forward launch of _Edge.forward
+ * (ictc_o3/operators.py:106-127 -> backends/k100/generated_cartesian_message.py:376-383):
+ *   out[e] = sum_p gate[e,p] * w[p] * CG_p(features[e], harmonics[e])         */
+int ictc_tp_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                const float* features, const float* harmonics, const float* gates,
+                const float* weight, int64_t edges, float* out, void* stream);
+
+/* First adjoint of ictc_tp_fwd; replaces generated_adjoint of _Edge.backward
+ * (operators.py:129-158 -> generated_cartesian_message.py:386-407).  Any of
+ * dfeatures [E, C*(LI+1)^2], dharmonics [E,(LE+1)^2], dgates [E,P*C] may be
+ * NULL to skip that role (required_gradients pruning,
+ * autograd/adjoint_requirements.py:13-27).  Outputs are overwritten.          */
+int ictc_tp_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                const float* features, const float* harmonics, const float* gates,
+                const float* weight, const float* grad, int64_t edges,
+                float* dfeatures, float* dharmonics, float* dgates, void* stream);
+
+/* ---- Receiver / source sorted CSR ---------------------------------------
+ * Replaces topology() (backends/k100/generated_csr_forward.py:22-31: bincount,
+ * cumsum, stable argsort).  keys [E] int64 node ids; builds
+ *   ptr   [nodes + 2] int32: edges of node n are order[ptr[n] .. ptr[n+1]);
+ *         ptr[nodes] .. ptr[nodes+1] holds edges whose key is out of range;
+ *   order [E] int32, a stable sort of edge ids by key.
+ * workspace must hold ictc_csr_workspace_bytes(edges, nodes) bytes.            */
+int64_t ictc_csr_workspace_bytes(int64_t edges, int64_t nodes);
+int ictc_csr_build(const int64_t* keys, int64_t edges, int64_t nodes, int32_t* ptr,
+                   int32_t* order, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---- Graph message (gather -> TP -> gate -> mask -> receiver sum) --------
+ * Replaces PackedGraphMessage.forward's native launches
+ * (operators.py:382-409 -> ops/rematerialized_message.py:166-205 ->
+ * generated_csr_forward.py:187-192 / generated_cartesian_message.py:376-383):
+ *   out[n] = sum_{e: dst[e]=n} mask[e] * TP(features[src[e]], harmonics[e], gates[e])
+ * features [nodes, C*(LI+1)^2]; out [nodes, C*NO] is fully overwritten.
+ * dst_ptr/dst_order: ictc_csr_build over dst (dst_order NULL = edges already
+ * sorted by dst with no out-of-range ids).  mask may be NULL.  Deterministic:
+ * one owner per output row, no floating-point atomics.                        */
+int ictc_msg_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                 const float* features, const float* harmonics, const float* gates,
+                 const float* weight, const float* mask, const int64_t* src,
+                 int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                 float* out, void* stream);
+
+/* First adjoint of ictc_msg_fwd; replaces _first
+ * (ops/rematerialized_message.py:25-83 -> generated_adjoint /
+ * generated_csr_adjoint.py:199-293 source_adjoint).  dfeatures uses the
+ * source-sorted CSR (src_ptr/src_order from ictc_csr_build over src);
+ * dharmonics and dgates use the receiver-sorted CSR.  NULL outputs are
+ * skipped; non-NULL outputs are fully overwritten.                            */
+int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                 const float* features, const float* harmonics, const float* gates,
+                 const float* weight, const float* mask, const int64_t* src, const int64_t* dst,
+                 int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                 const int32_t* src_ptr, const int32_t* src_order, const float* grad,
+                 float* dfeatures, float* dharmonics, float* dgates, void* stream);
+
+/* ---- Direction harmonics --------------------------------------------------
+ * Replaces direction_harmonics (operators.py:471-490 ->
+ * ops/generated_direction_harmonics.py:152-170, backends/k100/
+ * hip_direction_harmonics.py:35-63): directions [E,3] -> Y [E,(lmax+1)^2]
+ * packed by degree, Y_l = s_l t_l(n) G_l B_l (ictd_irreps.py:1153-1208).      */
+int ictc_sh_fwd(const float* directions, int64_t edges, int lmax, float* out, void* stream);
+/* ddirections [E,3] = J^T grad (overwritten). */
+int ictc_sh_bwd(const float* directions, const float* grad, int64_t edges, int lmax,
+                float* ddirections, void* stream);
+
+/* Second-order pieces of the harmonic map, used by force-loss training (the
+ * mixed derivatives of hip_direction_harmonics.py's adjoint,
+ * ops/generated_direction_harmonics.py:112-149):
+ *   ictc_sh_jvp: out [E,(lmax+1)^2] = J(n) h            (h [E,3])
+ *   ictc_sh_hvp: out [E,3] = Hess_n(sum_k grad_k Y_k) h  (grad [E,(lmax+1)^2]) */
+int ictc_sh_jvp(const float* directions, const float* tangent, int64_t edges, int lmax, float* out,
+                void* stream);
+int ictc_sh_hvp(const float* directions, const float* grad, const float* tangent, int64_t edges, int lmax,
+                float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ICTC_MI355X_H */

@@ -1,0 +1,103 @@
+"""Host-side checks: tables, generated code, C-ABI exports, API validation (no GPU compute)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import ictc_oracle as orc
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_product_tables_match_oracle():
+    from ictc_o3.basis import tables
+    for l1 in range(4):
+        for l2 in range(4):
+            for l3 in range(7):
+                assert np.abs(tables.coupling_component(l1, l2, l3) - orc.cg_component(l1, l2, l3)).max() < 1e-13
+    for l in range(4):
+        mono, coef = tables.harmonic_polynomials(l)
+        expect = orc.direction_projection(l) * orc.direction_scale(l) * orc.multinomials(l)[:, None]
+        assert np.abs(coef - expect).max() < 1e-13
+
+
+def test_product_path_table_offsets():
+    from ictc_o3.basis import tables
+    T = tables.PathTable(tables.natural_paths(2, 2, 2))
+    assert T.out_components == 35
+    _, offsets, counts = orc.path_tables(orc.natural_paths(2, 2, 2))
+    assert T.slot == offsets and T.counts == counts
+
+
+def _declared_symbols():
+    text = open(os.path.join(ROOT, "include", "ictc_mi355x.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ictc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    from ictc_o3 import _native
+    path = _native.library_path()
+    if not os.path.exists(path):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(path)
+    declared = _declared_symbols()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.exported_symbols())
+    assert _native.lib().ictc_version() == 100
+
+
+def test_host_only_entry_points():
+    from ictc_o3 import _native
+    if not os.path.exists(_native.library_path()):
+        pytest.skip("library not built")
+    assert _native.tp_shape(2, 2, 2) == (11, 35)
+    assert _native.tp_shape(2, 3, 3) == (17, 71)
+    assert _native.tp_shape(0, 2, 2) == (3, 9)
+    with pytest.raises(ValueError):
+        _native.tp_shape(4, 0, 4)
+    # invalid arguments are rejected before any device work
+    with pytest.raises(ValueError):
+        _native.call("ictc_tp_fwd", 2, 2, 2, 300, None, None, None, None, 1, None, None)
+    with pytest.raises(ValueError):
+        _native.call("ictc_sh_fwd", None, 4, 5, None, None)
+    assert _native.lib().ictc_csr_workspace_bytes(1000, 10) > 0
+    assert _native.lib().ictc_csr_workspace_bytes(-1, 10) < 0
+
+
+def test_generated_header_covers_natural_configs():
+    import sys
+    sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-k100_amd", "csrc"))
+    import gen_tables
+    s = gen_tables.tp_struct(2, 2, 2)
+    assert "NNZ = 93" in s and "NO = 35" in s and "P = 11" in s
+
+
+def test_api_validation_cpu():
+    from ictc_o3 import EdgeTensorProduct, direction_harmonics
+    with pytest.raises(ValueError, match="CUDA device"):
+        EdgeTensorProduct.create(input_lmax=2, edge_lmax=2, channels=32, device="cpu")
+    with pytest.raises(ValueError, match="nonnegative"):
+        EdgeTensorProduct.create(input_lmax=-1, edge_lmax=2, channels=32, device="cuda")
+    with pytest.raises(ValueError, match="positive"):
+        EdgeTensorProduct.create(input_lmax=1, edge_lmax=2, channels=0, device="cuda")
+    with pytest.raises(ValueError, match=r"\[E,3\]"):
+        direction_harmonics(torch.zeros(3, 2), 2)
+    with pytest.raises(ValueError, match="policy"):
+        direction_harmonics(torch.zeros(3, 3), 2, policy="bogus")
+    with pytest.raises(ValueError, match="CUDA FP32"):
+        direction_harmonics(torch.zeros(3, 3), 2)
+
+
+def test_tp_module_path_enumeration():
+    from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
+    tp = EdgeWeightedPathPreservingTensorProduct(8, 2, allowed_paths=orc.natural_paths(2, 2, 2))
+    assert tp.paths == orc.natural_paths(2, 2, 2)
+    assert tp.path_counts_by_l == {0: 3, 1: 4, 2: 4}
+    assert tp.kernel_degrees() == (2, 2, 2)
+    assert tp.weight.shape == (11, 8)

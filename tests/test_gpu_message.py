@@ -1,0 +1,146 @@
+"""GPU parity of the CSR graph message (PackedGraphMessage / GraphMessage) vs the float64 oracle.
+
+Tolerance 1e-5 relative (max-norm).  Also: bitwise determinism across runs,
+unsorted edge lists, masks, isolated nodes, empty graphs, out-of-range
+edge ids contributing nothing.
+"""
+import pytest
+import torch
+
+import ictc_oracle as orc
+from helpers import rel_err, unit_vectors
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+
+
+def _graph(N, E, C, li, le, lo, seed, sort=False, mask=False):
+    g = torch.Generator().manual_seed(seed)
+    P = len(orc.natural_paths(li, le, lo))
+    feats = torch.randn(N, C * (li + 1) ** 2, generator=g, dtype=torch.float64)
+    sh = torch.cat(orc.direction_harmonics(unit_vectors(E, seed + 1), le), -1)
+    gates = torch.randn(E, P * C, generator=g, dtype=torch.float64)
+    src = torch.randint(0, N, (E,), generator=g)
+    dst = torch.randint(0, N, (E,), generator=g)
+    if sort:
+        o = torch.argsort(dst, stable=True)
+        src, dst, sh, gates = src[o], dst[o], sh[o], gates[o]
+    m = (torch.rand(E, generator=g) > 0.3).double() if mask else None
+    return feats, sh, gates, src, dst, m
+
+
+CASES = [(64, 2000, 64, 2, 2, 2, False, False), (50, 700, 32, 2, 2, 2, True, True),
+         (40, 500, 128, 2, 3, 3, False, True), (30, 300, 128, 0, 3, 3, True, False),
+         (33, 400, 64, 0, 2, 2, False, False), (20, 150, 17, 1, 2, 2, False, True)]
+
+
+@pytest.mark.parametrize("N,E,C,li,le,lo,sort,mask", CASES)
+def test_message_forward_backward(device, N, E, C, li, le, lo, sort, mask):
+    from ictc_o3 import PackedGraphMessage
+    op = PackedGraphMessage.create(channels=C, input_lmax=li, edge_lmax=le, output_lmax=lo, device=device)
+    f64, sh64, g64, src, dst, m64 = _graph(N, E, C, li, le, lo, 10 + N, sort, mask)
+    ref_in = [t.clone().requires_grad_(True) for t in (f64, sh64, g64)]
+    ref = orc.message_packed(*ref_in, src, dst, m64, li, le, lo, C)
+    x = [t.float().to(device).requires_grad_(True) for t in (f64, sh64, g64)]
+    m = None if m64 is None else m64.float().to(device)
+    out = op(*x, src.to(device), dst.to(device), m)
+    assert rel_err(out, ref) < TOL
+    go = torch.randn(ref.shape, generator=torch.Generator().manual_seed(3), dtype=torch.float64)
+    torch.autograd.backward(ref, go)
+    torch.autograd.backward(out, go.float().to(device))
+    for a, b in zip(x, ref_in):
+        assert rel_err(a.grad, b.grad) < TOL
+
+
+@pytest.mark.parametrize("C,li,le,lo", [(64, 2, 2, 2), (128, 2, 3, 3)])
+def test_message_mixed_second_derivatives(device, C, li, le, lo):
+    from ictc_o3 import PackedGraphMessage
+    N, E = 24, 200
+    op = PackedGraphMessage.create(channels=C, input_lmax=li, edge_lmax=le, output_lmax=lo, device=device)
+    f64, sh64, g64, src, dst, m64 = _graph(N, E, C, li, le, lo, 77, mask=True)
+    gen = torch.Generator().manual_seed(78)
+    go64 = torch.randn(N, op.output_width, generator=gen, dtype=torch.float64)
+    v = [torch.randn(t.shape, generator=gen, dtype=torch.float64) for t in (f64, sh64, g64)]
+
+    def run(tensors, gov, fn):
+        xs = [t.clone().requires_grad_(True) for t in tensors]
+        gov = gov.clone().requires_grad_(True)
+        grads = torch.autograd.grad(fn(*xs), xs, gov, create_graph=True)
+        s = sum((gr * vv.to(gr)).sum() for gr, vv in zip(grads, v))
+        return torch.autograd.grad(s, xs + [gov])
+
+    ref = run((f64, sh64, g64), go64,
+              lambda a, b, c: orc.message_packed(a, b, c, src, dst, m64, li, le, lo, C))
+    s, d, m = src.to(device), dst.to(device), m64.float().to(device)
+    got = run([t.float().to(device) for t in (f64, sh64, g64)], go64.float().to(device),
+              lambda a, b, c: op(a, b, c, s, d, m))
+    for name, a, b in zip(("dx", "dsh", "dg", "dgo"), got, ref):
+        assert rel_err(a, b) < TOL, name
+
+
+def test_message_deterministic_bitwise(device):
+    from ictc_o3 import PackedGraphMessage
+    op = PackedGraphMessage.create(channels=64, input_lmax=2, edge_lmax=2, device=device)
+    f64, sh64, g64, src, dst, _ = _graph(100, 5000, 64, 2, 2, 2, 5)
+    x = [t.float().to(device).requires_grad_(True) for t in (f64, sh64, g64)]
+    results = []
+    for _ in range(2):
+        out = op(*x, src.to(device), dst.to(device))
+        grads = torch.autograd.grad(out, x, torch.ones_like(out))
+        results.append((out, *grads))
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
+
+
+def test_message_isolated_nodes_and_empty(device):
+    from ictc_o3 import PackedGraphMessage
+    op = PackedGraphMessage.create(channels=32, input_lmax=2, edge_lmax=2, device=device)
+    N = 10
+    f = torch.randn(N, 32 * 9, device=device, requires_grad=True)
+    e0 = torch.zeros(0, dtype=torch.int64, device=device)
+    out = op(f, torch.zeros(0, 9, device=device), torch.zeros(0, op.gate_width, device=device), e0, e0)
+    assert out.shape == (N, op.output_width) and torch.count_nonzero(out) == 0
+    out.sum().backward()
+    assert torch.count_nonzero(f.grad) == 0
+    # all edges into node 0: every other output row is exactly zero
+    f64, sh64, g64, src, _, _ = _graph(N, 50, 32, 2, 2, 2, 6)
+    dst = torch.zeros(50, dtype=torch.int64)
+    out = op(f64.float().to(device), sh64.float().to(device), g64.float().to(device), src.to(device), dst.to(device))
+    ref = orc.message_packed(f64, sh64, g64, src, dst, None, 2, 2, 2, 32)
+    assert rel_err(out, ref) < TOL
+    assert torch.count_nonzero(out[1:]) == 0
+
+
+def test_message_out_of_range_ids_contribute_nothing(device):
+    from ictc_o3 import PackedGraphMessage
+    op = PackedGraphMessage.create(channels=32, input_lmax=2, edge_lmax=2, device=device)
+    N = 12
+    f64, sh64, g64, src, dst, _ = _graph(N, 80, 32, 2, 2, 2, 7)
+    bad_src, bad_dst = src.clone(), dst.clone()
+    bad_src[::7] = N + 5
+    bad_dst[3::11] = -1
+    keep = (bad_src < N) & (bad_dst >= 0)
+    ref = orc.message_packed(f64, sh64[keep], g64[keep], src[keep], dst[keep], None, 2, 2, 2, 32)
+    x = [t.float().to(device).requires_grad_(True) for t in (f64, sh64, g64)]
+    out = op(*x, bad_src.to(device), bad_dst.to(device))
+    assert rel_err(out, ref) < TOL
+    out.sum().backward()
+    assert torch.count_nonzero(x[2].grad[~keep.to(device)]) == 0
+    assert torch.count_nonzero(x[1].grad[~keep.to(device)]) == 0
+
+
+def test_graph_message_dict_api(device):
+    from ictc_o3 import EdgeTensorProduct, GraphMessage
+    C, N, E = 16, 20, 120
+    edge = EdgeTensorProduct.create(input_lmax=2, edge_lmax=2, channels=C, device=device)
+    gm = GraphMessage(edge.tp, input_lmax=2, edge_lmax=2)
+    f64, sh64, g64, src, dst, _ = _graph(N, E, C, 2, 2, 2, 8)
+    blocks = orc.unpack_ir_mul(f64, C, 2)
+    feats = {l: blocks[l].float().to(device) for l in blocks}
+    harm = {l: sh64[:, l * l:(l + 1) ** 2].reshape(E, 1, 2 * l + 1).float().to(device) for l in range(3)}
+    out = gm(feats, harm, g64.float().to(device), src.to(device), dst.to(device))
+    ref = orc.message_packed(f64, sh64, g64, src, dst, None, 2, 2, 2, C)
+    paths = orc.natural_paths(2, 2, 2)
+    _, _, counts = orc.path_tables(paths)
+    packed = orc.pack_output({l: out[l].double().cpu() for l in out}, counts, C)
+    assert rel_err(packed, ref) < TOL
