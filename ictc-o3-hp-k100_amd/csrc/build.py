@@ -19,7 +19,8 @@ PKG = os.path.dirname(HERE)
 OUT_DIR = os.path.join(PKG, "ictc_o3", "_lib")
 LIB = os.path.join(OUT_DIR, "libictc_mi355x.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["capi.hip", "tp_edge.hip", "msg.hip"]
+SOURCES = ["capi.hip", "tp_edge.hip", "msg.hip", "sc.hip", "sc_part_low.hip", "sc_part_l3_t0.hip",
+           "sc_part_l3_t1.hip", "sc_part_l3_t2.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
          # Packed FP32 (v_pk_*_f32) stays off for all device code.
@@ -38,8 +39,10 @@ def _compile(src):
 
 def build(jobs: int | None = None) -> str:
     sys.path.insert(0, HERE)
+    import gen_sc
     import gen_tables
     gen_tables.generate(os.path.join(HERE, "generated", "ictc_tables.h"))
+    gen_sc.generate(os.path.join(HERE, "generated", "ictc_sc.h"))
     os.makedirs(BUILD_DIR, exist_ok=True)
     os.makedirs(OUT_DIR, exist_ok=True)
     jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 2)))

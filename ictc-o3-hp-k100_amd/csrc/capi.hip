@@ -125,6 +125,13 @@ __global__ void fill_zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
 
 }  // namespace
 
+namespace ictc {
+int set_error(int code, const char* msg) {
+  g_error = msg;
+  return code;
+}
+}  // namespace ictc
+
 extern "C" {
 
 int ictc_version(void) { return 100; }

@@ -36,6 +36,14 @@ _SIGNATURES = {
     "ictc_sh_bwd": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_jvp": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_hvp": (_i, [_p, _p, _p, _i64, _i, _p, _p]),
+    "ictc_sc_shape": (_i, [_i, _i, _i, _p, _p]),
+    "ictc_sc_workspace_bytes": (_i64, [_i, _i, _i, _i, _i64, _i]),
+    "ictc_sc_fwd": (_i, [_i, _i, _i, _i, _p, _p, _i, _p, _i64, _p, _p]),
+    "ictc_sc_bwd_x": (_i, [_i, _i, _i, _i, _p, _p, _i, _p, _i64, _p, _p, _p]),
+    "ictc_sc_bwd_w": (_i, [_i, _i, _i, _i, _p, _i, _i64, _p, _p, _p, _p, _p, _i64, _p]),
+    "ictc_sc_jvp": (_i, [_i, _i, _i, _i, _p, _p, _i, _p, _i64, _p, _p, _p]),
+    "ictc_sc_hvp": (_i, [_i, _i, _i, _i, _p, _p, _i, _p, _i64, _p, _p, _p, _p]),
+    "ictc_sc_bwd_w_jvp": (_i, [_i, _i, _i, _i, _p, _i, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
 }
 
 

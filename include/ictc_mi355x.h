@@ -120,6 +120,47 @@ int ictc_sh_jvp(const float* directions, const float* tangent, int64_t edges, in
 int ictc_sh_hvp(const float* directions, const float* grad, const float* tangent, int64_t edges, int lmax,
                 float* out, void* stream);
 
+/* ---- Symmetric contraction (bridge-U, correlation 1..3) -------------------
+ * Replaces the SC circuits of ICTDBridgeUSymmetricContractionSO3.forward
+ * (ictc_o3/ops/symmetric_contraction.py:98-147 -> factorized_contraction.py:
+ * 197-266 -> backends/k100/hip_circuit.py:28-115 run / :223 mixed / :248 reduce):
+ *   out[n, L, m, c] = sum_nu sum_p W(L,nu)[s_n, p, c] U(L,nu)[m, i1..inu, p] x[n,i1,c]..x[n,inu,c]
+ * with U the MACE coupling folded into the ICTC basis.  x [N, C*(lmax+1)^2]
+ * and out [N, C*sum_{L<=target}(2L+1)] use the packed component-major layout;
+ * species [N] int64 (out-of-range species give zero rows); weights is a host
+ * array of 12 device pointers, entry L*3 + (nu-1) -> W(L,nu) [S, P, C]
+ * (reference layout, _mace_symmetric_contraction.py:152-155), NULL where P=0.
+ * Compiled for (lmax, target_lmax) with lmax <= 2, target <= lmax, and
+ * lmax 3 with target 0..2; channels 1..4096.                                  */
+int ictc_sc_shape(int lmax, int target_lmax, int correlation, int* paths /* [12] */, int* num_weights);
+int ictc_sc_fwd(int lmax, int target_lmax, int correlation, int channels, const float* x, const int64_t* species,
+                int num_species, const float* const* weights, int64_t nodes, float* out, void* stream);
+/* dx = d(grad . out)/dx (overwritten). */
+int ictc_sc_bwd_x(int lmax, int target_lmax, int correlation, int channels, const float* x,
+                  const int64_t* species, int num_species, const float* const* weights, int64_t nodes,
+                  const float* grad, float* dx, void* stream);
+/* dW(L,nu)[s] = sum over nodes of species s (deterministic chunked reduction over
+ * the species-sorted CSR from ictc_csr_build(species, nodes, num_species)).
+ * workspace: ictc_sc_workspace_bytes(...) bytes.  dweights: 12 device pointers. */
+int64_t ictc_sc_workspace_bytes(int lmax, int target_lmax, int correlation, int channels, int64_t nodes,
+                                int num_species);
+int ictc_sc_bwd_w(int lmax, int target_lmax, int correlation, int channels, const float* x, int num_species,
+                  int64_t nodes, const float* grad, const int32_t* species_ptr, const int32_t* species_order,
+                  float* const* dweights, void* workspace, int64_t workspace_bytes, void* stream);
+/* Mixed second derivatives (force-loss training, hip_circuit.py:223):
+ *   jvp: out = J_x(out) h;  hvp: dx = Hess_x(grad . out) h;
+ *   bwd_w_jvp: dW = d/dW (grad . J_x(out) h).                                   */
+int ictc_sc_jvp(int lmax, int target_lmax, int correlation, int channels, const float* x, const int64_t* species,
+                int num_species, const float* const* weights, int64_t nodes, const float* tangent, float* out,
+                void* stream);
+int ictc_sc_hvp(int lmax, int target_lmax, int correlation, int channels, const float* x, const int64_t* species,
+                int num_species, const float* const* weights, int64_t nodes, const float* grad,
+                const float* tangent, float* dx, void* stream);
+int ictc_sc_bwd_w_jvp(int lmax, int target_lmax, int correlation, int channels, const float* x, int num_species,
+                      int64_t nodes, const float* grad, const float* tangent, const int32_t* species_ptr,
+                      const int32_t* species_order, float* const* dweights, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
