@@ -19,7 +19,7 @@ PKG = os.path.dirname(HERE)
 OUT_DIR = os.path.join(PKG, "ictc_o3", "_lib")
 LIB = os.path.join(OUT_DIR, "libictc_mi355x.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["capi.hip", "tp_edge.hip", "msg.hip", "sc.hip", "sc_part_low.hip", "sc_part_l3_t0.hip",
+SOURCES = ["capi.hip", "tp_edge.hip", "msg.hip", "misc.hip", "sc.hip", "sc_part_low.hip", "sc_part_l3_t0.hip",
            "sc_part_l3_t1.hip", "sc_part_l3_t2.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
@@ -28,8 +28,20 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-u
          "-munsafe-fp-atomics"]
 
 
-def _compile(src):
+def _deps_mtime():
+    paths = [os.path.join(HERE, f) for f in os.listdir(HERE) if f.endswith(".h")]
+    gen = os.path.join(HERE, "generated")
+    if os.path.isdir(gen):
+        paths += [os.path.join(gen, f) for f in os.listdir(gen)]
+    paths.append(os.path.join(os.path.dirname(PKG), "include", "ictc_mi355x.h"))
+    return max(os.path.getmtime(p) for p in paths if os.path.exists(p))
+
+
+def _compile(src, force=True):
     obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
+    if (not force and os.path.exists(obj)
+            and os.path.getmtime(obj) > max(os.path.getmtime(os.path.join(HERE, src)), _deps_mtime())):
+        return obj
     cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
@@ -37,7 +49,8 @@ def _compile(src):
     return obj
 
 
-def build(jobs: int | None = None) -> str:
+def build(jobs: int | None = None, force: bool = True) -> str:
+    """Compile every translation unit (``force=False``: only those older than their inputs)."""
     sys.path.insert(0, HERE)
     import gen_sc
     import gen_tables
@@ -47,7 +60,7 @@ def build(jobs: int | None = None) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     jobs = jobs or min(len(SOURCES), max(1, (os.cpu_count() or 2)))
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, force), SOURCES))
     tmp = LIB + ".tmp"
     r = subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp],
                        capture_output=True, text=True)
@@ -60,4 +73,6 @@ def build(jobs: int | None = None) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--incremental", action="store_true", help="skip objects newer than their inputs")
+    a = ap.parse_args()
+    print(build(a.jobs, force=not a.incremental))

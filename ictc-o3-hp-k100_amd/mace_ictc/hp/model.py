@@ -1,0 +1,274 @@
+"""MACE-ICTC baseline model (bridge-U product) on the MI355X kernels.
+
+Composition follows the reference's ``PureCartesianICTDFix`` for the route
+``create_model`` builds (mace_ictc/hp/runtime.py:6-83 ->
+models/factory.py:8-160 -> models/mace/backbone.py:60-726, forward :860-1250):
+
+  h0 = embedding[species]                                            (backbone.py:1016-1020)
+  per interaction i (layers.py:1042-1368):
+    x  = linear_up(h)                       per-degree C x C
+    m  = scatter_dst( TP(x[src], Y(e), fc(radial(r))) * mask )     CSR message kernel
+    m  = message_linear(m) / avg_num_neighbors                      path-preserving linear
+    sc = self_connection[species](h_l0)                             element-conditioned, l = 0
+  product i (products.py:792-841): h = linear(SC(m)) + sc on l = 0   (common.py:82-106)
+  readout: layer < last: Linear(C,1) on l = 0 (pure_cartesian_ictd_layers.py:89-115);
+           last: Linear(C,16) -> SiLU*1.679 -> Linear(16,1)          (heads.py:12-27)
+  atomic energy = sum of layer readouts.
+
+Parameter names, shapes and initialisation match the reference so state
+dicts line up.  Node features use the packed component-major layout of the
+kernels ([N, sum_l (2l+1) * C], component l*l+m at columns (l*l+m)*C..).
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ictc_o3.basis import tables
+from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
+from ictc_o3.ops import tensor_product as tpo
+from ictc_o3.ops.harmonics import harmonics_packed
+from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
+
+SILU_SCALE = 1.6791767923989418   # _Normalize2MomSiLU (layers.py:307-314)
+
+
+class NormalizedSiLU(nn.Module):
+    _scale = SILU_SCALE
+
+    def forward(self, x):
+        from ictc_o3.ops.activation import normalized_silu
+        return normalized_silu(x, self._scale)
+
+
+def _mace_linear_init(linear: nn.Linear):
+    """common.py:_init_mace_style_linear_: N(0, 1/sqrt(fan_in))."""
+    with torch.no_grad():
+        nn.init.normal_(linear.weight, mean=0.0, std=1.0 / math.sqrt(float(linear.in_features)))
+
+
+def degree_linear(x, weights: List[torch.Tensor], C: int, lmax: int, scale: float = 1.0):
+    """Per-degree channel map on the packed layout: out[n, l*l+m, :] = scale * W_l @ x[n, l*l+m, :]."""
+    from ictc_o3.ops.linear import degree_linear as impl
+    return impl(x, weights, C, lmax, scale)
+
+
+class ChannelLinear(nn.Module):
+    """EquivariantChannelLinearSO3 (ictd_irreps.py:207-227): adapters[str(l)] = Linear(C, C)."""
+
+    def __init__(self, channels, lmax):
+        super().__init__()
+        self.channels, self.lmax = channels, lmax
+        self.adapters = nn.ModuleDict({str(l): nn.Linear(channels, channels, bias=False) for l in range(lmax + 1)})
+        with torch.no_grad():
+            for a in self.adapters.values():
+                nn.init.eye_(a.weight)       # interaction_init="identity" (common.py:71-114)
+
+    def forward(self, x):
+        return degree_linear(x, [self.adapters[str(l)].weight for l in range(self.lmax + 1)], self.channels,
+                             self.lmax)
+
+
+class PathPreservingLinear(nn.Module):
+    """PathPreservingLinearSO3 (layers.py:317-355): weights[str(l)] [C, count_l*C]."""
+
+    def __init__(self, counts: Dict[int, int], channels: int, lmax: int):
+        super().__init__()
+        self.counts, self.channels, self.lmax = counts, channels, lmax
+        self.weights = nn.ParameterDict()
+        for l in range(lmax + 1):
+            k = counts.get(l, 0) * channels
+            w = nn.Parameter(torch.empty(channels, k))
+            if k:
+                nn.init.normal_(w, mean=0.0, std=1.0 / math.sqrt(float(k)))
+            self.weights[str(l)] = w
+
+    def forward(self, m, scale: float):
+        from ictc_o3.ops.linear import path_linear
+        return path_linear(m, [self.weights[str(l)] for l in range(self.lmax + 1)], self.counts, self.channels,
+                           self.lmax, scale)
+
+
+class ElementConditionedLinear(nn.Module):
+    """ElementConditionedLinearSO3 (layers.py:21-87), identity init (common.py:128-142)."""
+
+    def __init__(self, num_elements, channels, lmax):
+        super().__init__()
+        self.num_elements, self.channels, self.lmax = num_elements, channels, lmax
+        self.weights = nn.ParameterDict({str(l): nn.Parameter(
+            torch.eye(channels).unsqueeze(0).repeat(num_elements, 1, 1)) for l in range(lmax + 1)})
+        self.bias = None
+
+    def forward_l0(self, x0, species):
+        """out[n, o] = sum_i W[s_n, o, i] x0[n, i] for the scalar block."""
+        from ictc_o3.ops.linear import species_linear
+        return species_linear(x0, self.weights["0"], species)
+
+
+class ProductLinear(nn.Module):
+    """e3nn o3.Linear on Cx0e + Cx1o + ... : flat weight, per-degree [C_in, C_out] blocks, 1/sqrt(C) scale."""
+
+    def __init__(self, channels, lmax):
+        super().__init__()
+        self.channels, self.lmax = channels, lmax
+        self.weight = nn.Parameter(torch.randn((lmax + 1) * channels * channels))
+
+    def blocks(self):
+        C = self.channels
+        return [self.weight[l * C * C:(l + 1) * C * C].view(C, C).t() for l in range(self.lmax + 1)]
+
+    def forward(self, x):
+        return degree_linear(x, self.blocks(), self.channels, self.lmax, 1.0 / math.sqrt(self.channels))
+
+
+class Interaction(nn.Module):
+    def __init__(self, *, channels, edge_lmax, input_lmax, sc_lmax, number_of_basis, num_elements,
+                 radial_hidden=(64, 64, 64), avg_num_neighbors=50.0):
+        super().__init__()
+        self.channels, self.lmax, self.input_lmax = channels, edge_lmax, input_lmax
+        self.target_lmax, self.sc_lmax = edge_lmax, sc_lmax
+        self.avg_num_neighbors = avg_num_neighbors
+        self.linear_up = ChannelLinear(channels, input_lmax)
+        paths = tables.natural_paths(input_lmax, edge_lmax, edge_lmax)
+        self.tp = EdgeWeightedPathPreservingTensorProduct(channels=channels, lmax=edge_lmax, allowed_paths=paths,
+                                                          internal_compute_dtype=torch.float32)
+        with torch.no_grad():
+            self.tp.weight.fill_(1.0)
+        self.tp.weight.requires_grad_(False)     # freeze_conv_tp_weight=True (runtime.py:76)
+        sizes = (number_of_basis, *radial_hidden, self.tp.num_paths * channels)
+        layers = []
+        for k, (a, b) in enumerate(zip(sizes, sizes[1:])):
+            layers.append(nn.Linear(a, b, bias=False))
+            if k < len(sizes) - 2:
+                layers.append(NormalizedSiLU())
+        self.fc = nn.Sequential(*layers)
+        for m in self.fc:
+            if isinstance(m, nn.Linear):
+                _mace_linear_init(m)
+        self.message_linear = PathPreservingLinear(dict(self.tp.path_counts_by_l), channels, edge_lmax)
+        self.self_connection = ElementConditionedLinear(num_elements, channels, sc_lmax)
+        self._spec = None
+
+    def spec(self):
+        if self._spec is None:
+            self._spec = tpo.make_spec(self.input_lmax, self.lmax, self.lmax, self.channels, None)
+        return self._spec
+
+    def forward(self, h, species, Y, radial, topo, mask):
+        C = self.channels
+        x = self.linear_up(h)
+        gates = self.fc(radial)
+        m = tpo.message(x, Y, gates, self.spec(), topo, mask)
+        message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8))
+        sc = self.self_connection.forward_l0(h[:, :C], species)
+        return message, sc
+
+
+class Product(nn.Module):
+    def __init__(self, *, num_elements, channels, lmax, target_lmax, correlation):
+        super().__init__()
+        self.channels, self.target_lmax = channels, target_lmax
+        self.symmetric_contractions = ICTDBridgeUSymmetricContractionSO3(
+            num_elements=num_elements, channels=channels, lmax=lmax, target_lmax=target_lmax,
+            correlation=correlation)
+        self.linear = ProductLinear(channels, target_lmax)
+
+    def forward(self, message, sc, species):
+        out = self.linear(self.symmetric_contractions.contract(message, species))
+        C = self.channels
+        return torch.cat([out[:, :C] + sc, out[:, C:]], 1) if out.shape[1] > C else out + sc
+
+
+class ScalarReadout(nn.Module):
+    """EquivariantScalarReadoutSO3: readout = Linear(C, 1) on the l=0 block."""
+
+    def __init__(self, channels):
+        super().__init__()
+        self.readout = nn.Linear(channels, 1, bias=False)
+        nn.init.normal_(self.readout.weight, mean=0.0, std=1.0 / math.sqrt(channels))
+
+    def forward(self, h0):
+        return F.linear(h0, self.readout.weight)
+
+
+class MACEStyleReadout(nn.Module):
+    """MACEStyleScalarReadoutSO3: Linear(C,16) -> SiLU*1.679 -> Linear(16,1)."""
+
+    def __init__(self, channels, hidden=16):
+        super().__init__()
+        self.linear_1 = nn.Linear(channels, hidden, bias=False)
+        self.activation = NormalizedSiLU()
+        self.linear_2 = nn.Linear(hidden, 1, bias=False)
+        _mace_linear_init(self.linear_1)
+        _mace_linear_init(self.linear_2)
+
+    def forward(self, h0):
+        return F.linear(self.activation(F.linear(h0, self.linear_1.weight)), self.linear_2.weight)
+
+
+class PureCartesianICTDFix(nn.Module):
+    """The baseline MACE-ICTC backbone restricted to the create_model route."""
+
+    def __init__(self, *, channels=64, lmax=2, edge_lmax=None, num_interactions=2, correlation=3,
+                 atomic_numbers=(1, 6, 8), cutoff=5.0, avg_num_neighbors=50.0, number_of_basis=8,
+                 polynomial_cutoff_p=5, readout_hidden=16):
+        super().__init__()
+        edge_lmax = lmax if edge_lmax is None else edge_lmax
+        self.channels, self.lmax, self.ictd_fix_edge_lmax = channels, lmax, edge_lmax
+        self.num_interaction, self.max_radius = num_interactions, float(cutoff)
+        self.number_of_basis, self.polynomial_cutoff_p = number_of_basis, polynomial_cutoff_p
+        self.avg_num_neighbors = float(avg_num_neighbors)
+        self.atomic_numbers = tuple(sorted({int(z) for z in atomic_numbers}))
+        self.num_elements = len(self.atomic_numbers)
+        table = torch.full((max(119, max(self.atomic_numbers) + 1),), -1, dtype=torch.long)
+        for i, z in enumerate(self.atomic_numbers):
+            table[z] = i
+        self.register_buffer("atomic_number_to_index", table, persistent=False)
+        self.node_embedding = nn.Linear(self.num_elements, channels, bias=False)
+        self.interactions = nn.ModuleList()
+        self.products = nn.ModuleList()
+        for i in range(num_interactions):
+            target = lmax if i < num_interactions - 1 else 0
+            input_lmax = 0 if i == 0 else lmax
+            self.interactions.append(Interaction(
+                channels=channels, edge_lmax=edge_lmax, input_lmax=input_lmax, sc_lmax=0,
+                number_of_basis=number_of_basis, num_elements=self.num_elements,
+                avg_num_neighbors=self.avg_num_neighbors))
+            self.products.append(Product(num_elements=self.num_elements, channels=channels, lmax=edge_lmax,
+                                         target_lmax=target, correlation=correlation))
+        self.layer_energy_readouts = nn.ModuleList([ScalarReadout(channels) for _ in range(num_interactions - 1)])
+        self.last_layer_energy_readout = MACEStyleReadout(channels, readout_hidden)
+
+    # -- geometry ---------------------------------------------------------------
+    def radial_embedding(self, r):
+        """Bessel basis x MACE polynomial cutoff (radial_basis.py:11-92, sqrt_num_basis_norm=False)."""
+        from ictc_o3.ops.activation import radial_embedding
+        return radial_embedding(r, self.max_radius, self.number_of_basis, self.polynomial_cutoff_p)
+
+    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, topology=None):
+        N = pos.shape[0]
+        species = self.atomic_number_to_index[A.long()]
+        if topology is None:
+            topology = tpo.Topology(edge_src, edge_dst, N)
+        shift_vec = torch.einsum("ni,nij->nj", edge_shifts.to(pos.dtype), cell[batch[edge_src]])
+        vec = pos[edge_dst] - pos[edge_src] + shift_vec
+        r = vec.norm(dim=1)
+        n = vec / r.clamp(min=1e-8).unsqueeze(-1)
+        mask = (r <= self.max_radius).to(pos.dtype)
+        Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
+        radial = self.radial_embedding(r)
+        h = self.node_embedding.weight.t().index_select(0, species)
+        energy = None
+        for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
+            message, sc = inter(h, species, Y, radial, topology, mask)
+            h = prod(message, sc, species)
+            if i < self.num_interaction - 1:
+                e = self.layer_energy_readouts[i](h[:, :self.channels])
+            else:
+                e = self.last_layer_energy_readout(h[:, :self.channels])
+            energy = e if energy is None else energy + e
+        return energy

@@ -1,0 +1,93 @@
+"""Periodic radius graph on the GPU (receiver-sorted), for MD-style steps.
+
+The reference delegates neighbour search to ASE / matscipy / torch_cluster
+(examples/predict.py:62, data/preprocessing.py:11, utils/graph_utils.py:217-297).
+This builds the same directed edge list on the device: a cell list when every
+periodic direction holds >= 3 cells, else an image-enumerating all-pairs search.
+Edge convention (backbone.py:940-944): vec = pos[dst] - pos[src] + shift @ cell,
+with every pair at distance < cutoff (self-images included when in range).
+Edges come out sorted by receiver (dst).
+"""
+from __future__ import annotations
+
+import itertools
+import math
+
+import torch
+
+
+def radius_graph_pbc(pos: torch.Tensor, cell: torch.Tensor, cutoff: float):
+    """pos [N,3], cell [3,3] (rows = lattice vectors) -> (src, dst, shifts[E,3] float)."""
+    dev = pos.device
+    inv = torch.linalg.inv(cell.double())
+    frac = pos.double() @ inv
+    k = torch.floor(frac)
+    fw = frac - k
+    lengths = cell.double().norm(dim=1)
+    # perpendicular widths of the cell
+    vol = torch.abs(torch.det(cell.double()))
+    widths = torch.stack([vol / torch.linalg.cross(cell[1].double(), cell[2].double()).norm(),
+                          vol / torch.linalg.cross(cell[2].double(), cell[0].double()).norm(),
+                          vol / torch.linalg.cross(cell[0].double(), cell[1].double()).norm()])
+    ncell = torch.floor(widths / cutoff).long().clamp(min=1)
+    if bool((ncell >= 3).all()):
+        return _cell_list(pos, cell, cutoff, fw, k, ncell)
+    return _all_pairs(pos, cell, cutoff, fw, k, widths)
+
+
+def _cell_list(pos, cell, cutoff, fw, k, ncell):
+    dev = pos.device
+    N = pos.shape[0]
+    nc = ncell.tolist()
+    cidx = torch.minimum((fw * ncell.double()).long(), ncell - 1)            # [N,3]
+    flat = (cidx[:, 0] * nc[1] + cidx[:, 1]) * nc[2] + cidx[:, 2]
+    total = nc[0] * nc[1] * nc[2]
+    order = torch.argsort(flat, stable=True)
+    counts = torch.bincount(flat, minlength=total)
+    M = int(counts.max().item())
+    start = torch.cumsum(counts, 0) - counts
+    slot = torch.arange(N, device=dev) - start[flat[order]]
+    table = torch.full((total, M), -1, dtype=torch.long, device=dev)
+    table[flat[order], slot] = order
+    offs = torch.tensor(list(itertools.product((-1, 0, 1), repeat=3)), device=dev)      # [27,3]
+    nb = cidx[:, None, :] + offs[None]                                                 # [N,27,3]
+    wrap = torch.div(nb, ncell, rounding_mode="floor")                                 # image of the cell
+    nbw = nb - wrap * ncell
+    nflat = (nbw[..., 0] * nc[1] + nbw[..., 1]) * nc[2] + nbw[..., 2]                 # [N,27]
+    cand = table[nflat]                                                                # [N,27,M]
+    valid = cand >= 0
+    j = cand.clamp(min=0)
+    cellf = cell.double()
+    posw = fw @ cellf                                                                  # wrapped positions
+    img = wrap.double() @ cellf                                                        # [N,27,3]
+    # vec = pos_w[i] - (pos_w[j] + img)
+    vec = posw[:, None, None, :] - (posw[j] + img[:, :, None, :])
+    r2 = (vec * vec).sum(-1)
+    keep = valid & (r2 < cutoff * cutoff) & (r2 > 1e-20)
+    i_idx, o_idx, m_idx = torch.nonzero(keep, as_tuple=True)
+    src = j[i_idx, o_idx, m_idx]
+    dst = i_idx
+    # shift = k_j - k_i - image  (vec = pos[dst] - pos[src] + shift @ cell)
+    shifts = (k[src] - k[dst] - wrap[i_idx, o_idx].double())
+    return src, dst, shifts.to(pos.dtype)
+
+
+def _all_pairs(pos, cell, cutoff, fw, k, widths):
+    dev = pos.device
+    reps = torch.ceil(cutoff / widths).long().tolist()
+    imgs = torch.tensor(list(itertools.product(*[range(-r, r + 1) for r in reps])), device=dev, dtype=torch.double)
+    cellf = cell.double()
+    posw = fw @ cellf
+    src_l, dst_l, sh_l = [], [], []
+    N = pos.shape[0]
+    chunk = max(1, int(4e7 // max(1, N * imgs.shape[0])))
+    for s in range(0, N, chunk):
+        i = torch.arange(s, min(N, s + chunk), device=dev)
+        vec = posw[i, None, None, :] - (posw[None, :, None, :] + (imgs @ cellf)[None, None])
+        r2 = (vec * vec).sum(-1)
+        keep = (r2 < cutoff * cutoff) & (r2 > 1e-20)
+        a, b, c = torch.nonzero(keep, as_tuple=True)
+        dst_l.append(i[a])
+        src_l.append(b)
+        sh_l.append(k[b] - k[i[a]] - imgs[c])
+    return torch.cat(src_l), torch.cat(dst_l), torch.cat(sh_l).to(pos.dtype)

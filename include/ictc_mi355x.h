@@ -120,6 +120,19 @@ int ictc_sh_jvp(const float* directions, const float* tangent, int64_t edges, in
 int ictc_sh_hvp(const float* directions, const float* grad, const float* tangent, int64_t edges, int lmax,
                 float* out, void* stream);
 
+/* ---- Radial path elementwise maps -----------------------------------------
+ * ictc_silu replaces the normalized-SiLU kernels (operators.py:631-636 ->
+ * backends/k100/hip_activation.py:11-36): n elements, scale s,
+ *   mode 0: out = s x sig(x)   1: out = grad s silu'(x)   2: out = grad tangent s silu''(x)
+ * ictc_radial replaces mace_radial_embedding (mace_ictc/models/radial_basis.py:
+ * 42-92, Bessel x polynomial cutoff of order poly_p, no sqrt(num_basis) norm):
+ *   order 0: out [E,K] = b_k(r);  1: out [E] = sum_k grad[e,k] b_k'(r);
+ *   order 2: out [E] = tangent[e] sum_k grad[e,k] b_k''(r);  3: out [E,K] = b_k'(r) tangent[e] */
+int ictc_silu(int mode, const float* x, const float* grad, const float* tangent, float scale, int64_t n,
+              float* out, void* stream);
+int ictc_radial(int order, const float* r, const float* grad, const float* tangent, int64_t edges, int num_basis,
+                float cutoff, int poly_p, float* out, void* stream);
+
 /* ---- Symmetric contraction (bridge-U, correlation 1..3) -------------------
  * Replaces the SC circuits of ICTDBridgeUSymmetricContractionSO3.forward
  * (ictc_o3/ops/symmetric_contraction.py:98-147 -> factorized_contraction.py:

@@ -1,0 +1,90 @@
+"""Whole-model parity on the GPU vs the float64 oracle.
+
+Tolerances (north star): energies 1e-6 relative, forces 1e-5 relative
+(max-norm), force-loss parameter gradients relative L2 < 3e-5 (the
+reference's own gate, tests/test_foundation_species_precision.py:114).
+"""
+import pytest
+import torch
+
+import model_oracle as mo
+from helpers import rel_err
+from model_helpers import build_graph, fcc_cells
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(device, seed, C, lmax, edge_lmax, S, cells=1, ncell=2, cutoff=4.5):
+    from mace_ictc.hp import create_model
+    torch.manual_seed(seed)
+    zs = (1, 6, 8, 7, 9, 14, 15, 16, 17, 35)[:S]
+    model = create_model(channels=C, lmax=lmax, edge_lmax=edge_lmax, atomic_numbers=zs, cutoff=cutoff,
+                         avg_num_neighbors=40.0, device=device)
+    pos, Z, batch, cell = fcc_cells(ncell, 0.1, 0.3, seed, S, cells=cells, atomic_numbers=zs)
+    src, dst, sh = build_graph(pos, batch, cell, cutoff)
+    return model, pos, Z, batch, cell, src, dst, sh
+
+
+@pytest.mark.parametrize("C,lmax,edge_lmax,S,cells", [(16, 2, 2, 3, 1), (32, 2, 3, 10, 2), (64, 2, 2, 3, 1)])
+def test_energy_and_forces_match_oracle(device, C, lmax, edge_lmax, S, cells):
+    from mace_ictc.hp import energy_and_forces
+    model, pos, Z, batch, cell, src, dst, sh = _setup(device, 1, C, lmax, edge_lmax, S, cells)
+    E0, F0, A0 = mo.energy_and_forces(model.state_dict(), mo.config_of(model), pos, Z, batch, src, dst, sh, cell,
+                                      cells)
+    out = energy_and_forces(model, pos.float().to(device), Z.to(device), batch.to(device), src.to(device),
+                            dst.to(device), sh.float().to(device), cell.float().to(device))
+    # energy: 1e-6 relative to the scale of the summed atomic energies of each graph (sum |e_i|)
+    scale = torch.zeros(cells, dtype=torch.float64).index_add(0, batch, A0.abs())
+    assert bool(((out["energy"].double().cpu() - E0).abs() <= 1e-6 * scale).all())
+    assert rel_err(out["forces"], F0) < 1e-5
+    assert rel_err(out["atomic_energy"], A0) < 1e-5
+
+
+def test_force_loss_parameter_gradients(device):
+    """E+F MSE loss backward (mixed second derivatives) vs float64 autograd of the oracle."""
+    from mace_ictc.hp import energy_and_forces
+    model, pos, Z, batch, cell, src, dst, sh = _setup(device, 2, 16, 2, 3, 4, cells=2)
+    g = torch.Generator().manual_seed(3)
+    E_t = torch.randn(2, generator=g, dtype=torch.float64)
+    F_t = torch.randn(pos.shape, generator=g, dtype=torch.float64) * 0.5
+    # oracle
+    sd = {k: v.detach().double().cpu().clone() for k, v in model.state_dict().items()}
+    names = [k for k, p in model.named_parameters() if p.requires_grad]
+    for k in names:
+        sd[k].requires_grad_(True)
+    cfg = mo.config_of(model)
+    p = pos.clone().requires_grad_(True)
+    atomic = mo.forward(sd, cfg, p, Z, batch, src, dst, sh, cell)
+    E = torch.zeros(2, dtype=torch.float64).index_add(0, batch, atomic)
+    (gpos,) = torch.autograd.grad(E.sum(), p, create_graph=True)
+    loss = ((E - E_t) ** 2).mean() + ((-gpos - F_t) ** 2).mean()
+    ref = torch.autograd.grad(loss, [sd[k] for k in names], allow_unused=True)
+    # product
+    out = energy_and_forces(model, pos.float().to(device), Z.to(device), batch.to(device), src.to(device),
+                            dst.to(device), sh.float().to(device), cell.float().to(device), training=True)
+    loss_g = ((out["energy"].double() - E_t.to(device)) ** 2).mean() + \
+        ((out["forces"].double() - F_t.to(device)) ** 2).mean()
+    params = dict(model.named_parameters())
+    got = torch.autograd.grad(loss_g, [params[k] for k in names], allow_unused=True)
+    for k, a, b in zip(names, got, ref):
+        if b is None or float(b.norm()) == 0:
+            continue
+        assert a is not None, k
+        rl2 = float((a.double().cpu() - b).norm() / b.norm())
+        assert rl2 < 3e-5, (k, rl2)
+
+
+def test_configure_model_contract(device):
+    from mace_ictc.hp import configure_model, create_model
+    model = create_model(channels=8, lmax=2, device=device)
+    before = {k: v for k, v in model.named_parameters()}
+    info = configure_model(model, training=True)
+    assert info["selected"] == "generated"
+    assert info["training_gate_schedule"] == "materialized"
+    assert info["training_message_linear_layout"] == "node_component"
+    assert all(before[k] is v for k, v in model.named_parameters())
+    assert configure_model(model, policy="reference")["selected"] == "reference"
+    with pytest.raises(ValueError):
+        configure_model(model, layout="bogus")
+    with pytest.raises(ValueError):
+        configure_model(model, training=True, gate_cache_bytes=10)
