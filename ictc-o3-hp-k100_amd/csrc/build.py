@@ -19,7 +19,8 @@ PKG = os.path.dirname(HERE)
 OUT_DIR = os.path.join(PKG, "ictc_o3", "_lib")
 LIB = os.path.join(OUT_DIR, "libictc_mi355x.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["capi.hip", "tp_edge.hip", "msg.hip", "misc.hip", "sc.hip", "sc_part_low.hip", "sc_part_l3_t0.hip",
+SOURCES = ["capi.hip", "misc.hip", "sc.hip", "tp_edge_c1.hip", "tp_edge_c2.hip", "tp_edge_c4.hip",
+           "msg_c1.hip", "msg_c2.hip", "msg_c4.hip", "sc_part_low.hip", "sc_part_l3_t0.hip",
            "sc_part_l3_t1.hip", "sc_part_l3_t2.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
@@ -28,19 +29,30 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-u
          "-munsafe-fp-atomics"]
 
 
-def _deps_mtime():
-    paths = [os.path.join(HERE, f) for f in os.listdir(HERE) if f.endswith(".h")]
-    gen = os.path.join(HERE, "generated")
-    if os.path.isdir(gen):
-        paths += [os.path.join(gen, f) for f in os.listdir(gen)]
-    paths.append(os.path.join(os.path.dirname(PKG), "include", "ictc_mi355x.h"))
-    return max(os.path.getmtime(p) for p in paths if os.path.exists(p))
+def _includes(path, seen):
+    """Local headers reachable from ``path`` through #include "..." lines."""
+    import re
+    for line in open(path):
+        m = re.match(r'\s*#include\s+"([^"]+)"', line)
+        if not m:
+            continue
+        dep = os.path.normpath(os.path.join(os.path.dirname(path), m.group(1)))
+        if os.path.exists(dep) and dep not in seen:
+            seen.add(dep)
+            _includes(dep, seen)
+    return seen
+
+
+def _deps_mtime(src):
+    path = os.path.join(HERE, src)
+    deps = _includes(path, set()) | {path}
+    return max(os.path.getmtime(p) for p in deps)
 
 
 def _compile(src, force=True):
     obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
     if (not force and os.path.exists(obj)
-            and os.path.getmtime(obj) > max(os.path.getmtime(os.path.join(HERE, src)), _deps_mtime())):
+            and os.path.getmtime(obj) > _deps_mtime(src)):
         return obj
     cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)

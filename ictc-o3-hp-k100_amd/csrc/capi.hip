@@ -123,6 +123,31 @@ __global__ void fill_zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
+// Channels-per-lane routing onto the per-CPL launchers.
+#define ICTC_ROUTE(CALL, ...)                                                 \
+  switch (ictc::channels_per_lane(s.channels)) {                             \
+    case 1: return ictc::CALL##_c1(__VA_ARGS__);                             \
+    case 2: return ictc::CALL##_c2(__VA_ARGS__);                             \
+    default: return ictc::CALL##_c4(__VA_ARGS__);                            \
+  }
+
+hipError_t route_edge_fwd(const ictc::TpShape& s, const ictc::Operands& a, float* out, hipStream_t st) {
+  ICTC_ROUTE(launch_edge_fwd, s, a, out, st)
+}
+hipError_t route_edge_bwd(const ictc::TpShape& s, const ictc::Operands& a, const float* grad, float* dx, float* dsh,
+                          float* dg, hipStream_t st) {
+  ICTC_ROUTE(launch_edge_bwd, s, a, grad, dx, dsh, dg, st)
+}
+hipError_t route_msg_fwd(const ictc::TpShape& s, const ictc::Operands& a, const int64_t* src, ictc::Csr c,
+                         float* out, hipStream_t st) {
+  ICTC_ROUTE(launch_msg_fwd, s, a, src, c, out, st)
+}
+hipError_t route_msg_bwd(const ictc::TpShape& s, const ictc::Operands& a, const int64_t* src, const int64_t* dst,
+                         ictc::Csr dc, ictc::Csr sc, const float* grad, float* dx, float* dsh, float* dg,
+                         hipStream_t st) {
+  ICTC_ROUTE(launch_msg_bwd, s, a, src, dst, dc, sc, grad, dx, dsh, dg, st)
+}
+
 }  // namespace
 
 namespace ictc {
@@ -151,7 +176,7 @@ int ictc_tp_fwd(int li, int le, int lo, int C, const float* x, const float* sh, 
   if (E == 0) return ICTC_OK;
   if (!x || !sh || !g || !out) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_fwd: null operand");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(ictc::launch_edge_fwd(s, operands(x, sh, g, w, nullptr, E, E, C), out, (hipStream_t)stream),
+  return check_hip(route_edge_fwd(s, operands(x, sh, g, w, nullptr, E, E, C), out, (hipStream_t)stream),
                    "ictc_tp_fwd launch");
 }
 
@@ -162,7 +187,7 @@ int ictc_tp_bwd(int li, int le, int lo, int C, const float* x, const float* sh, 
   if (E == 0 || (!dx && !dsh && !dg)) return ICTC_OK;
   if (!x || !sh || !g || !grad) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_bwd: null operand");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(ictc::launch_edge_bwd(s, operands(x, sh, g, w, nullptr, E, E, C), grad, dx, dsh, dg,
+  return check_hip(route_edge_bwd(s, operands(x, sh, g, w, nullptr, E, E, C), grad, dx, dsh, dg,
                                          (hipStream_t)stream),
                    "ictc_tp_bwd launch");
 }
@@ -215,7 +240,7 @@ int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh,
   if (!x || !out || !dptr || (E > 0 && (!sh || !g || !src)))
     return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fwd: null operand");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(ictc::launch_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C), src, ictc::Csr{dptr, dorder}, out,
+  return check_hip(route_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C), src, ictc::Csr{dptr, dorder}, out,
                                         (hipStream_t)stream),
                    "ictc_msg_fwd launch");
 }
@@ -236,7 +261,7 @@ int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh,
   if (!x || !sh || !g || !src || !dst || !grad || !dptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: null operand");
   if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: dfeatures needs the source CSR");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(ictc::launch_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder},
+  return check_hip(route_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder},
                                         ictc::Csr{sptr, sorder}, grad, dx, dsh, dg, (hipStream_t)stream),
                    "ictc_msg_bwd launch");
 }

@@ -29,10 +29,24 @@ constexpr int kBlock = kWave * kWavesPerBlock;
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
+// Sum over the 64 lanes of a wave, returned wave-uniform.  Within each row of
+// 16 lanes the sum is formed with DPP moves (quad xor 1, quad xor 2, half-row
+// mirror, row mirror: VALU only, no LDS traffic); the four row sums are then
+// read with readlane and added in a fixed order (deterministic).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 struct Operands {
@@ -53,15 +67,23 @@ __device__ __forceinline__ void load_harmonics(const float* __restrict__ sh, int
   for (int j = 0; j < T::NY; ++j) y[j] = p[j];
 }
 
+// Gates of edge e for channel c, times the per-path weight (if any) and `scale`.
+// All P gate loads are issued before any use so they are in flight together;
+// the optional weight is a separate uniform branch after them.
 template <class T>
 __device__ __forceinline__ void load_gw(const Operands& a, int64_t e, int c, float scale, float* gw) {
   const float* g = a.gates + e * (int64_t)(T::P * a.channels) + c;
 #pragma unroll
-  for (int p = 0; p < T::P; ++p) {
-    float v = g[p * a.channels] * scale;
-    if (a.weight) v *= a.weight[p * a.channels + c];
-    gw[p] = v;
+  for (int p = 0; p < T::P; ++p) gw[p] = g[p * a.channels];
+  if (a.weight) {
+    float w[T::P];
+#pragma unroll
+    for (int p = 0; p < T::P; ++p) w[p] = a.weight[p * a.channels + c];
+#pragma unroll
+    for (int p = 0; p < T::P; ++p) gw[p] *= w[p];
   }
+#pragma unroll
+  for (int p = 0; p < T::P; ++p) gw[p] *= scale;
 }
 
 template <int N>
@@ -135,9 +157,9 @@ __global__ __launch_bounds__(kBlock) void edge_bwd_kernel(Operands a, const floa
       if (dgates) {
         float d[T::P];
         T::dg(xv, y, go, d);
+        if (a.weight) {
 #pragma unroll
-        for (int p = 0; p < T::P; ++p) {
-          if (a.weight) d[p] *= a.weight[p * C + c];
+          for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
         }
         store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
       }
@@ -162,8 +184,56 @@ struct Csr {
   const int32_t* order;  // [E] or nullptr
 };
 
+// Edge metadata of a chunk of up to 64 consecutive CSR positions, staged one
+// edge per lane with coalesced loads; the edge loop then reads it with
+// readlane (wave-uniform SGPR values, no memory latency inside the loop).
+template <class T>
+struct Chunk {
+  int32_t e;        // edge id of this lane's position
+  int32_t peer;     // src (receiver-sorted CSR) or dst (source-sorted CSR); 0 when out of range
+  float m;          // mask, 0 when the peer is out of range or the lane is past the chunk
+  float y[T::NY];   // harmonics of this lane's edge
+};
+
+template <class T>
+__device__ __forceinline__ void stage_chunk(const Operands& a, const int64_t* __restrict__ peer_ids,
+                                            const int32_t* __restrict__ order, int32_t pos, int32_t count,
+                                            Chunk<T>& ch) {
+  const int l = lane_id();
+  ch.e = 0;
+  ch.peer = 0;
+  ch.m = 0.f;
+#pragma unroll
+  for (int j = 0; j < T::NY; ++j) ch.y[j] = 0.f;
+  if (l < count) {
+    const int32_t e = order ? order[pos + l] : pos + l;
+    const int64_t p = peer_ids[e];
+    const bool ok = p >= 0 && p < a.rows;
+    ch.e = e;
+    ch.peer = ok ? (int32_t)p : 0;
+    ch.m = ok ? (a.mask ? a.mask[e] : 1.f) : 0.f;
+#pragma unroll
+    for (int j = 0; j < T::NY; ++j) ch.y[j] = a.sh[(int64_t)e * T::NY + j];
+  }
+}
+
+__device__ __forceinline__ int32_t lane_i(int32_t v, int i) { return __builtin_amdgcn_readlane(v, i); }
+__device__ __forceinline__ float lane_f(float v, int i) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+
+// Per-edge operands of one wave: harmonics (wave-uniform), gathered source row
+// and mask-scaled gates for each of the lane's CPL channels.
 template <class T, int CPL>
-__global__ __launch_bounds__(kBlock) void msg_fwd_kernel(Operands a, const int64_t* __restrict__ src, Csr csr,
+struct EdgeIn {
+  float y[T::NY];
+  float x[CPL][T::NX];
+  float gw[CPL][T::P];
+  float m;  // mask (0 for an out-of-range source)
+};
+
+template <class T, int CPL>
+__global__ __launch_bounds__(kBlock, 4) void msg_fwd_kernel(Operands a, const int64_t* __restrict__ src, Csr csr,
                                                          float* __restrict__ out) {
   const int64_t n = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
   if (n >= a.rows) return;
@@ -174,22 +244,27 @@ __global__ __launch_bounds__(kBlock) void msg_fwd_kernel(Operands a, const int64
 #pragma unroll
     for (int k = 0; k < T::NO; ++k) o[j][k] = 0.f;
   const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
-  for (int32_t k = beg; k < end; ++k) {
-    const int64_t e = csr.order ? (int64_t)csr.order[k] : (int64_t)k;
-    const int64_t s = src[e];
-    if (s < 0 || s >= a.rows) continue;
-    const float m = a.mask ? a.mask[e] : 1.f;
-    float y[T::NY];
-    load_harmonics<T>(a.sh, e, y);
-    const float* xr = a.x + s * (int64_t)(T::NX * C);
+  for (int32_t pos = beg; pos < end; pos += kWave) {
+    const int32_t count = min(end - pos, kWave);
+    Chunk<T> ch;
+    stage_chunk<T>(a, src, csr.order, pos, count, ch);
+    for (int i = 0; i < count; ++i) {
+      const int64_t e = lane_i(ch.e, i);
+      const int64_t s = lane_i(ch.peer, i);
+      const float m = lane_f(ch.m, i);
+      float y[T::NY];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = lane_id() + kWave * j;
-      if (c < C) {
-        float xv[T::NX], gw[T::P];
-        load_row<T::NX>(xr, C, c, xv);
-        load_gw<T>(a, e, c, m, gw);
-        T::fwd(xv, y, gw, o[j]);
+      for (int j = 0; j < T::NY; ++j) y[j] = lane_f(ch.y[j], i);
+      const float* xr = a.x + s * (int64_t)(T::NX * C);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane_id() + kWave * j;
+        if (c < C) {
+          float xv[T::NX], gw[T::P];
+          load_row<T::NX>(xr, C, c, xv);
+          load_gw<T>(a, e, c, m, gw);
+          T::fwd(xv, y, gw, o[j]);
+        }
       }
     }
   }
@@ -201,9 +276,45 @@ __global__ __launch_bounds__(kBlock) void msg_fwd_kernel(Operands a, const int64
   }
 }
 
+// Gate and harmonic gradients of one edge given the receiver's cotangent rows.
+template <class T, int CPL>
+__device__ __forceinline__ void edge_adjoint(const Operands& a, const float (&go)[CPL][T::NO], int64_t e,
+                                             const EdgeIn<T, CPL>& in, float* __restrict__ dsh,
+                                             float* __restrict__ dgates) {
+  const int C = a.channels;
+  float dyv[T::NY];
+#pragma unroll
+  for (int j = 0; j < T::NY; ++j) dyv[j] = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane_id() + kWave * j;
+    if (c < C) {
+      if (dsh) T::dy(in.x[j], in.gw[j], go[j], dyv);
+      if (dgates) {
+        float d[T::P];
+        T::dg(in.x[j], in.y, go[j], d);
+#pragma unroll
+        for (int p = 0; p < T::P; ++p) d[p] *= in.m;
+        if (a.weight) {
+#pragma unroll
+          for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
+        }
+        store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
+      }
+    }
+  }
+  if (dsh) {
+#pragma unroll
+    for (int j = 0; j < T::NY; ++j) {
+      const float s = wave_sum(dyv[j]);
+      if (lane_id() == 0) dsh[e * T::NY + j] = s;
+    }
+  }
+}
+
 // Receiver-owned adjoint: per-edge gate and harmonic gradients.
 template <class T, int CPL>
-__global__ __launch_bounds__(kBlock) void msg_bwd_edge_kernel(Operands a, const int64_t* __restrict__ src, Csr csr,
+__global__ __launch_bounds__(kBlock, 3) void msg_bwd_edge_kernel(Operands a, const int64_t* __restrict__ src, Csr csr,
                                                               const float* __restrict__ grad,
                                                               float* __restrict__ dsh, float* __restrict__ dgates) {
   // Waves 0..rows-1 own receivers; wave `rows` owns the out-of-range tail
@@ -224,57 +335,34 @@ __global__ __launch_bounds__(kBlock) void msg_bwd_edge_kernel(Operands a, const 
     }
   }
   const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
-  for (int32_t k = beg; k < end; ++k) {
-    const int64_t e = csr.order ? (int64_t)csr.order[k] : (int64_t)k;
-    const int64_t s = src[e];
-    const bool valid = s >= 0 && s < a.rows;
-    const float m = a.mask ? a.mask[e] : 1.f;
-    float y[T::NY], dyv[T::NY];
-    load_harmonics<T>(a.sh, e, y);
+  for (int32_t pos = beg; pos < end; pos += kWave) {
+    const int32_t count = min(end - pos, kWave);
+    Chunk<T> ch;
+    stage_chunk<T>(a, src, csr.order, pos, count, ch);
+    for (int i = 0; i < count; ++i) {
+      EdgeIn<T, CPL> in;
+      const int64_t e = lane_i(ch.e, i);
+      const int64_t s = lane_i(ch.peer, i);
+      in.m = lane_f(ch.m, i);
 #pragma unroll
-    for (int j = 0; j < T::NY; ++j) dyv[j] = 0.f;
-    const float* xr = a.x + (valid ? s : 0) * (int64_t)(T::NX * C);
+      for (int j = 0; j < T::NY; ++j) in.y[j] = lane_f(ch.y[j], i);
+      const float* xr = a.x + s * (int64_t)(T::NX * C);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = lane_id() + kWave * j;
-      if (c < C) {
-        float xv[T::NX];
-        if (valid) load_row<T::NX>(xr, C, c, xv);
-        else {
-#pragma unroll
-          for (int i = 0; i < T::NX; ++i) xv[i] = 0.f;
-        }
-        if (dsh) {
-          float gw[T::P];
-          load_gw<T>(a, e, c, m, gw);
-          T::dy(xv, gw, go[j], dyv);
-        }
-        if (dgates) {
-          float d[T::P];
-          T::dg(xv, y, go[j], d);
-#pragma unroll
-          for (int p = 0; p < T::P; ++p) {
-            float v = d[p] * m;
-            if (a.weight) v *= a.weight[p * C + c];
-            d[p] = v;
-          }
-          store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane_id() + kWave * j;
+        if (c < C) {
+          load_row<T::NX>(xr, C, c, in.x[j]);
+          load_gw<T>(a, e, c, in.m, in.gw[j]);
         }
       }
-    }
-    if (dsh) {
-#pragma unroll
-      for (int j = 0; j < T::NY; ++j) {
-        const float s2 = wave_sum(dyv[j]);
-        if (lane_id() == 0) dsh[e * T::NY + j] = s2;
-      }
+      edge_adjoint<T, CPL>(a, go, e, in, dsh, dgates);
     }
   }
 }
 
 // Source-owned adjoint: node feature gradient over the source-sorted CSR.
 template <class T, int CPL>
-__global__ __launch_bounds__(kBlock) void msg_bwd_x_kernel(Operands a, const int64_t* __restrict__ dst, Csr scsr,
+__global__ __launch_bounds__(kBlock, 3) void msg_bwd_x_kernel(Operands a, const int64_t* __restrict__ dst, Csr scsr,
                                                            const float* __restrict__ grad, float* __restrict__ dx) {
   const int64_t n = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
   if (n >= a.rows) return;
@@ -285,22 +373,28 @@ __global__ __launch_bounds__(kBlock) void msg_bwd_x_kernel(Operands a, const int
 #pragma unroll
     for (int i = 0; i < T::NX; ++i) d[j][i] = 0.f;
   const int32_t beg = scsr.ptr[n], end = scsr.ptr[n + 1];
-  for (int32_t k = beg; k < end; ++k) {
-    const int64_t e = scsr.order ? (int64_t)scsr.order[k] : (int64_t)k;
-    const int64_t r = dst[e];
-    if (r < 0 || r >= a.rows) continue;
-    const float m = a.mask ? a.mask[e] : 1.f;
-    float y[T::NY];
-    load_harmonics<T>(a.sh, e, y);
-    const float* gr = grad + r * (int64_t)(T::NO * C);
+  // An out-of-range receiver contributes zero (mask 0, row 0 read).
+  for (int32_t pos = beg; pos < end; pos += kWave) {
+    const int32_t count = min(end - pos, kWave);
+    Chunk<T> ch;
+    stage_chunk<T>(a, dst, scsr.order, pos, count, ch);
+    for (int i = 0; i < count; ++i) {
+      const int64_t e = lane_i(ch.e, i);
+      const int64_t r = lane_i(ch.peer, i);
+      const float m = lane_f(ch.m, i);
+      float y[T::NY];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = lane_id() + kWave * j;
-      if (c < C) {
-        float go[T::NO], gw[T::P];
-        load_row<T::NO>(gr, C, c, go);
-        load_gw<T>(a, e, c, m, gw);
-        T::dx(y, gw, go, d[j]);
+      for (int j = 0; j < T::NY; ++j) y[j] = lane_f(ch.y[j], i);
+      const float* gr = grad + r * (int64_t)(T::NO * C);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = lane_id() + kWave * j;
+        if (c < C) {
+          float go[T::NO], gw[T::P];
+          load_row<T::NO>(gr, C, c, go);
+          load_gw<T>(a, e, c, m, gw);
+          T::dx(y, gw, go, d[j]);
+        }
       }
     }
   }

@@ -1,4 +1,4 @@
-// CSR graph message forward / first adjoint instantiations (one wave per node).
+// CSR graph message forward / first adjoint launchers, CPL = 2 channels per lane.
 #include "ictc_launch.h"
 
 namespace ictc {
@@ -42,14 +42,15 @@ struct MsgBwd {
 };
 }  // namespace
 
-hipError_t launch_msg_fwd(const TpShape& s, const Operands& a, const int64_t* src, Csr dcsr, float* out,
-                          hipStream_t st) {
-  return dispatch(s, MsgFwd{a, src, dcsr, out, st});
+hipError_t launch_msg_fwd_c2(const TpShape& s, const Operands& a, const int64_t* src, Csr dcsr, float* out,
+                              hipStream_t st) {
+  return dispatch_cpl<2>(s, MsgFwd{a, src, dcsr, out, st});
 }
 
-hipError_t launch_msg_bwd(const TpShape& s, const Operands& a, const int64_t* src, const int64_t* dst, Csr dcsr,
-                          Csr scsr, const float* grad, float* dx, float* dsh, float* dg, hipStream_t st) {
-  return dispatch(s, MsgBwd{a, src, dst, dcsr, scsr, grad, dx, dsh, dg, st});
+hipError_t launch_msg_bwd_c2(const TpShape& s, const Operands& a, const int64_t* src, const int64_t* dst,
+                              Csr dcsr, Csr scsr, const float* grad, float* dx, float* dsh, float* dg,
+                              hipStream_t st) {
+  return dispatch_cpl<2>(s, MsgBwd{a, src, dst, dcsr, scsr, grad, dx, dsh, dg, st});
 }
 
 }  // namespace ictc

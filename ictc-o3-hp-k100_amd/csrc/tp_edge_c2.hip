@@ -1,4 +1,4 @@
-// Per-edge TP forward / first adjoint instantiations (one wave per edge).
+// Per-edge TP forward / first adjoint launchers, CPL = 2 channels per lane.
 #include "ictc_launch.h"
 
 namespace ictc {
@@ -28,13 +28,13 @@ struct EdgeBwd {
 };
 }  // namespace
 
-hipError_t launch_edge_fwd(const TpShape& s, const Operands& a, float* out, hipStream_t st) {
-  return dispatch(s, EdgeFwd{a, out, st});
+hipError_t launch_edge_fwd_c2(const TpShape& s, const Operands& a, float* out, hipStream_t st) {
+  return dispatch_cpl<2>(s, EdgeFwd{a, out, st});
 }
 
-hipError_t launch_edge_bwd(const TpShape& s, const Operands& a, const float* grad, float* dx, float* dsh, float* dg,
-                           hipStream_t st) {
-  return dispatch(s, EdgeBwd{a, grad, dx, dsh, dg, st});
+hipError_t launch_edge_bwd_c2(const TpShape& s, const Operands& a, const float* grad, float* dx, float* dsh,
+                               float* dg, hipStream_t st) {
+  return dispatch_cpl<2>(s, EdgeBwd{a, grad, dx, dsh, dg, st});
 }
 
 }  // namespace ictc

@@ -254,7 +254,12 @@ class PureCartesianICTDFix(nn.Module):
         species = self.atomic_number_to_index[A.long()]
         if topology is None:
             topology = tpo.Topology(edge_src, edge_dst, N)
-        shift_vec = torch.einsum("ni,nij->nj", edge_shifts.to(pos.dtype), cell[batch[edge_src]])
+        shifts = edge_shifts.to(pos.dtype)
+        if cell.shape[0] == 1:
+            shift_vec = shifts @ cell[0]
+        else:  # per-edge cell rows without a batched 1x3x3 GEMM per edge
+            cells = cell[batch[edge_src]]
+            shift_vec = (shifts.unsqueeze(-1) * cells).sum(1)
         vec = pos[edge_dst] - pos[edge_src] + shift_vec
         r = vec.norm(dim=1)
         n = vec / r.clamp(min=1e-8).unsqueeze(-1)

@@ -75,10 +75,12 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
         output = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, topology=topology)
         atomic = (output[0] if isinstance(output, tuple) else output).reshape(n)
         selected = atomic if owned_mask is None else atomic * owned_mask.to(atomic)
-        energy64 = selected.double().new_zeros(cell.shape[0]).index_add(0, batch, selected.double())
+        # per-graph sums in FP64 as a one-hot GEMV (no atomics: deterministic and contention free)
+        onehot = torch.nn.functional.one_hot(batch, cell.shape[0]).to(torch.float64)
+        energy64 = onehot.t() @ selected.double()
         force = -torch.autograd.grad(energy64.sum() + pos.sum() * 0.0, pos, create_graph=training,
                                      retain_graph=training)[0]
-        energy = energy64.to(atomic.dtype) if not training else energy64.to(atomic.dtype)
+        energy = energy64.to(atomic.dtype)
         result = {"energy": energy, "forces": force, "atomic_energy": atomic}
         return result if training else {key: value.detach() for key, value in result.items()}
 
