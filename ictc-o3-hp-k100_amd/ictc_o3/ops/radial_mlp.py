@@ -1,0 +1,79 @@
+"""Radial MLP of the interaction blocks with a fused HIP kernel for its hidden layers.
+
+fc = Linear(8,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64, P*C)
+on the radial basis of the edge lengths (mace_ictc/models/mace/layers.py:826-835,
+radial_basis.py:11-92).  ``radial_gates`` runs the radial basis and the three
+hidden layers in one MFMA kernel (writing only pre-activations and the last
+hidden activation), the 64 -> P*C gate GEMM through the ROCm BLAS library,
+and its adjoint fuses the hidden-layer backward down to d/dr.  It supports
+first derivatives (forces, first-order parameter gradients); callers that need
+second derivatives (force-loss training) use the composable path instead.
+"""
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from ictc_o3 import _native as nat
+
+
+def _c(t):
+    return t if t.is_contiguous() else t.contiguous()
+
+
+class _RadialGates(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, r, W1, W2, W3, W4, cutoff, poly_p, scale):
+        ctx.inputs = (r, W1, W2, W3, W4) if r.requires_grad or W1.requires_grad else None
+        r = _c(r)
+        W1, W2, W3, W4 = (_c(w.detach()) for w in (W1, W2, W3, W4))
+        E = r.shape[0]
+        z1, z2, z3, a3 = (r.new_empty(E, 64) for _ in range(4))
+        nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
+                 nat.ptr(W3), float(scale), nat.ptr(z1), nat.ptr(z2), nat.ptr(z3), nat.ptr(a3), nat.stream_of(r))
+        gates = torch.nn.functional.linear(a3, W4)
+        ctx.cfg = (cutoff, poly_p, scale)
+        ctx.save_for_backward(r, W1, W2, W3, W4, z1, z2, z3, a3)
+        return gates
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dg):
+        r, W1, W2, W3, W4, z1, z2, z3, a3 = ctx.saved_tensors
+        cutoff, poly_p, scale = ctx.cfg
+        dg = _c(dg)
+        E = r.shape[0]
+        from ictc_o3.autograd import required_gradients
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:5]) if ctx.inputs else ctx.needs_input_grad[:5]
+        ctx.inputs = None
+        need_w = any(needs[1:5])
+        da3 = torch.mm(dg, W4)
+        dr = r.new_empty(E)
+        dz = [r.new_empty(E, 64) for _ in range(3)] if need_w else [None, None, None]
+        nat.call("ictc_radial_mlp_bwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
+                 nat.ptr(W3), float(scale), nat.ptr(z1), nat.ptr(z2), nat.ptr(z3), nat.ptr(da3), nat.ptr(dr),
+                 nat.ptr(dz[0]), nat.ptr(dz[1]), nat.ptr(dz[2]), nat.stream_of(r))
+        dW = [None] * 4
+        if need_w:
+            from ictc_o3.ops.activation import _silu, _radial
+            a1 = _silu(0, z1, None, None, scale)
+            a2 = _silu(0, z2, None, None, scale)
+            R = _radial(0, r, None, None, 8, cutoff, poly_p)
+            dW = [dz[0].t() @ R, dz[1].t() @ a1, dz[2].t() @ a2, dg.t() @ a3]
+        return (dr if needs[0] else None, *[d if n else None for d, n in zip(dW, needs[1:5])], None, None, None)
+
+
+def fused_supported(fc: torch.nn.Sequential) -> bool:
+    """True when fc is Linear(8,64), act, Linear(64,64), act, Linear(64,64), act, Linear(64, M) without biases."""
+    lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
+    if len(lin) != 4 or any(m.bias is not None for m in lin):
+        return False
+    return (tuple(lin[0].weight.shape) == (64, 8) and tuple(lin[1].weight.shape) == (64, 64)
+            and tuple(lin[2].weight.shape) == (64, 64) and lin[3].weight.shape[1] == 64)
+
+
+def radial_gates(r: torch.Tensor, fc: torch.nn.Sequential, cutoff: float, poly_p: int, scale: float):
+    """[E] edge lengths -> [E, P*C] gates through the fused kernel (first derivatives only)."""
+    lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
+    return _RadialGates.apply(r, lin[0].weight, lin[1].weight, lin[2].weight, lin[3].weight, float(cutoff),
+                              int(poly_p), float(scale))

@@ -24,6 +24,7 @@ import torch.nn as nn
 from torch.autograd.function import once_differentiable
 
 from ictc_o3 import _native as nat
+from ictc_o3.autograd import required_gradients
 from ictc_o3.basis import e3nn_basis
 
 
@@ -123,8 +124,9 @@ class _SC(torch.autograd.Function):
         if go is None:
             return (None,) * (4 + len(ctx.spec.slots))
         x, *ws = ctx.saved_tensors
-        need_x = ctx.needs_input_grad[3]
-        need_w = any(ctx.needs_input_grad[4:])
+        needs = required_gradients((x, *ws), ctx.needs_input_grad[3:])
+        need_x = needs[0]
+        need_w = any(needs[1:])
         grads = _SCAdjoint.apply(ctx.spec, ctx.species, ctx.holder, need_x, need_w, x, _c(go), *ws)
         return (None, None, None, *grads)
 
@@ -144,8 +146,9 @@ class _SCAdjoint(torch.autograd.Function):
     def backward(ctx, hdx, *hdws):
         x, go, *ws = ctx.saved_tensors
         spec, species, holder = ctx.spec, ctx.species, ctx.holder
-        n_x, n_go = ctx.needs_input_grad[5], ctx.needs_input_grad[6]
-        n_w = ctx.needs_input_grad[7:]
+        needs = required_gradients((x, go, *ws), ctx.needs_input_grad[5:])
+        n_x, n_go = needs[0], needs[1]
+        n_w = needs[2:]
         have_hw = any(h is not None for h in hdws)
         hws = tuple(h if h is not None else torch.zeros_like(w) for h, w in zip(hdws, ws)) if have_hw else None
         dx = dgo = None

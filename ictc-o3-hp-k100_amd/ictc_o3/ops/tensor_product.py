@@ -25,6 +25,7 @@ from typing import Optional
 import torch
 
 from ictc_o3 import _native as nat
+from ictc_o3.autograd import required_gradients
 
 
 @dataclass(frozen=True)
@@ -105,7 +106,7 @@ class EdgeTP(torch.autograd.Function):
         if go is None:
             return None, None, None, None
         x, sh, g = ctx.saved_tensors
-        need = tuple(ctx.needs_input_grad[:3])
+        need = required_gradients((x, sh, g), ctx.needs_input_grad[:3])
         if not any(need):
             return None, None, None, None
         dx, dsh, dg = EdgeTPAdjoint.apply(x, sh, g, _c(go), ctx.spec, need)
@@ -133,7 +134,7 @@ class EdgeTPAdjoint(torch.autograd.Function):
     def backward(ctx, hx, hsh, hg):
         x, sh, g, go = ctx.saved_tensors
         spec = ctx.spec
-        nx, nsh, ng, ngo = ctx.needs_input_grad[:4]
+        nx, nsh, ng, ngo = required_gradients((x, sh, g, go), ctx.needs_input_grad[:4])
         dx = dsh = dg = dgo = None
         if ngo:
             if hx is not None:
@@ -233,7 +234,7 @@ class Message(torch.autograd.Function):
         if go is None:
             return (None,) * 6
         x, sh, g = ctx.saved_tensors
-        need = tuple(ctx.needs_input_grad[:3])
+        need = required_gradients((x, sh, g), ctx.needs_input_grad[:3])
         if not any(need):
             return (None,) * 6
         dx, dsh, dg = MessageAdjoint.apply(x, sh, g, _c(go), ctx.spec, ctx.topo, ctx.mask, need)
@@ -261,7 +262,7 @@ class MessageAdjoint(torch.autograd.Function):
     def backward(ctx, hx, hsh, hg):
         x, sh, g, go = ctx.saved_tensors
         spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
-        nx, nsh, ng, ngo = ctx.needs_input_grad[:4]
+        nx, nsh, ng, ngo = required_gradients((x, sh, g, go), ctx.needs_input_grad[:4])
         dx = dsh = dg = dgo = None
         if ngo:
             if hx is not None:

@@ -158,10 +158,15 @@ class Interaction(nn.Module):
             self._spec = tpo.make_spec(self.input_lmax, self.lmax, self.lmax, self.channels, None)
         return self._spec
 
-    def forward(self, h, species, Y, radial, topo, mask):
+    def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None):
+        """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path)."""
         C = self.channels
         x = self.linear_up(h)
-        gates = self.fc(radial)
+        if radial is None:
+            from ictc_o3.ops.radial_mlp import radial_gates
+            gates = radial_gates(r, self.fc, *radial_cfg)
+        else:
+            gates = self.fc(radial)
         m = tpo.message(x, Y, gates, self.spec(), topo, mask)
         message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8))
         sc = self.self_connection.forward_l0(h[:, :C], species)
@@ -249,7 +254,13 @@ class PureCartesianICTDFix(nn.Module):
         from ictc_o3.ops.activation import radial_embedding
         return radial_embedding(r, self.max_radius, self.number_of_basis, self.polynomial_cutoff_p)
 
-    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, topology=None):
+    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, topology=None, second_order=True):
+        """Per-atom energies [N, 1].
+
+        second_order=False allows the fused radial-MLP kernel, whose adjoint
+        supports first derivatives only (forces, parameter gradients); the
+        default keeps every operator differentiable to second order.
+        """
         N = pos.shape[0]
         species = self.atomic_number_to_index[A.long()]
         if topology is None:
@@ -265,11 +276,15 @@ class PureCartesianICTDFix(nn.Module):
         n = vec / r.clamp(min=1e-8).unsqueeze(-1)
         mask = (r <= self.max_radius).to(pos.dtype)
         Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
-        radial = self.radial_embedding(r)
+        from ictc_o3.ops.radial_mlp import fused_supported
+        fused = (not second_order and self.number_of_basis == 8
+                 and all(fused_supported(inter.fc) for inter in self.interactions))
+        radial = None if fused else self.radial_embedding(r)
+        radial_cfg = (self.max_radius, self.polynomial_cutoff_p, SILU_SCALE)
         h = self.node_embedding.weight.t().index_select(0, species)
         energy = None
         for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
-            message, sc = inter(h, species, Y, radial, topology, mask)
+            message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg)
             h = prod(message, sc, species)
             if i < self.num_interaction - 1:
                 e = self.layer_energy_readouts[i](h[:, :self.channels])

@@ -72,12 +72,16 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
         raise ValueError("owned_mask must be a fixed [N] tensor")
     with torch.enable_grad():
         pos = positions if positions.requires_grad else positions.detach().requires_grad_(True)
-        output = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, topology=topology)
+        output = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, topology=topology,
+                       second_order=training)
         atomic = (output[0] if isinstance(output, tuple) else output).reshape(n)
         selected = atomic if owned_mask is None else atomic * owned_mask.to(atomic)
-        # per-graph sums in FP64 as a one-hot GEMV (no atomics: deterministic and contention free)
-        onehot = torch.nn.functional.one_hot(batch, cell.shape[0]).to(torch.float64)
-        energy64 = onehot.t() @ selected.double()
+        # per-graph sums in FP64 without atomics (deterministic, contention free)
+        if cell.shape[0] == 1:
+            energy64 = selected.double().sum().reshape(1)
+        else:
+            onehot = torch.nn.functional.one_hot(batch, cell.shape[0]).to(torch.float64)
+            energy64 = onehot.t() @ selected.double()
         force = -torch.autograd.grad(energy64.sum() + pos.sum() * 0.0, pos, create_graph=training,
                                      retain_graph=training)[0]
         energy = energy64.to(atomic.dtype)

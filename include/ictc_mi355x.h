@@ -133,6 +133,22 @@ int ictc_silu(int mode, const float* x, const float* grad, const float* tangent,
 int ictc_radial(int order, const float* r, const float* grad, const float* tangent, int64_t edges, int num_basis,
                 float cutoff, int poly_p, float* out, void* stream);
 
+/* ---- Fused radial MLP (hidden layers) ---------------------------------------
+ * Replaces the hidden part of the interaction's radial MLP `fc`
+ * (mace_ictc/models/mace/layers.py:826-835, radial_basis.py:42-92) and its
+ * first adjoint: r [E] -> R = radial basis (num_basis 8, poly_p cutoff) ->
+ * z1 = R W1^T -> a1 = s silu(z1) -> z2 = a1 W2^T -> a2 -> z3 = a2 W3^T -> a3.
+ * W1 [64,8], W2/W3 [64,64] row-major (nn.Linear layout); outputs z1..z3, a3
+ * [E,64].  The adjoint takes da3 [E,64] and returns dr [E]; dz1..dz3 (may be
+ * NULL) are the pre-activation gradients for weight gradients.  MFMA FP32.   */
+int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                        const float* W1, const float* W2, const float* W3, float silu_scale, float* z1, float* z2,
+                        float* z3, float* a3, void* stream);
+int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                        const float* W1, const float* W2, const float* W3, float silu_scale, const float* z1,
+                        const float* z2, const float* z3, const float* da3, float* dr, float* dz1, float* dz2,
+                        float* dz3, void* stream);
+
 /* ---- Symmetric contraction (bridge-U, correlation 1..3) -------------------
  * Replaces the SC circuits of ICTDBridgeUSymmetricContractionSO3.forward
  * (ictc_o3/ops/symmetric_contraction.py:98-147 -> factorized_contraction.py:
