@@ -1,0 +1,144 @@
+// Edge geometry of the interaction input (mace_ictc/models/pure_cartesian_ictd_layers.py:
+// 1288-1297): vec = pos[dst] - pos[src] + shift, r = |vec|, n = vec / max(r, 1e-8),
+// mask = [r <= cutoff], and the first adjoint back to the positions.
+//
+// The adjoint is a deterministic gather, not a scatter: node i sums the edge
+// adjoints of its incoming edges (receiver-sorted CSR) and subtracts those of
+// its outgoing edges (source-sorted CSR), each in CSR order, so the result is
+// bitwise reproducible and needs no float atomics.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ictc_mi355x.h"
+
+namespace ictc {
+int set_error(int code, const char* msg);
+}
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr float kClamp = 1e-8f;
+
+__global__ __launch_bounds__(kBlock) void geometry_fwd_kernel(const float* __restrict__ pos,
+                                                              const float* __restrict__ shift,
+                                                              const int64_t* __restrict__ src,
+                                                              const int64_t* __restrict__ dst, int64_t E, float rc,
+                                                              float* __restrict__ r, float* __restrict__ n,
+                                                              float* __restrict__ mask) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  const int64_t s = src[e], d = dst[e];
+  float v[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) v[c] = pos[3 * d + c] - pos[3 * s + c] + (shift ? shift[3 * e + c] : 0.f);
+  const float len = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const float den = fmaxf(len, kClamp);
+  r[e] = len;
+#pragma unroll
+  for (int c = 0; c < 3; ++c) n[3 * e + c] = v[c] / den;
+  if (mask) mask[e] = len <= rc ? 1.f : 0.f;
+}
+
+// d vec of one edge from dr and dn:
+//   dr * vec / r + dn / max(r, eps) - [r > eps] (dn . vec) vec / (max(r, eps)^2 r)
+// which for r > eps is dr n + (dn - (dn . n) n) / r.
+__device__ __forceinline__ void edge_adjoint(const float* __restrict__ r, const float* __restrict__ n,
+                                             const float* __restrict__ dr, const float* __restrict__ dn, int64_t e,
+                                             float* out) {
+  const float len = r[e];
+  const float nx = n[3 * e], ny = n[3 * e + 1], nz = n[3 * e + 2];
+  const float g = dr ? dr[e] : 0.f;
+  float a[3] = {0.f, 0.f, 0.f};
+  if (dn) {
+    a[0] = dn[3 * e];
+    a[1] = dn[3 * e + 1];
+    a[2] = dn[3 * e + 2];
+  }
+  if (len > kClamp) {
+    const float inv = 1.f / len, dot = a[0] * nx + a[1] * ny + a[2] * nz;
+    out[0] = g * nx + (a[0] - dot * nx) * inv;
+    out[1] = g * ny + (a[1] - dot * ny) * inv;
+    out[2] = g * nz + (a[2] - dot * nz) * inv;
+  } else {
+    // Here vec = n * eps: dr vec / r = dr (eps / r) n (0 at r = 0, torch's convention), and the clamp passes no gradient.
+    const float inv = 1.f / kClamp, gr = len > 0.f ? g * kClamp / len : 0.f;
+    out[0] = gr * nx + a[0] * inv;
+    out[1] = gr * ny + a[1] * inv;
+    out[2] = gr * nz + a[2] * inv;
+  }
+}
+
+// One thread per node: dpos[i] = sum_{dst(e)=i} dvec_e - sum_{src(e)=i} dvec_e.
+__global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __restrict__ r,
+                                                              const float* __restrict__ n,
+                                                              const float* __restrict__ dr,
+                                                              const float* __restrict__ dn, int64_t N,
+                                                              const int32_t* __restrict__ dptr,
+                                                              const int32_t* __restrict__ dord,
+                                                              const int32_t* __restrict__ sptr,
+                                                              const int32_t* __restrict__ sord,
+                                                              float* __restrict__ dshift,
+                                                              float* __restrict__ dpos) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= N) return;
+  float acc[3] = {0.f, 0.f, 0.f}, t[3];
+  for (int32_t k = dptr[i]; k < dptr[i + 1]; ++k) {
+    const int64_t e = dord[k];
+    edge_adjoint(r, n, dr, dn, e, t);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) acc[c] += t[c];
+    if (dshift) {
+#pragma unroll
+      for (int c = 0; c < 3; ++c) dshift[3 * e + c] = t[c];
+    }
+  }
+  for (int32_t k = sptr[i]; k < sptr[i + 1]; ++k) {
+    edge_adjoint(r, n, dr, dn, sord[k], t);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) acc[c] -= t[c];
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) dpos[3 * i + c] = acc[c];
+}
+
+int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+int launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return ICTC_OK;
+  char buf[256];
+  snprintf(buf, sizeof(buf), "%s: %s", what, hipGetErrorString(e));
+  return fail(ICTC_ERR_RUNTIME, buf);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* src, const int64_t* dst,
+                           int64_t nodes, int64_t edges, float cutoff, float* r, float* n, float* mask,
+                           void* stream) {
+  if (nodes < 0 || edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge geometry: negative size");
+  if (edges == 0) return ICTC_OK;
+  if (!pos || !src || !dst || !r || !n) return fail(ICTC_ERR_ARGUMENT, "edge geometry: null operand");
+  hipLaunchKernelGGL(geometry_fwd_kernel, dim3((unsigned)((edges + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                     (hipStream_t)stream, pos, shift, src, dst, edges, cutoff, r, n, mask);
+  return launch_status("ictc_edge_geometry_fwd launch");
+}
+
+int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, const float* dn, int64_t nodes,
+                           int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order, const int32_t* src_ptr,
+                           const int32_t* src_order, float* dshift, float* dpos, void* stream) {
+  if (nodes < 0 || edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge geometry: negative size");
+  if (nodes == 0) return ICTC_OK;
+  if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!r || !n || !dst_order || !src_order)))
+    return fail(ICTC_ERR_ARGUMENT, "edge geometry adjoint: null operand");
+  hipLaunchKernelGGL(geometry_bwd_kernel, dim3((unsigned)((nodes + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                     (hipStream_t)stream, r, n, dr, dn, nodes, dst_ptr, dst_order, src_ptr, src_order, dshift, dpos);
+  return launch_status("ictc_edge_geometry_bwd launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+"""Edge geometry (vec, r, n, mask) with a deterministic CSR-gather adjoint to the positions.
+
+Forward follows mace_ictc/models/pure_cartesian_ictd_layers.py:1288-1297
+(vec = pos[dst] - pos[src] + shift, r = |vec|, n = vec / r.clamp(min=1e-8),
+mask = r <= cutoff).  The adjoint replaces the two index-gather backwards
+(scatter-adds into pos) with one kernel that sums, per node, the adjoints of its
+incoming edges minus those of its outgoing edges in CSR order.  First
+derivatives only: force-loss training keeps the composable torch path.
+"""
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from ictc_o3 import _native as nat
+
+
+def _c(t):
+    return t if t.is_contiguous() else t.contiguous()
+
+
+class _EdgeGeometry(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pos, shift, topo, cutoff):
+        pos = _c(pos.detach())
+        shift = None if shift is None else _c(shift.detach())
+        E, N = topo.src.numel(), pos.shape[0]
+        r = pos.new_empty(E)
+        n = pos.new_empty(E, 3)
+        mask = pos.new_empty(E)
+        nat.call("ictc_edge_geometry_fwd", nat.ptr(pos), nat.ptr(shift), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
+                 float(cutoff), nat.ptr(r), nat.ptr(n), nat.ptr(mask), nat.stream_of(pos))
+        ctx.topo, ctx.nodes = topo, N
+        ctx.mark_non_differentiable(mask)
+        ctx.save_for_backward(r, n)
+        return r, n, mask
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dr, dn, _dmask):
+        r, n = ctx.saved_tensors
+        topo, N = ctx.topo, ctx.nodes
+        E = r.numel()
+        dr = None if dr is None else _c(dr)
+        dn = None if dn is None else _c(dn)
+        dpos = r.new_empty(N, 3)
+        dshift = r.new_empty(E, 3) if ctx.needs_input_grad[1] else None
+        src_csr = topo.by_src
+        nat.call("ictc_edge_geometry_bwd", nat.ptr(r), nat.ptr(n), nat.ptr(dr), nat.ptr(dn), N, E,
+                 nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order), nat.ptr(src_csr.ptr), nat.ptr(src_csr.order),
+                 nat.ptr(dshift), nat.ptr(dpos), nat.stream_of(r))
+        return (dpos if ctx.needs_input_grad[0] else None), dshift, None, None
+
+
+def edge_geometry(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: float):
+    """(r [E], n [E,3], mask [E]) for the edges of ``topo`` (a Topology over src/dst), float32."""
+    if pos.dtype != torch.float32 or (shift is not None and shift.dtype != torch.float32):
+        raise TypeError("edge_geometry runs in float32")
+    if pos.dim() != 2 or pos.shape[1] != 3:
+        raise ValueError("pos must be [N, 3]")
+    if shift is not None and tuple(shift.shape) != (topo.src.numel(), 3):
+        raise ValueError("shift must be [E, 3]")
+    return _EdgeGeometry.apply(pos, shift, topo, float(cutoff))

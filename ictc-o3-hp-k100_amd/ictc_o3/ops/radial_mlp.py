@@ -28,18 +28,18 @@ class _RadialGates(torch.autograd.Function):
         r = _c(r)
         W1, W2, W3, W4 = (_c(w.detach()) for w in (W1, W2, W3, W4))
         E = r.shape[0]
-        z1, z2, z3, a3 = (r.new_empty(E, 64) for _ in range(4))
+        a3 = r.new_empty(E, 64)
         nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
-                 nat.ptr(W3), float(scale), nat.ptr(z1), nat.ptr(z2), nat.ptr(z3), nat.ptr(a3), nat.stream_of(r))
+                 nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
         gates = torch.nn.functional.linear(a3, W4)
         ctx.cfg = (cutoff, poly_p, scale)
-        ctx.save_for_backward(r, W1, W2, W3, W4, z1, z2, z3, a3)
+        ctx.save_for_backward(r, W1, W2, W3, W4, a3)
         return gates
 
     @staticmethod
     @once_differentiable
     def backward(ctx, dg):
-        r, W1, W2, W3, W4, z1, z2, z3, a3 = ctx.saved_tensors
+        r, W1, W2, W3, W4, a3 = ctx.saved_tensors
         cutoff, poly_p, scale = ctx.cfg
         dg = _c(dg)
         E = r.shape[0]
@@ -49,17 +49,16 @@ class _RadialGates(torch.autograd.Function):
         need_w = any(needs[1:5])
         da3 = torch.mm(dg, W4)
         dr = r.new_empty(E)
-        dz = [r.new_empty(E, 64) for _ in range(3)] if need_w else [None, None, None]
+        extra = [r.new_empty(E, 64) for _ in range(5)] if need_w else [None] * 5   # dz1, dz2, dz3, a1, a2
         nat.call("ictc_radial_mlp_bwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
-                 nat.ptr(W3), float(scale), nat.ptr(z1), nat.ptr(z2), nat.ptr(z3), nat.ptr(da3), nat.ptr(dr),
-                 nat.ptr(dz[0]), nat.ptr(dz[1]), nat.ptr(dz[2]), nat.stream_of(r))
+                 nat.ptr(W3), float(scale), nat.ptr(da3), nat.ptr(dr), *[nat.ptr(t) for t in extra],
+                 nat.stream_of(r))
         dW = [None] * 4
         if need_w:
-            from ictc_o3.ops.activation import _silu, _radial
-            a1 = _silu(0, z1, None, None, scale)
-            a2 = _silu(0, z2, None, None, scale)
+            from ictc_o3.ops.activation import _radial
+            dz1, dz2, dz3, a1, a2 = extra
             R = _radial(0, r, None, None, 8, cutoff, poly_p)
-            dW = [dz[0].t() @ R, dz[1].t() @ a1, dz[2].t() @ a2, dg.t() @ a3]
+            dW = [dz1.t() @ R, dz2.t() @ a1, dz3.t() @ a2, dg.t() @ a3]
         return (dr if needs[0] else None, *[d if n else None for d, n in zip(dW, needs[1:5])], None, None, None)
 
 

@@ -271,10 +271,14 @@ class PureCartesianICTDFix(nn.Module):
         else:  # per-edge cell rows without a batched 1x3x3 GEMM per edge
             cells = cell[batch[edge_src]]
             shift_vec = (shifts.unsqueeze(-1) * cells).sum(1)
-        vec = pos[edge_dst] - pos[edge_src] + shift_vec
-        r = vec.norm(dim=1)
-        n = vec / r.clamp(min=1e-8).unsqueeze(-1)
-        mask = (r <= self.max_radius).to(pos.dtype)
+        if second_order or pos.dtype != torch.float32:
+            vec = pos[edge_dst] - pos[edge_src] + shift_vec
+            r = vec.norm(dim=1)
+            n = vec / r.clamp(min=1e-8).unsqueeze(-1)
+            mask = (r <= self.max_radius).to(pos.dtype)
+        else:
+            from ictc_o3.ops.geometry import edge_geometry
+            r, n, mask = edge_geometry(pos, shift_vec, topology, self.max_radius)
         Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
         from ictc_o3.ops.radial_mlp import fused_supported
         fused = (not second_order and self.number_of_basis == 8

@@ -133,21 +133,37 @@ int ictc_silu(int mode, const float* x, const float* grad, const float* tangent,
 int ictc_radial(int order, const float* r, const float* grad, const float* tangent, int64_t edges, int num_basis,
                 float cutoff, int poly_p, float* out, void* stream);
 
+/* ---- Edge geometry ---------------------------------------------------------
+ * Replaces the edge-vector block of the model forward
+ * (mace_ictc/models/pure_cartesian_ictd_layers.py:1288-1297, backbone.py:944):
+ * vec = pos[dst] - pos[src] + shift (shift [E,3] may be NULL), r = |vec|,
+ * n = vec / max(r, 1e-8), mask = [r <= cutoff] (mask may be NULL).  pos [N,3].
+ * The adjoint takes dr [E] and dn [E,3] (either may be NULL = zero) and writes
+ * dpos [N,3] = sum over incoming edges - sum over outgoing edges of d vec, as
+ * a gather over the receiver- and source-sorted CSRs (ictc_csr_build over dst
+ * and over src), in CSR order: deterministic, no atomics.  dshift [E,3] (may
+ * be NULL) receives d vec per edge.  Every src/dst id must lie in [0, N).     */
+int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* src, const int64_t* dst,
+                           int64_t nodes, int64_t edges, float cutoff, float* r, float* n, float* mask,
+                           void* stream);
+int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, const float* dn, int64_t nodes,
+                           int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order, const int32_t* src_ptr,
+                           const int32_t* src_order, float* dshift, float* dpos, void* stream);
+
 /* ---- Fused radial MLP (hidden layers) ---------------------------------------
  * Replaces the hidden part of the interaction's radial MLP `fc`
  * (mace_ictc/models/mace/layers.py:826-835, radial_basis.py:42-92) and its
- * first adjoint: r [E] -> R = radial basis (num_basis 8, poly_p cutoff) ->
- * z1 = R W1^T -> a1 = s silu(z1) -> z2 = a1 W2^T -> a2 -> z3 = a2 W3^T -> a3.
- * W1 [64,8], W2/W3 [64,64] row-major (nn.Linear layout); outputs z1..z3, a3
- * [E,64].  The adjoint takes da3 [E,64] and returns dr [E]; dz1..dz3 (may be
- * NULL) are the pre-activation gradients for weight gradients.  MFMA FP32.   */
+ * first adjoint: r [E] -> R = radial basis (num_basis 8, cutoff polynomial of
+ * order poly_p >= 2) -> a1 = s silu(R W1^T) -> a2 = s silu(a1 W2^T) ->
+ * a3 = s silu(a2 W3^T), written to a3 [E,64].  W1 [64,8], W2/W3 [64,64]
+ * row-major (nn.Linear layout).  The adjoint recomputes the forward, takes
+ * da3 [E,64] and writes dr [E]; dz1..dz3 (pre-activation gradients) and a1, a2
+ * [E,64] may be NULL and are only needed for weight gradients.  MFMA FP32.  */
 int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
-                        const float* W1, const float* W2, const float* W3, float silu_scale, float* z1, float* z2,
-                        float* z3, float* a3, void* stream);
+                        const float* W1, const float* W2, const float* W3, float silu_scale, float* a3, void* stream);
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
-                        const float* W1, const float* W2, const float* W3, float silu_scale, const float* z1,
-                        const float* z2, const float* z3, const float* da3, float* dr, float* dz1, float* dz2,
-                        float* dz3, void* stream);
+                        const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
+                        float* dr, float* dz1, float* dz2, float* dz3, float* a1, float* a2, void* stream);
 
 /* ---- Symmetric contraction (bridge-U, correlation 1..3) -------------------
  * Replaces the SC circuits of ICTDBridgeUSymmetricContractionSO3.forward

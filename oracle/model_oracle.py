@@ -40,6 +40,15 @@ def radial(r, r_max, K=8, p=5):
     return emb * (env * (r < r_max).to(r.dtype))[:, None]
 
 
+def edge_geometry(pos, src, dst, shift_vec, cutoff):
+    """vec = pos[dst] - pos[src] + shift, r = |vec|, n = vec / max(r, 1e-8), mask = [r <= cutoff]
+    (mace_ictc/models/pure_cartesian_ictd_layers.py:1293-1297)."""
+    vec = pos[dst] - pos[src] + shift_vec
+    r = vec.norm(dim=1)
+    n = vec / r.clamp(min=1e-8)[:, None]
+    return r, n, (r <= cutoff).to(pos.dtype)
+
+
 def _silu(x):
     return torch.nn.functional.silu(x) * SILU
 
@@ -51,10 +60,8 @@ def forward(sd, cfg, pos, A, batch, src, dst, shifts, cell, dtype=torch.float64)
     table = cfg["z_table"]
     species = table[A.long()]
     g = lambda k: sd[k].to(device="cpu", dtype=dtype)
-    vec = pos[dst] - pos[src] + torch.einsum("ni,nij->nj", shifts.to(dtype), cell[batch[src]].to(dtype))
-    r = vec.norm(dim=1)
-    n = vec / r.clamp(min=1e-8)[:, None]
-    mask = (r <= cfg["cutoff"]).to(dtype)
+    shift_vec = torch.einsum("ni,nij->nj", shifts.to(dtype), cell[batch[src]].to(dtype))
+    r, n, mask = edge_geometry(pos, src, dst, shift_vec, cfg["cutoff"])
     Y = orc.direction_harmonics(n, Le)
     rad = radial(r, cfg["cutoff"], 8, 5)
     N, E = pos.shape[0], src.numel()

@@ -1,0 +1,68 @@
+"""GPU parity of the edge-geometry op (r, n, mask and the CSR-gather adjoint to positions).
+
+Compared with the float64 restatement model_oracle.edge_geometry under torch
+autograd: r and n within 2e-6 relative (fp32 rounding of vec), position / shift gradients within 1e-5
+relative (max-norm); mask bit-exact away from the cutoff.  The oracle's own
+gradient is pinned by finite differences (test_geometry_oracle_gradcheck), and
+translation invariance (sum over nodes of dpos = 0) checks the gather signs.
+"""
+import pytest
+import torch
+
+import model_oracle as mo
+from helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(N, E, seed, sort):
+    g = torch.Generator().manual_seed(seed)
+    pos = (torch.rand(N, 3, generator=g, dtype=torch.float64) * 6.0).float().double()   # fp32-representable
+    src = torch.randint(0, N, (E,), generator=g)
+    dst = torch.randint(0, N, (E,), generator=g)
+    keep = src != dst
+    src, dst = src[keep], dst[keep]
+    if sort:
+        o = torch.argsort(dst, stable=True)
+        src, dst = src[o], dst[o]
+    shift = torch.randn(src.numel(), 3, generator=g, dtype=torch.float64).float().double()
+    return pos, src, dst, shift
+
+
+@pytest.mark.parametrize("N,E,seed,sort,with_shift", [(200, 4000, 1, True, True), (57, 900, 2, False, True),
+                                                      (40, 300, 3, True, False), (7, 0, 4, True, True),
+                                                      (1000, 20000, 5, False, False)])
+def test_edge_geometry(device, N, E, seed, sort, with_shift):
+    from ictc_o3.ops.geometry import edge_geometry
+    from ictc_o3.ops.tensor_product import Topology
+    pos, src, dst, shift = _case(N, E, seed, sort)
+    E = src.numel()
+    g = torch.Generator().manual_seed(seed + 100)
+    gr = torch.randn(E, generator=g, dtype=torch.float64)
+    gn = torch.randn(E, 3, generator=g, dtype=torch.float64)
+
+    p64 = pos.clone().requires_grad_(True)
+    s64 = shift.clone().requires_grad_(True)
+    r, n, m = mo.edge_geometry(p64, src, dst, s64 if with_shift else torch.zeros_like(shift), 4.5)
+    if E:
+        torch.autograd.backward([r, n], [gr, gn])
+
+    pd = pos.float().to(device).requires_grad_(True)
+    sd = shift.float().to(device).requires_grad_(True) if with_shift else None
+    topo = Topology(src.to(device), dst.to(device), N)
+    r2, n2, m2 = edge_geometry(pd, sd, topo, 4.5)
+    if E:
+        assert rel_err(r2, r) < 2e-6 and rel_err(n2, n) < 2e-6
+        far = (r - 4.5).abs() > 1e-4
+        assert torch.equal(m2.cpu()[far].double(), m[far])
+        torch.autograd.backward([r2, n2], [gr.float().to(device), gn.float().to(device)])
+        assert rel_err(pd.grad, p64.grad) < 1e-5
+        assert pd.grad.double().sum(0).abs().max().item() < 1e-4 * pd.grad.abs().max().item()
+        if with_shift:
+            assert rel_err(sd.grad, s64.grad) < 1e-5
+        # deterministic: a second adjoint is bitwise equal
+        first = pd.grad.clone()
+        pd.grad = None
+        r3, n3, _ = edge_geometry(pd, sd, topo, 4.5)
+        torch.autograd.backward([r3, n3], [gr.float().to(device), gn.float().to(device)])
+        assert torch.equal(first, pd.grad)

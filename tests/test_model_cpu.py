@@ -83,3 +83,19 @@ def test_model_parameter_names_follow_reference():
               "products.0.linear.weight", "layer_energy_readouts.0.readout.weight",
               "last_layer_energy_readout.linear_1.weight", "last_layer_energy_readout.linear_2.weight"]:
         assert k in keys, k
+
+
+def test_geometry_oracle_gradcheck():
+    """The oracle's edge geometry is differentiable as the reference formula says (finite differences)."""
+    import model_oracle as mo
+    g = torch.Generator().manual_seed(0)
+    pos = (torch.rand(6, 3, generator=g, dtype=torch.float64) * 3).requires_grad_(True)
+    src = torch.tensor([0, 1, 2, 3, 4, 5, 0, 2])
+    dst = torch.tensor([1, 2, 3, 4, 5, 0, 3, 5])
+    shift = torch.randn(8, 3, generator=g, dtype=torch.float64).requires_grad_(True)
+    f = lambda p, s: tuple(mo.edge_geometry(p, src, dst, s, 4.5)[:2])
+    assert torch.autograd.gradcheck(f, (pos, shift))
+    r, n, _ = mo.edge_geometry(pos, src, dst, shift, 4.5)
+    vec = pos[dst] - pos[src] + shift
+    assert torch.allclose((n * n).sum(1), torch.ones(8, dtype=torch.float64))
+    assert torch.allclose((n * vec).sum(1), r)
