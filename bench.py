@@ -38,6 +38,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-k100_amd"))
 
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFLOPS = 157.3
+METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 
 
 def log(*a):
@@ -192,7 +194,7 @@ def run_cfg2(args):
     dom = max(kern, key=kern.get)
     achieved = nbytes[dom] / kern[dom] / 1e9
     result = {
-        "metric": "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline",
+        "metric": METRIC,
         "value": E / dt, "unit": "edges/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic (seeded uniform periodic positions, N(0,1) features, random-init MLP)",
@@ -279,33 +281,11 @@ def run_cfg4(args):
     dt = (time.perf_counter() - t0) / args.steps
     log(f"cfg4: N={N} E={E} step={dt * 1e3:.2f} ms energy={float(out['energy'][0]):.6f}")
 
-    # live timing of the dominant message kernels at layer-1 shapes (P11, C64)
-    stream = torch.cuda.current_stream(dev)
-    src, dst, sh = radius_graph_pbc(pos, cell[0], 4.5)
-    topo = tpo.Topology(src, dst, N)
-    inter = model.interactions[1]
-    spec = inter.spec()
-    g = torch.Generator(device=dev).manual_seed(3)
-    x = torch.randn(N, 9 * 64, device=dev, generator=g)
-    Y = torch.randn(E, 9, device=dev, generator=g)
-    with torch.no_grad():
-        r = torch.rand(E, device=dev, generator=g) * 3 + 1.5
-        gates = inter.fc(model.radial_embedding(r))
-    go = torch.randn(N, spec.out_components * 64, device=dev, generator=g)
-    t_fwd = time_launches(lambda: tpo._msg_fwd_raw(spec, topo, x, Y, gates, None), 5, stream)
-    t_bwd_e = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True)), 5,
-                            stream)
-    topo.by_src
-    t_bwd_x = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, False, False)), 5,
-                            stream)
-    nbytes = message_bytes(N, E, 64, 9, 9, spec.num_paths, spec.out_components)
-    kern = {"msg_fwd": t_fwd, "msg_bwd_edge": t_bwd_e, "msg_bwd_x": t_bwd_x}
-    for k, t in kern.items():
-        log(f"  layer-1 {k}: {t * 1e6:.1f} us  {nbytes[k] / t / 1e9:.0f} GB/s ({nbytes[k] / 1e6:.1f} MB)")
-    dom = "msg_fwd"
-    achieved = nbytes[dom] / kern[dom] / 1e9
+    src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
+    kern, nbytes = layer_message_kernels(model, src, dst, N)
+    achieved = nbytes["msg_fwd"] / kern["msg_fwd"] / 1e9
     result = {
-        "metric": "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline",
+        "metric": METRIC,
         "value": N / dt, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32",
@@ -322,26 +302,351 @@ def run_cfg4(args):
     return result, model
 
 
+def layer_message_kernels(model, src, dst, N, reps=5):
+    """Live HIP-event timing of the last interaction's message kernels (fwd, bwd_edge, bwd_x) at the run's shapes."""
+    import torch
+    from ictc_o3.ops import tensor_product as tpo
+    dev = src.device
+    stream = torch.cuda.current_stream(dev)
+    topo = tpo.Topology(src, dst, N)
+    inter = model.interactions[-1]
+    spec = inter.spec()
+    C = spec.channels
+    NX, NY = (spec.li + 1) ** 2, (spec.le + 1) ** 2
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(N, NX * C, device=dev, generator=g)
+    Y = torch.randn(src.numel(), NY, device=dev, generator=g)
+    with torch.no_grad():
+        r = torch.rand(src.numel(), device=dev, generator=g) * 3 + 1.5
+        gates = inter.fc(model.radial_embedding(r))
+    go = torch.randn(N, spec.out_components * C, device=dev, generator=g)
+    t_fwd = time_launches(lambda: tpo._msg_fwd_raw(spec, topo, x, Y, gates, None), reps, stream)
+    t_bwd_e = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True)), reps,
+                            stream)
+    topo.by_src
+    t_bwd_x = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, False, False)), reps,
+                            stream)
+    nbytes = message_bytes(N, src.numel(), C, NX, NY, spec.num_paths, spec.out_components)
+    kern = {"msg_fwd": t_fwd, "msg_bwd_edge": t_bwd_e, "msg_bwd_x": t_bwd_x}
+    for k, t in kern.items():
+        log(f"  last-layer {k}: {t * 1e6:.1f} us  {nbytes[k] / t / 1e9:.0f} GB/s ({nbytes[k] / 1e6:.1f} MB)")
+    return kern, nbytes
+
+
+def run_cfg1(args):
+    """EdgeTensorProduct fwd+bwd, C32 L2 ir_mul, E=257 (launch-latency bound) plus the same shapes at E=2^20."""
+    import torch
+    from ictc_o3 import EdgeTensorProduct, direction_harmonics
+    from ictc_o3.ops import tensor_product as tpo
+    dev = torch.device("cuda:0")
+    C, E = 32, 257
+    op = EdgeTensorProduct.create(input_lmax=2, edge_lmax=2, output_lmax=2, channels=C, device=dev)
+    torch.manual_seed(0)
+    blocks = {l: torch.randn(E, C, 2 * l + 1) for l in range(3)}
+    v = torch.randn(E, 3)
+    gates = torch.randn(E, op.gate_width)
+    x = op.pack_input({l: b.to(dev) for l, b in blocks.items()}).requires_grad_(True)
+    sh = torch.cat(direction_harmonics((v / v.norm(dim=1, keepdim=True)).to(dev), 2), -1).requires_grad_(True)
+    g = gates.to(dev).requires_grad_(True)
+
+    def step():
+        out = op(x, sh, g)
+        (out * out).mean().backward()
+
+    for _ in range(max(args.warmup, 3)):
+        step()
+    torch.cuda.synchronize()
+    steps = max(args.steps, 200)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    log(f"cfg1: E={E} step={dt * 1e6:.1f} us")
+
+    # kernel roofline at E = 2^20 (same shapes)
+    spec = op._prepare()
+    Eb = 1 << 20
+    gb = torch.Generator(device=dev).manual_seed(1)
+    xb = torch.randn(Eb, x.shape[1], device=dev, generator=gb)
+    shb = torch.randn(Eb, 9, device=dev, generator=gb)
+    gbt = torch.randn(Eb, op.gate_width, device=dev, generator=gb)
+    gob = torch.randn(Eb, op.output_width, device=dev, generator=gb)
+    stream = torch.cuda.current_stream(dev)
+    t_f = time_launches(lambda: tpo._edge_fwd_raw(spec, xb, shb, gbt), 20, stream)
+    t_b = time_launches(lambda: tpo._edge_bwd_raw(spec, xb, shb, gbt, gob, (True, True, True)), 20, stream)
+    per_edge_f = (x.shape[1] + 9 + op.gate_width + op.output_width) * 4
+    per_edge_b = (x.shape[1] + 9 + op.gate_width + op.output_width) * 4 + (x.shape[1] + 9 + op.gate_width) * 4
+    ach_f, ach_b = Eb * per_edge_f / t_f / 1e9, Eb * per_edge_b / t_b / 1e9
+    log(f"  E=2^20 tp_fwd {t_f * 1e6:.1f} us {ach_f:.0f} GB/s; tp_bwd {t_b * 1e6:.1f} us {ach_b:.0f} GB/s")
+    result = {
+        "metric": METRIC, "value": E / dt, "unit": "edges/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(args.warmup, 3), "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic (seeded N(0,1) blocks, directions, gates)",
+        "config": {"workload": "cfg1: EdgeTensorProduct fwd+bwd (loss mean(out^2)), C32 lmax2 ir_mul, E=257; "
+                               "kernel roofline at the same shapes with E=2^20",
+                   "edges": E, "channels": C, "lmax": 2, "us_per_step": dt * 1e6,
+                   "kernel_us_E2^20": {"tp_fwd": round(t_f * 1e6, 2), "tp_bwd": round(t_b * 1e6, 2)},
+                   "algorithmic_bytes_per_edge": {"tp_fwd": per_edge_f, "tp_bwd": per_edge_b},
+                   "tp_bwd_frac": ach_b / HBM_PEAK_GBS},
+        "roofline": {"bound": "hbm", "kernel": "tp_fwd (E=2^20, C32, P11)", "achieved": ach_f,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach_f / HBM_PEAK_GBS, "traffic": None},
+    }
+    return result, (blocks, v, gates, C)
+
+
+def cpu_baseline_tp(data, budget_s=15.0):
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import ictc_oracle as orc
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    blocks, v, gates, C = data
+    E = v.shape[0]
+    feats = torch.cat([blocks[l].transpose(1, 2).reshape(E, -1) for l in range(3)], -1)
+    sh = torch.cat(orc.direction_harmonics((v / v.norm(dim=1, keepdim=True)).double(), 2), -1).float()
+
+    def step():
+        a = feats.clone().requires_grad_(True)
+        b = sh.clone().requires_grad_(True)
+        c = gates.clone().requires_grad_(True)
+        out = orc.edge_tp_packed(a, b, c, 2, 2, 2, C)
+        (out * out).mean().backward()
+    step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 50 and time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": E / med, "unit": "edges/s", "cores": threads, "kind": "port",
+            "sample": f"cfg1 in full (E=257, C32), oracle FP32 torch eager fwd+bwd, median of {len(times)} runs, "
+                      f"{torch.get_num_threads()} threads"}
+
+
+def run_cfg3(args):
+    """Symmetric contraction corr 3, fwd + dx: 32,768 nodes, C64, lmax 2 -> L<=1, 4 species."""
+    import torch
+    from ictc_o3 import create_symmetric_contraction
+    from ictc_o3.ops import symmetric_contraction as sco
+    dev = torch.device("cuda:0")
+    N, C, S = 32768, 64, 4
+    torch.manual_seed(11)
+    mod = create_symmetric_contraction(num_elements=S, lmax=2, target_lmax=1, channels=C, correlation=3,
+                                       device=dev)
+    for p in mod.parameters():
+        p.requires_grad_(False)
+    g = torch.Generator(device=dev).manual_seed(12)
+    x = torch.randn(N, 9 * C, device=dev, generator=g).requires_grad_(True)
+    species = torch.randint(0, S, (N,), device=dev, generator=g)
+    go = torch.randn(N, 4 * C, device=dev, generator=g)
+
+    def step():
+        out = mod.contract(x, species)
+        torch.autograd.backward(out, go)
+
+    for _ in range(max(args.warmup, 3)):
+        step()
+    torch.cuda.synchronize()
+    steps = max(args.steps, 50)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    spec = mod.spec()
+    ws = mod.slot_weights()
+    stream = torch.cuda.current_stream(dev)
+    xd = x.detach()
+    t_f = time_launches(lambda: sco._fwd_raw(spec, xd, species, ws), 50, stream)
+    t_x = time_launches(lambda: sco._dx_raw(spec, xd, species, ws, go), 50, stream)
+    fwd_bytes = N * 9 * C * 4 + N * 8 + N * 4 * C * 4
+    dx_bytes = N * 9 * C * 4 + N * 4 * C * 4 + N * 8 + N * 9 * C * 4
+    terms = sco.term_count(spec)
+    fwd_flops = 2.0 * terms * N * C
+    ach_f = fwd_bytes / t_f / 1e9
+    log(f"cfg3: step {dt * 1e6:.1f} us; sc_fwd {t_f * 1e6:.1f} us {ach_f:.0f} GB/s "
+        f"{fwd_flops / t_f / 1e12:.1f} TFLOP/s; sc_dx {t_x * 1e6:.1f} us {dx_bytes / t_x / 1e9:.0f} GB/s")
+    result = {
+        "metric": METRIC, "value": N / dt, "unit": "node-steps/s", "n_gpus": 1, "steps": steps,
+        "warmup": max(args.warmup, 3), "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32", "data": "synthetic (seeded N(0,1) features, uniform species)",
+        "config": {"workload": "cfg3: symmetric contraction corr 3 fwd + dx, 32768 nodes, C64, lmax2 -> L<=1, "
+                               "4 species", "nodes": N, "channels": C,
+                   "kernel_us": {"sc_fwd": round(t_f * 1e6, 2), "sc_dx": round(t_x * 1e6, 2)},
+                   "algorithmic_bytes": {"sc_fwd": fwd_bytes, "sc_dx": dx_bytes},
+                   "fwd_flops": fwd_flops, "fwd_flops_per_byte": fwd_flops / fwd_bytes,
+                   "fwd_fp32_frac": fwd_flops / t_f / 1e12 / FP32_PEAK_TFLOPS,
+                   "dx_hbm_frac": dx_bytes / t_x / 1e9 / HBM_PEAK_GBS},
+        "roofline": {"bound": "hbm", "kernel": "sc_fwd (corr 3, C64, L2 -> L<=1)", "achieved": ach_f,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach_f / HBM_PEAK_GBS, "traffic": None},
+    }
+    return result, (mod, x.detach().cpu(), species.cpu(), go.cpu())
+
+
+def cpu_baseline_sc(data, budget_s=15.0):
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import sc_oracle as so
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    mod, x, species, go = data
+    take = 2048
+    W = {L: {nu: c.weight_for(nu).detach().float().cpu() for nu in range(1, c.correlation + 1)}
+         for L, c in enumerate(mod.symmetric_contractions.contractions)}
+    C = mod.channels
+    xs = x[:take].reshape(take, 9, C).transpose(1, 2).contiguous()
+    sp = species[:take]
+    gos = go[:take]
+
+    def step():
+        a = xs.clone().requires_grad_(True)
+        out = so.symmetric_contraction(a, sp, W, 2, 1, 3)
+        out.backward(gos[:, :out.shape[1]])
+    step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and (time.perf_counter() < t_end or not times):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": take / med, "unit": "node-steps/s", "cores": threads, "kind": "port",
+            "sample": f"first {take} nodes of cfg3, oracle FP32 torch eager SC fwd + dx, median of {len(times)} "
+                      f"runs, {torch.get_num_threads()} threads"}
+
+
+def batched_cells(cells, n, density, jitter, seed, species, cutoff, device):
+    """`cells` independent periodic FCC n^3 cells as one batch with per-cell neighbour lists (a data set)."""
+    import torch
+    from mace_ictc.hp import radius_graph_pbc
+    P, Zs, B, S, D, SH, cellv = [], [], [], [], [], [], []
+    off = 0
+    for b in range(cells):
+        pos, _, cell, _ = fcc_system(n, density, jitter, seed + b, 3, device)
+        g = torch.Generator().manual_seed(seed + 1000 + b)
+        Z = torch.tensor(species)[torch.randint(0, len(species), (pos.shape[0],), generator=g)].to(device)
+        src, dst, sh = radius_graph_pbc(pos, cell[0], cutoff)
+        P.append(pos), Zs.append(Z), B.append(torch.full((pos.shape[0],), b, dtype=torch.long, device=device))
+        S.append(src + off), D.append(dst + off), SH.append(sh), cellv.append(cell)
+        off += pos.shape[0]
+    cat = torch.cat
+    return cat(P), cat(Zs), cat(B), cat(S), cat(D), cat(SH), cat(cellv)
+
+
+def run_cfg5(args):
+    """Force-loss training step: C128, edge L3, hidden L2, 10 species, 32 cells x 256 atoms, cutoff 5 A."""
+    import torch
+    from mace_ictc.hp import create_model, energy_and_forces
+    from ictc_o3.ops import tensor_product as tpo
+    dev = torch.device("cuda:0")
+    torch.manual_seed(55)
+    species = tuple(range(1, 11))
+    model = create_model(channels=128, lmax=2, edge_lmax=3, num_interactions=2, correlation=3,
+                         atomic_numbers=species, cutoff=5.0, device=dev)
+    pos, Z, batch, src, dst, sh, cell = batched_cells(32, 4, 0.1, 0.3, 500, species, 5.0, dev)
+    N, E, B = pos.shape[0], src.numel(), cell.shape[0]
+    g = torch.Generator(device=dev).manual_seed(56)
+    E_t = torch.randn(B, device=dev, generator=g) * math.sqrt(256)
+    F_t = torch.randn(N, 3, device=dev, generator=g) * 0.5
+    topo = tpo.Topology(src, dst, N)
+    opt = torch.optim.Adam(model.parameters(), lr=1e-4)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        out = energy_and_forces(model, pos, Z, batch, src, dst, sh, cell, training=True, topology=topo)
+        loss = ((out["energy"] - E_t) ** 2).mean() + ((out["forces"] - F_t) ** 2).mean()
+        loss.backward()
+        opt.step()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    log(f"cfg5: N={N} E={E} step={dt * 1e3:.2f} ms loss={float(loss):.4f}")
+    kern, nbytes = layer_message_kernels(model, src, dst, N, reps=10)
+    achieved = nbytes["msg_fwd"] / kern["msg_fwd"] / 1e9
+    result = {
+        "metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic (32 seeded jittered FCC 4^3 cells, uniform species 1..10, N(0,1) per-atom energy and "
+                "N(0,0.5) force targets, random-init weights; neighbour lists built once like a data set)",
+        "config": {"workload": "cfg5: force-loss training step (E+F MSE backward through mixed second "
+                               "derivatives + Adam), C128, edge L3, hidden L2, 2 interactions, corr 3, rc 5 A, "
+                               "10 species, 32 cells x 256 atoms",
+                   "atoms": N, "edges": E, "channels": 128,
+                   "kernel_us_layer1": {k: round(t * 1e6, 2) for k, t in kern.items()},
+                   "kernel_algorithmic_MB_layer1": {k: round(v / 1e6, 2) for k, v in nbytes.items()}},
+        "roofline": {"bound": "hbm", "kernel": "msg_fwd (layer 1, P17 C128)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None},
+    }
+    return result, model
+
+
+def cpu_baseline_train(model, budget_s=25.0):
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import model_oracle as mo
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    species = tuple(range(1, 11))
+    pos, Z, batch, src, dst, sh, cell = batched_cells(1, 4, 0.1, 0.3, 500, species, 5.0, "cpu")
+    sd = {k: v.detach().float().cpu().clone() for k, v in model.state_dict().items()}
+    names = [k for k, p in model.named_parameters() if p.requires_grad]
+    cfg = mo.config_of(model)
+    E_t = torch.zeros(1)
+    F_t = torch.zeros_like(pos)
+
+    def step():
+        for k in names:
+            sd[k] = sd[k].detach().requires_grad_(True)
+        p = pos.clone().requires_grad_(True)
+        atomic = mo.forward(sd, cfg, p, Z, batch, src, dst, sh, cell, dtype=torch.float32)
+        En = atomic.sum().reshape(1)
+        (gp,) = torch.autograd.grad(En.sum(), p, create_graph=True)
+        loss = ((En - E_t) ** 2).mean() + ((-gp - F_t) ** 2).mean()
+        torch.autograd.grad(loss, [sd[k] for k in names], allow_unused=True)
+    step()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 and (time.perf_counter() < t_end or not times):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    return {"value": pos.shape[0] / med, "unit": "atom-steps/s", "cores": threads, "kind": "port",
+            "sample": f"one 256-atom cell of cfg5 (E={src.numel()}), oracle FP32 torch eager E+F+force-loss "
+                      f"parameter gradients, median of {len(times)} steps, {torch.get_num_threads()} threads"}
+
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="cfg4", choices=["cfg4", "cfg2"])
+    ap.add_argument("--workload", default="cfg4", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one-GPU hot path by design); "
               "run with --gpus 1", file=sys.stderr)
         sys.exit(2)
-    if args.workload == "cfg4":
-        result, model = run_cfg4(args)
-        if not args.no_cpu_baseline:
-            result["cpu_baseline"] = cpu_baseline_model(model)
-    else:
-        result, data = run_cfg2(args)
-        if not args.no_cpu_baseline:
-            result["cpu_baseline"] = cpu_baseline(data)
+    runners = {"cfg1": (run_cfg1, cpu_baseline_tp), "cfg2": (run_cfg2, cpu_baseline),
+               "cfg3": (run_cfg3, cpu_baseline_sc), "cfg4": (run_cfg4, cpu_baseline_model),
+               "cfg5": (run_cfg5, cpu_baseline_train)}
+    run, cpu = runners[args.workload]
+    result, data = run(args)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu(data)
     print(json.dumps(result), flush=True)
 
 

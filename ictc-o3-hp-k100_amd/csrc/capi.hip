@@ -50,7 +50,7 @@ int check_shape(int li, int le, int lo, int C) {
   if (!tp_counts(li, le, lo, &P, nullptr))
     return fail(ICTC_ERR_UNSUPPORTED, "degrees (%d, %d, %d) are outside the compiled coverage (0..3, nonempty paths)",
                 li, le, lo);
-  if (C < 1 || ictc::channels_per_lane(C) == 0)
+  if (ictc::channel_groups(C) == 0)
     return fail(ICTC_ERR_UNSUPPORTED, "channels=%d outside the supported range 1..256", C);
   return ICTC_OK;
 }
@@ -123,29 +123,21 @@ __global__ void fill_zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
-// Channels-per-lane routing onto the per-CPL launchers.
-#define ICTC_ROUTE(CALL, ...)                                                 \
-  switch (ictc::channels_per_lane(s.channels)) {                             \
-    case 1: return ictc::CALL##_c1(__VA_ARGS__);                             \
-    case 2: return ictc::CALL##_c2(__VA_ARGS__);                             \
-    default: return ictc::CALL##_c4(__VA_ARGS__);                            \
-  }
-
 hipError_t route_edge_fwd(const ictc::TpShape& s, const ictc::Operands& a, float* out, hipStream_t st) {
-  ICTC_ROUTE(launch_edge_fwd, s, a, out, st)
+  return ictc::launch_edge_fwd(s, a, out, st);
 }
 hipError_t route_edge_bwd(const ictc::TpShape& s, const ictc::Operands& a, const float* grad, float* dx, float* dsh,
                           float* dg, hipStream_t st) {
-  ICTC_ROUTE(launch_edge_bwd, s, a, grad, dx, dsh, dg, st)
+  return ictc::launch_edge_bwd(s, a, grad, dx, dsh, dg, st);
 }
 hipError_t route_msg_fwd(const ictc::TpShape& s, const ictc::Operands& a, const int64_t* src, ictc::Csr c,
                          float* out, hipStream_t st) {
-  ICTC_ROUTE(launch_msg_fwd, s, a, src, c, out, st)
+  return ictc::launch_msg_fwd(s, a, src, c, out, st);
 }
 hipError_t route_msg_bwd(const ictc::TpShape& s, const ictc::Operands& a, const int64_t* src, const int64_t* dst,
                          ictc::Csr dc, ictc::Csr sc, const float* grad, float* dx, float* dsh, float* dg,
                          hipStream_t st) {
-  ICTC_ROUTE(launch_msg_bwd, s, a, src, dst, dc, sc, grad, dx, dsh, dg, st)
+  return ictc::launch_msg_bwd(s, a, src, dst, dc, sc, grad, dx, dsh, dg, st);
 }
 
 }  // namespace

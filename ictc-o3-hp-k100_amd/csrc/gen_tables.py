@@ -44,6 +44,7 @@ def tp_struct(li, le, lo):
     T = tables.PathTable(paths, lmax_out=lo)
     NX, NY, P, NO = (li + 1) ** 2, (le + 1) ** 2, len(paths), T.out_components
     lines = [f"template <> struct Tp<{li}, {le}, {lo}> {{",
+             f"  static constexpr int LI = {li}, LE = {le}, LO = {lo};",
              f"  static constexpr int NX = {NX}, NY = {NY}, P = {P}, NO = {NO};"]
     # entries: (p, xi, yj, ok, coef)
     ent = []

@@ -7,7 +7,7 @@
 //   gates                 [E, P*C]       path p at p*C + c
 //   TP output             [rows, NO*C]   output slot k at k*C + c
 // One wave owns one row (an edge for the edge TP, a node for the CSR message)
-// and one lane owns channel c = lane + 64*j (j < CPL), so every feature,
+// and one group of 64 channels, lane l owning channel c = 64*group + l, so every feature,
 // gate and output access is a fully coalesced 256-byte wave transaction and
 // every per-edge scalar (indices, harmonics, mask) is wave-uniform.
 //
@@ -99,78 +99,127 @@ __device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c
 }
 
 // ---------------------------------------------------------------------------
-// Edge TP: one wave per edge.
+// Launch geometry.  A channel group is 64 consecutive channels, one per lane
+// (c = 64 * group + lane); G = ceil(C / 64) groups, C <= 256.
+//   * Kernels without a cross-channel reduction run 4 rows per 256-thread
+//     block and take the group from blockIdx.y.
+//   * Kernels that reduce over channels (the harmonic gradient) run, for
+//     G == 1, 4 rows per block as above; for G > 1 one row per block of G
+//     waves (wave = group), combining the groups' partial sums through LDS
+//     in group order.  Every wave of such a block walks the same row, so the
+//     block barriers are uniform.
+// Register budgets: the minimum waves per SIMD requested from the compiler
+// drop for the wide degree triples so that their accumulators stay in VGPRs.
 // ---------------------------------------------------------------------------
-template <class T, int CPL>
-__global__ __launch_bounds__(kBlock) void edge_fwd_kernel(Operands a, float* __restrict__ out) {
-  const int64_t e = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
-  if (e >= a.rows) return;
-  const int C = a.channels;
-  float y[T::NY];
-  load_harmonics<T>(a.sh, e, y);
-  const float* xr = a.x + e * (int64_t)(T::NX * C);
-  float* orow = out + e * (int64_t)(T::NO * C);
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane_id() + kWave * j;
-    if (c < C) {
-      float xv[T::NX], gw[T::P], o[T::NO];
-      load_row<T::NX>(xr, C, c, xv);
-      load_gw<T>(a, e, c, 1.f, gw);
-#pragma unroll
-      for (int k = 0; k < T::NO; ++k) o[k] = 0.f;
-      T::fwd(xv, y, gw, o);
-      store_row<T::NO>(orow, C, c, o);
-    }
-  }
+constexpr int kMaxGroups = 4;
+
+// Minimum waves per SIMD requested for each (kernel, degree triple): the
+// highest of 4, 3, 2, 1 at which the kernel compiles without register spills,
+// found by tune_occupancy.py and recorded in generated/ictc_occupancy.h.
+enum KernelKind { kEdgeFwd, kEdgeBwd, kMsgFwd, kMsgBwdEdge, kMsgBwdX };
+template <int K, int LI, int LE, int LO>
+struct Occupancy {
+#ifdef ICTC_OCCUPANCY_PROBE
+  static constexpr int value = ICTC_OCCUPANCY_PROBE;
+#else
+  static constexpr int value = 4;
+#endif
+};
+
+#ifndef ICTC_OCCUPANCY_PROBE
+#include "generated/ictc_occupancy.h"
+#endif
+
+struct RowGroup {
+  int64_t row;
+  int group;
+};
+
+__device__ __forceinline__ RowGroup row_group_y() {
+  return {(int64_t)blockIdx.x * kWavesPerBlock + wave_id(), (int)blockIdx.y};
 }
 
-template <class T, int CPL>
-__global__ __launch_bounds__(kBlock) void edge_bwd_kernel(Operands a, const float* __restrict__ grad,
-                                                          float* __restrict__ dx, float* __restrict__ dsh,
-                                                          float* __restrict__ dgates) {
-  const int64_t e = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
+__device__ __forceinline__ RowGroup row_group_reduce(int G) {
+  if (G == 1) return {(int64_t)blockIdx.x * kWavesPerBlock + wave_id(), 0};
+  return {(int64_t)blockIdx.x, wave_id()};
+}
+
+// ---------------------------------------------------------------------------
+// Edge TP: one wave per (edge, channel group).
+// ---------------------------------------------------------------------------
+template <class T>
+__global__ __launch_bounds__(kBlock, (Occupancy<kEdgeFwd, T::LI, T::LE, T::LO>::value)) void edge_fwd_kernel(
+    Operands a, float* __restrict__ out) {
+  const RowGroup rg = row_group_y();
+  const int64_t e = rg.row;
   if (e >= a.rows) return;
-  const int C = a.channels;
+  const int C = a.channels, c = 64 * rg.group + lane_id();
+  if (c >= C) return;
+  float y[T::NY], xv[T::NX], gw[T::P], o[T::NO];
+  load_harmonics<T>(a.sh, e, y);
+  load_row<T::NX>(a.x + e * (int64_t)(T::NX * C), C, c, xv);
+  load_gw<T>(a, e, c, 1.f, gw);
+#pragma unroll
+  for (int k = 0; k < T::NO; ++k) o[k] = 0.f;
+  T::fwd(xv, y, gw, o);
+  store_row<T::NO>(out + e * (int64_t)(T::NO * C), C, c, o);
+}
+
+template <class T>
+__global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::value)) void edge_bwd_kernel(
+    Operands a, const float* __restrict__ grad, float* __restrict__ dx, float* __restrict__ dsh,
+    float* __restrict__ dgates, int G) {
+  extern __shared__ float red[];  // [G][NY] when G > 1
+  const RowGroup rg = row_group_reduce(G);
+  const int64_t e = rg.row;
+  if (e >= a.rows) return;
+  const int C = a.channels, c = 64 * rg.group + lane_id();
+  const bool active = c < C;
   float y[T::NY], dyv[T::NY];
   load_harmonics<T>(a.sh, e, y);
 #pragma unroll
   for (int j = 0; j < T::NY; ++j) dyv[j] = 0.f;
-  const float* xr = a.x + e * (int64_t)(T::NX * C);
-  const float* gr = grad + e * (int64_t)(T::NO * C);
+  if (active) {
+    float xv[T::NX], gw[T::P], go[T::NO];
+    load_row<T::NX>(a.x + e * (int64_t)(T::NX * C), C, c, xv);
+    load_row<T::NO>(grad + e * (int64_t)(T::NO * C), C, c, go);
+    load_gw<T>(a, e, c, 1.f, gw);
+    if (dx) {
+      float d[T::NX];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane_id() + kWave * j;
-    if (c < C) {
-      float xv[T::NX], gw[T::P], go[T::NO];
-      load_row<T::NX>(xr, C, c, xv);
-      load_row<T::NO>(gr, C, c, go);
-      load_gw<T>(a, e, c, 1.f, gw);
-      if (dx) {
-        float d[T::NX];
+      for (int i = 0; i < T::NX; ++i) d[i] = 0.f;
+      T::dx(y, gw, go, d);
+      store_row<T::NX>(dx + e * (int64_t)(T::NX * C), C, c, d);
+    }
+    if (dsh) T::dy(xv, gw, go, dyv);
+    if (dgates) {
+      float d[T::P];
+      T::dg(xv, y, go, d);
+      if (a.weight) {
 #pragma unroll
-        for (int i = 0; i < T::NX; ++i) d[i] = 0.f;
-        T::dx(y, gw, go, d);
-        store_row<T::NX>(dx + e * (int64_t)(T::NX * C), C, c, d);
+        for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
       }
-      if (dsh) T::dy(xv, gw, go, dyv);
-      if (dgates) {
-        float d[T::P];
-        T::dg(xv, y, go, d);
-        if (a.weight) {
-#pragma unroll
-          for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
-        }
-        store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
-      }
+      store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
     }
   }
-  if (dsh) {
+  if (!dsh) return;
+  // lane j (< NY) ends up holding this group's sum of component j
+  float mine = 0.f;
 #pragma unroll
-    for (int j = 0; j < T::NY; ++j) {
-      const float s = wave_sum(dyv[j]);
-      if (lane_id() == 0) dsh[e * T::NY + j] = s;
-    }
+  for (int j = 0; j < T::NY; ++j) {
+    const float s = wave_sum(dyv[j]);
+    mine = lane_id() == j ? s : mine;
+  }
+  if (G == 1) {
+    if (lane_id() < T::NY) dsh[e * T::NY + lane_id()] = mine;
+    return;
+  }
+  if (lane_id() < T::NY) red[rg.group * T::NY + lane_id()] = mine;
+  __syncthreads();
+  if (rg.group == 0 && lane_id() < T::NY) {
+    float s = red[lane_id()];
+    for (int g = 1; g < G; ++g) s += red[g * T::NY + lane_id()];
+    dsh[e * T::NY + lane_id()] = s;
   }
 }
 
@@ -222,27 +271,17 @@ __device__ __forceinline__ float lane_f(float v, int i) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
 
-// Per-edge operands of one wave: harmonics (wave-uniform), gathered source row
-// and mask-scaled gates for each of the lane's CPL channels.
-template <class T, int CPL>
-struct EdgeIn {
-  float y[T::NY];
-  float x[CPL][T::NX];
-  float gw[CPL][T::P];
-  float m;  // mask (0 for an out-of-range source)
-};
-
-template <class T, int CPL>
-__global__ __launch_bounds__(kBlock, 4) void msg_fwd_kernel(Operands a, const int64_t* __restrict__ src, Csr csr,
-                                                         float* __restrict__ out) {
-  const int64_t n = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
+template <class T>
+__global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::value)) void msg_fwd_kernel(
+    Operands a, const int64_t* __restrict__ src, Csr csr, float* __restrict__ out) {
+  const RowGroup rg = row_group_y();
+  const int64_t n = rg.row;
   if (n >= a.rows) return;
-  const int C = a.channels;
-  float o[CPL][T::NO];
+  const int C = a.channels, c = 64 * rg.group + lane_id();
+  const bool active = c < C;
+  float o[T::NO];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j)
-#pragma unroll
-    for (int k = 0; k < T::NO; ++k) o[j][k] = 0.f;
+  for (int k = 0; k < T::NO; ++k) o[k] = 0.f;
   const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
   for (int32_t pos = beg; pos < end; pos += kWave) {
     const int32_t count = min(end - pos, kWave);
@@ -255,123 +294,118 @@ __global__ __launch_bounds__(kBlock, 4) void msg_fwd_kernel(Operands a, const in
       float y[T::NY];
 #pragma unroll
       for (int j = 0; j < T::NY; ++j) y[j] = lane_f(ch.y[j], i);
-      const float* xr = a.x + s * (int64_t)(T::NX * C);
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane_id() + kWave * j;
-        if (c < C) {
-          float xv[T::NX], gw[T::P];
-          load_row<T::NX>(xr, C, c, xv);
-          load_gw<T>(a, e, c, m, gw);
-          T::fwd(xv, y, gw, o[j]);
-        }
+      if (active) {
+        float xv[T::NX], gw[T::P];
+        load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
+        load_gw<T>(a, e, c, m, gw);
+        T::fwd(xv, y, gw, o);
       }
     }
   }
-  float* orow = out + n * (int64_t)(T::NO * C);
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane_id() + kWave * j;
-    if (c < C) store_row<T::NO>(orow, C, c, o[j]);
-  }
+  if (active) store_row<T::NO>(out + n * (int64_t)(T::NO * C), C, c, o);
 }
 
-// Gate and harmonic gradients of one edge given the receiver's cotangent rows.
-template <class T, int CPL>
-__device__ __forceinline__ void edge_adjoint(const Operands& a, const float (&go)[CPL][T::NO], int64_t e,
-                                             const EdgeIn<T, CPL>& in, float* __restrict__ dsh,
-                                             float* __restrict__ dgates) {
-  const int C = a.channels;
-  float dyv[T::NY];
-#pragma unroll
-  for (int j = 0; j < T::NY; ++j) dyv[j] = 0.f;
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane_id() + kWave * j;
-    if (c < C) {
-      if (dsh) T::dy(in.x[j], in.gw[j], go[j], dyv);
-      if (dgates) {
-        float d[T::P];
-        T::dg(in.x[j], in.y, go[j], d);
-#pragma unroll
-        for (int p = 0; p < T::P; ++p) d[p] *= in.m;
-        if (a.weight) {
-#pragma unroll
-          for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
-        }
-        store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
-      }
-    }
-  }
-  if (dsh) {
-#pragma unroll
-    for (int j = 0; j < T::NY; ++j) {
-      const float s = wave_sum(dyv[j]);
-      if (lane_id() == 0) dsh[e * T::NY + j] = s;
-    }
-  }
-}
-
-// Receiver-owned adjoint: per-edge gate and harmonic gradients.
-template <class T, int CPL>
-__global__ __launch_bounds__(kBlock, 3) void msg_bwd_edge_kernel(Operands a, const int64_t* __restrict__ src, Csr csr,
-                                                              const float* __restrict__ grad,
-                                                              float* __restrict__ dsh, float* __restrict__ dgates) {
-  // Waves 0..rows-1 own receivers; wave `rows` owns the out-of-range tail
-  // segment ptr[rows]..ptr[rows+1] and writes zero gradients for it.
-  const int64_t n = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
+// Receiver-owned adjoint: per-edge gate and harmonic gradients.  Waves of
+// row `rows` own the out-of-range tail segment ptr[rows]..ptr[rows+1] and
+// write zero gradients for it (mask 0, zero cotangent).
+template <class T>
+__global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO>::value)) void msg_bwd_edge_kernel(
+    Operands a, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad, float* __restrict__ dsh,
+    float* __restrict__ dgates, int G) {
+  extern __shared__ float red[];  // [G][64][NY] when G > 1 and dsh
+  const RowGroup rg = row_group_reduce(G);
+  const int64_t n = rg.row;
   if (n > a.rows) return;
   const bool tail = n == a.rows;
-  const int C = a.channels;
-  float go[CPL][T::NO];
-  const float* gr = grad + (tail ? 0 : n) * (int64_t)(T::NO * C);
+  const int C = a.channels, c = 64 * rg.group + lane_id();
+  const bool active = c < C;
+  float go[T::NO];
+  if (active && !tail) load_row<T::NO>(grad + n * (int64_t)(T::NO * C), C, c, go);
+  else {
 #pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane_id() + kWave * j;
-    if (c < C && !tail) load_row<T::NO>(gr, C, c, go[j]);
-    else {
-#pragma unroll
-      for (int k = 0; k < T::NO; ++k) go[j][k] = 0.f;
-    }
+    for (int k = 0; k < T::NO; ++k) go[k] = 0.f;
   }
   const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
   for (int32_t pos = beg; pos < end; pos += kWave) {
     const int32_t count = min(end - pos, kWave);
     Chunk<T> ch;
     stage_chunk<T>(a, src, csr.order, pos, count, ch);
+    float acc[T::NY];  // lane i: this group's harmonic gradient of the chunk's edge i
+#pragma unroll
+    for (int j = 0; j < T::NY; ++j) acc[j] = 0.f;
     for (int i = 0; i < count; ++i) {
-      EdgeIn<T, CPL> in;
       const int64_t e = lane_i(ch.e, i);
       const int64_t s = lane_i(ch.peer, i);
-      in.m = lane_f(ch.m, i);
+      const float m = lane_f(ch.m, i);
+      float y[T::NY], dyv[T::NY];
 #pragma unroll
-      for (int j = 0; j < T::NY; ++j) in.y[j] = lane_f(ch.y[j], i);
-      const float* xr = a.x + s * (int64_t)(T::NX * C);
+      for (int j = 0; j < T::NY; ++j) {
+        y[j] = lane_f(ch.y[j], i);
+        dyv[j] = 0.f;
+      }
+      if (active) {
+        float xv[T::NX], gw[T::P];
+        load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
+        load_gw<T>(a, e, c, m, gw);
+        if (dsh) T::dy(xv, gw, go, dyv);
+        if (dgates) {
+          float d[T::P];
+          T::dg(xv, y, go, d);
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane_id() + kWave * j;
-        if (c < C) {
-          load_row<T::NX>(xr, C, c, in.x[j]);
-          load_gw<T>(a, e, c, in.m, in.gw[j]);
+          for (int p = 0; p < T::P; ++p) d[p] *= m;
+          if (a.weight) {
+#pragma unroll
+            for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
+          }
+          store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
         }
       }
-      edge_adjoint<T, CPL>(a, go, e, in, dsh, dgates);
+      if (dsh) {
+#pragma unroll
+        for (int j = 0; j < T::NY; ++j) {
+          const float v = wave_sum(dyv[j]);
+          acc[j] = lane_id() == i ? v : acc[j];
+        }
+      }
     }
+    if (!dsh) continue;
+    const bool mine = lane_id() < count;
+    if (G == 1) {
+      if (mine) {
+#pragma unroll
+        for (int j = 0; j < T::NY; ++j) dsh[(int64_t)ch.e * T::NY + j] = acc[j];
+      }
+      continue;
+    }
+    float* r = red + (rg.group * kWave + lane_id()) * T::NY;
+#pragma unroll
+    for (int j = 0; j < T::NY; ++j) r[j] = acc[j];
+    __syncthreads();
+    if (rg.group == 0 && mine) {
+      for (int g = 1; g < G; ++g) {
+        const float* q = red + (g * kWave + lane_id()) * T::NY;
+#pragma unroll
+        for (int j = 0; j < T::NY; ++j) acc[j] += q[j];
+      }
+#pragma unroll
+      for (int j = 0; j < T::NY; ++j) dsh[(int64_t)ch.e * T::NY + j] = acc[j];
+    }
+    __syncthreads();
   }
 }
 
 // Source-owned adjoint: node feature gradient over the source-sorted CSR.
-template <class T, int CPL>
-__global__ __launch_bounds__(kBlock, 3) void msg_bwd_x_kernel(Operands a, const int64_t* __restrict__ dst, Csr scsr,
-                                                           const float* __restrict__ grad, float* __restrict__ dx) {
-  const int64_t n = (int64_t)blockIdx.x * kWavesPerBlock + wave_id();
+template <class T>
+__global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::value)) void msg_bwd_x_kernel(
+    Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx) {
+  const RowGroup rg = row_group_y();
+  const int64_t n = rg.row;
   if (n >= a.rows) return;
-  const int C = a.channels;
-  float d[CPL][T::NX];
+  const int C = a.channels, c = 64 * rg.group + lane_id();
+  const bool active = c < C;
+  float d[T::NX];
 #pragma unroll
-  for (int j = 0; j < CPL; ++j)
-#pragma unroll
-    for (int i = 0; i < T::NX; ++i) d[j][i] = 0.f;
+  for (int i = 0; i < T::NX; ++i) d[i] = 0.f;
   const int32_t beg = scsr.ptr[n], end = scsr.ptr[n + 1];
   // An out-of-range receiver contributes zero (mask 0, row 0 read).
   for (int32_t pos = beg; pos < end; pos += kWave) {
@@ -385,25 +419,15 @@ __global__ __launch_bounds__(kBlock, 3) void msg_bwd_x_kernel(Operands a, const 
       float y[T::NY];
 #pragma unroll
       for (int j = 0; j < T::NY; ++j) y[j] = lane_f(ch.y[j], i);
-      const float* gr = grad + r * (int64_t)(T::NO * C);
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        const int c = lane_id() + kWave * j;
-        if (c < C) {
-          float go[T::NO], gw[T::P];
-          load_row<T::NO>(gr, C, c, go);
-          load_gw<T>(a, e, c, m, gw);
-          T::dx(y, gw, go, d[j]);
-        }
+      if (active) {
+        float go[T::NO], gw[T::P];
+        load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
+        load_gw<T>(a, e, c, m, gw);
+        T::dx(y, gw, go, d);
       }
     }
   }
-  float* xr = dx + n * (int64_t)(T::NX * C);
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const int c = lane_id() + kWave * j;
-    if (c < C) store_row<T::NX>(xr, C, c, d[j]);
-  }
+  if (active) store_row<T::NX>(dx + n * (int64_t)(T::NX * C), C, c, d);
 }
 
 // ---------------------------------------------------------------------------

@@ -35,7 +35,7 @@ int chunks_for(int64_t nodes) { return ictc::sc::chunks_for(nodes); }
 // Host-side table of path counts and weight slots per configuration.
 struct Shape {
   int P[4][3];
-  int nw, nx, no;
+  int nw, nx, no, terms;
 };
 
 template <class T>
@@ -46,6 +46,7 @@ Shape shape_of() {
   s.nw = T::NW;
   s.nx = T::NX;
   s.no = T::NO;
+  s.terms = T::TERMS;
   return s;
 }
 
@@ -146,6 +147,12 @@ int ictc_sc_shape(int lmax, int target_lmax, int correlation, int* paths, int* n
       for (int n = 0; n < 3; ++n) paths[L * 3 + n] = sh.P[L][n];
   if (num_weights) *num_weights = sh.nw;
   return ICTC_OK;
+}
+
+int ictc_sc_terms(int lmax, int target_lmax, int correlation) {
+  Shape sh;
+  if (int rc = dispatch(lmax, target_lmax, correlation, GetShape{&sh})) return rc;
+  return sh.terms;
 }
 
 int64_t ictc_sc_workspace_bytes(int lmax, int target_lmax, int correlation, int channels, int64_t nodes,

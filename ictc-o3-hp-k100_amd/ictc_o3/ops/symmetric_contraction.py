@@ -64,6 +64,14 @@ def _c(t):
     return t if t.is_contiguous() else t.contiguous()
 
 
+def term_count(spec) -> int:
+    """Monomial x weight terms per (node, channel) of the generated forward (2 FLOPs each)."""
+    n = int(nat.lib().ictc_sc_terms(spec.lmax, spec.target_lmax, spec.corr))
+    if n < 0:
+        raise ValueError(nat.lib().ictc_last_error().decode(errors="replace"))
+    return n
+
+
 def _fwd_raw(spec, x, species, ws, tangent=None):
     out = x.new_empty(x.shape[0], spec.no * spec.channels)
     if tangent is None:

@@ -178,6 +178,11 @@ int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden
  * Compiled for (lmax, target_lmax) with lmax <= 2, target <= lmax, and
  * lmax 3 with target 0..2; channels 1..4096.                                  */
 int ictc_sc_shape(int lmax, int target_lmax, int correlation, int* paths /* [12] */, int* num_weights);
+/* Measurement helper with no reference counterpart: the number of (monomial x
+ * weight-combination) terms the forward evaluates per (node, channel), summed
+ * over output components; algorithmic forward FLOPs = 2 * terms * N * C.
+ * Returns the count (>= 0) or a negative error code.                          */
+int ictc_sc_terms(int lmax, int target_lmax, int correlation);
 int ictc_sc_fwd(int lmax, int target_lmax, int correlation, int channels, const float* x, const int64_t* species,
                 int num_species, const float* const* weights, int64_t nodes, float* out, void* stream);
 /* dx = d(grad . out)/dx (overwritten). */
