@@ -102,6 +102,9 @@ def _deriv(key):
     return out
 
 
+DW_BLOCK = 32   # weights per weight-gradient wave (kDwBlock in sc_kernels.h)
+
+
 def sc_struct(li, lt, corr):
     outs, terms, counts = polynomial(li, lt, corr)
     nx, no = (li + 1) ** 2, len(outs)
@@ -153,17 +156,39 @@ def sc_struct(li, lt, corr):
         L.append("    }")
     L.append(f"    for (int i = 0; i < {nx}; ++i) d[i] = a[i];")
     L.append("  }")
-    # dw: per weight q, sum_k go[k] * coef * mono
-    L.append("  __device__ __forceinline__ static void dw(const float* __restrict__ x, const float* __restrict__ go,"
-             " float* __restrict__ dwv) {")
+    # dw: per weight q, sum_k go[k] * coef * mono; emitted in blocks of DW_BLOCK weights
+    # (dwb<B> accumulates weights B*DW_BLOCK ...) so one wave holds one block's accumulators.
     per_q = {q: [] for q in range(nq)}
     for k in range(no):
         for key, e in terms[k].items():
             for (Lo, nu, p, v) in e:
                 per_q[qindex[(Lo, nu, p)]].append((k, key, v))
-    for q in range(nq):
-        expr = " + ".join(f"{f(v)} * (go[{k}] * ({_mono_expr(key)}))" for k, key, v in per_q[q]) or "0.f"
-        L.append(f"    dwv[{q}] = {expr};")
+    nb = max(1, (nq + DW_BLOCK - 1) // DW_BLOCK)
+
+    def by_monomial(b):
+        """{mono key: {local q: [(k, coef)]}} for the weights of block b, in first-use order."""
+        groups = {}
+        for q in range(b * DW_BLOCK, min(nq, (b + 1) * DW_BLOCK)):
+            for k, key, v in per_q[q]:
+                groups.setdefault(key, {}).setdefault(q - b * DW_BLOCK, []).append((k, v))
+        return groups
+
+    def go_combo(lst):
+        return " + ".join(f"{f(v)} * go[{k}]" for k, v in lst)
+
+    # Each monomial is formed once and consumed at once (short live ranges).
+    L.append(f"  static constexpr int NB = {nb};")
+    L.append("  template <int B>")
+    L.append("  __device__ __forceinline__ static void dwb(const float* __restrict__ x, const float* __restrict__ go,"
+             " float* __restrict__ acc) {")
+    for b in range(nb):
+        L.append(f"    {'if' if b == 0 else 'else if'} constexpr (B == {b}) {{")
+        for key, qs in by_monomial(b).items():
+            L.append(f"      {{ const float m = {_mono_expr(key)};")
+            for ql, lst in qs.items():
+                L.append(f"        acc[{ql}] = fmaf(m, {go_combo(lst)}, acc[{ql}]);")
+            L.append("      }")
+        L.append("    }")
     L.append("  }")
     # jvp: directional derivative of o along h
     L.append("  __device__ __forceinline__ static void jvp(const float* __restrict__ x, const ScWeights& t, int s,"
@@ -195,16 +220,21 @@ def sc_struct(li, lt, corr):
         L.append("    }")
     L.append(f"    for (int i = 0; i < {nx}; ++i) d[i] = a[i];")
     L.append("  }")
-    # dwjvp: dw[q] = sum_k go[k] coef * (d mono . h)
-    L.append("  __device__ __forceinline__ static void dwjvp(const float* __restrict__ x, const float* __restrict__ go,"
-             " const float* __restrict__ h, float* __restrict__ dwv) {")
-    for q in range(nq):
-        parts = []
-        for k, key, v in per_q[q]:
+    # dwjvp: dw[q] = sum_k go[k] coef * (d mono . h), in the same weight blocks as dwb
+    L.append("  template <int B>")
+    L.append("  __device__ __forceinline__ static void dwjvpb(const float* __restrict__ x, const float* __restrict__ go,"
+             " const float* __restrict__ h, float* __restrict__ acc) {")
+    for b in range(nb):
+        L.append(f"    {'if' if b == 0 else 'else if'} constexpr (B == {b}) {{")
+        for key, qs in by_monomial(b).items():
             dparts = [f"{float(mult)}f * ({_mono_expr(rest)}) * h[{i}]" for i, mult, rest in _deriv(key)]
-            if dparts:
-                parts.append(f"{f(v)} * (go[{k}] * ({' + '.join(dparts)}))")
-        L.append(f"    dwv[{q}] = {' + '.join(parts) or '0.f'};")
+            if not dparts:
+                continue
+            L.append(f"      {{ const float m = {' + '.join(dparts)};")
+            for ql, lst in qs.items():
+                L.append(f"        acc[{ql}] = fmaf(m, {go_combo(lst)}, acc[{ql}]);")
+            L.append("      }")
+        L.append("    }")
     L.append("  }")
     # weight slot table: q -> (L, nu-1, p)
     L.append(f"  static constexpr int WQ[{max(nq, 1)}][3] = {{"

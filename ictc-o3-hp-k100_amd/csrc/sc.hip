@@ -30,7 +30,9 @@ int hip_status(hipError_t e, const char* what) {
   return fail(ICTC_ERR_RUNTIME, "%s: %s", what, hipGetErrorString(e));
 }
 
-int chunks_for(int64_t nodes) { return ictc::sc::chunks_for(nodes); }
+int64_t partial_bytes(int64_t nodes, int species, int nw, int channels) {
+  return ictc::sc::partial_bytes(nodes, species, nw, channels);
+}
 
 // Host-side table of path counts and weight slots per configuration.
 struct Shape {
@@ -160,8 +162,7 @@ int64_t ictc_sc_workspace_bytes(int lmax, int target_lmax, int correlation, int 
   Shape sh;
   if (dispatch(lmax, target_lmax, correlation, GetShape{&sh})) return -1;
   if (nodes < 0 || num_species < 1 || channels < 1) return -1;
-  const int64_t chunks = chunks_for(nodes > 0 ? nodes : 1);
-  return (int64_t)num_species * chunks * sh.nw * channels * (int64_t)sizeof(float);
+  return partial_bytes(nodes, num_species, sh.nw, channels) + (int64_t)(num_species + 1) * (int64_t)sizeof(int32_t);
 }
 
 int ictc_sc_fwd(int li, int lt, int corr, int C, const float* x, const int64_t* species, int S,

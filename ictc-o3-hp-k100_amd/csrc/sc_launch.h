@@ -7,7 +7,12 @@
 namespace ictc {
 namespace sc {
 
-inline int chunks_for(int64_t nodes) { return (int)((nodes + kChunk - 1) / kChunk); }
+// Upper bound on the weight-gradient chunks of N nodes over S species.
+inline int64_t max_chunks(int64_t nodes, int species) { return (nodes + kChunk - 1) / kChunk + species; }
+// Partial buffer bytes (256-aligned); the chunk table [S+1] int32 follows it.
+inline int64_t partial_bytes(int64_t nodes, int species, int nw, int channels) {
+  return (max_chunks(nodes, species) * nw * channels * (int64_t)sizeof(float) + 255) / 256 * 256;
+}
 inline unsigned node_blocks(int64_t n) { return (unsigned)((n + kWaves - 1) / kWaves); }
 
 template <class T>
@@ -43,14 +48,16 @@ struct Launch {
                                      const int32_t* order, float* const* dwp, float* partial, int mode,              \
                                      hipStream_t st) {                                                               \
     using T = Sc<A, B, C>;                                                                                           \
-    const int chunks = chunks_for(a.nodes);                                                                          \
-    const int64_t waves = (int64_t)a.num_species * chunks;                                                           \
+    const int64_t chunks = max_chunks(a.nodes, a.num_species);                                                       \
+    int32_t* cbeg = (int32_t*)((char*)partial + partial_bytes(a.nodes, a.num_species, T::NW, a.channels));           \
+    hipLaunchKernelGGL(chunk_table_kernel<0>, dim3(1), dim3(64), 0, st, ptr, a.num_species, cbeg);                      \
+    const dim3 grid(node_blocks(chunks), (a.channels + 63) / 64, T::NB);                                             \
     if (mode == 0)                                                                                                   \
-      hipLaunchKernelGGL((dw_partial_kernel<T, 0>), dim3(node_blocks(waves)), dim3(256), 0, st, a, go, h, ptr,       \
-                         order, chunks, partial);                                                                    \
+      hipLaunchKernelGGL((dw_partial_kernel<T, 0>), grid, dim3(256), 0, st, a, go, h, ptr, order, cbeg, chunks,      \
+                         partial);                                                                                   \
     else                                                                                                             \
-      hipLaunchKernelGGL((dw_partial_kernel<T, 1>), dim3(node_blocks(waves)), dim3(256), 0, st, a, go, h, ptr,       \
-                         order, chunks, partial);                                                                    \
+      hipLaunchKernelGGL((dw_partial_kernel<T, 1>), grid, dim3(256), 0, st, a, go, h, ptr, order, cbeg, chunks,      \
+                         partial);                                                                                   \
     hipError_t e = hipGetLastError();                                                                                \
     if (e != hipSuccess) return e;                                                                                   \
     WeightGrads g;                                                                                                   \
@@ -58,7 +65,7 @@ struct Launch {
       for (int n = 0; n < 3; ++n) g.w[L][n] = T::P[L][n] > 0 ? dwp[L * 3 + n] : nullptr;                             \
     const int64_t total = (int64_t)a.num_species * T::NW * a.channels;                                               \
     hipLaunchKernelGGL((dw_reduce_kernel<T>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, partial,      \
-                       a.num_species, chunks, a.channels, g);                                                        \
+                       a.num_species, cbeg, a.channels, g);                                                          \
     return hipGetLastError();                                                                                        \
   }
 
