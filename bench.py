@@ -40,6 +40,10 @@ sys.path.insert(0, os.path.join(ROOT, "ictc-o3-hp-k100_amd"))
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
+# HBM bytes per launch of the cfg4 layer-1 msg_fwd (P11, C64, E=5,262,704), from rocprofv3
+# FETCH_SIZE + WRITE_SIZE runs of `bench.py --workload probe`, each scaled by the counter's reading
+# for a 1 GiB copy (FETCH x2.0, WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.
+MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 20.05e9}
 
 
 def log(*a):
@@ -297,7 +301,8 @@ def run_cfg4(args):
                    "kernel_us_layer1": {k: round(t * 1e6, 2) for k, t in kern.items()},
                    "kernel_algorithmic_MB_layer1": {k: round(v / 1e6, 2) for k, v in nbytes.items()}},
         "roofline": {"bound": "hbm", "kernel": "msg_fwd (layer 1, P11 C64)", "achieved": achieved,
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": MEASURED_TRAFFIC.get(("msg_fwd", N, E, 64))},
     }
     return result, model
 
@@ -628,12 +633,55 @@ def cpu_baseline_train(model, budget_s=25.0):
 
 
 
+def run_probe(args):
+    """Counter-collection workload: the cfg4 layer-1 message kernels, then a 1 GiB device copy.
+
+    Run under ``rocprofv3 --pmc FETCH_SIZE`` (and separately ``WRITE_SIZE``): the
+    copy (1 GiB read, 1 GiB written) calibrates the counters, the message
+    kernels give HBM bytes per dispatch.  Prints nothing but a short log.
+    """
+    import torch
+    from mace_ictc.hp import create_model, radius_graph_pbc
+    from ictc_o3.ops import tensor_product as tpo
+    dev = torch.device("cuda:0")
+    torch.manual_seed(2024)
+    model = create_model(channels=64, lmax=2, num_interactions=2, correlation=3, atomic_numbers=(1, 6, 8),
+                         cutoff=4.5, avg_num_neighbors=42.0, device=dev)
+    pos, Z, cell, a = fcc_system(32, 0.1, 0.3, 1234, 3, dev)
+    N = pos.shape[0]
+    src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
+    topo = tpo.Topology(src, dst, N)
+    inter = model.interactions[-1]
+    spec = inter.spec()
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(N, 9 * 64, device=dev, generator=g)
+    Y = torch.randn(src.numel(), 9, device=dev, generator=g)
+    with torch.no_grad():
+        r = torch.rand(src.numel(), device=dev, generator=g) * 3 + 1.5
+        gates = inter.fc(model.radial_embedding(r))
+    go = torch.randn(N, spec.out_components * 64, device=dev, generator=g)
+    topo.by_src
+    for _ in range(args.steps):
+        tpo._msg_fwd_raw(spec, topo, x, Y, gates, None)
+        tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True))
+        tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, False, False))
+    a = torch.empty(1 << 28, device=dev)
+    b = torch.randn(1 << 28, device=dev)
+    for _ in range(args.steps):
+        a.copy_(b)
+    torch.cuda.synchronize()
+    nbytes = message_bytes(N, src.numel(), 64, 9, 9, spec.num_paths, spec.out_components)
+    log(f"probe: N={N} E={src.numel()} algorithmic bytes {nbytes}; copy {4 << 28} bytes each way")
+    return None, None
+
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="cfg4", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"])
+    ap.add_argument("--workload", default="cfg4", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "probe"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -643,6 +691,9 @@ def main():
     runners = {"cfg1": (run_cfg1, cpu_baseline_tp), "cfg2": (run_cfg2, cpu_baseline),
                "cfg3": (run_cfg3, cpu_baseline_sc), "cfg4": (run_cfg4, cpu_baseline_model),
                "cfg5": (run_cfg5, cpu_baseline_train)}
+    if args.workload == "probe":
+        run_probe(args)
+        return
     run, cpu = runners[args.workload]
     result, data = run(args)
     if not args.no_cpu_baseline:

@@ -135,13 +135,34 @@ struct RowGroup {
   int group;
 };
 
+// Workgroups are dispatched round-robin over the 8 XCDs (block b runs on XCD
+// b % 8), each with its own L2.  The message kernels gather neighbour rows,
+// and neighbouring rows have nearby indices, so hand each XCD a contiguous
+// range of logical blocks: a bijection of [0, nb) that keeps the gathered
+// rows of concurrently running blocks in one L2.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int64_t xcd_block(int64_t b, int64_t nb) {
+  const int64_t q = nb / kXcds, r = nb % kXcds, x = b % kXcds, i = b / kXcds;
+  return x < r ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
 __device__ __forceinline__ RowGroup row_group_y() {
   return {(int64_t)blockIdx.x * kWavesPerBlock + wave_id(), (int)blockIdx.y};
+}
+
+// Row-parallel kernels over graph rows (the CSR message): XCD-local row ranges.
+__device__ __forceinline__ RowGroup row_group_y_xcd() {
+  return {xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + wave_id(), (int)blockIdx.y};
 }
 
 __device__ __forceinline__ RowGroup row_group_reduce(int G) {
   if (G == 1) return {(int64_t)blockIdx.x * kWavesPerBlock + wave_id(), 0};
   return {(int64_t)blockIdx.x, wave_id()};
+}
+
+__device__ __forceinline__ RowGroup row_group_reduce_xcd(int G) {
+  if (G == 1) return {xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + wave_id(), 0};
+  return {xcd_block(blockIdx.x, gridDim.x), wave_id()};
 }
 
 // ---------------------------------------------------------------------------
@@ -274,7 +295,7 @@ __device__ __forceinline__ float lane_f(float v, int i) {
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::value)) void msg_fwd_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, float* __restrict__ out) {
-  const RowGroup rg = row_group_y();
+  const RowGroup rg = row_group_y_xcd();
   const int64_t n = rg.row;
   if (n >= a.rows) return;
   const int C = a.channels, c = 64 * rg.group + lane_id();
@@ -313,7 +334,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
     Operands a, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad, float* __restrict__ dsh,
     float* __restrict__ dgates, int G) {
   extern __shared__ float red[];  // [G][64][NY] when G > 1 and dsh
-  const RowGroup rg = row_group_reduce(G);
+  const RowGroup rg = row_group_reduce_xcd(G);
   const int64_t n = rg.row;
   if (n > a.rows) return;
   const bool tail = n == a.rows;
@@ -398,7 +419,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::value)) void msg_bwd_x_kernel(
     Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx) {
-  const RowGroup rg = row_group_y();
+  const RowGroup rg = row_group_y_xcd();
   const int64_t n = rg.row;
   if (n >= a.rows) return;
   const int C = a.channels, c = 64 * rg.group + lane_id();
