@@ -634,7 +634,7 @@ def cpu_baseline_train(model, budget_s=25.0):
 
 
 def run_probe(args):
-    """Counter-collection workload: the cfg4 layer-1 message kernels, then a 1 GiB device copy.
+    """Counter-collection workload: the cfg4 layer-1 message kernels and gate projection, then a 1 GiB copy.
 
     Run under ``rocprofv3 --pmc FETCH_SIZE`` (and separately ``WRITE_SIZE``): the
     copy (1 GiB read, 1 GiB written) calibrates the counters, the message
@@ -665,6 +665,12 @@ def run_probe(args):
         tpo._msg_fwd_raw(spec, topo, x, Y, gates, None)
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True))
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, False, False))
+    from ictc_o3.ops.radial_mlp import gate_projection
+    lin = [m for m in inter.fc if isinstance(m, torch.nn.Linear)]
+    hidden = torch.randn(src.numel(), 64, device=dev, generator=g)
+    for _ in range(args.steps):
+        gate_projection(hidden, lin[-1].weight.detach())
+    del hidden
     a = torch.empty(1 << 28, device=dev)
     b = torch.randn(1 << 28, device=dev)
     for _ in range(args.steps):

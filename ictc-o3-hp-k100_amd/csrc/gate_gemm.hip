@@ -1,0 +1,182 @@
+// Gate projection of the radial MLP on bf16 MFMA with a three-way operand split:
+//   gates[E, M] = h[E, 64] . W^T,  W [M, 64] (nn.Linear layout)
+// (the last Linear of `fc`, mace_ictc/models/mace/layers.py:826-835; the
+// reference runs it as a library GEMM, streamed_gate_message.py:51-57).
+//
+// FP32 accuracy from bf16 MFMA: each operand is written exactly as
+// x = hi + mid + lo + r with hi, mid, lo bf16 (round-to-nearest-even at each
+// level) and |r| <= 2^-27 |x|.  The product keeps the six terms whose size is
+// at least 2^-24 of hi*hi (lo*hi, hi*lo, mid*mid, mid*hi, hi*mid, hi*hi,
+// accumulated smallest first in FP32 across both k-steps); the dropped terms are below 2^-25
+// relative, under FP32 rounding.  bf16 has FP32's exponent range, so there is
+// no overflow or scaling concern.  Six v_mfma_f32_16x16x32_bf16 (16 cycles
+// each) replace eight v_mfma_f32_16x16x4_f32 (32 cycles each) per 16x16x32
+// block, which makes the projection HBM-bound (it writes E * M floats).
+//
+// Tiling: a block owns 256 edges, staged from HBM into LDS once; its 4 waves
+// take 64-row slices of W in turn.  A wave holds its slice pre-split in
+// registers (A operand: 4 row blocks x 2 k-steps x 3 parts) and streams
+// 16-edge tiles of h from LDS (B operand), so every gate is produced by one
+// wave and stored as a 16-byte vector per lane.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ictc_mi355x.h"
+
+namespace ictc {
+int set_error(int code, const char* msg);
+}
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kK = 64;           // hidden width (reduction length)
+constexpr int kEdgesPerBlock = 256;
+constexpr int kTiles = kEdgesPerBlock / 16;
+
+union Bf8 {
+  bf16x8 v;
+  uint16_t u[8];
+};
+
+struct Split {
+  bf16x8 hi, mid, lo;
+};
+
+// bf16 (as the upper half of an FP32 bit pattern) nearest to x, ties to even.
+__device__ __forceinline__ uint32_t round_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u & 0xFFFF0000u;
+}
+
+__device__ __forceinline__ Split split8(const float* v) {
+  Bf8 h, m, l;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t hb = round_bf16(v[e]);
+    const float r1 = v[e] - __uint_as_float(hb);
+    const uint32_t mb = round_bf16(r1);
+    const float r2 = r1 - __uint_as_float(mb);
+    const uint32_t lb = round_bf16(r2);
+    h.u[e] = (uint16_t)(hb >> 16);
+    m.u[e] = (uint16_t)(mb >> 16);
+    l.u[e] = (uint16_t)(lb >> 16);
+  }
+  return {h.v, m.v, l.v};
+}
+
+__device__ __forceinline__ v4f mfma(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void load8(const float* __restrict__ p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+
+constexpr int kRow = kK + 4;  // LDS row pitch (floats): spreads the 16 edge rows of an operand read over the banks
+
+// The 16-edge tiles of one 64-row slice.  The NRB row blocks are independent
+// accumulator chains, interleaved so that no MFMA waits on its predecessor.
+template <int NRB>
+__device__ __forceinline__ void slice_tiles(const Split (&A)[4][2], const float* __restrict__ tile, int64_t e_base,
+                                            int64_t E, int M, int s, float* __restrict__ out) {
+  const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
+  for (int t = 0; t < kTiles; ++t) {
+    const int64_t e = e_base + 16 * t + i;
+    float cur[16];
+    load8(tile + (16 * t + i) * kRow + 8 * g, cur);
+    load8(tile + (16 * t + i) * kRow + 32 + 8 * g, cur + 8);
+    const Split B0 = split8(cur), B1 = split8(cur + 8);
+    v4f acc[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) acc[rb] = v4f{0.f, 0.f, 0.f, 0.f};
+#define ICTC_STEP(PA, PB, KS, BB) \
+  _Pragma("unroll") for (int rb = 0; rb < NRB; ++rb) acc[rb] = mfma(A[rb][KS].PA, BB.PB, acc[rb]);
+    ICTC_STEP(lo, hi, 0, B0) ICTC_STEP(hi, lo, 0, B0) ICTC_STEP(mid, mid, 0, B0)
+    ICTC_STEP(lo, hi, 1, B1) ICTC_STEP(hi, lo, 1, B1) ICTC_STEP(mid, mid, 1, B1)
+    ICTC_STEP(mid, hi, 0, B0) ICTC_STEP(hi, mid, 0, B0) ICTC_STEP(mid, hi, 1, B1)
+    ICTC_STEP(hi, mid, 1, B1) ICTC_STEP(hi, hi, 0, B0) ICTC_STEP(hi, hi, 1, B1)
+#undef ICTC_STEP
+    if (e < E) {
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) *reinterpret_cast<v4f*>(out + e * M + 64 * s + 16 * rb + 4 * g) = acc[rb];
+    }
+  }
+}
+
+// MFMA operand layout (both operands use the same k order, which is all the
+// instruction requires): lane l holds row/column l % 16 and k = 32*ks + 8*(l/16) + e.
+// D: lane l holds column l % 16 (an edge) and rows 4*(l/16) + r (gate outputs).
+// The block's 256 hidden rows are staged in LDS once, so the gate stream
+// cannot evict them between the slices that reuse them.
+__global__ __launch_bounds__(256, 2) void gate_gemm_nt_kernel(const float* __restrict__ h, int64_t E,
+                                                              const float* __restrict__ W, int M,
+                                                              float* __restrict__ out) {
+  __shared__ float tile[kEdgesPerBlock * kRow];
+  const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = l & 15, g = l >> 4;
+  const int64_t e_base = (int64_t)blockIdx.x * kEdgesPerBlock;
+  for (int idx = threadIdx.x; idx < kEdgesPerBlock * (kK / 4); idx += 256) {
+    const int r = idx / (kK / 4), q = idx % (kK / 4);
+    const int64_t e = e_base + r;
+    const float4 v = e < E ? *reinterpret_cast<const float4*>(h + e * kK + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
+    *reinterpret_cast<float4*>(tile + r * kRow + 4 * q) = v;
+  }
+  __syncthreads();
+  const int slices = (M + 63) / 64;
+  for (int s = wave; s < slices; s += 4) {
+    const int nrb = min(4, (M - 64 * s) / 16);
+    Split A[4][2];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (rb < nrb) load8(W + (int64_t)(64 * s + 16 * rb + i) * kK + 32 * ks + 8 * g, v);
+        A[rb][ks] = split8(v);
+      }
+    }
+    switch (nrb) {
+      case 4: slice_tiles<4>(A, tile, e_base, E, M, s, out); break;
+      case 3: slice_tiles<3>(A, tile, e_base, E, M, s, out); break;
+      case 2: slice_tiles<2>(A, tile, e_base, E, M, s, out); break;
+      default: slice_tiles<1>(A, tile, e_base, E, M, s, out); break;
+    }
+  }
+}
+
+int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+}  // namespace
+
+extern "C" {
+
+int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, const float* weight, int gates,
+                       float* out, void* stream) {
+  if (hidden_width != kK) return fail(ICTC_ERR_UNSUPPORTED, "gate projection is compiled for a 64-wide hidden layer");
+  if (edges < 0 || gates <= 0 || gates % 16 != 0)
+    return fail(ICTC_ERR_ARGUMENT, "gate projection: edges >= 0 and a positive multiple of 16 gates required");
+  if (edges == 0) return ICTC_OK;
+  if (!hidden || !weight || !out) return fail(ICTC_ERR_ARGUMENT, "gate projection: null operand");
+  if ((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out)) &
+      15)
+    return fail(ICTC_ERR_ARGUMENT, "gate projection: operands must be 16-byte aligned");
+  const unsigned blocks = (unsigned)((edges + kEdgesPerBlock - 1) / kEdgesPerBlock);
+  hipLaunchKernelGGL(gate_gemm_nt_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, hidden, edges, weight,
+                     gates, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "ictc_gate_gemm_fwd launch: %s", hipGetErrorString(e));
+    return fail(ICTC_ERR_RUNTIME, buf);
+  }
+  return ICTC_OK;
+}
+
+}  // extern "C"

@@ -3,8 +3,8 @@
 fc = Linear(8,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64, P*C)
 on the radial basis of the edge lengths (mace_ictc/models/mace/layers.py:826-835,
 radial_basis.py:11-92).  ``radial_gates`` runs the radial basis and the three
-hidden layers in one MFMA kernel (writing only pre-activations and the last
-hidden activation), the 64 -> P*C gate GEMM through the ROCm BLAS library,
+hidden layers in one MFMA kernel (writing only the last hidden activation),
+the 64 -> P*C gate projection on a split-bf16 MFMA kernel,
 and its adjoint fuses the hidden-layer backward down to d/dr.  It supports
 first derivatives (forces, first-order parameter gradients); callers that need
 second derivatives (force-loss training) use the composable path instead.
@@ -21,6 +21,17 @@ def _c(t):
     return t if t.is_contiguous() else t.contiguous()
 
 
+def gate_projection(h: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
+    """h [E, 64] . W^T ([M, 64], M a multiple of 16) on the split-bf16 MFMA kernel (FP32-level accuracy)."""
+    E, M = h.shape[0], W.shape[0]
+    if h.dim() != 2 or h.shape[1] != 64 or W.shape[1] != 64 or M % 16:
+        raise ValueError("gate projection needs h [E, 64] and W [M, 64] with M a multiple of 16")
+    h, W = _c(h), _c(W)
+    out = h.new_empty(E, M)
+    nat.call("ictc_gate_gemm_fwd", nat.ptr(h), E, 64, nat.ptr(W), M, nat.ptr(out), nat.stream_of(h))
+    return out
+
+
 class _RadialGates(torch.autograd.Function):
     @staticmethod
     def forward(ctx, r, W1, W2, W3, W4, cutoff, poly_p, scale):
@@ -31,7 +42,7 @@ class _RadialGates(torch.autograd.Function):
         a3 = r.new_empty(E, 64)
         nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
                  nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
-        gates = torch.nn.functional.linear(a3, W4)
+        gates = gate_projection(a3, W4)
         ctx.cfg = (cutoff, poly_p, scale)
         ctx.save_for_backward(r, W1, W2, W3, W4, a3)
         return gates
@@ -68,7 +79,8 @@ def fused_supported(fc: torch.nn.Sequential) -> bool:
     if len(lin) != 4 or any(m.bias is not None for m in lin):
         return False
     return (tuple(lin[0].weight.shape) == (64, 8) and tuple(lin[1].weight.shape) == (64, 64)
-            and tuple(lin[2].weight.shape) == (64, 64) and lin[3].weight.shape[1] == 64)
+            and tuple(lin[2].weight.shape) == (64, 64) and lin[3].weight.shape[1] == 64
+            and lin[3].weight.shape[0] % 16 == 0)
 
 
 def radial_gates(r: torch.Tensor, fc: torch.nn.Sequential, cutoff: float, poly_p: int, scale: float):

@@ -133,6 +133,16 @@ int ictc_silu(int mode, const float* x, const float* grad, const float* tangent,
 int ictc_radial(int order, const float* r, const float* grad, const float* tangent, int64_t edges, int num_basis,
                 float cutoff, int poly_p, float* out, void* stream);
 
+/* ---- Gate projection --------------------------------------------------------
+ * Replaces the last Linear of the radial MLP `fc` as the gate projection
+ * (layers.py:826-835; streamed_gate_message.py:51-57 `_gate_projection`):
+ * out [E, gates] = hidden [E, 64] . weight^T, weight [gates, 64] row-major
+ * (nn.Linear layout), gates a positive multiple of 16, operands 16-byte
+ * aligned.  bf16 MFMA with a three-way operand split (FP32-level accuracy,
+ * FP32 range).                                                                 */
+int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, const float* weight, int gates,
+                       float* out, void* stream);
+
 /* ---- Edge geometry ---------------------------------------------------------
  * Replaces the edge-vector block of the model forward
  * (mace_ictc/models/pure_cartesian_ictd_layers.py:1288-1297, backbone.py:944):

@@ -1,0 +1,44 @@
+"""GPU accuracy of the split-bf16 MFMA gate projection vs a float64 matmul.
+
+The kernel's error bound is FP32-level: |got - ref| <= 4e-7 * (|h| . |W|^T)
+elementwise (the dot product of magnitudes), checked on N(0,1) data, on data
+spanning 1e-20 .. 1e20 (bf16 keeps FP32's exponent range), and on ragged
+edge counts that end inside a 16-edge tile and inside a 256-edge block.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(device, E, M, scale_h=None, seed=0):
+    from ictc_o3.ops.radial_mlp import gate_projection
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(E, 64, generator=g, dtype=torch.float64)
+    W = torch.randn(M, 64, generator=g, dtype=torch.float64) / 8
+    if scale_h is not None:
+        h = h * torch.pow(10.0, torch.randint(-scale_h, scale_h + 1, (E, 1), generator=g).double())
+    h32, W32 = h.float(), W.float()
+    ref = h32.double() @ W32.double().t()
+    bound = h32.double().abs() @ W32.double().abs().t()
+    got = gate_projection(h32.to(device), W32.to(device)).double().cpu()
+    assert got.shape == (E, M)
+    assert bool(((got - ref).abs() <= 4e-7 * bound + 1e-45).all()), float(((got - ref).abs() / bound).max())
+
+
+@pytest.mark.parametrize("E,M", [(1000, 704), (77, 192), (4099, 64), (16, 16), (257, 2176), (1, 48)])
+def test_gate_projection_accuracy(device, E, M):
+    _check(device, E, M)
+
+
+def test_gate_projection_range(device):
+    _check(device, 3000, 704, scale_h=20, seed=1)
+
+
+def test_gate_projection_rejects(device):
+    from ictc_o3.ops.radial_mlp import gate_projection
+    with pytest.raises(ValueError):
+        gate_projection(torch.zeros(4, 64, device=device), torch.zeros(20, 64, device=device))
+    with pytest.raises(ValueError):
+        gate_projection(torch.zeros(4, 32, device=device), torch.zeros(16, 32, device=device))
+    assert gate_projection(torch.zeros(0, 64, device=device), torch.zeros(16, 64, device=device)).shape == (0, 16)
