@@ -1,0 +1,172 @@
+// Channel-mixing linears on the packed component-major layout, on FP32 MFMA
+// (v_mfma_f32_16x16x4_f32).  One kernel covers
+//   EquivariantChannelLinearSO3 / product o3.Linear (ictd_irreps.py:207-227, products.py:817):
+//       out[n, l, m, :] = s_l W_l x[n, l, m, :]                       (1 path in, 1 path out)
+//   PathPreservingLinearSO3 (layers.py:317-355, common.py:368-374):
+//       out[n, l, m, :] = s_l W_l concat_k msg[n, l, k, m, :]         (K_l paths in)
+//   and their input adjoints (W_l^T, the path count moved to the output).
+// Row layout of every degree block: [paths][2l+1][channels] (the message
+// kernels' output order), so no transpose or concatenation is materialized.
+//
+// A degree block is a GEMM of (N rows per component m) x (paths_in * Cin) by
+// (paths_in * Cin) x (paths_out * Cout).  A wave computes 16 nodes x 64
+// output columns of one component; the block's 4 waves share the weight
+// panel (64 output columns x 64 k) staged in LDS per k-chunk.  Operand k
+// order (consistent for A and B, which is all the MFMA needs): at k-step j,
+// lane group g = l/16 supplies k = 16 g + j of the chunk, so each lane reads
+// 16 contiguous floats of its row (four 16-byte loads).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ictc_mi355x.h"
+
+namespace ictc {
+int set_error(int code, const char* msg);
+}
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxDeg = 4;
+constexpr int kPanel = 64 + 4;  // LDS row pitch of the weight panel
+
+struct LinearDesc {
+  const float* w[kMaxDeg];   // [paths_out * Cout, paths_in * Cin] row-major
+  int64_t in_off[kMaxDeg];   // column offset of the degree block in an input row
+  int64_t out_off[kMaxDeg];
+  int pin[kMaxDeg], pout[kMaxDeg];
+  float scale[kMaxDeg];
+  int lmax;
+};
+
+__device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void packed_linear_kernel(const float* __restrict__ in, int64_t in_stride,
+                                                            float* __restrict__ out, int64_t out_stride, int Ci,
+                                                            int Co, int64_t N, LinearDesc d) {
+  __shared__ float panel[64 * kPanel];
+  // blockIdx.y enumerates the (degree, component) pairs in order.
+  int l = 0, m = blockIdx.y;
+  while (m >= 2 * l + 1) {
+    m -= 2 * l + 1;
+    ++l;
+  }
+  const int w = 2 * l + 1;
+  const int K = d.pin[l] * Ci, ncols = d.pout[l] * Co;
+  const int col0 = 64 * blockIdx.z;
+  if (col0 >= ncols) return;
+  const float* __restrict__ W = d.w[l];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = lane & 15, g = lane >> 4;
+  const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * 16;
+  const int64_t n = n0 + i;
+  v4f acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int kc = 0; kc < K; kc += 64) {
+    // Stage W[col0 .. col0+64) x [kc .. kc+64) (zero outside).
+    __syncthreads();
+    for (int t = threadIdx.x; t < 64 * 16; t += 256) {
+      const int r = t >> 4, q = t & 15;
+      const int col = col0 + r, k = kc + 4 * q;
+      float4 v = {0.f, 0.f, 0.f, 0.f};
+      if (col < ncols && k < K) v = *reinterpret_cast<const float4*>(W + (int64_t)col * K + k);
+      *reinterpret_cast<float4*>(panel + r * kPanel + 4 * q) = v;
+    }
+    __syncthreads();
+    // A: node n, k = kc + 16 g + j (16 contiguous channels of one input path).
+    float a[16];
+    const int k0 = kc + 16 * g;
+    if (n < N && k0 < K) {
+      const int p = k0 / Ci, c = k0 % Ci;
+      const float* src = in + n * in_stride + d.in_off[l] + ((int64_t)p * w + m) * Ci + c;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+        a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a[j] = 0.f;
+    }
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      float b[16];
+      const float* row = panel + (16 * cb + i) * kPanel + 16 * g;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 v = *reinterpret_cast<const float4*>(row + 4 * q);
+        b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[cb] = mfma(a[j], b[j], acc[cb]);
+    }
+  }
+  // D: lane holds output column col0 + 16 cb + i for nodes n0 + 4 g + r.
+  const float s = d.scale[l];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int col = col0 + 16 * cb + i;
+    if (col >= ncols) continue;
+    const int p = col / Co, c = col % Co;
+    float* dst = out + d.out_off[l] + ((int64_t)p * w + m) * Co + c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t nn = n0 + 4 * g + r;
+      if (nn < N) dst[nn * out_stride] = s * acc[cb][r];
+    }
+  }
+}
+
+int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+}  // namespace
+
+extern "C" {
+
+int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float* in, int64_t in_stride,
+                       const int* in_paths, const int64_t* in_offsets, float* out, int64_t out_stride,
+                       const int* out_paths, const int64_t* out_offsets, const float* const* weights,
+                       const float* scales, int64_t nodes, void* stream) {
+  if (lmax < 0 || lmax >= kMaxDeg) return fail(ICTC_ERR_UNSUPPORTED, "packed linear: lmax must be 0..3");
+  if (channels_in < 16 || channels_out < 16 || channels_in % 16 || channels_out % 16)
+    return fail(ICTC_ERR_UNSUPPORTED, "packed linear: channel counts must be positive multiples of 16");
+  if (nodes < 0 || in_stride < 0 || out_stride < 0 || !in_paths || !in_offsets || !out_paths || !out_offsets ||
+      !weights || !scales)
+    return fail(ICTC_ERR_ARGUMENT, "packed linear: invalid arguments");
+  if (in_stride % 4 || out_stride % 4)
+    return fail(ICTC_ERR_ARGUMENT, "packed linear: row strides must be multiples of 4 floats");
+  LinearDesc d{};
+  d.lmax = lmax;
+  int maxcols = 0;
+  for (int l = 0; l <= lmax; ++l) {
+    if (in_paths[l] < 1 || out_paths[l] < 1 || in_offsets[l] % 4 || out_offsets[l] < 0 || in_offsets[l] < 0)
+      return fail(ICTC_ERR_ARGUMENT, "packed linear: bad path counts or offsets");
+    if (!weights[l]) return fail(ICTC_ERR_ARGUMENT, "packed linear: null weight");
+    d.w[l] = weights[l];
+    d.in_off[l] = in_offsets[l];
+    d.out_off[l] = out_offsets[l];
+    d.pin[l] = in_paths[l];
+    d.pout[l] = out_paths[l];
+    d.scale[l] = scales[l];
+    if (out_paths[l] * channels_out > maxcols) maxcols = out_paths[l] * channels_out;
+  }
+  if (nodes == 0) return ICTC_OK;
+  if (!in || !out) return fail(ICTC_ERR_ARGUMENT, "packed linear: null operand");
+  const dim3 grid((unsigned)((nodes + 63) / 64), (lmax + 1) * (lmax + 1), (maxcols + 63) / 64);
+  hipLaunchKernelGGL(packed_linear_kernel, grid, dim3(256), 0, (hipStream_t)stream, in, in_stride, out, out_stride,
+                     channels_in, channels_out, nodes, d);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "ictc_packed_linear launch: %s", hipGetErrorString(e));
+    return fail(ICTC_ERR_RUNTIME, buf);
+  }
+  return ICTC_OK;
+}
+
+}  // extern "C"

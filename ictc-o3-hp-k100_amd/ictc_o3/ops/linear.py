@@ -5,7 +5,10 @@ site).  Shapes (C channels, N nodes):
   degree_linear  out[n, l*l+m, :] = scale * W_l @ x[n, l*l+m, :]            (linear_up, product linear)
   path_linear    out[n, l*l+m, :] = scale * W_l @ concat_k msg[n, l, k, m, :] (message_linear / avg_num_neighbors)
   species_linear out[n, :] = W[s_n] @ x[n, :]                               (element-conditioned self-connection)
-Here they are dense FP32 GEMMs through the ROCm BLAS library (TF32 off).
+The composable forms below are FP32 GEMMs through the ROCm BLAS library (TF32
+off) and stay differentiable to any order; ``degree_linear_fast`` /
+``path_linear_fast`` run the same maps on the hand-written MFMA kernel
+(``ictc_packed_linear``) for first-derivative callers (energy + forces).
 """
 from __future__ import annotations
 
@@ -48,3 +51,95 @@ def channel_linear(features: torch.Tensor, weight: torch.Tensor, bias=None):
     angular = features.movedim(-2, -1).contiguous()
     out = torch.nn.functional.linear(angular.reshape(-1, weight.shape[1]), weight, bias)
     return out.reshape(*angular.shape[:-1], weight.shape[0]).movedim(-1, -2)
+
+
+# ---------------------------------------------------------------------------
+# MFMA kernel path (first derivatives): one launch per linear, reading the
+# path-major degree blocks in place.
+# ---------------------------------------------------------------------------
+import ctypes
+
+from ictc_o3 import _native as nat
+
+
+def _packed_call(x, Ci, Co, lmax, pin, in_off, pout, out_off, weights, scales, out_cols):
+    N = x.shape[0]
+    out = x.new_empty(N, out_cols)
+    L = lmax + 1
+    ip, op = (ctypes.c_int * L)(*pin), (ctypes.c_int * L)(*pout)
+    io, oo = (ctypes.c_int64 * L)(*in_off), (ctypes.c_int64 * L)(*out_off)
+    ws = (ctypes.c_void_p * L)(*[w.data_ptr() for w in weights])
+    sc = (ctypes.c_float * L)(*scales)
+    nat.call("ictc_packed_linear", lmax, Ci, Co, nat.ptr(x), x.stride(0), ip, io, nat.ptr(out), out.stride(0), op,
+             oo, ws, sc, N, nat.stream_of(x))
+    return out
+
+
+class _PackedLinear(torch.autograd.Function):
+    """out = packed linear of x (first derivatives; weight gradients by einsum when required)."""
+
+    @staticmethod
+    def forward(ctx, x, layout, *weights):
+        lmax, Ci, Co, pin, in_off, out_off, scales, in_cols = layout
+        ctx.layout = layout
+        ctx.inputs = (x, *weights)
+        x = x if x.is_contiguous() else x.contiguous()
+        ws = [w.detach().contiguous() for w in weights]
+        ctx.save_for_backward(x, *ws)
+        return _packed_call(x, Ci, Co, lmax, pin, in_off, [1] * (lmax + 1), out_off, ws, scales,
+                            (lmax + 1) ** 2 * Co)
+
+    @staticmethod
+    def backward(ctx, dout):
+        from ictc_o3.autograd import required_gradients
+        if torch.is_grad_enabled():
+            raise RuntimeError("the MFMA linear path is first-order; build the model with second_order=True")
+        x, *ws = ctx.saved_tensors
+        lmax, Ci, Co, pin, in_off, out_off, scales, in_cols = ctx.layout
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:1] + ctx.needs_input_grad[2:])
+        ctx.inputs = None
+        dout = dout if dout.is_contiguous() else dout.contiguous()
+        dx = None
+        if needs[0]:
+            wt = [w.t().contiguous() for w in ws]
+            dx = _packed_call(dout, Co, Ci, lmax, [1] * (lmax + 1), out_off, pin, in_off, wt, scales, in_cols)
+        dws = []
+        N = x.shape[0]
+        for l, (w, need) in enumerate(zip(ws, needs[1:])):
+            if not need:
+                dws.append(None)
+                continue
+            k, m = pin[l], 2 * l + 1
+            xin = x[:, in_off[l]:in_off[l] + k * m * Ci].reshape(N, k, m, Ci)
+            dl = dout[:, out_off[l]:out_off[l] + m * Co].reshape(N, m, Co)
+            dws.append(scales[l] * torch.einsum("nmo,nkmc->okc", dl, xin).reshape(Co, k * Ci))
+        return (dx, None, *dws)
+
+
+def _fast_ok(x, weights, C):
+    return (x.is_cuda and x.dtype == torch.float32 and C % 16 == 0 and len(weights) <= 4
+            and all(w.numel() > 0 and w.dtype == torch.float32 for w in weights))
+
+
+def degree_linear_fast(x, weights, C, lmax, scale=1.0):
+    """degree_linear on the MFMA kernel (first derivatives only)."""
+    if not _fast_ok(x, weights, C):
+        return degree_linear(x, weights, C, lmax, scale)
+    Co = weights[0].shape[0]
+    layout = (lmax, C, Co, [1] * (lmax + 1), [l * l * C for l in range(lmax + 1)],
+              [l * l * Co for l in range(lmax + 1)], [float(scale)] * (lmax + 1), (lmax + 1) ** 2 * C)
+    return _PackedLinear.apply(x, layout, *weights[:lmax + 1])
+
+
+def path_linear_fast(m, weights, counts, C, lmax, scale=1.0):
+    """path_linear on the MFMA kernel (first derivatives only)."""
+    if not _fast_ok(m, weights, C) or any(counts.get(l, 0) == 0 for l in range(lmax + 1)):
+        return path_linear(m, weights, counts, C, lmax, scale)
+    Co = weights[0].shape[0]
+    pin, in_off, off = [], [], 0
+    for l in range(lmax + 1):
+        pin.append(counts[l])
+        in_off.append(off)
+        off += counts[l] * (2 * l + 1) * C
+    layout = (lmax, C, Co, pin, in_off, [l * l * Co for l in range(lmax + 1)], [float(scale)] * (lmax + 1), off)
+    return _PackedLinear.apply(m, layout, *weights[:lmax + 1])

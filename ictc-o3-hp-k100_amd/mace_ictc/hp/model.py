@@ -51,10 +51,12 @@ def _mace_linear_init(linear: nn.Linear):
         nn.init.normal_(linear.weight, mean=0.0, std=1.0 / math.sqrt(float(linear.in_features)))
 
 
-def degree_linear(x, weights: List[torch.Tensor], C: int, lmax: int, scale: float = 1.0):
-    """Per-degree channel map on the packed layout: out[n, l*l+m, :] = scale * W_l @ x[n, l*l+m, :]."""
-    from ictc_o3.ops.linear import degree_linear as impl
-    return impl(x, weights, C, lmax, scale)
+def degree_linear(x, weights: List[torch.Tensor], C: int, lmax: int, scale: float = 1.0, first_order=False):
+    """Per-degree channel map on the packed layout: out[n, l*l+m, :] = scale * W_l @ x[n, l*l+m, :].
+
+    first_order=True runs the MFMA kernel, whose adjoint supports first derivatives only."""
+    from ictc_o3.ops.linear import degree_linear as impl, degree_linear_fast
+    return (degree_linear_fast if first_order else impl)(x, weights, C, lmax, scale)
 
 
 class ChannelLinear(nn.Module):
@@ -68,9 +70,9 @@ class ChannelLinear(nn.Module):
             for a in self.adapters.values():
                 nn.init.eye_(a.weight)       # interaction_init="identity" (common.py:71-114)
 
-    def forward(self, x):
+    def forward(self, x, first_order=False):
         return degree_linear(x, [self.adapters[str(l)].weight for l in range(self.lmax + 1)], self.channels,
-                             self.lmax)
+                             self.lmax, first_order=first_order)
 
 
 class PathPreservingLinear(nn.Module):
@@ -87,10 +89,10 @@ class PathPreservingLinear(nn.Module):
                 nn.init.normal_(w, mean=0.0, std=1.0 / math.sqrt(float(k)))
             self.weights[str(l)] = w
 
-    def forward(self, m, scale: float):
-        from ictc_o3.ops.linear import path_linear
-        return path_linear(m, [self.weights[str(l)] for l in range(self.lmax + 1)], self.counts, self.channels,
-                           self.lmax, scale)
+    def forward(self, m, scale: float, first_order=False):
+        from ictc_o3.ops.linear import path_linear, path_linear_fast
+        return (path_linear_fast if first_order else path_linear)(
+            m, [self.weights[str(l)] for l in range(self.lmax + 1)], self.counts, self.channels, self.lmax, scale)
 
 
 class ElementConditionedLinear(nn.Module):
@@ -121,8 +123,9 @@ class ProductLinear(nn.Module):
         C = self.channels
         return [self.weight[l * C * C:(l + 1) * C * C].view(C, C).t() for l in range(self.lmax + 1)]
 
-    def forward(self, x):
-        return degree_linear(x, self.blocks(), self.channels, self.lmax, 1.0 / math.sqrt(self.channels))
+    def forward(self, x, first_order=False):
+        return degree_linear(x, self.blocks(), self.channels, self.lmax, 1.0 / math.sqrt(self.channels),
+                             first_order=first_order)
 
 
 class Interaction(nn.Module):
@@ -161,14 +164,15 @@ class Interaction(nn.Module):
     def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None):
         """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path)."""
         C = self.channels
-        x = self.linear_up(h)
+        first_order = radial is None
+        x = self.linear_up(h, first_order)
         if radial is None:
             from ictc_o3.ops.radial_mlp import radial_gates
             gates = radial_gates(r, self.fc, *radial_cfg)
         else:
             gates = self.fc(radial)
         m = tpo.message(x, Y, gates, self.spec(), topo, mask)
-        message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8))
+        message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8), first_order)
         sc = self.self_connection.forward_l0(h[:, :C], species)
         return message, sc
 
@@ -182,8 +186,8 @@ class Product(nn.Module):
             correlation=correlation)
         self.linear = ProductLinear(channels, target_lmax)
 
-    def forward(self, message, sc, species):
-        out = self.linear(self.symmetric_contractions.contract(message, species))
+    def forward(self, message, sc, species, first_order=False):
+        out = self.linear(self.symmetric_contractions.contract(message, species), first_order)
         C = self.channels
         return torch.cat([out[:, :C] + sc, out[:, C:]], 1) if out.shape[1] > C else out + sc
 
@@ -289,7 +293,7 @@ class PureCartesianICTDFix(nn.Module):
         energy = None
         for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
             message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg)
-            h = prod(message, sc, species)
+            h = prod(message, sc, species, first_order=radial is None)
             if i < self.num_interaction - 1:
                 e = self.layer_energy_readouts[i](h[:, :self.channels])
             else:

@@ -133,6 +133,23 @@ int ictc_silu(int mode, const float* x, const float* grad, const float* tangent,
 int ictc_radial(int order, const float* r, const float* grad, const float* tangent, int64_t edges, int num_basis,
                 float cutoff, int poly_p, float* out, void* stream);
 
+/* ---- Packed channel linears (MFMA) ------------------------------------------
+ * Replaces the per-degree channel maps of EquivariantChannelLinearSO3
+ * (ictd_irreps.py:207-227), the product o3.Linear (products.py:817) and
+ * PathPreservingLinearSO3 (layers.py:317-355, common.py:368-374), and their
+ * input adjoints, on the packed layout: for each degree l <= lmax and
+ * component m, out[n, out_offsets[l] + (p*(2l+1) + m)*Cout + c] =
+ *   scales[l] * sum_{q, c'} W_l[p*Cout + c, q*Cin + c'] in[n, in_offsets[l] + (q*(2l+1) + m)*Cin + c'],
+ * p < out_paths[l], q < in_paths[l]; W_l = weights[l] (device pointer),
+ * row-major [out_paths*Cout, in_paths*Cin].  Channel counts multiples of 16,
+ * strides and offsets in floats (multiples of 4), 16-byte aligned operands.
+ * Host arrays: in_paths, in_offsets, out_paths, out_offsets, weights, scales
+ * (lmax + 1 entries each).  FP32 MFMA, FP32 accumulate.                       */
+int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float* in, int64_t in_stride,
+                       const int* in_paths, const int64_t* in_offsets, float* out, int64_t out_stride,
+                       const int* out_paths, const int64_t* out_offsets, const float* const* weights,
+                       const float* scales, int64_t nodes, void* stream);
+
 /* ---- Gate projection --------------------------------------------------------
  * Replaces the last Linear of the radial MLP `fc` as the gate projection
  * (layers.py:826-835; streamed_gate_message.py:51-57 `_gate_projection`):
