@@ -3,7 +3,10 @@
 The reference delegates neighbour search to ASE / matscipy / torch_cluster
 (examples/predict.py:62, data/preprocessing.py:11, utils/graph_utils.py:217-297).
 This builds the same directed edge list on the device: a cell list when every
-periodic direction holds >= 3 cells, else an image-enumerating all-pairs search.
+periodic direction holds >= 3 cells (the HIP kernels ictc_neighbors_count /
+_fill for FP32 ROCm positions, the torch formulation below for CPU tensors,
+both emitting the same edges in the same order), else an image-enumerating
+all-pairs search.
 Edge convention (backbone.py:940-944): vec = pos[dst] - pos[src] + shift @ cell,
 with every pair at distance < cutoff (self-images included when in range).
 Edges come out sorted by receiver (dst).
@@ -16,8 +19,49 @@ import math
 import torch
 
 
+def _ncell(cell_cpu: torch.Tensor, cutoff: float):
+    c = cell_cpu.double()
+    vol = abs(float(torch.det(c)))
+    widths = [vol / float(torch.linalg.cross(c[(d + 1) % 3], c[(d + 2) % 3]).norm()) for d in range(3)]
+    return [max(1, int(math.floor(w / cutoff))) for w in widths], widths
+
+
+def _cell_list_hip(pos, cell_cpu, cutoff, ncell):
+    import ctypes
+    from ictc_o3 import _native as nat
+    pos = pos.contiguous()
+    N, dev = pos.shape[0], pos.device
+    nc = (ctypes.c_int * 3)(*ncell)
+    cellh = (ctypes.c_double * 9)(*cell_cpu.double().reshape(-1).tolist())
+    ws_bytes = int(nat.lib().ictc_neighbors_workspace_bytes(N, nc))
+    if ws_bytes < 0:
+        raise ValueError("radius_graph_pbc: system too large for the int32 cell list")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    count = torch.zeros(1, dtype=torch.int64, device=dev)
+    stream = nat.stream_of(pos)
+    nat.call("ictc_neighbors_count", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
+             nat.ptr(count), stream)
+    E = int(count.item())
+    src = torch.empty(E, dtype=torch.int64, device=dev)
+    dst = torch.empty(E, dtype=torch.int64, device=dev)
+    shifts = torch.empty(E, 3, dtype=torch.float32, device=dev)
+    if E:
+        nat.call("ictc_neighbors_fill", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
+                 nat.ptr(src), nat.ptr(dst), nat.ptr(shifts), stream)
+    return src, dst, shifts
+
+
 def radius_graph_pbc(pos: torch.Tensor, cell: torch.Tensor, cutoff: float):
     """pos [N,3], cell [3,3] (rows = lattice vectors) -> (src, dst, shifts[E,3] float)."""
+    cell_cpu = cell.detach().to("cpu", torch.float64)
+    ncell, widths = _ncell(cell_cpu, cutoff)
+    if pos.is_cuda and pos.dtype == torch.float32 and all(n >= 3 for n in ncell):
+        return _cell_list_hip(pos.detach(), cell_cpu, cutoff, ncell)
+    return _radius_graph_torch(pos, cell, cutoff)
+
+
+def _radius_graph_torch(pos: torch.Tensor, cell: torch.Tensor, cutoff: float):
+    """The same edge list with torch device ops (CPU tensors, non-FP32 positions, few cells)."""
     dev = pos.device
     inv = torch.linalg.inv(cell.double())
     frac = pos.double() @ inv

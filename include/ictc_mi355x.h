@@ -160,6 +160,23 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
 int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, const float* weight, int gates,
                        float* out, void* stream);
 
+/* ---- Periodic radius graph ---------------------------------------------------
+ * Replaces the host neighbour search the reference delegates to ASE / matscipy
+ * / torch_cluster (examples/predict.py:62, utils/graph_utils.py:217-297):
+ * all directed pairs with 1e-20 < |vec|^2 < cutoff^2, vec = pos[dst] - pos[src]
+ * + shift @ cell (backbone.py:940-944), periodic self-images included, edges
+ * receiver-sorted in a fixed order.  cell: host [3][3] (rows = lattice
+ * vectors); ncell: host [3] cells per direction, each >= 3 with cell width >=
+ * cutoff.  Two calls: _count writes the edge count to edges (device int64[1]),
+ * then the caller allocates src/dst [E] int64 and shifts [E,3] float and calls
+ * _fill with the same workspace (ictc_neighbors_workspace_bytes bytes).      */
+int64_t ictc_neighbors_workspace_bytes(int64_t atoms, const int* ncell);
+int ictc_neighbors_count(const float* pos, int64_t atoms, const double* cell, double cutoff, const int* ncell,
+                         void* workspace, int64_t workspace_bytes, int64_t* edges, void* stream);
+int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, double cutoff, const int* ncell,
+                        const void* workspace, int64_t workspace_bytes, int64_t* src, int64_t* dst, float* shifts,
+                        void* stream);
+
 /* ---- Edge geometry ---------------------------------------------------------
  * Replaces the edge-vector block of the model forward
  * (mace_ictc/models/pure_cartesian_ictd_layers.py:1288-1297, backbone.py:944):
