@@ -115,7 +115,7 @@ constexpr int kMaxGroups = 4;
 
 // Minimum waves per SIMD requested for each (kernel, degree triple): the
 // highest of 4, 3, 2, 1 at which the kernel compiles without register spills,
-// found by tune_occupancy.py and recorded in generated/ictc_occupancy.h.
+// found by tune_occupancy.py and recorded in ictc_occupancy.h.
 enum KernelKind { kEdgeFwd, kEdgeBwd, kMsgFwd, kMsgBwdEdge, kMsgBwdX };
 template <int K, int LI, int LE, int LO>
 struct Occupancy {
@@ -127,7 +127,7 @@ struct Occupancy {
 };
 
 #ifndef ICTC_OCCUPANCY_PROBE
-#include "generated/ictc_occupancy.h"
+#include "ictc_occupancy.h"
 #endif
 
 struct RowGroup {
