@@ -157,7 +157,7 @@ def run_cfg2(args):
     Ws = [(torch.randn(o, i, device=dev, generator=g) / math.sqrt(i)).requires_grad_(True)
           for i, o in zip(widths[:-1], widths[1:])]
     go = torch.randn(N, op.output_width, device=dev, generator=g)
-    topo = tpo.Topology(src, dst, N)
+    topo = tpo.Topology(src, dst, N, positions=pos)
 
     def mlp(h):
         for k, W in enumerate(Ws):
@@ -286,7 +286,7 @@ def run_cfg4(args):
     log(f"cfg4: N={N} E={E} step={dt * 1e3:.2f} ms energy={float(out['energy'][0]):.6f}")
 
     src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
-    kern, nbytes = layer_message_kernels(model, src, dst, N)
+    kern, nbytes = layer_message_kernels(model, src, dst, N, pos)
     achieved = nbytes["msg_fwd"] / kern["msg_fwd"] / 1e9
     result = {
         "metric": METRIC,
@@ -307,13 +307,14 @@ def run_cfg4(args):
     return result, model
 
 
-def layer_message_kernels(model, src, dst, N, reps=5):
-    """Live HIP-event timing of the last interaction's message kernels (fwd, bwd_edge, bwd_x) at the run's shapes."""
+def layer_message_kernels(model, src, dst, N, pos, reps=5):
+    """Live HIP-event timing of the last interaction's message kernels (fwd, bwd_edge, bwd_x) at the run's shapes,
+    visiting rows in the spatial order the model uses (and, for the log only, in index order)."""
     import torch
     from ictc_o3.ops import tensor_product as tpo
     dev = src.device
     stream = torch.cuda.current_stream(dev)
-    topo = tpo.Topology(src, dst, N)
+    topo = tpo.Topology(src, dst, N, positions=pos)
     inter = model.interactions[-1]
     spec = inter.spec()
     C = spec.channels
@@ -335,6 +336,14 @@ def layer_message_kernels(model, src, dst, N, reps=5):
     kern = {"msg_fwd": t_fwd, "msg_bwd_edge": t_bwd_e, "msg_bwd_x": t_bwd_x}
     for k, t in kern.items():
         log(f"  last-layer {k}: {t * 1e6:.1f} us  {nbytes[k] / t / 1e9:.0f} GB/s ({nbytes[k] / 1e6:.1f} MB)")
+    plain = tpo.Topology(src, dst, N)
+    plain.by_src
+    t_idx = [time_launches(lambda: tpo._msg_fwd_raw(spec, plain, x, Y, gates, None), reps, stream),
+             time_launches(lambda: tpo._msg_bwd_raw(spec, plain, x, Y, gates, None, go, (False, True, True)), reps,
+                           stream),
+             time_launches(lambda: tpo._msg_bwd_raw(spec, plain, x, Y, gates, None, go, (True, False, False)), reps,
+                           stream)]
+    log("  index-order rows: " + ", ".join(f"{k} {t * 1e6:.1f} us" for k, t in zip(kern, t_idx)))
     return kern, nbytes
 
 
@@ -555,7 +564,7 @@ def run_cfg5(args):
     g = torch.Generator(device=dev).manual_seed(56)
     E_t = torch.randn(B, device=dev, generator=g) * math.sqrt(256)
     F_t = torch.randn(N, 3, device=dev, generator=g) * 0.5
-    topo = tpo.Topology(src, dst, N)
+    topo = tpo.Topology(src, dst, N, positions=pos)
     opt = torch.optim.Adam(model.parameters(), lr=1e-4)
 
     def step():
@@ -650,7 +659,7 @@ def run_probe(args):
     pos, Z, cell, a = fcc_system(32, 0.1, 0.3, 1234, 3, dev)
     N = pos.shape[0]
     src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
-    topo = tpo.Topology(src, dst, N)
+    topo = tpo.Topology(src, dst, N, positions=pos)
     inter = model.interactions[-1]
     spec = inter.spec()
     g = torch.Generator(device=dev).manual_seed(3)

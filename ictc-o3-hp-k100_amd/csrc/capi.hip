@@ -111,6 +111,42 @@ size_t sort_temp_bytes(int64_t E, int64_t N) {
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
+// ---- Spatial (Morton) row order -------------------------------------------
+// Spread the low 10 bits of v so that bit i moves to bit 3i.
+__device__ __forceinline__ uint32_t spread3(uint32_t v) {
+  v &= 0x3FFu;
+  v = (v | (v << 16)) & 0x030000FFu;
+  v = (v | (v << 8)) & 0x0300F00Fu;
+  v = (v | (v << 4)) & 0x030C30C3u;
+  v = (v | (v << 2)) & 0x09249249u;
+  return v;
+}
+
+// 30-bit Morton key of the grid cell floor(pos / spacing) (each coordinate
+// taken modulo 1024: a wrap only costs locality, never correctness).
+__global__ void morton_keys_kernel(const float* __restrict__ pos, int64_t N, float inv_spacing,
+                                   int32_t* __restrict__ keys, int32_t* __restrict__ ids) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= N) return;
+  uint32_t q[3];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    const float v = pos[3 * i + d] * inv_spacing;
+    // NaN / huge coordinates fall into cell 0 (locality only)
+    const float f = (v == v && fabsf(v) < 1.0e9f) ? floorf(v) : 0.f;
+    q[d] = (uint32_t)((int64_t)f & 0x3FF);
+  }
+  keys[i] = (int32_t)(spread3(q[0]) | (spread3(q[1]) << 1) | (spread3(q[2]) << 2));
+  ids[i] = (int32_t)i;
+}
+
+size_t morton_temp_bytes(int64_t N) {
+  size_t bytes = 0;
+  (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
+                                     (const int32_t*)nullptr, (int32_t*)nullptr, (int)N, 0, 30);
+  return bytes;
+}
+
 // Zero fill as a kernel (not hipMemsetAsync) so the call stays valid under
 // HIP graph capture.
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
@@ -223,16 +259,47 @@ int ictc_csr_build(const int64_t* keys, int64_t E, int64_t N, int32_t* ptr, int3
   return check_hip(hipGetLastError(), "csr ptr");
 }
 
+int64_t ictc_morton_workspace_bytes(int64_t N) {
+  if (N < 0 || N >= (int64_t(1) << 31)) return -1;
+  return (int64_t)(3 * align256(sizeof(int32_t) * (size_t)(N > 0 ? N : 1)) + align256(morton_temp_bytes(N)));
+}
+
+int ictc_morton_order(const float* pos, int64_t N, float spacing, int32_t* order, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
+  if (N < 0) return fail(ICTC_ERR_ARGUMENT, "morton order: negative size");
+  if (N >= (int64_t(1) << 31)) return fail(ICTC_ERR_UNSUPPORTED, "morton order: more than 2^31 rows");
+  if (!(spacing > 0.f)) return fail(ICTC_ERR_ARGUMENT, "morton order: spacing must be positive");
+  if (N == 0) return ICTC_OK;
+  if (!pos || !order || !workspace) return fail(ICTC_ERR_ARGUMENT, "morton order: null operand");
+  const int64_t need = ictc_morton_workspace_bytes(N);
+  if (workspace_bytes < need)
+    return fail(ICTC_ERR_ARGUMENT, "morton order: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)need);
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)workspace;
+  const size_t slab = align256(sizeof(int32_t) * (size_t)N);
+  int32_t* keys = (int32_t*)ws;
+  int32_t* ids = (int32_t*)(ws + slab);
+  int32_t* sorted_keys = (int32_t*)(ws + 2 * slab);
+  void* temp = ws + 3 * slab;
+  size_t temp_bytes = morton_temp_bytes(N);
+  hipLaunchKernelGGL(morton_keys_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, pos, N, 1.f / spacing,
+                     keys, ids);
+  if (int rc = check_hip(hipGetLastError(), "morton keys")) return rc;
+  return check_hip(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, sorted_keys, ids, order, (int)N, 0, 30, st),
+                   "morton sort");
+}
+
 int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
                  const float* mask, const int64_t* src, int64_t N, int64_t E, const int32_t* dptr,
-                 const int32_t* dorder, float* out, void* stream) {
+                 const int32_t* dorder, const int32_t* dst_rows, float* out, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
   if (N == 0) return ICTC_OK;
   if (!x || !out || !dptr || (E > 0 && (!sh || !g || !src)))
     return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fwd: null operand");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(route_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C), src, ictc::Csr{dptr, dorder}, out,
+  return check_hip(route_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C), src, ictc::Csr{dptr, dorder, dst_rows}, out,
                                         (hipStream_t)stream),
                    "ictc_msg_fwd launch");
 }
@@ -240,7 +307,7 @@ int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh,
 int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
                  const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
                  const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
-                 const float* grad, float* dx, float* dsh, float* dg, void* stream) {
+                 const int32_t* dst_rows, const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dg, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
   if (E == 0 && dx) {
@@ -253,8 +320,8 @@ int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh,
   if (!x || !sh || !g || !src || !dst || !grad || !dptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: null operand");
   if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: dfeatures needs the source CSR");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(route_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder},
-                                        ictc::Csr{sptr, sorder}, grad, dx, dsh, dg, (hipStream_t)stream),
+  return check_hip(route_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder, dst_rows},
+                                        ictc::Csr{sptr, sorder, src_rows}, grad, dx, dsh, dg, (hipStream_t)stream),
                    "ictc_msg_bwd launch");
 }
 

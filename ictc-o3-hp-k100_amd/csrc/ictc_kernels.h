@@ -252,7 +252,19 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
 struct Csr {
   const int32_t* ptr;    // [N+2]: ptr[N]..ptr[N+1] holds out-of-range edges
   const int32_t* order;  // [E] or nullptr
+  const int32_t* rows;   // [N] row traversal order (a permutation of 0..N-1) or nullptr for 0..N-1
 };
+
+// Row visited by logical row slot `slot`.  A spatially ordered traversal keeps
+// the neighbour rows gathered by concurrently running waves (and by the blocks
+// of one XCD) in a compact region, so they hit in L2.  Slots at or past `rows`
+// (the out-of-range tail slot) map to themselves; an entry outside [0, rows)
+// yields -1 and its wave does nothing.
+__device__ __forceinline__ int64_t visit_row(const Csr& csr, int64_t slot, int64_t rows) {
+  if (!csr.rows || slot >= rows) return slot;
+  const int64_t n = csr.rows[slot];
+  return n >= 0 && n < rows ? n : -1;
+}
 
 // Edge metadata of a chunk of up to 64 consecutive CSR positions, staged one
 // edge per lane with coalesced loads; the edge loop then reads it with
@@ -296,8 +308,9 @@ template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::value)) void msg_fwd_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, float* __restrict__ out) {
   const RowGroup rg = row_group_y_xcd();
-  const int64_t n = rg.row;
-  if (n >= a.rows) return;
+  if (rg.row >= a.rows) return;
+  const int64_t n = visit_row(csr, rg.row, a.rows);
+  if (n < 0) return;
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
   float o[T::NO];
@@ -335,8 +348,9 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
     float* __restrict__ dgates, int G) {
   extern __shared__ float red[];  // [G][64][NY] when G > 1 and dsh
   const RowGroup rg = row_group_reduce_xcd(G);
-  const int64_t n = rg.row;
-  if (n > a.rows) return;
+  if (rg.row > a.rows) return;
+  const int64_t n = visit_row(csr, rg.row, a.rows);
+  if (n < 0) return;
   const bool tail = n == a.rows;
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
@@ -420,8 +434,9 @@ template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::value)) void msg_bwd_x_kernel(
     Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx) {
   const RowGroup rg = row_group_y_xcd();
-  const int64_t n = rg.row;
-  if (n >= a.rows) return;
+  if (rg.row >= a.rows) return;
+  const int64_t n = visit_row(scsr, rg.row, a.rows);
+  if (n < 0) return;
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
   float d[T::NX];

@@ -3,16 +3,31 @@
 // (mace_ictc/models/mace/layers.py:826-835 `fc` without its last Linear,
 // radial_basis.py:11-92), forward and the first adjoint down to d/dr.
 //
-// Tiling: a wave owns 16 edges; a block of 4 waves owns 64 edges.  Each
-// 16 x 64 x K product is a chain of v_mfma_f32_16x16x4_f32 (A 16x4, B 4x16,
-// C/D 16x16, FP32 in and out).  Operand layouts for lane l (l = 0..63):
-//   A[i][k]: i = l % 16, k = l / 16          B[k][j]: k = l / 16, j = l % 16
-//   D[i][j]: j = l % 16, i = 4 * (l / 16) + r for the lane's 4 registers r.
-// D -> A re-layout between layers goes through a per-wave LDS tile.  The
-// weights of the three hidden layers are staged in LDS once per block.
+// Every product is computed transposed, D[unit][edge] = sum_k A[unit][k] B[k][edge],
+// on 16-edge tiles (one wave per tile, grid-stride over tiles).  With the
+// 16x16 MFMA register layouts (lane l: A row l%16, B column l%16, k-chunk
+// l/16; D column l%16, rows 4*(l/16)+r) a lane ends every layer holding 16
+// hidden units of ONE edge, units 16*nb + 4*(l/16) + r (nb, r = 0..3).  The
+// reduction index of an MFMA may be permuted freely as long as A and B use
+// the same permutation, so the next layer takes exactly those 16 registers as
+// its B operand (k-chunk e of k-step ks <-> unit 16*(2ks + e/4) + 4*(l/16) + e%4)
+// and the weights are staged in LDS already permuted: no LDS round-trip of
+// activations between layers.
+//
+// Precision: the radial layer (8 -> 64) and the final d/dR product run on
+// FP32 MFMA (v_mfma_f32_16x16x4f32).  The 64x64 layers run on bf16 MFMA with a
+// three-way operand split: x = hi + mid + lo + r (bf16 parts, |r| <= 2^-27 |x|),
+// keeping the six partial products of size >= 2^-24 (hi*hi, hi*mid, mid*hi,
+// mid*mid, hi*lo, lo*hi), accumulated smallest first in FP32: FP32-level
+// accuracy and FP32's exponent range.  Six v_mfma_f32_16x16x32_bf16 (16 cycles)
+// replace eight v_mfma_f32_16x16x4f32 (32 cycles) per 16x16x32 block.
+//
+// Weights are split and permuted once per block into LDS (forward: 50 KB;
+// adjoint: 102 KB); blocks are persistent (about one resident set per CU).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdio.h>
 
 #include "../../include/ictc_mi355x.h"
 
@@ -23,18 +38,55 @@ int set_error(int code, const char* msg);
 namespace {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int H = 64;        // hidden width (compiled for 64)
-constexpr int KB = 8;        // radial basis size (compiled for 8)
-constexpr int EW = 16;       // edges per wave
-constexpr int WAVES = 4;
-constexpr int EB = EW * WAVES;
-constexpr int LA = H + 2;    // activation tile row: A-operand reads (row l%16, col l/16) conflict free
-constexpr int LW = H + 17;   // weight tile row: row- and column-wise operand reads nearly conflict free
+constexpr int H = 64;          // hidden width (compiled for 64)
+constexpr int KB = 8;          // radial basis size (compiled for 8)
+constexpr int FWD_WAVES = 4;   // waves per forward block (three blocks per CU: 51 KB of LDS each)
+constexpr int BWD_WAVES = 8;   // waves per adjoint block (one block per CU: 102 KB of LDS)
 
-__device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
+// ---- split-bf16 helpers ------------------------------------------------------
+union Bf8 {
+  bf16x8 v;
+  uint16_t u[8];
+};
+
+struct Split {
+  bf16x8 p[3];  // hi, mid, lo
+};
+
+// bf16 (as the upper half of an FP32 bit pattern) nearest to x, ties to even.
+__device__ __forceinline__ uint32_t round_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return u & 0xFFFF0000u;
+}
+
+__device__ __forceinline__ Split split8(const float* v) {
+  Bf8 h, m, l;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t hb = round_bf16(v[e]);
+    const float r1 = v[e] - __uint_as_float(hb);
+    const uint32_t mb = round_bf16(r1);
+    const float r2 = r1 - __uint_as_float(mb);
+    const uint32_t lb = round_bf16(r2);
+    h.u[e] = (uint16_t)(hb >> 16);
+    m.u[e] = (uint16_t)(mb >> 16);
+    l.u[e] = (uint16_t)(lb >> 16);
+  }
+  return {{h.v, m.v, l.v}};
+}
+
+__device__ __forceinline__ v4f mfma32(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ v4f mfma16(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Hidden unit carried by k-chunk element e of k-step ks in lane group g.
+__device__ __forceinline__ int unit_of(int ks, int g, int e) { return 16 * (2 * ks + (e >> 2)) + 4 * g + (e & 3); }
 
 // Logistic function on the hardware exp2/reciprocal (1 ulp each); saturates cleanly
 // (x -> -inf: exp2 -> inf, rcp -> 0; x -> +inf: exp2 -> 0, rcp -> 1).
@@ -81,224 +133,231 @@ __device__ __forceinline__ void radial_one(const Radial& q, float x, int k, floa
   db = q.pre * (w * cs * inv - sn * inv * inv) * env + f * denv;
 }
 
-// Radial basis of the wave's 16 edges into tile rows (b) and optionally dbt (db/dr):
-// lane l handles edge l % 16 and basis functions 2*(l/16), 2*(l/16)+1.
-__device__ __forceinline__ void radial_tile(const Radial& q, const float* __restrict__ r, int64_t e0, int64_t E,
-                                            float (*tile)[LA], float (*dbt)[KB]) {
-  const int l = threadIdx.x & 63, i = l & 15, kq = l >> 4;
-  const int64_t e = e0 + i;
-  const float x = e < E ? r[e] : 2.f * q.rc;
+// ---- weights in LDS ----------------------------------------------------------
+// Forward formats.  wf[L][part][jb][ks][lane] = split part of
+// W[16*jb + l%16][unit_of(ks, l/16, e)], e = 0..7 (W = W2 for L = 0, W3 for L = 1);
+// w1f[jb][ks][lane] = W1[16*jb + l%16][2*(l/16) + ks] (radial layer, FP32).
+struct FwdWeights {
+  bf16x8 wf[2][3][4][2][64];
+  float w1f[4][2][64];
+};
+
+// Adjoint formats.  wa[L][part][kb][ks][lane] = split part of
+// W[unit_of(ks, l/16, e)][16*kb + l%16] (the transposed map);
+// w1a[ks][lane]: row q = l%16 of dR (basis 2*(q/4) + q%4 when q%4 < 2, else a
+// zero row), k = unit 16*(ks/4) + 4*(l/16) + ks%4: W1[unit][basis].
+struct AdjWeights {
+  bf16x8 wa[2][3][4][2][64];
+  float w1a[16][64];
+};
+
+__device__ __forceinline__ void stage_fwd(FwdWeights& w, const float* __restrict__ W1, const float* __restrict__ W2,
+                                          const float* __restrict__ W3) {
+  for (int t = threadIdx.x; t < 2 * 4 * 2 * 64; t += blockDim.x) {
+    const int L = t >> 9, jb = (t >> 7) & 3, ks = (t >> 6) & 1, l = t & 63;
+    const float* W = L ? W3 : W2;
+    const int j = 16 * jb + (l & 15), g = l >> 4;
+    float v[8];
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int k = 2 * kq + t;
-    float b, db;
-    radial_one(q, x, k + 1, b, db);
-    tile[i][k] = b;
-    if (dbt) dbt[i][k] = db;
+    for (int e = 0; e < 8; ++e) v[e] = W[j * H + unit_of(ks, g, e)];
+    const Split s = split8(v);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) w.wf[L][p][jb][ks][l] = s.p[p];
+  }
+  for (int t = threadIdx.x; t < 4 * 2 * 64; t += blockDim.x) {
+    const int jb = t >> 7, ks = (t >> 6) & 1, l = t & 63;
+    w.w1f[jb][ks][l] = W1[(16 * jb + (l & 15)) * KB + 2 * (l >> 4) + ks];
   }
 }
 
-// Stage W (row-major [H, K], nn.Linear layout) transposed: wt[k][j] = W[j][k].
-__device__ __forceinline__ void stage_t(float (*wt)[LW], const float* __restrict__ W, int K) {
-  for (int t = threadIdx.x; t < H * K; t += blockDim.x) wt[t % K][t / K] = W[t];
+__device__ __forceinline__ void stage_adj(AdjWeights& w, const float* __restrict__ W1, const float* __restrict__ W2,
+                                          const float* __restrict__ W3) {
+  for (int t = threadIdx.x; t < 2 * 4 * 2 * 64; t += blockDim.x) {
+    const int L = t >> 9, kb = (t >> 7) & 3, ks = (t >> 6) & 1, l = t & 63;
+    const float* W = L ? W3 : W2;
+    const int k = 16 * kb + (l & 15), g = l >> 4;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = W[unit_of(ks, g, e) * H + k];
+    const Split s = split8(v);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) w.wa[L][p][kb][ks][l] = s.p[p];
+  }
+  for (int t = threadIdx.x; t < 16 * 64; t += blockDim.x) {
+    const int ks = t >> 6, l = t & 63, q = l & 15, g = l >> 4;
+    const int j = 16 * (ks >> 2) + 4 * g + (ks & 3);
+    w.w1a[ks][l] = (q & 3) < 2 ? W1[j * KB + 2 * (q >> 2) + (q & 3)] : 0.f;
+  }
 }
 
-// acc (16 x 64) = A (LDS activation tile, 16 x 64) @ B with B[k][j] = wt[k][j] (transposed weight).
-__device__ __forceinline__ void gemm_fwd(const float (*a)[LA], const float (*wt)[LW], v4f* acc) {
-  const int l = threadIdx.x & 63, i = l & 15, kq = l >> 4;
+// The weight formats are loop invariant: without this the compiler hoists every
+// LDS operand read out of the tile loop and spills.  Passing the LDS pointer
+// through an empty asm statement each tile keeps the reads next to their MFMAs.
+template <class T>
+__device__ __forceinline__ const T* opaque(const T* p) {
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
+// acc[nb] (units 16*nb + 4*(l/16) + r of the lane's edge) = sum_k A[unit][k] B[k],
+// A from an LDS format [3][4][2][64], B = the split activations (two k-steps).
+// The 4 row blocks are independent accumulator chains, interleaved.
+__device__ __forceinline__ void gemm6(const bf16x8 (*A)[4][2][64], const Split* B, v4f* acc) {
+  const int l = threadIdx.x & 63;
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb) acc[nb] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int kk = 0; kk < H / 4; ++kk) {
-    const float av = a[i][4 * kk + kq];
+#define ICTC_STEP(PA, PB, KS) \
+  _Pragma("unroll") for (int nb = 0; nb < 4; ++nb) acc[nb] = mfma16(A[PA][nb][KS][l], B[KS].p[PB], acc[nb]);
+  // smallest terms first: lo*hi, hi*lo, mid*mid, then mid*hi, hi*mid, then hi*hi
+  ICTC_STEP(2, 0, 0) ICTC_STEP(0, 2, 0) ICTC_STEP(1, 1, 0)
+  ICTC_STEP(2, 0, 1) ICTC_STEP(0, 2, 1) ICTC_STEP(1, 1, 1)
+  ICTC_STEP(1, 0, 0) ICTC_STEP(0, 1, 0) ICTC_STEP(1, 0, 1)
+  ICTC_STEP(0, 1, 1) ICTC_STEP(0, 0, 0) ICTC_STEP(0, 0, 1)
+#undef ICTC_STEP
+}
+
+// Split the lane's 16 values (units by register) into the two k-steps' B operands.
+__device__ __forceinline__ void split_units(const v4f* a, Split* B) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) acc[nb] = mfma(av, wt[4 * kk + kq][16 * nb + i], acc[nb]);
+  for (int ks = 0; ks < 2; ++ks) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = a[2 * ks + (e >> 2)][e & 3];
+    B[ks] = split8(v);
   }
 }
 
-// acc (16 x 64) = A (16 x 64) @ W with W[k][j] = wt[j][k] (the adjoint of gemm_fwd's map).
-__device__ __forceinline__ void gemm_adj(const float (*a)[LA], const float (*wt)[LW], v4f* acc) {
-  const int l = threadIdx.x & 63, i = l & 15, kq = l >> 4;
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) acc[nb] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int kk = 0; kk < H / 4; ++kk) {
-    const float av = a[i][4 * kk + kq];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) acc[nb] = mfma(av, wt[16 * nb + i][4 * kk + kq], acc[nb]);
-  }
-}
-
-__device__ __forceinline__ void d_to_lds(float (*t)[LA], const v4f* d) {
-  const int l = threadIdx.x & 63, j = l & 15, i0 = 4 * (l >> 4);
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) t[i0 + r][16 * nb + j] = d[nb][r];
-}
-
-__device__ __forceinline__ void d_store(float* __restrict__ out, int64_t e0, int64_t E, const v4f* d) {
-  const int l = threadIdx.x & 63, j = l & 15, i0 = 4 * (l >> 4);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t e = e0 + i0 + r;
-    if (e < E) {
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) out[e * H + 16 * nb + j] = d[nb][r];
-    }
-  }
-}
-
-__device__ __forceinline__ void d_load(const float* __restrict__ in, int64_t e0, int64_t E, v4f* d) {
-  const int l = threadIdx.x & 63, j = l & 15, i0 = 4 * (l >> 4);
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t e = e0 + i0 + r;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) d[nb][r] = e < E ? in[e * H + 16 * nb + j] : 0.f;
-  }
-}
-
-// d <- s silu(d); with `keep`, z <- s silu'(z) = s sig(z) (1 + z (1 - sig(z))) for the adjoint.
-__device__ __forceinline__ void act(v4f* d, v4f* z, float s, bool keep) {
+// a <- s silu(z); with `keep`, slope <- s silu'(z) = s sig(z) (1 + z (1 - sig(z))).
+template <bool KEEP>
+__device__ __forceinline__ void act(const v4f* z, float s, v4f* a, v4f* slope) {
 #pragma unroll
   for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const float x = d[nb][t], g = sigm(x);
-      d[nb][t] = s * x * g;
-      if (keep) z[nb][t] = s * g * (1.f + x * (1.f - g));
+      const float x = z[nb][t], g = sigm(x);
+      a[nb][t] = s * x * g;
+      if (KEEP) slope[nb][t] = s * g * (1.f + x * (1.f - g));
     }
 }
 
-struct Smem {
-  float w1t[KB][LW];
-  float w2t[H][LW];
-  float w3t[H][LW];
-  float tile[WAVES][EW][LA];
-  float dbt[WAVES][EW][KB];
-};
-
-__device__ __forceinline__ void stage_weights(Smem& sm, const float* W1, const float* W2, const float* W3) {
-  stage_t(sm.w1t, W1, KB);
-  stage_t(sm.w2t, W2, H);
-  stage_t(sm.w3t, W3, H);
+// Row-major [E, 64] arrays in the lane layout: edge e0 + l%16, units 16*nb + 4*(l/16) .. +3.
+__device__ __forceinline__ void store_units(float* __restrict__ out, int64_t e, bool ok, const v4f* v) {
+  if (!ok) return;
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) *reinterpret_cast<v4f*>(out + e * H + 16 * nb + 4 * g) = v[nb];
 }
 
-// Forward pass of one wave's 16 edges; leaves a3 in `a` and, with want_db, the
-// activation slopes s silu'(z_k) in z1, z2, z3 and db/dr in LDS.
-// Optional global outputs (nullptr to skip): a1, a2 (training weight gradients).
-__device__ __forceinline__ void forward_tile(Smem& sm, int w, const float* __restrict__ r, int64_t e0, int64_t E,
-                                             const Radial& q, float s, bool want_db, v4f* z1, v4f* z2, v4f* z3,
-                                             v4f* a, float* a1_out, float* a2_out) {
-  const int l = threadIdx.x & 63, i = l & 15, kq = l >> 4;
-  radial_tile(q, r, e0, E, sm.tile[w], want_db ? sm.dbt[w] : nullptr);
-  __syncthreads();
+__device__ __forceinline__ void load_units(const float* __restrict__ in, int64_t e, bool ok, v4f* v) {
+  const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) z1[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < 4; ++nb)
+    v[nb] = ok ? *reinterpret_cast<const v4f*>(in + e * H + 16 * nb + 4 * g) : v4f{0.f, 0.f, 0.f, 0.f};
+}
+
+// Forward of one 16-edge tile for the lane's edge (e, in range `ok`).  Leaves
+// the last activation in a3; with KEEP, the slopes and db/dr of the lane's two
+// basis functions (2*(l/16), 2*(l/16)+1).
+template <bool KEEP>
+__device__ __forceinline__ void forward_tile(const FwdWeights& w, const Radial& q, float x, float s, v4f* a3,
+                                             v4f* s1, v4f* s2, v4f* s3, float* db, float* a1_out, float* a2_out,
+                                             int64_t e, bool ok) {
+  const int l = threadIdx.x & 63, g = l >> 4;
+  float b[2];
+  radial_one(q, x, 2 * g + 1, b[0], db[0]);
+  radial_one(q, x, 2 * g + 2, b[1], db[1]);
+  v4f z[4], a[4];
 #pragma unroll
-  for (int kk = 0; kk < KB / 4; ++kk) {
-    const float av = sm.tile[w][i][4 * kk + kq];
+  for (int jb = 0; jb < 4; ++jb) {
+    z[jb] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) z1[nb] = mfma(av, sm.w1t[4 * kk + kq][16 * nb + i], z1[nb]);
+    for (int ks = 0; ks < 2; ++ks) z[jb] = mfma32(w.w1f[jb][ks][l], b[ks], z[jb]);
   }
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) a[nb] = z1[nb];
-  act(a, z1, s, want_db);
-  if (a1_out) d_store(a1_out, e0, E, a);
-  __syncthreads();
-  d_to_lds(sm.tile[w], a);
-  __syncthreads();
-  gemm_fwd(sm.tile[w], sm.w2t, z2);
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) a[nb] = z2[nb];
-  act(a, z2, s, want_db);
-  if (a2_out) d_store(a2_out, e0, E, a);
-  __syncthreads();
-  d_to_lds(sm.tile[w], a);
-  __syncthreads();
-  gemm_fwd(sm.tile[w], sm.w3t, z3);
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb) a[nb] = z3[nb];
-  act(a, z3, s, want_db);
+  act<KEEP>(z, s, a, s1);
+  if (a1_out) store_units(a1_out, e, ok, a);
+  Split B[2];
+  split_units(a, B);
+  gemm6(w.wf[0], B, z);
+  act<KEEP>(z, s, a, s2);
+  if (a2_out) store_units(a2_out, e, ok, a);
+  split_units(a, B);
+  gemm6(w.wf[1], B, z);
+  act<KEEP>(z, s, a3, s3);
 }
 
 // Forward: a3 = s silu(W3 s silu(W2 s silu(W1 R(r)))), written to a3 [E, 64].
-__global__ __launch_bounds__(256) void mlp_fwd_kernel(const float* __restrict__ r, int64_t E, float rc, int p,
-                                                      const float* __restrict__ W1, const float* __restrict__ W2,
-                                                      const float* __restrict__ W3, float s,
-                                                      float* __restrict__ a3) {
-  __shared__ Smem sm;
-  stage_weights(sm, W1, W2, W3);
-  const int w = threadIdx.x >> 6;
-  const int64_t e0 = ((int64_t)blockIdx.x * WAVES + w) * EW;
+__global__ __launch_bounds__(FWD_WAVES * 64) void mlp_fwd_kernel(const float* __restrict__ r, int64_t E, float rc,
+                                                                 int p, const float* __restrict__ W1,
+                                                                 const float* __restrict__ W2,
+                                                                 const float* __restrict__ W3, float s,
+                                                                 float* __restrict__ a3) {
+  __shared__ FwdWeights ws;
+  stage_fwd(ws, W1, W2, W3);
+  __syncthreads();
   const Radial q = radial_consts(rc, p);
-  v4f z1[4], z2[4], z3[4], a[4];
-  forward_tile(sm, w, r, e0, E, q, s, false, z1, z2, z3, a, nullptr, nullptr);
-  d_store(a3, e0, E, a);
+  const int waves = blockDim.x >> 6;
+  const int64_t tiles = (E + 15) / 16, stride = (int64_t)gridDim.x * waves;
+  for (int64_t t = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6); t < tiles; t += stride) {
+    const int64_t e = 16 * t + (threadIdx.x & 15);
+    const bool ok = e < E;
+    const float x = ok ? r[e] : 2.f * rc;
+    const FwdWeights& w = *opaque(&ws);
+    v4f a[4];
+    float db[2];
+    forward_tile<false>(w, q, x, s, a, nullptr, nullptr, nullptr, db, nullptr, nullptr, e, ok);
+    store_units(a3, e, ok, a);
+  }
 }
 
 // Adjoint: recomputes the forward in registers, then given da3 returns dr [E];
 // optional outputs dz1..dz3, a1, a2 (nullptr to skip) feed weight gradients.
-__global__ __launch_bounds__(256) void mlp_bwd_kernel(const float* __restrict__ r, int64_t E, float rc, int p,
-                                                      const float* __restrict__ W1, const float* __restrict__ W2,
-                                                      const float* __restrict__ W3, float s,
-                                                      const float* __restrict__ da3, float* __restrict__ dr,
-                                                      float* __restrict__ dz1, float* __restrict__ dz2,
-                                                      float* __restrict__ dz3, float* __restrict__ a1_out,
-                                                      float* __restrict__ a2_out) {
-  __shared__ Smem sm;
-  stage_weights(sm, W1, W2, W3);
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, kq = l >> 4;
-  const int64_t e0 = ((int64_t)blockIdx.x * WAVES + w) * EW;
+__global__ __launch_bounds__(BWD_WAVES * 64) void mlp_bwd_kernel(
+    const float* __restrict__ r, int64_t E, float rc, int p, const float* __restrict__ W1,
+    const float* __restrict__ W2, const float* __restrict__ W3, float s, const float* __restrict__ da3,
+    float* __restrict__ dr, float* __restrict__ dz1, float* __restrict__ dz2, float* __restrict__ dz3,
+    float* __restrict__ a1_out, float* __restrict__ a2_out) {
+  __shared__ FwdWeights wfs;
+  __shared__ AdjWeights was;
+  stage_fwd(wfs, W1, W2, W3);
+  stage_adj(was, W1, W2, W3);
+  __syncthreads();
   const Radial q = radial_consts(rc, p);
-  v4f z1[4], z2[4], z3[4], g[4];
-  forward_tile(sm, w, r, e0, E, q, s, true, z1, z2, z3, g, a1_out, a2_out);
-  d_load(da3, e0, E, g);
+  const int l = threadIdx.x & 63;
+  const int waves = blockDim.x >> 6;
+  const int64_t tiles = (E + 15) / 16, stride = (int64_t)gridDim.x * waves;
+  for (int64_t t = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6); t < tiles; t += stride) {
+    const int64_t e = 16 * t + (l & 15);
+    const bool ok = e < E;
+    const float x = ok ? r[e] : 2.f * rc;
+    const FwdWeights& wf = *opaque(&wfs);
+    const AdjWeights& wa = *opaque(&was);
+    v4f s1[4], s2[4], s3[4], gv[4];
+    float db[2];
+    forward_tile<true>(wf, q, x, s, gv, s1, s2, s3, db, a1_out, a2_out, e, ok);
+    load_units(da3, e, ok, gv);
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < 4; ++nb) gv[nb] *= s3[nb];
+    if (dz3) store_units(dz3, e, ok, gv);
+    Split B[2];
+    split_units(gv, B);
+    gemm6(wa.wa[1], B, gv);  // da2 = dz3 W3
 #pragma unroll
-    for (int t = 0; t < 4; ++t) g[nb][t] *= z3[nb][t];
-  if (dz3) d_store(dz3, e0, E, g);
-  __syncthreads();
-  d_to_lds(sm.tile[w], g);
-  __syncthreads();
-  gemm_adj(sm.tile[w], sm.w3t, g);    // da2 = dz3 W3
+    for (int nb = 0; nb < 4; ++nb) gv[nb] *= s2[nb];
+    if (dz2) store_units(dz2, e, ok, gv);
+    split_units(gv, B);
+    gemm6(wa.wa[0], B, gv);  // da1 = dz2 W2
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+    for (int nb = 0; nb < 4; ++nb) gv[nb] *= s1[nb];
+    if (dz1) store_units(dz1, e, ok, gv);
+    // dR = dz1 W1 on FP32 MFMA: k-step ks takes the lane's unit 16*(ks/4) + 4*(l/16) + ks%4.
+    v4f dR = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 4; ++t) g[nb][t] *= z2[nb][t];
-  if (dz2) d_store(dz2, e0, E, g);
-  __syncthreads();
-  d_to_lds(sm.tile[w], g);
-  __syncthreads();
-  gemm_adj(sm.tile[w], sm.w2t, g);    // da1 = dz2 W2
-#pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) g[nb][t] *= z1[nb][t];
-  if (dz1) d_store(dz1, e0, E, g);
-  __syncthreads();
-  d_to_lds(sm.tile[w], g);
-  __syncthreads();
-  // dR = dz1 W1 (16 x 8): one MFMA column block, B[k][j] = W1[k][j] = w1t[j][k] for j < 8, else 0.
-  v4f dR = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int kk = 0; kk < H / 4; ++kk) {
-    const float av = sm.tile[w][i][4 * kk + kq];
-    const float bv = i < KB ? sm.w1t[i][4 * kk + kq] : 0.f;
-    dR = mfma(av, bv, dR);
-  }
-  // dr[e] = sum_k dR[e][k] db_k(r_e): lane holds k = l % 16, rows 4*(l/16) + t.
-  const int j = l & 15, i0 = 4 * (l >> 4);
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    float v = j < KB ? dR[t] * sm.dbt[w][i0 + t][j] : 0.f;
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));   // quad xor 1
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));   // quad xor 2
-    v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));  // half-row mirror
-    const int64_t e = e0 + i0 + t;
-    if (j == 0 && e < E) dr[e] = v;
+    for (int ks = 0; ks < 16; ++ks) dR = mfma32(wa.w1a[ks][l], gv[ks >> 2][ks & 3], dR);
+    // lane holds dR of basis 2*(l/16) + r in rows r = 0, 1; dr = sum_k dR_k db_k over the 4 lane groups
+    float v = dR[0] * db[0] + dR[1] * db[1];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (l < 16 && ok) dr[e] = v;
   }
 }
 
@@ -312,6 +371,27 @@ int launch_status(const char* what) {
   return fail(ICTC_ERR_RUNTIME, buf);
 }
 
+// Compute units of the current device (queried once per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+unsigned grid_for(int64_t edges, int waves, int blocks_per_cu) {
+  const int64_t tiles = (edges + 15) / 16, need = (tiles + waves - 1) / waves;
+  const int64_t cap = (int64_t)cu_count() * blocks_per_cu;
+  return (unsigned)(need < cap ? need : cap);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 extern "C" {
@@ -322,9 +402,9 @@ int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden
   if (edges < 0 || !(cutoff > 0.f) || poly_p < 2) return fail(ICTC_ERR_ARGUMENT, "radial MLP: invalid arguments");
   if (edges == 0) return ICTC_OK;
   if (!r || !W1 || !W2 || !W3 || !a3) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
-  const unsigned blocks = (unsigned)((edges + EB - 1) / EB);
-  hipLaunchKernelGGL(mlp_fwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, r, edges, cutoff, poly_p, W1,
-                     W2, W3, silu_scale, a3);
+  if (!aligned16(a3)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: a3 must be 16-byte aligned");
+  hipLaunchKernelGGL(mlp_fwd_kernel, dim3(grid_for(edges, FWD_WAVES, 3)), dim3(FWD_WAVES * 64), 0,
+                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, a3);
   return launch_status("ictc_radial_mlp_fwd launch");
 }
 
@@ -335,9 +415,12 @@ int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden
   if (edges < 0 || !(cutoff > 0.f) || poly_p < 2) return fail(ICTC_ERR_ARGUMENT, "radial MLP: invalid arguments");
   if (edges == 0) return ICTC_OK;
   if (!r || !W1 || !W2 || !W3 || !da3 || !dr) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
-  const unsigned blocks = (unsigned)((edges + EB - 1) / EB);
-  hipLaunchKernelGGL(mlp_bwd_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, r, edges, cutoff, poly_p, W1,
-                     W2, W3, silu_scale, da3, dr, dz1, dz2, dz3, a1, a2);
+  for (const float* p : {da3, (const float*)dz1, (const float*)dz2, (const float*)dz3, (const float*)a1,
+                         (const float*)a2})
+    if (p && !aligned16(p)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: [E, 64] operands must be 16-byte aligned");
+  hipLaunchKernelGGL(mlp_bwd_kernel, dim3(grid_for(edges, BWD_WAVES, 1)), dim3(BWD_WAVES * 64), 0,
+                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, dr, dz1, dz2, dz3,
+                     a1, a2);
   return launch_status("ictc_radial_mlp_bwd launch");
 }
 

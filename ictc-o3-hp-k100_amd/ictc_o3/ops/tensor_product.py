@@ -182,13 +182,39 @@ class Csr:
                  nat.ptr(ws), ws_bytes, nat.stream_of(keys))
 
 
-class Topology:
-    """Receiver-sorted CSR (forward, gate / harmonic adjoints) and source-sorted CSR (feature adjoint)."""
+def morton_order(positions: torch.Tensor, spacing: float) -> torch.Tensor:
+    """int32 [N] rows sorted (stably) by the Morton key of their grid cell floor(pos / spacing)."""
+    pos = _c(positions.detach().float())
+    N = pos.shape[0]
+    order = torch.empty(max(N, 1), dtype=torch.int32, device=pos.device)
+    ws_bytes = int(nat.lib().ictc_morton_workspace_bytes(N))
+    if ws_bytes < 0:
+        raise ValueError("too many rows for an int32 row order")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=pos.device)
+    nat.call("ictc_morton_order", nat.ptr(pos), N, float(spacing), nat.ptr(order), nat.ptr(ws), ws_bytes,
+             nat.stream_of(pos))
+    return order[:N]
 
-    def __init__(self, src: torch.Tensor, dst: torch.Tensor, nodes: int):
+
+class Topology:
+    """Receiver-sorted CSR (forward, gate / harmonic adjoints) and source-sorted CSR (feature adjoint).
+
+    ``positions`` (optional, [N,3]) sets a spatial (Morton) order in which the
+    source-owned feature adjoint visits rows (``src_rows``), so that the
+    receiver cotangent rows gathered by concurrent waves share the L2.  The
+    receiver-owned passes keep index order (``dst_rows`` None): with the edge
+    arrays stored receiver-sorted it streams the gate rows sequentially, which
+    measured faster than a spatial order on the cfg4 shapes.  Results are
+    bit-identical for any row order.
+    """
+
+    def __init__(self, src: torch.Tensor, dst: torch.Tensor, nodes: int, positions: torch.Tensor | None = None,
+                 spacing: float = 2.0):
         self.src, self.dst, self.nodes = _c(src), _c(dst), nodes
         self.by_dst = Csr(self.dst, nodes)
         self._by_src = None
+        self.dst_rows = None
+        self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None
 
     @property
     def by_src(self):
@@ -202,7 +228,7 @@ def _msg_fwd_raw(spec, topo, x, sh, g, mask):
     out = x.new_empty(N, spec.out_components * spec.channels)
     nat.call("ictc_msg_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), N, E, nat.ptr(topo.by_dst.ptr),
-             nat.ptr(topo.by_dst.order), nat.ptr(out), nat.stream_of(x))
+             nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.stream_of(x))
     return out
 
 
@@ -215,7 +241,8 @@ def _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need):
     nat.call("ictc_msg_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
              nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
-             nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(go),
+             nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
+             nat.ptr(topo.src_rows), nat.ptr(go),
              nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.stream_of(x))
     return dx, dsh, dg
 

@@ -268,7 +268,7 @@ class PureCartesianICTDFix(nn.Module):
         N = pos.shape[0]
         species = self.atomic_number_to_index[A.long()]
         if topology is None:
-            topology = tpo.Topology(edge_src, edge_dst, N)
+            topology = tpo.Topology(edge_src, edge_dst, N, positions=pos)
         shifts = edge_shifts.to(pos.dtype)
         if cell.shape[0] == 1:
             shift_vec = shifts @ cell[0]

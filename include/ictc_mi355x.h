@@ -72,6 +72,15 @@ int64_t ictc_csr_workspace_bytes(int64_t edges, int64_t nodes);
 int ictc_csr_build(const int64_t* keys, int64_t edges, int64_t nodes, int32_t* ptr,
                    int32_t* order, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ---- Spatial row order --------------------------------------------------
+ * No counterpart in the reference (its kernels visit rows in index order).
+ * order [N] int32 = the rows sorted (stably) by the 30-bit Morton key of the
+ * grid cell floor(pos / spacing), pos [N,3] FP32; used as the row order (dst_rows / src_rows) of the
+ * graph-message calls.  workspace: ictc_morton_workspace_bytes(N) bytes.      */
+int64_t ictc_morton_workspace_bytes(int64_t rows);
+int ictc_morton_order(const float* pos, int64_t rows, float spacing, int32_t* order, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
 /* ---- Graph message (gather -> TP -> gate -> mask -> receiver sum) --------
  * Replaces PackedGraphMessage.forward's native launches
  * (operators.py:382-409 -> ops/rematerialized_message.py:166-205 ->
@@ -79,25 +88,34 @@ int ictc_csr_build(const int64_t* keys, int64_t edges, int64_t nodes, int32_t* p
  *   out[n] = sum_{e: dst[e]=n} mask[e] * TP(features[src[e]], harmonics[e], gates[e])
  * features [nodes, C*(LI+1)^2]; out [nodes, C*NO] is fully overwritten.
  * dst_ptr/dst_order: ictc_csr_build over dst (dst_order NULL = edges already
- * sorted by dst with no out-of-range ids).  mask may be NULL.  Deterministic:
- * one owner per output row, no floating-point atomics.                        */
+ * sorted by dst with no out-of-range ids).  mask may be NULL.  dst_rows
+ * [nodes] int32 (NULL = 0..nodes-1) is the order in which output rows are
+ * visited: a permutation of 0..nodes-1, e.g. spatial (ictc_morton_order), so
+ * that the neighbour rows gathered by concurrent waves share the L2.  It
+ * changes no result bit.  Entries outside [0, nodes) are skipped.  (When the
+ * edge arrays are stored receiver-sorted, index order also streams the gate
+ * rows sequentially and is the better choice.)  Deterministic: one owner per
+ * output row, no floating-point atomics.                                      */
 int ictc_msg_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                  const float* features, const float* harmonics, const float* gates,
                  const float* weight, const float* mask, const int64_t* src,
                  int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
-                 float* out, void* stream);
+                 const int32_t* dst_rows, float* out, void* stream);
 
 /* First adjoint of ictc_msg_fwd; replaces _first
  * (ops/rematerialized_message.py:25-83 -> generated_adjoint /
  * generated_csr_adjoint.py:199-293 source_adjoint).  dfeatures uses the
  * source-sorted CSR (src_ptr/src_order from ictc_csr_build over src);
- * dharmonics and dgates use the receiver-sorted CSR.  NULL outputs are
- * skipped; non-NULL outputs are fully overwritten.                            */
+ * dharmonics and dgates use the receiver-sorted CSR, visiting receivers in
+ * dst_rows order; dfeatures visits sources in src_rows order (both as
+ * dst_rows of ictc_msg_fwd; NULL = index order).  NULL outputs are skipped;
+ * non-NULL outputs are fully overwritten.                                     */
 int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                  const float* features, const float* harmonics, const float* gates,
                  const float* weight, const float* mask, const int64_t* src, const int64_t* dst,
                  int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
-                 const int32_t* src_ptr, const int32_t* src_order, const float* grad,
+                 const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
+                 const int32_t* src_rows, const float* grad,
                  float* dfeatures, float* dharmonics, float* dgates, void* stream);
 
 /* ---- Direction harmonics --------------------------------------------------

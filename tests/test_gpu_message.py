@@ -144,3 +144,50 @@ def test_graph_message_dict_api(device):
     _, _, counts = orc.path_tables(paths)
     packed = orc.pack_output({l: out[l].double().cpu() for l in out}, counts, C)
     assert rel_err(packed, ref) < TOL
+
+
+def _morton_np(pos, spacing):
+    """Stable argsort of the 30-bit Morton key of floor(pos / spacing) mod 1024 (bit i of axis d -> bit 3i+d)."""
+    import numpy as np
+    q = (np.floor(pos.astype(np.float32) * np.float32(1.0 / spacing)).astype(np.int64) & 0x3FF)
+    key = np.zeros(len(pos), dtype=np.int64)
+    for i in range(10):
+        for d in range(3):
+            key |= ((q[:, d] >> i) & 1) << (3 * i + d)
+    return np.argsort(key, kind="stable")
+
+
+def test_morton_order_matches_restatement(device):
+    from ictc_o3.ops.tensor_product import morton_order
+    g = torch.Generator().manual_seed(11)
+    pos = (torch.rand(5000, 3, generator=g) * 80 - 20).float()
+    got = morton_order(pos.to(device), 2.0).cpu().numpy()
+    assert (got == _morton_np(pos.numpy(), 2.0)).all()
+    assert morton_order(pos[:0].to(device), 2.0).numel() == 0
+
+
+@pytest.mark.parametrize("li,le,lo,C", [(2, 2, 2, 64), (2, 3, 3, 128), (0, 2, 2, 17)])
+def test_message_row_order_bitwise_identical(device, li, le, lo, C):
+    """Visiting rows in a spatial or random order changes no bit of the output or of any gradient."""
+    from ictc_o3 import PackedGraphMessage
+    from ictc_o3.ops import tensor_product as tpo
+    N, E = 300, 6000
+    op = PackedGraphMessage.create(channels=C, input_lmax=li, edge_lmax=le, output_lmax=lo, device=device)
+    f64, sh64, g64, src, dst, m64 = _graph(N, E, C, li, le, lo, 21, mask=True)
+    s, d, m = src.to(device), dst.to(device), m64.float().to(device)
+    pos = torch.rand(N, 3, generator=torch.Generator().manual_seed(4)).to(device) * 30
+    results = []
+    for rows in (None, "morton", "random"):
+        topo = tpo.Topology(s, d, N, positions=pos if rows == "morton" else None)
+        if rows == "random":
+            topo.dst_rows = torch.randperm(N, generator=torch.Generator().manual_seed(5)).int().to(device)
+            topo.src_rows = torch.randperm(N, generator=torch.Generator().manual_seed(6)).int().to(device)
+        elif rows == "morton":
+            topo.dst_rows = topo.src_rows
+        x = [t.float().to(device).requires_grad_(True) for t in (f64, sh64, g64)]
+        out = op(*x, s, d, m, topology=topo)
+        grads = torch.autograd.grad(out, x, torch.cos(out))
+        results.append((out, *grads))
+    for other in results[1:]:
+        for a, b in zip(results[0], other):
+            assert torch.equal(a, b)
