@@ -163,22 +163,56 @@ hipError_t route_edge_fwd(const ictc::TpShape& s, const ictc::Operands& a, float
   return ictc::launch_edge_fwd(s, a, out, st);
 }
 hipError_t route_edge_bwd(const ictc::TpShape& s, const ictc::Operands& a, const float* grad, float* dx, float* dsh,
-                          float* dg, hipStream_t st) {
-  return ictc::launch_edge_bwd(s, a, grad, dx, dsh, dg, st);
+                          float* dg, float* ws, hipStream_t st) {
+  return ictc::launch_edge_bwd(s, a, grad, dx, dsh, dg, ws, st);
 }
 hipError_t route_msg_fwd(const ictc::TpShape& s, const ictc::Operands& a, const int64_t* src, ictc::Csr c,
                          float* out, hipStream_t st) {
   return ictc::launch_msg_fwd(s, a, src, c, out, st);
 }
+hipError_t route_edge_second(const ictc::TpShape& s, const ictc::Operands& a, const ictc::Tangents& t,
+                             const float* grad, float* dgrad, float* dx, float* dsh, float* dg, float* ws,
+                             hipStream_t st) {
+  return ictc::launch_edge_second(s, a, t, grad, dgrad, dx, dsh, dg, ws, st);
+}
 hipError_t route_msg_bwd(const ictc::TpShape& s, const ictc::Operands& a, const int64_t* src, const int64_t* dst,
-                         ictc::Csr dc, ictc::Csr sc, const float* grad, float* dx, float* dsh, float* dg,
+                         ictc::Csr dc, ictc::Csr sc, const float* grad, float* dx, float* dsh, float* dg, float* ws,
                          hipStream_t st) {
-  return ictc::launch_msg_bwd(s, a, src, dst, dc, sc, grad, dx, dsh, dg, st);
+  return ictc::launch_msg_bwd(s, a, src, dst, dc, sc, grad, dx, dsh, dg, ws, st);
+}
+
+// Workspace floats for the channel groups' partial harmonic gradients.
+int64_t group_ws_floats(int le, int C, int64_t E) {
+  const int G = ictc::channel_groups(C);
+  return G > 1 ? (int64_t)(G - 1) * E * (le + 1) * (le + 1) : 0;
+}
+
+int check_ws(const float* dsh, const float* ws, int64_t ws_bytes, int le, int C, int64_t E, const char* who) {
+  const int64_t need = group_ws_floats(le, C, E) * (int64_t)sizeof(float);
+  if (!dsh || need == 0) return ICTC_OK;
+  if (!ws || ws_bytes < need)
+    return fail(ICTC_ERR_ARGUMENT, "%s: dharmonics with %d channels needs a workspace of %lld bytes", who, C,
+                (long long)need);
+  return ICTC_OK;
+}
+
+__global__ void group_sum_kernel(float* __restrict__ out, const float* __restrict__ part, int64_t n, int slabs) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float v = out[i];
+  for (int s = 0; s < slabs; ++s) v += part[s * n + i];
+  out[i] = v;
 }
 
 }  // namespace
 
 namespace ictc {
+hipError_t launch_group_sum(float* out, const float* part, int64_t n, int slabs, hipStream_t st) {
+  if (slabs <= 0 || n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(group_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, part, n, slabs);
+  return hipGetLastError();
+}
+
 int set_error(int code, const char* msg) {
   g_error = msg;
   return code;
@@ -208,14 +242,21 @@ int ictc_tp_fwd(int li, int le, int lo, int C, const float* x, const float* sh, 
                    "ictc_tp_fwd launch");
 }
 
+int64_t ictc_tp_workspace_bytes(int edge_lmax, int channels, int64_t edges) {
+  if (edge_lmax < 0 || edge_lmax > 3 || ictc::channel_groups(channels) == 0 || edges < 0) return -1;
+  return group_ws_floats(edge_lmax, channels, edges) * (int64_t)sizeof(float);
+}
+
 int ictc_tp_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
-                const float* grad, int64_t E, float* dx, float* dsh, float* dg, void* stream) {
+                const float* grad, int64_t E, float* dx, float* dsh, float* dg, void* workspace,
+                int64_t workspace_bytes, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (E < 0) return fail(ICTC_ERR_ARGUMENT, "edges must be nonnegative");
   if (E == 0 || (!dx && !dsh && !dg)) return ICTC_OK;
   if (!x || !sh || !g || !grad) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_bwd: null operand");
+  if (int rc = check_ws(dsh, (const float*)workspace, workspace_bytes, le, C, E, "ictc_tp_bwd")) return rc;
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(route_edge_bwd(s, operands(x, sh, g, w, nullptr, E, E, C), grad, dx, dsh, dg,
+  return check_hip(route_edge_bwd(s, operands(x, sh, g, w, nullptr, E, E, C), grad, dx, dsh, dg, (float*)workspace,
                                          (hipStream_t)stream),
                    "ictc_tp_bwd launch");
 }
@@ -307,7 +348,8 @@ int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh,
 int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
                  const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
                  const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
-                 const int32_t* dst_rows, const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dg, void* stream) {
+                 const int32_t* dst_rows, const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dg,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
   if (E == 0 && dx) {
@@ -319,10 +361,71 @@ int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh,
   if (N == 0 && E == 0) return ICTC_OK;
   if (!x || !sh || !g || !src || !dst || !grad || !dptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: null operand");
   if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: dfeatures needs the source CSR");
+  if (int rc = check_ws(dsh, (const float*)workspace, workspace_bytes, le, C, E, "ictc_msg_bwd")) return rc;
   const ictc::TpShape s{li, le, lo, C};
   return check_hip(route_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder, dst_rows},
-                                        ictc::Csr{sptr, sorder, src_rows}, grad, dx, dsh, dg, (hipStream_t)stream),
+                                        ictc::Csr{sptr, sorder, src_rows}, grad, dx, dsh, dg, (float*)workspace,
+                                        (hipStream_t)stream),
                    "ictc_msg_bwd launch");
+}
+
+int ictc_tp_second(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                   const float* grad, const float* tx, const float* tsh, const float* tg, int64_t E, float* dgrad,
+                   float* dx, float* dsh, float* dg, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (E < 0) return fail(ICTC_ERR_ARGUMENT, "edges must be nonnegative");
+  if (E == 0 || (!dgrad && !dx && !dsh && !dg)) return ICTC_OK;
+  if (!x || !sh || !g) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_second: null operand");
+  if ((dx || dsh || dg) && !grad) return fail(ICTC_ERR_ARGUMENT, "ictc_tp_second: dfeatures/dharmonics/dgates need grad");
+  if (int rc = check_ws(dsh, (const float*)workspace, workspace_bytes, le, C, E, "ictc_tp_second")) return rc;
+  const ictc::TpShape s{li, le, lo, C};
+  const ictc::Tangents t{tx, tsh, tg};
+  return check_hip(route_edge_second(s, operands(x, sh, g, w, nullptr, E, E, C), t, grad, dgrad, dx, dsh, dg,
+                                     (float*)workspace, (hipStream_t)stream),
+                   "ictc_tp_second launch");
+}
+
+int ictc_msg_second(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                    const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
+                    const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
+                    const int32_t* dst_rows, const int32_t* src_rows, const float* grad, const float* tx,
+                    const float* tsh, const float* tg, float* dgrad, float* dx, float* dsh, float* dg, void* workspace,
+                    int64_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  hipStream_t st = (hipStream_t)stream;
+  if (E == 0) {  // node outputs are zero; there are no edge outputs
+    int P = 0, NO = 0;
+    tp_counts(li, le, lo, &P, &NO);
+    const int64_t sizes[2] = {N * (int64_t)(C * NO), N * (int64_t)(C * (li + 1) * (li + 1))};
+    float* outs[2] = {dgrad, dx};
+    for (int k = 0; k < 2; ++k) {
+      if (!outs[k] || sizes[k] == 0) continue;
+      hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((sizes[k] + 255) / 256)), dim3(256), 0, st, outs[k],
+                         sizes[k]);
+      if (int rc = check_hip(hipGetLastError(), "ictc_msg_second fill")) return rc;
+    }
+    return ICTC_OK;
+  }
+  if (N == 0 || (!dgrad && !dx && !dsh && !dg)) return ICTC_OK;
+  if (!x || !sh || !g || !src || !dst || !dptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_second: null operand");
+  if ((dx || dsh || dg) && !grad)
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_second: dfeatures/dharmonics/dgates need grad");
+  if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_second: dfeatures needs the source CSR");
+  if (int rc = check_ws(dsh, (const float*)workspace, workspace_bytes, le, C, E, "ictc_msg_second")) return rc;
+  const ictc::TpShape s{li, le, lo, C};
+  const ictc::Tangents t{tx, tsh, tg};
+  const ictc::Operands a = operands(x, sh, g, w, mask, N, E, C);
+  if (dgrad || dsh || dg) {
+    if (int rc = check_hip(ictc::launch_msg_second_rcv(s, a, t, src, ictc::Csr{dptr, dorder, dst_rows}, grad, dgrad,
+                                                       dsh, dg, (float*)workspace, st),
+                           "ictc_msg_second launch"))
+      return rc;
+  }
+  if (dx)
+    return check_hip(ictc::launch_msg_second_src(s, a, t, dst, ictc::Csr{sptr, sorder, src_rows}, grad, dx, st),
+                     "ictc_msg_second launch");
+  return ICTC_OK;
 }
 
 int ictc_sh_fwd(const float* n, int64_t E, int lmax, float* out, void* stream) {

@@ -100,14 +100,12 @@ __device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c
 
 // ---------------------------------------------------------------------------
 // Launch geometry.  A channel group is 64 consecutive channels, one per lane
-// (c = 64 * group + lane); G = ceil(C / 64) groups, C <= 256.
-//   * Kernels without a cross-channel reduction run 4 rows per 256-thread
-//     block and take the group from blockIdx.y.
-//   * Kernels that reduce over channels (the harmonic gradient) run, for
-//     G == 1, 4 rows per block as above; for G > 1 one row per block of G
-//     waves (wave = group), combining the groups' partial sums through LDS
-//     in group order.  Every wave of such a block walks the same row, so the
-//     block barriers are uniform.
+// (c = 64 * group + lane); G = ceil(C / 64) groups, C <= 256.  Every kernel
+// runs 4 rows per 256-thread block and takes the group from blockIdx.y.
+// Kernels that reduce over channels (the harmonic gradient) write group 0's
+// partial sum to the output and group g's to slab g-1 of a workspace; a
+// second pass (launch_group_sum) adds the slabs in group order, so the result
+// is deterministic and no block ever waits on another wave.
 // Register budgets: the minimum waves per SIMD requested from the compiler
 // drop for the wide degree triples so that their accumulators stay in VGPRs.
 // ---------------------------------------------------------------------------
@@ -116,7 +114,7 @@ constexpr int kMaxGroups = 4;
 // Minimum waves per SIMD requested for each (kernel, degree triple): the
 // highest of 4, 3, 2, 1 at which the kernel compiles without register spills,
 // found by tune_occupancy.py and recorded in ictc_occupancy.h.
-enum KernelKind { kEdgeFwd, kEdgeBwd, kMsgFwd, kMsgBwdEdge, kMsgBwdX };
+enum KernelKind { kEdgeFwd, kEdgeBwd, kMsgFwd, kMsgBwdEdge, kMsgBwdX, kEdgeSecond, kMsgFwd2, kMsgBwdEdge2, kMsgBwdX2 };
 template <int K, int LI, int LE, int LO>
 struct Occupancy {
 #ifdef ICTC_OCCUPANCY_PROBE
@@ -155,14 +153,10 @@ __device__ __forceinline__ RowGroup row_group_y_xcd() {
   return {xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + wave_id(), (int)blockIdx.y};
 }
 
-__device__ __forceinline__ RowGroup row_group_reduce(int G) {
-  if (G == 1) return {(int64_t)blockIdx.x * kWavesPerBlock + wave_id(), 0};
-  return {(int64_t)blockIdx.x, wave_id()};
-}
-
-__device__ __forceinline__ RowGroup row_group_reduce_xcd(int G) {
-  if (G == 1) return {xcd_block(blockIdx.x, gridDim.x) * kWavesPerBlock + wave_id(), 0};
-  return {xcd_block(blockIdx.x, gridDim.x), wave_id()};
+// Harmonic-gradient target of a channel group: group 0 writes the output,
+// group g > 0 slab g-1 of the workspace ([G-1][rows][NY]).
+__device__ __forceinline__ float* group_target(float* dsh, float* part, int group, int64_t rows, int ny) {
+  return (dsh && group > 0) ? part + (int64_t)(group - 1) * rows * ny : dsh;
 }
 
 // ---------------------------------------------------------------------------
@@ -189,9 +183,8 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeFwd, T::LI, T::LE, T::LO>::
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::value)) void edge_bwd_kernel(
     Operands a, const float* __restrict__ grad, float* __restrict__ dx, float* __restrict__ dsh,
-    float* __restrict__ dgates, int G) {
-  extern __shared__ float red[];  // [G][NY] when G > 1
-  const RowGroup rg = row_group_reduce(G);
+    float* __restrict__ dsh_part, float* __restrict__ dgates) {
+  const RowGroup rg = row_group_y();
   const int64_t e = rg.row;
   if (e >= a.rows) return;
   const int C = a.channels, c = 64 * rg.group + lane_id();
@@ -224,6 +217,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
     }
   }
   if (!dsh) return;
+  float* out = group_target(dsh, dsh_part, rg.group, a.rows, T::NY);
   // lane j (< NY) ends up holding this group's sum of component j
   float mine = 0.f;
 #pragma unroll
@@ -231,17 +225,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
     const float s = wave_sum(dyv[j]);
     mine = lane_id() == j ? s : mine;
   }
-  if (G == 1) {
-    if (lane_id() < T::NY) dsh[e * T::NY + lane_id()] = mine;
-    return;
-  }
-  if (lane_id() < T::NY) red[rg.group * T::NY + lane_id()] = mine;
-  __syncthreads();
-  if (rg.group == 0 && lane_id() < T::NY) {
-    float s = red[lane_id()];
-    for (int g = 1; g < G; ++g) s += red[g * T::NY + lane_id()];
-    dsh[e * T::NY + lane_id()] = s;
-  }
+  if (lane_id() < T::NY) out[e * T::NY + lane_id()] = mine;
 }
 
 // ---------------------------------------------------------------------------
@@ -345,15 +329,15 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO>::value)) void msg_bwd_edge_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad, float* __restrict__ dsh,
-    float* __restrict__ dgates, int G) {
-  extern __shared__ float red[];  // [G][64][NY] when G > 1 and dsh
-  const RowGroup rg = row_group_reduce_xcd(G);
+    float* __restrict__ dsh_part, float* __restrict__ dgates) {
+  const RowGroup rg = row_group_y_xcd();
   if (rg.row > a.rows) return;
   const int64_t n = visit_row(csr, rg.row, a.rows);
   if (n < 0) return;
   const bool tail = n == a.rows;
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
+  float* dsh_g = group_target(dsh, dsh_part, rg.group, a.edges, T::NY);
   float go[T::NO];
   if (active && !tail) load_row<T::NO>(grad + n * (int64_t)(T::NO * C), C, c, go);
   else {
@@ -403,29 +387,10 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
         }
       }
     }
-    if (!dsh) continue;
-    const bool mine = lane_id() < count;
-    if (G == 1) {
-      if (mine) {
+    if (dsh && lane_id() < count) {
 #pragma unroll
-        for (int j = 0; j < T::NY; ++j) dsh[(int64_t)ch.e * T::NY + j] = acc[j];
-      }
-      continue;
+      for (int j = 0; j < T::NY; ++j) dsh_g[(int64_t)ch.e * T::NY + j] = acc[j];
     }
-    float* r = red + (rg.group * kWave + lane_id()) * T::NY;
-#pragma unroll
-    for (int j = 0; j < T::NY; ++j) r[j] = acc[j];
-    __syncthreads();
-    if (rg.group == 0 && mine) {
-      for (int g = 1; g < G; ++g) {
-        const float* q = red + (g * kWave + lane_id()) * T::NY;
-#pragma unroll
-        for (int j = 0; j < T::NY; ++j) acc[j] += q[j];
-      }
-#pragma unroll
-      for (int j = 0; j < T::NY; ++j) dsh[(int64_t)ch.e * T::NY + j] = acc[j];
-    }
-    __syncthreads();
   }
 }
 

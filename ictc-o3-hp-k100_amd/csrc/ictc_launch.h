@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "ictc_kernels.h"
+#include "ictc_second.h"
 
 namespace ictc {
 
@@ -18,11 +19,22 @@ inline int channel_groups(int C) { return C < 1 || C > 64 * kMaxGroups ? 0 : (C 
 
 hipError_t launch_edge_fwd(const TpShape& s, const Operands& a, float* out, hipStream_t st);
 hipError_t launch_edge_bwd(const TpShape& s, const Operands& a, const float* grad, float* dx, float* dsh, float* dg,
-                           hipStream_t st);
+                           float* ws, hipStream_t st);
 hipError_t launch_msg_fwd(const TpShape& s, const Operands& a, const int64_t* src, Csr dcsr, float* out,
                           hipStream_t st);
 hipError_t launch_msg_bwd(const TpShape& s, const Operands& a, const int64_t* src, const int64_t* dst, Csr dcsr,
-                          Csr scsr, const float* grad, float* dx, float* dsh, float* dg, hipStream_t st);
+                          Csr scsr, const float* grad, float* dx, float* dsh, float* dg, float* ws, hipStream_t st);
+
+hipError_t launch_edge_second(const TpShape& s, const Operands& a, const Tangents& t, const float* grad, float* dgrad,
+                              float* dx, float* dsh, float* dg, float* ws, hipStream_t st);
+hipError_t launch_msg_second_rcv(const TpShape& s, const Operands& a, const Tangents& t, const int64_t* src, Csr dcsr,
+                                 const float* grad, float* dgrad, float* dsh, float* dg, float* ws, hipStream_t st);
+hipError_t launch_msg_second_src(const TpShape& s, const Operands& a, const Tangents& t, const int64_t* dst, Csr scsr,
+                                 const float* grad, float* dx, hipStream_t st);
+
+// out[i] += sum_{s < slabs} part[s * n + i], slabs added in order (deterministic
+// combination of the channel groups' harmonic gradients).  No-op for slabs == 0.
+hipError_t launch_group_sum(float* out, const float* part, int64_t n, int slabs, hipStream_t st);
 
 // Dispatch a runtime (LI, LE, LO) onto a functor templated on Tp<...>.
 template <class F>

@@ -10,21 +10,18 @@ struct MsgBwd {
   const int64_t *src, *dst;
   Csr dcsr, scsr;
   const float* grad;
-  float *dx, *dsh, *dg;
+  float *dx, *dsh, *dg, *ws;
   hipStream_t st;
   template <class T>
   hipError_t run() {
     const int G = channel_groups(a.channels);
     if (dsh || dg) {
       // rows + 1 row slots: the last one zero-fills the out-of-range tail segment.
-      if (G == 1)
-        hipLaunchKernelGGL((msg_bwd_edge_kernel<T>), dim3(blocks_for(a.rows + 1)), dim3(kBlock), 0, st, a, src,
-                           dcsr, grad, dsh, dg, G);
-      else
-        hipLaunchKernelGGL((msg_bwd_edge_kernel<T>), dim3((unsigned)(a.rows + 1)), dim3(kWave * G),
-                           dsh ? G * kWave * T::NY * sizeof(float) : 0, st, a, src, dcsr, grad, dsh, dg, G);
+      hipLaunchKernelGGL((msg_bwd_edge_kernel<T>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock), 0, st, a, src,
+                         dcsr, grad, dsh, ws, dg);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
+      if (dsh && (err = launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st)) != hipSuccess) return err;
     }
     if (dx) {
       hipLaunchKernelGGL((msg_bwd_x_kernel<T>), dim3(blocks_for(a.rows), G), dim3(kBlock), 0, st, a, dst, scsr, grad,
@@ -37,8 +34,8 @@ struct MsgBwd {
 }  // namespace
 
 hipError_t launch_msg_bwd(const TpShape& s, const Operands& a, const int64_t* src, const int64_t* dst, Csr dcsr,
-                          Csr scsr, const float* grad, float* dx, float* dsh, float* dg, hipStream_t st) {
-  return dispatch_tp(s, MsgBwd{a, src, dst, dcsr, scsr, grad, dx, dsh, dg, st});
+                          Csr scsr, const float* grad, float* dx, float* dsh, float* dg, float* ws, hipStream_t st) {
+  return dispatch_tp(s, MsgBwd{a, src, dst, dcsr, scsr, grad, dx, dsh, dg, ws, st});
 }
 
 }  // namespace ictc

@@ -18,18 +18,16 @@ struct EdgeFwd {
 struct EdgeBwd {
   const Operands& a;
   const float* grad;
-  float *dx, *dsh, *dg;
+  float *dx, *dsh, *dg, *ws;
   hipStream_t st;
   template <class T>
   hipError_t run() {
     const int G = channel_groups(a.channels);
-    if (G == 1)
-      hipLaunchKernelGGL((edge_bwd_kernel<T>), dim3(blocks_for(a.rows)), dim3(kBlock), 0, st, a, grad, dx, dsh, dg,
-                         G);
-    else
-      hipLaunchKernelGGL((edge_bwd_kernel<T>), dim3((unsigned)a.rows), dim3(kWave * G), G * T::NY * sizeof(float),
-                         st, a, grad, dx, dsh, dg, G);
-    return hipGetLastError();
+    hipLaunchKernelGGL((edge_bwd_kernel<T>), dim3(blocks_for(a.rows), G), dim3(kBlock), 0, st, a, grad, dx, dsh, ws,
+                       dg);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || !dsh) return err;
+    return launch_group_sum(dsh, ws, a.rows * T::NY, G - 1, st);
   }
 };
 }  // namespace
@@ -39,8 +37,8 @@ hipError_t launch_edge_fwd(const TpShape& s, const Operands& a, float* out, hipS
 }
 
 hipError_t launch_edge_bwd(const TpShape& s, const Operands& a, const float* grad, float* dx, float* dsh, float* dg,
-                           hipStream_t st) {
-  return dispatch_tp(s, EdgeBwd{a, grad, dx, dsh, dg, st});
+                           float* ws, hipStream_t st) {
+  return dispatch_tp(s, EdgeBwd{a, grad, dx, dsh, dg, ws, st});
 }
 
 }  // namespace ictc

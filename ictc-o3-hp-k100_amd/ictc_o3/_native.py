@@ -26,14 +26,18 @@ _SIGNATURES = {
     "ictc_last_error": (ctypes.c_char_p, []),
     "ictc_tp_shape": (_i, [_i, _i, _i, ctypes.POINTER(_i), ctypes.POINTER(_i)]),
     "ictc_tp_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _i64, _p, _p]),
-    "ictc_tp_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p]),
+    "ictc_tp_workspace_bytes": (_i64, [_i, _i, _i64]),
+    "ictc_tp_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _i64, _p]),
+    "ictc_tp_second": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p]),
+    "ictc_msg_second": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p,
+                             _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_csr_workspace_bytes": (_i64, [_i64, _i64]),
     "ictc_csr_build": (_i, [_p, _i64, _i64, _p, _p, _p, _i64, _p]),
     "ictc_morton_workspace_bytes": (_i64, [_i64]),
     "ictc_morton_order": (_i, [_p, _i64, ctypes.c_float, _p, _p, _i64, _p]),
     "ictc_msg_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
     "ictc_msg_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
-                          _p, _p, _p, _p, _p, _p]),
+                          _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_sh_fwd": (_i, [_p, _i64, _i, _p, _p]),
     "ictc_sh_bwd": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_jvp": (_i, [_p, _p, _i64, _i, _p, _p]),

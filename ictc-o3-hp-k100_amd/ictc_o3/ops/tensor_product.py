@@ -82,14 +82,54 @@ def _edge_fwd_raw(spec, x, sh, g):
     return out
 
 
+def _group_ws(spec, E, dsh):
+    """Workspace of the channel groups' partial harmonic gradients (None when not needed)."""
+    if dsh is None:
+        return None, 0
+    nbytes = int(nat.lib().ictc_tp_workspace_bytes(spec.le, spec.channels, E))
+    if nbytes <= 0:
+        return None, 0
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=dsh.device), nbytes
+
+
 def _edge_bwd_raw(spec, x, sh, g, go, need):
     E = x.shape[0]
     dx = torch.empty_like(x) if need[0] else None
     dsh = torch.empty_like(sh) if need[1] else None
     dg = torch.empty_like(g) if need[2] else None
+    ws, ws_bytes = _group_ws(spec, E, dsh)
     nat.call("ictc_tp_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
-             _w(spec), nat.ptr(go), E, nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.stream_of(x))
+             _w(spec), nat.ptr(go), E, nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.ptr(ws), ws_bytes,
+             nat.stream_of(x))
     return dx, dsh, dg
+
+
+def _tangents(tx, tsh, tg):
+    return tuple(None if t is None else _c(t) for t in (tx, tsh, tg))
+
+
+def _second_outputs(need, tx, tsh, tg):
+    """Which of (dx, dsh, dg, dgo) have a contributing tangent (the others are None)."""
+    nx, nsh, ng, ngo = need
+    return (nx and (tsh is not None or tg is not None), nsh and (tx is not None or tg is not None),
+            ng and (tx is not None or tsh is not None), ngo and any(t is not None for t in (tx, tsh, tg)))
+
+
+def _edge_second_raw(spec, x, sh, g, go, tx, tsh, tg, need):
+    """Fused mixed second derivative of the edge TP adjoint (one kernel); returns (dx, dsh, dg, dgo)."""
+    E = x.shape[0]
+    tx, tsh, tg = _tangents(tx, tsh, tg)
+    wx, wsh, wg, wgo = _second_outputs(need, tx, tsh, tg)
+    dx = torch.empty_like(x) if wx else None
+    dsh = torch.empty_like(sh) if wsh else None
+    dg = torch.empty_like(g) if wg else None
+    dgo = torch.empty_like(go) if wgo else None
+    if wx or wsh or wg or wgo:
+        ws, ws_bytes = _group_ws(spec, E, dsh)
+        nat.call("ictc_tp_second", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+                 _w(spec), nat.ptr(go), nat.ptr(tx), nat.ptr(tsh), nat.ptr(tg), E, nat.ptr(dgo), nat.ptr(dx),
+                 nat.ptr(dsh), nat.ptr(dg), nat.ptr(ws), ws_bytes, nat.stream_of(x))
+    return dx, dsh, dg, dgo
 
 
 class EdgeTP(torch.autograd.Function):
@@ -135,6 +175,11 @@ class EdgeTPAdjoint(torch.autograd.Function):
         x, sh, g, go = ctx.saved_tensors
         spec = ctx.spec
         nx, nsh, ng, ngo = required_gradients((x, sh, g, go), ctx.needs_input_grad[:4])
+        if not torch.is_grad_enabled():
+            # the mixed second derivative itself is the last order asked for: one fused kernel
+            dx, dsh, dg, dgo = _edge_second_raw(spec, x, sh, g, go, hx, hsh, hg, (nx, nsh, ng, ngo))
+            return dx, dsh, dg, dgo, None, None
+        # higher orders: compose differentiable first-order operators (multilinearity)
         dx = dsh = dg = dgo = None
         if ngo:
             if hx is not None:
@@ -238,13 +283,35 @@ def _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need):
     dsh = torch.empty_like(sh) if need[1] else None
     dg = torch.empty_like(g) if need[2] else None
     sp = topo.by_src if need[0] else None
+    ws, ws_bytes = _group_ws(spec, E, dsh)
     nat.call("ictc_msg_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
              nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
              nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
              nat.ptr(topo.src_rows), nat.ptr(go),
-             nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.stream_of(x))
+             nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.ptr(ws), ws_bytes, nat.stream_of(x))
     return dx, dsh, dg
+
+
+def _msg_second_raw(spec, topo, x, sh, g, mask, go, tx, tsh, tg, need):
+    """Fused mixed second derivative of the message adjoint; returns (dx, dsh, dg, dgo)."""
+    N, E = x.shape[0], sh.shape[0]
+    tx, tsh, tg = _tangents(tx, tsh, tg)
+    wx, wsh, wg, wgo = _second_outputs(need, tx, tsh, tg)
+    dx = torch.empty_like(x) if wx else None
+    dsh = torch.empty_like(sh) if wsh else None
+    dg = torch.empty_like(g) if wg else None
+    dgo = torch.empty_like(go) if wgo else None
+    if wx or wsh or wg or wgo:
+        sp = topo.by_src if wx else None
+        ws, ws_bytes = _group_ws(spec, E, dsh)
+        nat.call("ictc_msg_second", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+                 _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
+                 nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
+                 nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
+                 nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(tx), nat.ptr(tsh), nat.ptr(tg), nat.ptr(dgo),
+                 nat.ptr(dx), nat.ptr(dsh), nat.ptr(dg), nat.ptr(ws), ws_bytes, nat.stream_of(x))
+    return dx, dsh, dg, dgo
 
 
 class Message(torch.autograd.Function):
@@ -290,6 +357,11 @@ class MessageAdjoint(torch.autograd.Function):
         x, sh, g, go = ctx.saved_tensors
         spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
         nx, nsh, ng, ngo = required_gradients((x, sh, g, go), ctx.needs_input_grad[:4])
+        if not torch.is_grad_enabled():
+            # the mixed second derivative itself is the last order asked for: fused kernels
+            dx, dsh, dg, dgo = _msg_second_raw(spec, topo, x, sh, g, mask, go, hx, hsh, hg, (nx, nsh, ng, ngo))
+            return dx, dsh, dg, dgo, None, None, None, None
+        # higher orders: compose differentiable first-order operators (multilinearity)
         dx = dsh = dg = dgo = None
         if ngo:
             if hx is not None:

@@ -268,7 +268,9 @@ class PureCartesianICTDFix(nn.Module):
         N = pos.shape[0]
         species = self.atomic_number_to_index[A.long()]
         if topology is None:
-            topology = tpo.Topology(edge_src, edge_dst, N, positions=pos)
+            # spatial row order for one periodic system; batched graphs keep index order (their
+            # atoms are contiguous per graph, and the graphs' coordinates overlap)
+            topology = tpo.Topology(edge_src, edge_dst, N, positions=pos if cell.shape[0] == 1 else None)
         shifts = edge_shifts.to(pos.dtype)
         if cell.shape[0] == 1:
             shift_vec = shifts @ cell[0]

@@ -55,11 +55,35 @@ int ictc_tp_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
  * (operators.py:129-158 -> generated_cartesian_message.py:386-407).  Any of
  * dfeatures [E, C*(LI+1)^2], dharmonics [E,(LE+1)^2], dgates [E,P*C] may be
  * NULL to skip that role (required_gradients pruning,
- * autograd/adjoint_requirements.py:13-27).  Outputs are overwritten.          */
+ * autograd/adjoint_requirements.py:13-27).  Outputs are overwritten.
+ * dharmonics with more than 64 channels needs a workspace of
+ * ictc_tp_workspace_bytes(edge_lmax, channels, edges) bytes (the channel
+ * groups' partial sums, added in group order; NULL/0 when not needed).       */
+int64_t ictc_tp_workspace_bytes(int edge_lmax, int channels, int64_t edges);
 int ictc_tp_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                 const float* features, const float* harmonics, const float* gates,
                 const float* weight, const float* grad, int64_t edges,
-                float* dfeatures, float* dharmonics, float* dgates, void* stream);
+                float* dfeatures, float* dharmonics, float* dgates, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* Mixed second derivative of ictc_tp_bwd: the derivative of the first
+ * adjoint (features, harmonics, gates; grad) -> (dfeatures, dharmonics,
+ * dgates) along tangents tfeatures / tharmonics / tgates of its three outputs
+ * (NULL = zero tangent).  Replaces generated_second
+ * (backends/k100/generated_message_second.py:178,330-368, edge mode) and the
+ * _EdgeAdjoint.backward composition (operators.py:72-103):
+ *   dgrad      = fwd(tf, h, g) + fwd(f, th, g) + fwd(f, h, tg)   [E, C*NO]
+ *   dfeatures  = dx(th, g, grad) + dx(h, tg, grad)               [E, C*(LI+1)^2]
+ *   dharmonics = dy(tf, g, grad) + dy(f, tg, grad)               [E, (LE+1)^2]
+ *   dgates     = dg(tf, h, grad) + dg(f, th, grad)               [E, P*C]
+ * NULL outputs are skipped; non-NULL outputs are fully overwritten.
+ * workspace as in ictc_tp_bwd.                                               */
+int ictc_tp_second(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                   const float* features, const float* harmonics, const float* gates,
+                   const float* weight, const float* grad, const float* tfeatures,
+                   const float* tharmonics, const float* tgates, int64_t edges,
+                   float* dgrad, float* dfeatures, float* dharmonics, float* dgates, void* workspace,
+                   int64_t workspace_bytes, void* stream);
 
 /* ---- Receiver / source sorted CSR ---------------------------------------
  * Replaces topology() (backends/k100/generated_csr_forward.py:22-31: bincount,
@@ -109,14 +133,40 @@ int ictc_msg_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
  * dharmonics and dgates use the receiver-sorted CSR, visiting receivers in
  * dst_rows order; dfeatures visits sources in src_rows order (both as
  * dst_rows of ictc_msg_fwd; NULL = index order).  NULL outputs are skipped;
- * non-NULL outputs are fully overwritten.                                     */
+ * non-NULL outputs are fully overwritten.  dharmonics with more than 64
+ * channels needs ictc_tp_workspace_bytes(edge_lmax, channels, edges) bytes of
+ * workspace.                                                                  */
 int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                  const float* features, const float* harmonics, const float* gates,
                  const float* weight, const float* mask, const int64_t* src, const int64_t* dst,
                  int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
                  const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
                  const int32_t* src_rows, const float* grad,
-                 float* dfeatures, float* dharmonics, float* dgates, void* stream);
+                 float* dfeatures, float* dharmonics, float* dgates, void* workspace,
+                 int64_t workspace_bytes, void* stream);
+
+/* Mixed second derivative of ictc_msg_bwd along tangents of its outputs
+ * (tfeatures [nodes, C*(LI+1)^2], tharmonics [E, NY], tgates [E, P*C]; NULL =
+ * zero tangent); replaces generated_second (graph mode,
+ * generated_message_second.py:78-204,232-310) behind
+ * rematerialized_message._Adjoint.backward (ops/rematerialized_message.py:146-163)
+ * and the formula of ops/fused_message.py:677-729 (_second_raw):
+ *   dgrad[n]   = sum_{e->n} mask (fwd(tf[src], h, g) + fwd(f[src], th, g) + fwd(f[src], h, tg))
+ *   dfeatures[s] = sum_{e: src=s} mask (dx(th, g, grad[dst]) + dx(h, tg, grad[dst]))
+ *   dharmonics[e] = mask (dy(tf[src], g, grad[dst]) + dy(f[src], tg, grad[dst]))
+ *   dgates[e]  = mask (dg(tf[src], h, grad[dst]) + dg(f[src], th, grad[dst]))
+ * CSR arguments, row orders and output conventions as in ictc_msg_bwd
+ * (dgrad, dharmonics, dgates: receiver CSR; dfeatures: source CSR; workspace
+ * for dharmonics beyond 64 channels).                                         */
+int ictc_msg_second(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                    const float* features, const float* harmonics, const float* gates,
+                    const float* weight, const float* mask, const int64_t* src, const int64_t* dst,
+                    int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                    const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
+                    const int32_t* src_rows, const float* grad, const float* tfeatures,
+                    const float* tharmonics, const float* tgates, float* dgrad, float* dfeatures,
+                    float* dharmonics, float* dgates, void* workspace, int64_t workspace_bytes,
+                    void* stream);
 
 /* ---- Direction harmonics --------------------------------------------------
  * Replaces direction_harmonics (operators.py:471-490 ->

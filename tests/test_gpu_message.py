@@ -52,8 +52,12 @@ def test_message_forward_backward(device, N, E, C, li, le, lo, sort, mask):
         assert rel_err(a.grad, b.grad) < TOL
 
 
-@pytest.mark.parametrize("C,li,le,lo", [(64, 2, 2, 2), (128, 2, 3, 3)])
-def test_message_mixed_second_derivatives(device, C, li, le, lo):
+@pytest.mark.parametrize("C,li,le,lo,which,create", [
+    (64, 2, 2, 2, (0, 1, 2), False), (128, 2, 3, 3, (0, 1, 2), False), (64, 2, 2, 2, (0, 1, 2), True),
+    (128, 2, 3, 3, (0,), False), (64, 2, 2, 2, (1, 2), False), (33, 0, 2, 2, (2,), False), (64, 1, 2, 2, (1,), True)])
+def test_message_mixed_second_derivatives(device, C, li, le, lo, which, create):
+    """Fused (create=False) and composed (create=True) mixed second derivatives vs float64 autograd;
+    ``which`` selects the first-order gradients the objective uses (the rest give absent tangents)."""
     from ictc_o3 import PackedGraphMessage
     N, E = 24, 200
     op = PackedGraphMessage.create(channels=C, input_lmax=li, edge_lmax=le, output_lmax=lo, device=device)
@@ -66,8 +70,8 @@ def test_message_mixed_second_derivatives(device, C, li, le, lo):
         xs = [t.clone().requires_grad_(True) for t in tensors]
         gov = gov.clone().requires_grad_(True)
         grads = torch.autograd.grad(fn(*xs), xs, gov, create_graph=True)
-        s = sum((gr * vv.to(gr)).sum() for gr, vv in zip(grads, v))
-        return torch.autograd.grad(s, xs + [gov])
+        s = sum((grads[k] * v[k].to(grads[k])).sum() for k in which)
+        return torch.autograd.grad(s, xs + [gov], allow_unused=True, create_graph=create)
 
     ref = run((f64, sh64, g64), go64,
               lambda a, b, c: orc.message_packed(a, b, c, src, dst, m64, li, le, lo, C))
@@ -75,7 +79,46 @@ def test_message_mixed_second_derivatives(device, C, li, le, lo):
     got = run([t.float().to(device) for t in (f64, sh64, g64)], go64.float().to(device),
               lambda a, b, c: op(a, b, c, s, d, m))
     for name, a, b in zip(("dx", "dsh", "dg", "dgo"), got, ref):
-        assert rel_err(a, b) < TOL, name
+        if b is None or not b.abs().max() > 0:
+            assert a is None or torch.count_nonzero(a) == 0, name
+        else:
+            assert rel_err(a, b) < TOL, name
+
+
+def test_message_second_raw_abi(device):
+    """ictc_msg_second directly: no edges zero-fills the node outputs; out-of-range ids and masks drop edges."""
+    from ictc_o3 import PackedGraphMessage
+    from ictc_o3.ops import tensor_product as tpo
+    op = PackedGraphMessage.create(channels=32, input_lmax=2, edge_lmax=2, device=device)
+    spec = op.edge._prepare()
+    N = 9
+    x = torch.randn(N, 32 * 9, device=device)
+    e0 = torch.zeros(0, dtype=torch.int64, device=device)
+    topo = tpo.Topology(e0, e0, N)
+    go = torch.randn(N, op.output_width, device=device)
+    tx = torch.randn_like(x)
+    dx, dsh, dg, dgo = tpo._msg_second_raw(spec, topo, x, torch.zeros(0, 9, device=device),
+                                           torch.zeros(0, op.gate_width, device=device), None, go, tx, None, None,
+                                           (True, True, True, True))
+    assert dx is None and dgo is not None and torch.count_nonzero(dgo) == 0
+    # out-of-range ids contribute nothing: same as dropping those edges
+    f64, sh64, g64, src, dst, m64 = _graph(N, 120, 32, 2, 2, 2, 31, mask=True)
+    bad_src, bad_dst = src.clone(), dst.clone()
+    bad_src[::5] = N + 2
+    bad_dst[2::7] = -3
+    keep = (bad_src < N) & (bad_dst >= 0)
+    args = [t.float().to(device) for t in (f64, sh64, g64)]
+    tans = [torch.randn_like(t) for t in args]
+    m = m64.float().to(device)
+    full = tpo._msg_second_raw(spec, tpo.Topology(bad_src.to(device), bad_dst.to(device), N), *args, m, go, *tans,
+                               (True, True, True, True))
+    k = keep.to(device)
+    part = tpo._msg_second_raw(spec, tpo.Topology(src[keep].to(device), dst[keep].to(device), N), args[0],
+                               args[1][k], args[2][k], m[k], go, tans[0], tans[1][k], tans[2][k],
+                               (True, True, True, True))
+    assert rel_err(full[0], part[0]) < TOL and rel_err(full[3], part[3]) < TOL
+    assert rel_err(full[1][k], part[1]) < TOL and rel_err(full[2][k], part[2]) < TOL
+    assert torch.count_nonzero(full[1][~k]) == 0 and torch.count_nonzero(full[2][~k]) == 0
 
 
 def test_message_deterministic_bitwise(device):
