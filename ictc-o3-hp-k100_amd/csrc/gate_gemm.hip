@@ -151,7 +151,95 @@ __global__ __launch_bounds__(256, 2) void gate_gemm_nt_kernel(const float* __res
   }
 }
 
+// ---- adjoint: dh[E, 64] = dg[E, M] . W (W [M, 64]) ------------------------
+// Transposed product D[k][e] = sum_m W[m][k] dg[e][m].  Wave s of a block owns
+// the reduction slice m in [64 s, 64 s + 64), holds W's slice pre-split as the
+// A operand (4 row blocks x 2 k-steps x 3 parts) and reads its 16 x 64 block
+// of dg per 16-edge tile (B operand: lane l reads 32 contiguous bytes of edge
+// l % 16), so dg streams from HBM exactly once.  The slices' partial sums meet
+// in LDS and are added in slice order (deterministic); the LDS tile is double
+// buffered so one barrier per tile suffices.  The next tile's dg block is
+// loaded while the current one is multiplied.
+constexpr int kMaxSlices = 12;  // up to 768 gates: 12 waves per block leave 170 VGPRs per lane
+constexpr int kRedRow = 68;  // LDS row pitch (floats) of a partial 16 x 64 tile
+
+__device__ __forceinline__ void load_dg(const float* __restrict__ dg, int64_t e, int64_t E, int M, int s, float* v) {
+  const int g = (threadIdx.x & 63) >> 4;
+  if (e < E) {
+    load8(dg + e * M + 64 * s + 8 * g, v);
+    load8(dg + e * M + 64 * s + 32 + 8 * g, v + 8);
+  } else {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) v[q] = 0.f;
+  }
+}
+
+__global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const float* __restrict__ dg, int64_t E,
+                                                                       const float* __restrict__ W, int M,
+                                                                       float* __restrict__ dh) {
+  extern __shared__ float red[];  // [2][S][16][kRedRow]
+  const int l = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
+  const int i = l & 15, g = l >> 4;
+  // A operand: row k = 16 kb + i, reduction index m = 64 s + 32 ks + 8 g + e  ->  W[m][k]
+  Split A[4][2];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = W[(int64_t)(64 * s + 32 * ks + 8 * g + e) * kK + 16 * kb + i];
+      A[kb][ks] = split8(v);
+    }
+  const int64_t tiles = (E + 15) / 16;
+  float next[16];
+  int64_t t = blockIdx.x;
+  if (t < tiles) load_dg(dg, 16 * t + i, E, M, s, next);
+  for (int buf = 0; t < tiles; t += gridDim.x, buf ^= 1) {
+    float cur[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) cur[q] = next[q];
+    if (t + gridDim.x < tiles) load_dg(dg, 16 * (t + gridDim.x) + i, E, M, s, next);
+    const Split B0 = split8(cur), B1 = split8(cur + 8);
+    v4f acc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) acc[kb] = v4f{0.f, 0.f, 0.f, 0.f};
+#define ICTC_STEP(PA, PB, KS, BB) \
+  _Pragma("unroll") for (int kb = 0; kb < 4; ++kb) acc[kb] = mfma(A[kb][KS].PA, BB.PB, acc[kb]);
+    ICTC_STEP(lo, hi, 0, B0) ICTC_STEP(hi, lo, 0, B0) ICTC_STEP(mid, mid, 0, B0)
+    ICTC_STEP(lo, hi, 1, B1) ICTC_STEP(hi, lo, 1, B1) ICTC_STEP(mid, mid, 1, B1)
+    ICTC_STEP(mid, hi, 0, B0) ICTC_STEP(hi, mid, 0, B0) ICTC_STEP(mid, hi, 1, B1)
+    ICTC_STEP(hi, mid, 1, B1) ICTC_STEP(hi, hi, 0, B0) ICTC_STEP(hi, hi, 1, B1)
+#undef ICTC_STEP
+    // D: lane holds edge i, k = 16 kb + 4 g + r
+    float* part = red + ((int64_t)(buf * S + s) * 16 + i) * kRedRow;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) *reinterpret_cast<v4f*>(part + 16 * kb + 4 * g) = acc[kb];
+    __syncthreads();
+    for (int q = threadIdx.x; q < 16 * 16; q += blockDim.x) {  // 16 edges x 16 float4 of k
+      const int edge = q >> 4, kq = q & 15;
+      const float* src = red + ((int64_t)(buf * S) * 16 + edge) * kRedRow + 4 * kq;
+      v4f sum = *reinterpret_cast<const v4f*>(src);
+      for (int w = 1; w < S; ++w) sum += *reinterpret_cast<const v4f*>(src + (int64_t)w * 16 * kRedRow);
+      const int64_t e = 16 * t + edge;
+      if (e < E) *reinterpret_cast<v4f*>(dh + e * kK + 4 * kq) = sum;
+    }
+  }
+}
+
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 }  // namespace
 
@@ -174,6 +262,32 @@ int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, con
   if (e != hipSuccess) {
     char buf[256];
     snprintf(buf, sizeof(buf), "ictc_gate_gemm_fwd launch: %s", hipGetErrorString(e));
+    return fail(ICTC_ERR_RUNTIME, buf);
+  }
+  return ICTC_OK;
+}
+
+int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float* weight, int hidden_width,
+                       float* dhidden, void* stream) {
+  if (hidden_width != kK) return fail(ICTC_ERR_UNSUPPORTED, "gate adjoint is compiled for a 64-wide hidden layer");
+  if (edges < 0 || gates <= 0 || gates % 64 != 0 || gates > 64 * kMaxSlices)
+    return fail(ICTC_ERR_UNSUPPORTED, "gate adjoint: gates must be a positive multiple of 64, at most 768");
+  if (edges == 0) return ICTC_OK;
+  if (!grad || !weight || !dhidden) return fail(ICTC_ERR_ARGUMENT, "gate adjoint: null operand");
+  if ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(dhidden)) & 15)
+    return fail(ICTC_ERR_ARGUMENT, "gate adjoint: operands must be 16-byte aligned");
+  const int S = gates / 64;
+  const int64_t tiles = (edges + 15) / 16;
+  const int per_cu = S >= 8 ? 1 : (S >= 4 ? 2 : 4);
+  const int64_t want = (int64_t)cu_count() * per_cu;
+  const unsigned blocks = (unsigned)(tiles < want ? tiles : want);
+  const size_t lds = sizeof(float) * 2 * S * 16 * kRedRow;
+  hipLaunchKernelGGL(gate_gemm_nn_kernel, dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream, grad, edges, weight,
+                     gates, dhidden);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "ictc_gate_gemm_bwd launch: %s", hipGetErrorString(e));
     return fail(ICTC_ERR_RUNTIME, buf);
   }
   return ICTC_OK;

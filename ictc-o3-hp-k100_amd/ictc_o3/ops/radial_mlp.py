@@ -3,11 +3,12 @@
 fc = Linear(8,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64, P*C)
 on the radial basis of the edge lengths (mace_ictc/models/mace/layers.py:826-835,
 radial_basis.py:11-92).  ``radial_gates`` runs the radial basis and the three
-hidden layers in one MFMA kernel (writing only the last hidden activation),
-the 64 -> P*C gate projection on a split-bf16 MFMA kernel,
-and its adjoint fuses the hidden-layer backward down to d/dr.  It supports
-first derivatives (forces, first-order parameter gradients); callers that need
-second derivatives (force-loss training) use the composable path instead.
+hidden layers in one MFMA kernel (writing only the last hidden activation) and
+the 64 -> P*C gate projection on a split-bf16 MFMA kernel; its adjoint runs the
+projection's hidden-layer adjoint on a second split-bf16 kernel and fuses the
+hidden-layer backward down to d/dr.  It supports first derivatives (forces,
+first-order parameter gradients); callers that need second derivatives
+(force-loss training) use the composable path instead.
 """
 from __future__ import annotations
 
@@ -29,6 +30,19 @@ def gate_projection(h: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
     h, W = _c(h), _c(W)
     out = h.new_empty(E, M)
     nat.call("ictc_gate_gemm_fwd", nat.ptr(h), E, 64, nat.ptr(W), M, nat.ptr(out), nat.stream_of(h))
+    return out
+
+
+def gate_projection_adjoint(dg: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
+    """dg [E, M] . W ([M, 64]) on the split-bf16 MFMA kernel when M is a multiple of 64 up to 768."""
+    E, M = dg.shape[0], W.shape[0]
+    if dg.dim() != 2 or dg.shape[1] != M or W.shape[1] != 64:
+        raise ValueError("gate adjoint needs dg [E, M] and W [M, 64]")
+    if M % 64 or M > 768:
+        return torch.mm(dg, W)   # shapes outside the kernel's register budget: library GEMM (TF32 off)
+    dg, W = _c(dg), _c(W)
+    out = dg.new_empty(E, 64)
+    nat.call("ictc_gate_gemm_bwd", nat.ptr(dg), E, M, nat.ptr(W), 64, nat.ptr(out), nat.stream_of(dg))
     return out
 
 
@@ -58,7 +72,7 @@ class _RadialGates(torch.autograd.Function):
         needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:5]) if ctx.inputs else ctx.needs_input_grad[:5]
         ctx.inputs = None
         need_w = any(needs[1:5])
-        da3 = torch.mm(dg, W4)
+        da3 = gate_projection_adjoint(dg, W4)
         dr = r.new_empty(E)
         extra = [r.new_empty(E, 64) for _ in range(5)] if need_w else [None] * 5   # dz1, dz2, dz3, a1, a2
         nat.call("ictc_radial_mlp_bwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),

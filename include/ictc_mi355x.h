@@ -228,6 +228,15 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
 int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, const float* weight, int gates,
                        float* out, void* stream);
 
+/* Adjoint of ictc_gate_gemm_fwd with respect to the hidden layer (replaces
+ * the library GEMM `grad @ weight` in the gate projection's backward,
+ * streamed_gate_message.py:51-57 / the autograd of layers.py:826-835):
+ * dhidden [E, 64] = grad [E, gates] . weight, gates a positive multiple of 64
+ * up to 768, operands 16-byte aligned; same split-bf16 arithmetic.  The
+ * per-slice partial sums are added in a fixed order (deterministic).          */
+int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float* weight, int hidden_width,
+                       float* dhidden, void* stream);
+
 /* ---- Periodic radius graph ---------------------------------------------------
  * Replaces the host neighbour search the reference delegates to ASE / matscipy
  * / torch_cluster (examples/predict.py:62, utils/graph_utils.py:217-297):
