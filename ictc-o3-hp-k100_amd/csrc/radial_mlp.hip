@@ -309,6 +309,109 @@ __global__ __launch_bounds__(FWD_WAVES * 64) void mlp_fwd_kernel(const float* __
   }
 }
 
+// ---- fused radial gates: MLP forward + gate projection ----------------------
+// gates[E, M] = s silu(...) (the MLP's last activation a3) . W4^T, W4 [M, 64]
+// (the last Linear of `fc`).  a3 never leaves the chip: each wave runs the MLP
+// for one 16-edge tile and leaves a3 split into bf16 parts in exactly the B
+// operand layout of the projection (units under the permuted reduction index),
+// the block's four tiles meet in LDS, and the waves then take 16-output row
+// blocks of W4 in turn (A operands pre-split once per call into a workspace,
+// read from L2 and reused across the four tiles).  Same split-bf16 arithmetic
+// as the hidden layers.  Workspace format: ws[rb][ks][part][lane] = part of
+// W4[16 rb + l%16][unit_of(ks, l/16, e)], e = 0..7 (M * 384 bytes).
+constexpr int GATE_TILES = 4;  // 16-edge tiles per block iteration (one per wave)
+
+__global__ void gates_split_kernel(const float* __restrict__ W4, int M, bf16x8* __restrict__ ws) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)(M / 16) * 2 * 64) return;
+  const int l = (int)(t & 63), ks = (int)((t >> 6) & 1), rb = (int)(t >> 7);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = W4[(int64_t)(16 * rb + (l & 15)) * H + unit_of(ks, l >> 4, e)];
+  const Split sp = split8(v);
+#pragma unroll
+  for (int p = 0; p < 3; ++p) ws[((int64_t)(rb * 2 + ks) * 3 + p) * 64 + l] = sp.p[p];
+}
+
+__global__ __launch_bounds__(GATE_TILES * 64) void gates_fwd_kernel(
+    const float* __restrict__ r, int64_t E, float rc, int p, const float* __restrict__ W1,
+    const float* __restrict__ W2, const float* __restrict__ W3, float s, const bf16x8* __restrict__ w4s, int M,
+    float* __restrict__ gates) {
+  __shared__ FwdWeights ws;
+  __shared__ bf16x8 bsh[GATE_TILES][2][3][64];
+  stage_fwd(ws, W1, W2, W3);
+  __syncthreads();
+  const Radial q = radial_consts(rc, p);
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6, g = l >> 4, i = l & 15;
+  const int64_t groups = (E + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
+  const int nrb = M / 16;
+  for (int64_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+    const int64_t e0 = 16 * GATE_TILES * grp;
+    {
+      const FwdWeights& wf = *opaque(&ws);
+      const int64_t e = e0 + 16 * w + i;
+      const bool ok = e < E;
+      const float x = ok ? r[e] : 2.f * rc;
+      v4f a[4];
+      float db[2];
+      forward_tile<false>(wf, q, x, s, a, nullptr, nullptr, nullptr, db, nullptr, nullptr, e, ok);
+      Split B[2];
+      split_units(a, B);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 3; ++pt) bsh[w][ks][pt][l] = B[ks].p[pt];
+    }
+    __syncthreads();
+    Split Bt[GATE_TILES][2];
+#pragma unroll
+    for (int t = 0; t < GATE_TILES; ++t)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 3; ++pt) Bt[t][ks].p[pt] = bsh[t][ks][pt][l];
+    // A operands of the wave's next row block are in flight while the current one multiplies
+    bf16x8 An[2][3];
+    if (w < nrb) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 3; ++pt) An[ks][pt] = w4s[((int64_t)w * 6 + ks * 3 + pt) * 64 + l];
+    }
+    for (int rb = w; rb < nrb; rb += GATE_TILES) {
+      bf16x8 Aop[2][3];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 3; ++pt) Aop[ks][pt] = An[ks][pt];
+      if (rb + GATE_TILES < nrb) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int pt = 0; pt < 3; ++pt)
+            An[ks][pt] = w4s[((int64_t)(rb + GATE_TILES) * 6 + ks * 3 + pt) * 64 + l];
+      }
+      v4f acc[GATE_TILES];
+#pragma unroll
+      for (int t = 0; t < GATE_TILES; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#define ICTC_STEP(PA, PB, KS) \
+  _Pragma("unroll") for (int t = 0; t < GATE_TILES; ++t) acc[t] = mfma16(Aop[KS][PA], Bt[t][KS].p[PB], acc[t]);
+      ICTC_STEP(2, 0, 0) ICTC_STEP(0, 2, 0) ICTC_STEP(1, 1, 0)
+      ICTC_STEP(2, 0, 1) ICTC_STEP(0, 2, 1) ICTC_STEP(1, 1, 1)
+      ICTC_STEP(1, 0, 0) ICTC_STEP(0, 1, 0) ICTC_STEP(1, 0, 1)
+      ICTC_STEP(0, 1, 1) ICTC_STEP(0, 0, 0) ICTC_STEP(0, 0, 1)
+#undef ICTC_STEP
+      // D: lane holds edge i of tile t, outputs 16 rb + 4 g + r
+#pragma unroll
+      for (int t = 0; t < GATE_TILES; ++t) {
+        const int64_t e = e0 + 16 * t + i;
+        if (e < E) *reinterpret_cast<v4f*>(gates + e * M + 16 * rb + 4 * g) = acc[t];
+      }
+    }
+    __syncthreads();  // bsh is rewritten by the next group
+  }
+}
+
 // Adjoint: recomputes the forward in registers, then given da3 returns dr [E];
 // optional outputs dz1..dz3, a1, a2 (nullptr to skip) feed weight gradients.
 __global__ __launch_bounds__(BWD_WAVES * 64) void mlp_bwd_kernel(
@@ -406,6 +509,34 @@ int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden
   hipLaunchKernelGGL(mlp_fwd_kernel, dim3(grid_for(edges, FWD_WAVES, 3)), dim3(FWD_WAVES * 64), 0,
                      (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, a3);
   return launch_status("ictc_radial_mlp_fwd launch");
+}
+
+int64_t ictc_radial_gates_workspace_bytes(int gates) {
+  if (gates <= 0 || gates % 16) return -1;
+  return (int64_t)gates * 384;
+}
+
+int ictc_radial_gates_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                          const float* W1, const float* W2, const float* W3, const float* W4, int gates,
+                          float silu_scale, float* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
+  if (edges < 0 || !(cutoff > 0.f) || poly_p < 2 || gates <= 0 || gates % 16)
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: invalid arguments (gates must be a positive multiple of 16)");
+  if (edges == 0) return ICTC_OK;
+  if (!r || !W1 || !W2 || !W3 || !W4 || !out || !workspace) return fail(ICTC_ERR_ARGUMENT, "radial gates: null operand");
+  if (workspace_bytes < ictc_radial_gates_workspace_bytes(gates))
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: workspace too small");
+  if (!aligned16(out) || !aligned16(workspace)) return fail(ICTC_ERR_ARGUMENT, "radial gates: operands must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const int split_threads = (gates / 16) * 2 * 64;
+  hipLaunchKernelGGL(gates_split_kernel, dim3((split_threads + 255) / 256), dim3(256), 0, st, W4, gates,
+                     (bf16x8*)workspace);
+  if (int rc = launch_status("ictc_radial_gates_fwd split")) return rc;
+  const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
+  const int64_t cap = (int64_t)cu_count() * 3;
+  hipLaunchKernelGGL(gates_fwd_kernel, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0, st, r,
+                     edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates, out);
+  return launch_status("ictc_radial_gates_fwd launch");
 }
 
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,

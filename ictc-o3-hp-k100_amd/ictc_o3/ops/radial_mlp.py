@@ -2,9 +2,9 @@
 
 fc = Linear(8,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64,64) -> SiLU*s -> Linear(64, P*C)
 on the radial basis of the edge lengths (mace_ictc/models/mace/layers.py:826-835,
-radial_basis.py:11-92).  ``radial_gates`` runs the radial basis and the three
-hidden layers in one MFMA kernel (writing only the last hidden activation) and
-the 64 -> P*C gate projection on a split-bf16 MFMA kernel; its adjoint runs the
+radial_basis.py:11-92).  ``radial_gates`` runs the radial basis, the three
+hidden layers and the 64 -> P*C gate projection in one MFMA kernel (the hidden
+activations stay on chip); its adjoint runs the
 projection's hidden-layer adjoint on a second split-bf16 kernel and fuses the
 hidden-layer backward down to d/dr.  It supports first derivatives (forces,
 first-order parameter gradients); callers that need second derivatives
@@ -52,19 +52,22 @@ class _RadialGates(torch.autograd.Function):
         ctx.inputs = (r, W1, W2, W3, W4) if r.requires_grad or W1.requires_grad else None
         r = _c(r)
         W1, W2, W3, W4 = (_c(w.detach()) for w in (W1, W2, W3, W4))
-        E = r.shape[0]
-        a3 = r.new_empty(E, 64)
-        nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
-                 nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
-        gates = gate_projection(a3, W4)
+        E, M = r.shape[0], W4.shape[0]
+        # MLP and projection in one kernel: the hidden activation never goes to HBM
+        gates = r.new_empty(E, M)
+        ws_bytes = int(nat.lib().ictc_radial_gates_workspace_bytes(M))
+        ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=r.device)
+        nat.call("ictc_radial_gates_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
+                 nat.ptr(W2), nat.ptr(W3), nat.ptr(W4), M, float(scale), nat.ptr(gates), nat.ptr(ws), ws_bytes,
+                 nat.stream_of(r))
         ctx.cfg = (cutoff, poly_p, scale)
-        ctx.save_for_backward(r, W1, W2, W3, W4, a3)
+        ctx.save_for_backward(r, W1, W2, W3, W4)
         return gates
 
     @staticmethod
     @once_differentiable
     def backward(ctx, dg):
-        r, W1, W2, W3, W4, a3 = ctx.saved_tensors
+        r, W1, W2, W3, W4 = ctx.saved_tensors
         cutoff, poly_p, scale = ctx.cfg
         dg = _c(dg)
         E = r.shape[0]
@@ -82,6 +85,9 @@ class _RadialGates(torch.autograd.Function):
         if need_w:
             from ictc_o3.ops.activation import _radial
             dz1, dz2, dz3, a1, a2 = extra
+            a3 = r.new_empty(E, 64)   # recomputed: the forward kept it on chip
+            nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
+                     nat.ptr(W2), nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
             R = _radial(0, r, None, None, 8, cutoff, poly_p)
             dW = [dz1.t() @ R, dz2.t() @ a1, dz3.t() @ a2, dg.t() @ a3]
         return (dr if needs[0] else None, *[d if n else None for d, n in zip(dW, needs[1:5])], None, None, None)

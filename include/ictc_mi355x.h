@@ -282,6 +282,17 @@ int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, cons
  * [E,64] may be NULL and are only needed for weight gradients.  MFMA FP32.  */
 int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                         const float* W1, const float* W2, const float* W3, float silu_scale, float* a3, void* stream);
+/* Fused radial gates: ictc_radial_mlp_fwd followed by the gate projection
+ * (ictc_gate_gemm_fwd with weight W4 [gates, 64]) without writing the hidden
+ * activation: out [E, gates] = a3 . W4^T; gates a positive multiple of 16,
+ * out 16-byte aligned.  workspace (ictc_radial_gates_workspace_bytes(gates),
+ * 16-byte aligned) receives W4 split into bf16 parts in MFMA operand order.
+ * Replaces the whole of `fc` (layers.py:826-835) as the reference's radial
+ * path computes it before streamed_gate_message.py:51-57.                    */
+int64_t ictc_radial_gates_workspace_bytes(int gates);
+int ictc_radial_gates_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                          const float* W1, const float* W2, const float* W3, const float* W4, int gates,
+                          float silu_scale, float* out, void* workspace, int64_t workspace_bytes, void* stream);
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
                         float* dr, float* dz1, float* dz2, float* dz3, float* a1, float* a2, void* stream);
