@@ -4,7 +4,7 @@
 //
 // The adjoint is a deterministic gather, not a scatter: node i sums the edge
 // adjoints of its incoming edges (receiver-sorted CSR) and subtracts those of
-// its outgoing edges (source-sorted CSR), each in CSR order, so the result is
+// its outgoing edges (source-sorted CSR) in a fixed order, so the result is
 // bitwise reproducible and needs no float atomics.
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -71,7 +71,17 @@ __device__ __forceinline__ void edge_adjoint(const float* __restrict__ r, const 
   }
 }
 
-// One thread per node: dpos[i] = sum_{dst(e)=i} dvec_e - sum_{src(e)=i} dvec_e.
+// One wave per node: dpos[i] = sum_{dst(e)=i} dvec_e - sum_{src(e)=i} dvec_e.
+// Lane j takes CSR positions j, j+64, ... of the node's incoming and outgoing
+// segments (coalesced index reads, independent gathers in flight across the
+// lanes); the lanes' partial sums are combined by a fixed butterfly, so the
+// result is still bitwise reproducible.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) v += __shfl_xor(v, m);
+  return v;
+}
+
 __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __restrict__ r,
                                                               const float* __restrict__ n,
                                                               const float* __restrict__ dr,
@@ -82,10 +92,11 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
                                                               const int32_t* __restrict__ sord,
                                                               float* __restrict__ dshift,
                                                               float* __restrict__ dpos) {
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t i = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
   if (i >= N) return;
+  const int lane = threadIdx.x & 63;
   float acc[3] = {0.f, 0.f, 0.f}, t[3];
-  for (int32_t k = dptr[i]; k < dptr[i + 1]; ++k) {
+  for (int32_t k = dptr[i] + lane; k < dptr[i + 1]; k += 64) {
     const int64_t e = dord[k];
     edge_adjoint(r, n, dr, dn, e, t);
 #pragma unroll
@@ -95,13 +106,14 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
       for (int c = 0; c < 3; ++c) dshift[3 * e + c] = t[c];
     }
   }
-  for (int32_t k = sptr[i]; k < sptr[i + 1]; ++k) {
+  for (int32_t k = sptr[i] + lane; k < sptr[i + 1]; k += 64) {
     edge_adjoint(r, n, dr, dn, sord[k], t);
 #pragma unroll
     for (int c = 0; c < 3; ++c) acc[c] -= t[c];
   }
 #pragma unroll
-  for (int c = 0; c < 3; ++c) dpos[3 * i + c] = acc[c];
+  for (int c = 0; c < 3; ++c) acc[c] = wave_sum(acc[c]);
+  if (lane < 3) dpos[3 * i + lane] = lane == 0 ? acc[0] : (lane == 1 ? acc[1] : acc[2]);
 }
 
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
@@ -136,7 +148,7 @@ int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, cons
   if (nodes == 0) return ICTC_OK;
   if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!r || !n || !dst_order || !src_order)))
     return fail(ICTC_ERR_ARGUMENT, "edge geometry adjoint: null operand");
-  hipLaunchKernelGGL(geometry_bwd_kernel, dim3((unsigned)((nodes + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+  hipLaunchKernelGGL(geometry_bwd_kernel, dim3((unsigned)((nodes + kBlock / 64 - 1) / (kBlock / 64))), dim3(kBlock), 0,
                      (hipStream_t)stream, r, n, dr, dn, nodes, dst_ptr, dst_order, src_ptr, src_order, dshift, dpos);
   return launch_status("ictc_edge_geometry_bwd launch");
 }
