@@ -161,12 +161,12 @@ def run_cfg2(args):
     go = torch.randn(N, op.output_width, device=dev, generator=g)
     topo = tpo.Topology(src, dst, N, positions=pos)
 
-    def mlp(h):
-        for k, W in enumerate(Ws):
-            h = torch.nn.functional.linear(h, W)
-            if k < len(Ws) - 1:
-                h = torch.nn.functional.silu(h) * 1.6791767923989418
-        return h
+    from ictc_o3.ops.radial_mlp import _RadialGates
+
+    def mlp(_rb):
+        # the library's fused radial path: Bessel x cutoff basis, 3 SiLU layers and the gate projection in one
+        # kernel; its adjoint gives the MLP weight gradients
+        return _RadialGates.apply(r, *Ws, cutoff, 5, 1.6791767923989418)
 
     def step():
         gates = mlp(rb)
