@@ -241,15 +241,33 @@ def morton_order(positions: torch.Tensor, spacing: float) -> torch.Tensor:
     return order[:N]
 
 
+def _index_order_scattered(positions: torch.Tensor, rows: torch.Tensor) -> bool:
+    """True when consecutively numbered atoms lie, on average, over twice as far apart as consecutive ``rows``.
+
+    A lattice or domain-ordered numbering lands near 1x (both orders step to a
+    neighbour, measured within 2 % of each other on the receiver passes); a
+    shuffled numbering lands near (box / neighbour spacing) x.
+    """
+    pos = positions.detach().float()
+    step_index = (pos[1:] - pos[:-1]).norm(dim=1).mean()
+    spatial = pos[rows.long()]
+    step_rows = (spatial[1:] - spatial[:-1]).norm(dim=1).mean()
+    return bool(step_index > 2.0 * step_rows)
+
+
 class Topology:
     """Receiver-sorted CSR (forward, gate / harmonic adjoints) and source-sorted CSR (feature adjoint).
 
     ``positions`` (optional, [N,3]) sets a spatial (Morton) order in which the
     source-owned feature adjoint visits rows (``src_rows``), so that the
     receiver cotangent rows gathered by concurrent waves share the L2.  The
-    receiver-owned passes keep index order (``dst_rows`` None): with the edge
-    arrays stored receiver-sorted it streams the gate rows sequentially, which
-    measured faster than a spatial order on the cfg4 shapes.  Results are
+    receiver-owned passes use the same Morton order (``dst_rows``) only when
+    the atom numbering is far less local than it (mean distance between
+    consecutively numbered atoms over twice that of the Morton rows).  A numbering that is already
+    spatial (a lattice, a domain-decomposed system) keeps index order, which
+    streams the receiver-sorted gate rows sequentially; a scattered numbering
+    (atoms shuffled, read from an unordered file) gets the Morton order, which
+    keeps the gathered sender rows of concurrent waves in L2.  Results are
     bit-identical for any row order.
     """
 
@@ -260,6 +278,8 @@ class Topology:
         self._by_src = None
         self.dst_rows = None
         self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None
+        if self.src_rows is not None and nodes > 1 and _index_order_scattered(positions, self.src_rows):
+            self.dst_rows = self.src_rows
 
     @property
     def by_src(self):

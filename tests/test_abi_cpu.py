@@ -101,3 +101,24 @@ def test_tp_module_path_enumeration():
     assert tp.path_counts_by_l == {0: 3, 1: 4, 2: 4}
     assert tp.kernel_degrees() == (2, 2, 2)
     assert tp.weight.shape == (11, 8)
+
+
+def test_receiver_row_order_choice():
+    """A spatial atom numbering keeps index order for the receiver passes; a shuffled one takes the Morton rows."""
+    from ictc_o3.ops.tensor_product import _index_order_scattered
+    g = torch.Generator().manual_seed(3)
+    n = 12
+    grid = torch.stack(torch.meshgrid(*[torch.arange(n)] * 3, indexing="ij"), -1).reshape(-1, 3).float() * 3.0
+    pos = grid + (torch.rand(grid.shape, generator=g) - 0.5) * 0.6
+    cell = torch.floor((pos - pos.min(0).values) / 2.0).long()
+    key = torch.zeros(pos.shape[0], dtype=torch.long)
+    for b in range(10):
+        for d in range(3):
+            key |= ((cell[:, d] >> b) & 1) << (3 * b + d)
+    rows = torch.sort(key, stable=True).indices.int()
+    assert not _index_order_scattered(pos, rows)
+    perm = torch.randperm(pos.shape[0], generator=g)
+    shuffled = pos[perm]
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    assert _index_order_scattered(shuffled, inv[rows.long()].int())
