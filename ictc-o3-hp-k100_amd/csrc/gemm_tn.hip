@@ -1,0 +1,213 @@
+// Weight gradients of the per-edge linears: out[M, N] = A^T B, A [K, M] and
+// B [K, N] row-major with K = edges (hundreds of thousands) and M, N the layer
+// widths (8 .. a few thousand).  This is the dW = dy^T x of every Linear of
+// the radial MLP `fc` (mace_ictc/models/mace/layers.py:826-835) in the
+// force-loss training step, where autograd runs it through the library GEMM.
+// With a 64 x 64 output the library tiles the output only (two workgroups
+// for 424k reduction rows); here the reduction rows are split instead.
+//
+// Grid: (output tile of 64 x 64) x (chunk of reduction rows).  A block of 4
+// waves stages 16-row slabs of A and B (64 columns each) through LDS with
+// 256-byte coalesced loads, prefetching the next slab into registers while
+// the MFMAs run on the current one.  Wave w owns output rows 16w .. 16w+15 of
+// the tile and all four 16-column blocks (v_mfma_f32_16x16x4_f32, FP32
+// products and sums).  Each block writes its partial tile to the workspace;
+// a second kernel adds the chunks of every output in a fixed order (chunks
+// interleaved over 16 waves, the 16 wave sums combined in wave order), so the
+// result does not depend on scheduling.
+//
+// Block order: the tiles of one chunk are consecutive logical blocks, and the
+// logical range is split contiguously over the 8 XCDs, so the chunk's rows of
+// the shared operand are fetched into one XCD's L2 and reused by its tiles.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ictc_mi355x.h"
+
+namespace ictc {
+int set_error(int code, const char* msg);
+}
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 64;
+constexpr int kSlab = 16;        // reduction rows per LDS stage
+constexpr int kPitch = 80;       // LDS row pitch: rows r and r+1 fall in disjoint bank halves
+constexpr int kXcds = 8;
+constexpr int kSumWaves = 16;
+
+int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+struct Plan {
+  int mt, nt, chunks;
+  int64_t rows;      // reduction rows per chunk (multiple of kSlab)
+  int64_t blocks;    // launched blocks (logical count rounded up to a multiple of kXcds)
+};
+
+Plan plan_for(int64_t K, int M, int N) {
+  Plan p;
+  p.mt = (M + kTile - 1) / kTile;
+  p.nt = (N + kTile - 1) / kTile;
+  const int64_t tiles = (int64_t)p.mt * p.nt;
+  const int64_t want = (int64_t)cu_count() * 8;          // about 8 blocks (32 waves) per CU
+  int64_t chunks = (want + tiles - 1) / tiles;
+  const int64_t max_chunks = (K + 63) / 64;               // at least 64 rows per chunk
+  if (chunks > max_chunks) chunks = max_chunks;
+  if (chunks > 1024) chunks = 1024;
+  if (chunks < 1) chunks = 1;
+  int64_t rows = (K + chunks - 1) / chunks;
+  rows = (rows + kSlab - 1) / kSlab * kSlab;
+  if (rows < kSlab) rows = kSlab;
+  chunks = K > 0 ? (K + rows - 1) / rows : 1;
+  p.chunks = (int)chunks;
+  p.rows = rows;
+  const int64_t logical = tiles * chunks;
+  p.blocks = (logical + kXcds - 1) / kXcds * kXcds;
+  return p;
+}
+
+__device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __restrict__ A, int64_t K, int M,
+                                                              int64_t lda, const float* __restrict__ B, int N,
+                                                              int64_t ldb, float* __restrict__ part, int mt,
+                                                              int nt, int chunks, int64_t rows, int64_t blocks) {
+  // Physical block p runs on XCD p % 8; give XCD x the logical range [x * per, (x + 1) * per).
+  const int64_t per = blocks / kXcds;
+  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  const int64_t tiles = (int64_t)mt * nt;
+  if (logical >= tiles * chunks) return;
+  const int tile = (int)(logical % tiles);
+  const int chunk = (int)(logical / tiles);
+  const int m0 = (tile % mt) * kTile, n0 = (tile / mt) * kTile;
+  const int64_t k0 = (int64_t)chunk * rows;
+  const int64_t k1 = k0 + rows < K ? k0 + rows : K;
+
+  __shared__ float sa[kSlab * kPitch];
+  __shared__ float sb[kSlab * kPitch];
+  const int t = threadIdx.x, col = t & 63, r0 = t >> 6;
+  const int lane = t & 63, wave = t >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const bool a_col = m0 + col < M, b_col = n0 + col < N;
+  const float* __restrict__ Ap = A + m0 + col;
+  const float* __restrict__ Bp = B + n0 + col;
+
+  float ra[4], rb[4];
+  auto load = [&](int64_t k) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t kr = k + r0 + 4 * j;
+      const bool in = kr < k1;
+      ra[j] = (in && a_col) ? Ap[kr * lda] : 0.f;
+      rb[j] = (in && b_col) ? Bp[kr * ldb] : 0.f;
+    }
+  };
+
+  v4f acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+  if (k0 < k1) load(k0);
+  for (int64_t k = k0; k < k1; k += kSlab) {
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sa[(r0 + 4 * j) * kPitch + col] = ra[j];
+      sb[(r0 + 4 * j) * kPitch + col] = rb[j];
+    }
+    __syncthreads();
+    if (k + kSlab < k1) load(k + kSlab);
+#pragma unroll
+    for (int kk = 0; kk < kSlab / 4; ++kk) {
+      const int row = (4 * kk + lg) * kPitch;
+      const float a = sa[row + 16 * wave + li];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] = mfma(a, sb[row + 16 * j + li], acc[j]);
+    }
+  }
+
+  float* __restrict__ P = part + (int64_t)chunk * M * N;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 16 * j + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 16 * wave + 4 * lg + r;
+      if (m < M && n < N) P[(int64_t)m * N + n] = acc[j][r];
+    }
+  }
+}
+
+// out[i] = sum over chunks of part[c][i]: wave w of a block adds chunks
+// w, w + 16, ... for 64 consecutive outputs; the wave sums meet in LDS and
+// are added in wave order.
+__global__ __launch_bounds__(64 * kSumWaves) void gemm_tn_sum_kernel(const float* __restrict__ part, int64_t n,
+                                                                     int chunks, float* __restrict__ out) {
+  __shared__ float red[kSumWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  float v = 0.f;
+  if (i < n)
+    for (int c = wave; c < chunks; c += kSumWaves) v += part[(int64_t)c * n + i];
+  red[wave][lane] = v;
+  __syncthreads();
+  if (wave == 0 && i < n) {
+    float s = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < kSumWaves; ++w) s += red[w][lane];
+    out[i] = s;
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t ictc_gemm_tn_workspace_bytes(int64_t k, int64_t m, int64_t n) {
+  if (k < 0 || m <= 0 || n <= 0 || m > (1 << 20) || n > (1 << 20)) return -1;
+  const Plan p = plan_for(k, (int)m, (int)n);
+  return (int64_t)p.chunks * m * n * (int64_t)sizeof(float);
+}
+
+int ictc_gemm_tn(const float* a, int64_t k, int64_t m, int64_t lda, const float* b, int64_t n, int64_t ldb,
+                 float* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (k < 0 || m <= 0 || n <= 0 || m > (1 << 20) || n > (1 << 20) || lda < m || ldb < n)
+    return fail(ICTC_ERR_ARGUMENT, "gemm_tn: need k >= 0, 0 < m, n <= 2^20, lda >= m, ldb >= n");
+  if (!out || (k > 0 && (!a || !b))) return fail(ICTC_ERR_ARGUMENT, "gemm_tn: null operand");
+  const Plan p = plan_for(k, (int)m, (int)n);
+  const int64_t need = (int64_t)p.chunks * m * n * (int64_t)sizeof(float);
+  if (!workspace || workspace_bytes < need)
+    return fail(ICTC_ERR_ARGUMENT, "gemm_tn: workspace smaller than ictc_gemm_tn_workspace_bytes");
+  float* part = static_cast<float*>(workspace);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(gemm_tn_partial_kernel, dim3((unsigned)p.blocks), dim3(256), 0, st, a, k, (int)m, lda, b,
+                     (int)n, ldb, part, p.mt, p.nt, p.chunks, p.rows, p.blocks);
+  const int64_t total = m * n;
+  hipLaunchKernelGGL(gemm_tn_sum_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64 * kSumWaves), 0, st, part,
+                     total, p.chunks, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "ictc_gemm_tn launch: %s", hipGetErrorString(e));
+    return fail(ICTC_ERR_RUNTIME, buf);
+  }
+  return ICTC_OK;
+}
+
+}  // extern "C"

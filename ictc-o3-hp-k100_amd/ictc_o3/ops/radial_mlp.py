@@ -8,7 +8,10 @@ activations stay on chip); its adjoint runs the
 projection's hidden-layer adjoint on a second split-bf16 kernel and fuses the
 hidden-layer backward down to d/dr.  It supports first derivatives (forces,
 first-order parameter gradients); callers that need second derivatives
-(force-loss training) use the composable path instead.
+(force-loss training) use the composable path ``radial_mlp``, whose Linears
+(``edge_linear``) take their weight gradients dW = dy^T x from a
+split-reduction MFMA kernel (``ictc_gemm_tn``) instead of a library GEMM that
+tiles only the small output.
 """
 from __future__ import annotations
 
@@ -44,6 +47,104 @@ def gate_projection_adjoint(dg: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
     out = dg.new_empty(E, 64)
     nat.call("ictc_gate_gemm_bwd", nat.ptr(dg), E, M, nat.ptr(W), 64, nat.ptr(out), nat.stream_of(dg))
     return out
+
+
+_TN_MIN_ROWS = 16384   # below this the library GEMM's output tiling is enough
+
+
+def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a [K, M], b [K, N] -> a^T b [M, N] on the split-reduction MFMA kernel (deterministic)."""
+    a, b = _c(a.detach()), _c(b.detach())
+    K, M = a.shape
+    N = b.shape[1]
+    out = a.new_empty(M, N)
+    ws_bytes = int(nat.lib().ictc_gemm_tn_workspace_bytes(K, M, N))
+    if ws_bytes < 0:
+        raise ValueError("gemm_tn: unsupported shape")
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=a.device)
+    nat.call("ictc_gemm_tn", nat.ptr(a), K, M, M, nat.ptr(b), N, N, nat.ptr(out), nat.ptr(ws), ws_bytes,
+             nat.stream_of(a))
+    return out
+
+
+class _WeightGrad(torch.autograd.Function):
+    """a^T b over edge rows (a weight gradient); differentiable in a and b."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda:
+            return _gemm_tn(a, b)
+        return a.t() @ b
+
+    @staticmethod
+    def backward(ctx, h):
+        a, b = ctx.saved_tensors
+        da = b @ h.t() if ctx.needs_input_grad[0] else None
+        db = a @ h if ctx.needs_input_grad[1] else None
+        return da, db
+
+
+class _EdgeLinear(torch.autograd.Function):
+    """y = x W^T over edge rows; the weight gradient runs on the split-reduction kernel."""
+
+    @staticmethod
+    def forward(ctx, x, W):
+        ctx.save_for_backward(x, W)
+        ctx.inputs = (x, W)
+        return x @ W.t()
+
+    @staticmethod
+    def backward(ctx, g):
+        from ictc_o3.autograd import required_gradients
+        x, W = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad) if ctx.inputs else ctx.needs_input_grad
+        ctx.inputs = None
+        dx = _EdgeLinearT.apply(g, W) if needs[0] else None
+        dW = _WeightGrad.apply(g, x) if needs[1] else None
+        return dx, dW
+
+
+class _EdgeLinearT(torch.autograd.Function):
+    """z = u W over edge rows (the input adjoint of _EdgeLinear), differentiable in u and W."""
+
+    @staticmethod
+    def forward(ctx, u, W):
+        ctx.save_for_backward(u, W)
+        ctx.inputs = (u, W)
+        return u @ W
+
+    @staticmethod
+    def backward(ctx, h):
+        from ictc_o3.autograd import required_gradients
+        u, W = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad) if ctx.inputs else ctx.needs_input_grad
+        ctx.inputs = None
+        du = _EdgeLinear.apply(h, W) if needs[0] else None
+        dW = _WeightGrad.apply(u, h) if needs[1] else None
+        return du, dW
+
+
+def edge_linear(x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
+    """x [E, in] . W^T ([out, in], nn.Linear layout) with weight gradients on the split-reduction kernel.
+
+    Same values as torch.nn.functional.linear without bias; every derivative
+    order is supported (the adjoints are built from the same two operators).
+    """
+    if x.dim() != 2 or W.dim() != 2 or x.shape[1] != W.shape[1]:
+        raise ValueError("edge_linear needs x [E, in] and W [out, in]")
+    return _EdgeLinear.apply(x, W)
+
+
+def radial_mlp(radial: torch.Tensor, fc: torch.nn.Sequential) -> torch.Tensor:
+    """fc(radial) with its bias-free Linears as edge_linear (the composable, any-order path)."""
+    h = radial
+    for m in fc:
+        if isinstance(m, torch.nn.Linear) and m.bias is None:
+            h = edge_linear(h, m.weight)
+        else:
+            h = m(h)
+    return h
 
 
 class _RadialGates(torch.autograd.Function):

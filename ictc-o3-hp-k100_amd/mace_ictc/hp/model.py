@@ -170,7 +170,8 @@ class Interaction(nn.Module):
             from ictc_o3.ops.radial_mlp import radial_gates
             gates = radial_gates(r, self.fc, *radial_cfg)
         else:
-            gates = self.fc(radial)
+            from ictc_o3.ops.radial_mlp import radial_mlp
+            gates = radial_mlp(radial, self.fc)
         m = tpo.message(x, Y, gates, self.spec(), topo, mask)
         message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8), first_order)
         sc = self.self_connection.forward_l0(h[:, :C], species)

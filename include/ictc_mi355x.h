@@ -237,6 +237,18 @@ int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, con
 int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float* weight, int hidden_width,
                        float* dhidden, void* stream);
 
+/* Weight gradient of a per-edge linear (replaces the library GEMM dW = dy^T x
+ * that autograd runs for every Linear of the radial MLP fc in the force-loss
+ * training step, mace_ictc/models/mace/layers.py:826-835 via
+ * radial_checkpoint.py:133-164): out [m, n] = a^T b with a [k, m] (row pitch
+ * lda) and b [k, n] (row pitch ldb), FP32 MFMA.  The k rows are split into
+ * chunks whose partial products go to the workspace
+ * (ictc_gemm_tn_workspace_bytes(k, m, n) bytes) and are added in a fixed
+ * order (deterministic).  k = 0 writes zeros.                                  */
+int64_t ictc_gemm_tn_workspace_bytes(int64_t k, int64_t m, int64_t n);
+int ictc_gemm_tn(const float* a, int64_t k, int64_t m, int64_t lda, const float* b, int64_t n, int64_t ldb,
+                 float* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- Periodic radius graph ---------------------------------------------------
  * Replaces the host neighbour search the reference delegates to ASE / matscipy
  * / torch_cluster (examples/predict.py:62, utils/graph_utils.py:217-297):
