@@ -73,7 +73,9 @@ class _WeightGrad(torch.autograd.Function):
     @staticmethod
     def forward(ctx, a, b):
         ctx.save_for_backward(a, b)
-        if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda:
+        tiles = -(-a.shape[1] // 64) * -(-b.shape[1] // 64)
+        # the split pays off while the output alone cannot fill the GPU (up to 16 tiles of 64 x 64)
+        if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda and tiles <= 16:
             return _gemm_tn(a, b)
         return a.t() @ b
 
@@ -92,6 +94,9 @@ class _EdgeLinear(torch.autograd.Function):
     def forward(ctx, x, W):
         ctx.save_for_backward(x, W)
         ctx.inputs = (x, W)
+        if (x.is_cuda and x.shape[0] >= _TN_MIN_ROWS and x.shape[1] == 64 and W.shape[0] % 16 == 0
+                and W.shape[0] > 64):
+            return gate_projection(x, W)   # the wide gate projection: split-bf16 MFMA, FP32-level accuracy
         return x @ W.t()
 
     @staticmethod
@@ -112,6 +117,9 @@ class _EdgeLinearT(torch.autograd.Function):
     def forward(ctx, u, W):
         ctx.save_for_backward(u, W)
         ctx.inputs = (u, W)
+        M = W.shape[0]
+        if u.is_cuda and u.shape[0] >= _TN_MIN_ROWS and W.shape[1] == 64 and M % 64 == 0 and 64 < M <= 768:
+            return gate_projection_adjoint(u, W)   # split-bf16 MFMA, FP32-level accuracy
         return u @ W
 
     @staticmethod

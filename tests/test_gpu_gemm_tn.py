@@ -75,8 +75,8 @@ def test_edge_linear_derivatives(device):
     g = torch.Generator().manual_seed(12)
     x0 = torch.randn(E, 64, generator=g).to(device)
     W1_0 = (torch.randn(64, 64, generator=g) / 8).to(device)
-    W2_0 = (torch.randn(96, 64, generator=g) / 8).to(device)
-    t = torch.randn(E, 96, generator=g).to(device)
+    W2_0 = (torch.randn(192, 64, generator=g) / 8).to(device)   # the split-bf16 projection and adjoint kernels
+    t = torch.randn(E, 192, generator=g).to(device)
 
     def run(lin):
         x = x0.clone().requires_grad_(True)
