@@ -71,6 +71,18 @@ __device__ __forceinline__ void edge_adjoint(const float* __restrict__ r, const 
   }
 }
 
+template <bool VEC>
+__device__ __forceinline__ void edge_cotangent(const float* __restrict__ r, const float* __restrict__ n,
+                                               const float* __restrict__ dr, const float* __restrict__ dn,
+                                               int64_t e, float* out) {
+  if (VEC) {
+#pragma unroll
+    for (int c = 0; c < 3; ++c) out[c] = dn[3 * e + c];
+  } else {
+    edge_adjoint(r, n, dr, dn, e, out);
+  }
+}
+
 // One wave per node: dpos[i] = sum_{dst(e)=i} dvec_e - sum_{src(e)=i} dvec_e.
 // Lane j takes CSR positions j, j+64, ... of the node's incoming and outgoing
 // segments (coalesced index reads, independent gathers in flight across the
@@ -82,6 +94,8 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// VEC: the cotangent is given per edge vector (dn holds dvec [E, 3]; r, n, dr unused).
+template <bool VEC>
 __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __restrict__ r,
                                                               const float* __restrict__ n,
                                                               const float* __restrict__ dr,
@@ -98,7 +112,7 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
   float acc[3] = {0.f, 0.f, 0.f}, t[3];
   for (int32_t k = dptr[i] + lane; k < dptr[i + 1]; k += 64) {
     const int64_t e = dord[k];
-    edge_adjoint(r, n, dr, dn, e, t);
+    edge_cotangent<VEC>(r, n, dr, dn, e, t);
 #pragma unroll
     for (int c = 0; c < 3; ++c) acc[c] += t[c];
     if (dshift) {
@@ -107,7 +121,7 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
     }
   }
   for (int32_t k = sptr[i] + lane; k < sptr[i + 1]; k += 64) {
-    edge_adjoint(r, n, dr, dn, sord[k], t);
+    edge_cotangent<VEC>(r, n, dr, dn, sord[k], t);
 #pragma unroll
     for (int c = 0; c < 3; ++c) acc[c] -= t[c];
   }
@@ -148,9 +162,22 @@ int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, cons
   if (nodes == 0) return ICTC_OK;
   if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!r || !n || !dst_order || !src_order)))
     return fail(ICTC_ERR_ARGUMENT, "edge geometry adjoint: null operand");
-  hipLaunchKernelGGL(geometry_bwd_kernel, dim3((unsigned)((nodes + kBlock / 64 - 1) / (kBlock / 64))), dim3(kBlock), 0,
+  hipLaunchKernelGGL(geometry_bwd_kernel<false>, dim3((unsigned)((nodes + kBlock / 64 - 1) / (kBlock / 64))), dim3(kBlock), 0,
                      (hipStream_t)stream, r, n, dr, dn, nodes, dst_ptr, dst_order, src_ptr, src_order, dshift, dpos);
   return launch_status("ictc_edge_geometry_bwd launch");
+}
+
+int ictc_edge_vector_bwd(const float* dvec, int64_t nodes, int64_t edges, const int32_t* dst_ptr,
+                         const int32_t* dst_order, const int32_t* src_ptr, const int32_t* src_order, float* dpos,
+                         void* stream) {
+  if (nodes < 0 || edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge vector adjoint: negative size");
+  if (nodes == 0) return ICTC_OK;
+  if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!dvec || !dst_order || !src_order)))
+    return fail(ICTC_ERR_ARGUMENT, "edge vector adjoint: null operand");
+  hipLaunchKernelGGL(geometry_bwd_kernel<true>, dim3((unsigned)((nodes + kBlock / 64 - 1) / (kBlock / 64))),
+                     dim3(kBlock), 0, (hipStream_t)stream, nullptr, nullptr, nullptr, dvec, nodes, dst_ptr, dst_order,
+                     src_ptr, src_order, nullptr, dpos);
+  return launch_status("ictc_edge_vector_bwd launch");
 }
 
 }  // extern "C"

@@ -5,7 +5,9 @@ Forward follows mace_ictc/models/pure_cartesian_ictd_layers.py:1288-1297
 mask = r <= cutoff).  The adjoint replaces the two index-gather backwards
 (scatter-adds into pos) with one kernel that sums, per node, the adjoints of its
 incoming edges minus those of its outgoing edges in CSR order.  First
-derivatives only: force-loss training keeps the composable torch path.
+derivatives only.  Force-loss training differentiates the edge vectors twice
+and uses ``edge_vectors``: the gather and its CSR adjoint are each other's
+adjoints, so every derivative order stays deterministic and atomic-free.
 """
 from __future__ import annotations
 
@@ -61,3 +63,50 @@ def edge_geometry(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: f
     if shift is not None and tuple(shift.shape) != (topo.src.numel(), 3):
         raise ValueError("shift must be [E, 3]")
     return _EdgeGeometry.apply(pos, shift, topo, float(cutoff))
+
+
+def _vector_adjoint(dvec: torch.Tensor, topo, N: int) -> torch.Tensor:
+    dvec = _c(dvec.detach())
+    dpos = dvec.new_empty(N, 3)
+    src_csr = topo.by_src
+    nat.call("ictc_edge_vector_bwd", nat.ptr(dvec), N, dvec.shape[0], nat.ptr(topo.by_dst.ptr),
+             nat.ptr(topo.by_dst.order), nat.ptr(src_csr.ptr), nat.ptr(src_csr.order), nat.ptr(dpos),
+             nat.stream_of(dvec))
+    return dpos
+
+
+class _EdgeVectors(torch.autograd.Function):
+    """vec = pos[dst] - pos[src] (+ shift); the adjoint is _EdgeVectorAdjoint."""
+
+    @staticmethod
+    def forward(ctx, pos, shift, topo):
+        ctx.topo, ctx.nodes = topo, pos.shape[0]
+        vec = pos.index_select(0, topo.dst) - pos.index_select(0, topo.src)
+        return vec if shift is None else vec + shift
+
+    @staticmethod
+    def backward(ctx, dvec):
+        dpos = _EdgeVectorAdjoint.apply(dvec, ctx.topo, ctx.nodes) if ctx.needs_input_grad[0] else None
+        return dpos, (dvec if ctx.needs_input_grad[1] else None), None
+
+
+class _EdgeVectorAdjoint(torch.autograd.Function):
+    """dpos = sum_in dvec - sum_out dvec (CSR gather); the adjoint is _EdgeVectors without shift."""
+
+    @staticmethod
+    def forward(ctx, dvec, topo, N):
+        ctx.topo = topo
+        return _vector_adjoint(dvec, topo, N)
+
+    @staticmethod
+    def backward(ctx, h):
+        return _EdgeVectors.apply(h, None, ctx.topo), None, None
+
+
+def edge_vectors(pos: torch.Tensor, shift: torch.Tensor | None, topo) -> torch.Tensor:
+    """vec [E, 3] = pos[dst] - pos[src] + shift for the edges of ``topo``, differentiable to any order."""
+    if pos.dim() != 2 or pos.shape[1] != 3:
+        raise ValueError("pos must be [N, 3]")
+    if not pos.is_cuda or pos.dtype != torch.float32:
+        raise TypeError("edge_vectors runs on float32 device tensors")
+    return _EdgeVectors.apply(pos, shift, topo)

@@ -279,7 +279,11 @@ class PureCartesianICTDFix(nn.Module):
             cells = cell[batch[edge_src]]
             shift_vec = (shifts.unsqueeze(-1) * cells).sum(1)
         if second_order or pos.dtype != torch.float32:
-            vec = pos[edge_dst] - pos[edge_src] + shift_vec
+            if pos.dtype == torch.float32 and pos.is_cuda:
+                from ictc_o3.ops.geometry import edge_vectors
+                vec = edge_vectors(pos, shift_vec, topology)
+            else:
+                vec = pos[edge_dst] - pos[edge_src] + shift_vec
             r = vec.norm(dim=1)
             n = vec / r.clamp(min=1e-8).unsqueeze(-1)
             mask = (r <= self.max_radius).to(pos.dtype)

@@ -283,6 +283,16 @@ int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, cons
                            int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order, const int32_t* src_ptr,
                            const int32_t* src_order, float* dshift, float* dpos, void* stream);
 
+/* Adjoint of the edge-vector gather alone (the training path differentiates
+ * vec = pos[dst] - pos[src] + shift twice, backbone.py:944 under
+ * create_graph): dpos [N,3] = sum over incoming edges - sum over outgoing
+ * edges of dvec [E,3], the same CSR-order gather as ictc_edge_geometry_bwd
+ * (deterministic, no atomics; it replaces the index_put scatter-adds of the
+ * gathers' autograd).                                                          */
+int ictc_edge_vector_bwd(const float* dvec, int64_t nodes, int64_t edges, const int32_t* dst_ptr,
+                         const int32_t* dst_order, const int32_t* src_ptr, const int32_t* src_order, float* dpos,
+                         void* stream);
+
 /* ---- Fused radial MLP (hidden layers) ---------------------------------------
  * Replaces the hidden part of the interaction's radial MLP `fc`
  * (mace_ictc/models/mace/layers.py:826-835, radial_basis.py:42-92) and its

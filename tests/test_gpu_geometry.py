@@ -66,3 +66,36 @@ def test_edge_geometry(device, N, E, seed, sort, with_shift):
         r3, n3, _ = edge_geometry(pd, sd, topo, 4.5)
         torch.autograd.backward([r3, n3], [gr.float().to(device), gn.float().to(device)])
         assert torch.equal(first, pd.grad)
+
+
+@pytest.mark.parametrize("N,E,seed", [(200, 4000, 11), (31, 200, 12), (1000, 30000, 13)])
+def test_edge_vectors_second_order(device, N, E, seed):
+    """edge_vectors through a force-loss style double backward equals float64 gathers; repeatable bitwise."""
+    from ictc_o3.ops.geometry import edge_vectors
+    from ictc_o3.ops.tensor_product import Topology
+    pos, src, dst, shift = _case(N, E, seed, True)
+    E = src.numel()
+    g = torch.Generator().manual_seed(seed + 7)
+    t = torch.randn(N, 3, generator=g, dtype=torch.float64)
+
+    def run(p, s, vec_fn):
+        vec = vec_fn(p, s)
+        e = (vec.norm(dim=1) ** 3).sum() + (vec[:, 0] * vec[:, 1]).sum()
+        gp, = torch.autograd.grad(e, p, create_graph=True)
+        loss = (gp * t.to(gp)).sum() + 0.5 * e
+        loss.backward()
+        return vec.detach(), gp.detach(), p.grad, s.grad
+
+    p64, s64 = pos.clone().requires_grad_(True), shift.clone().requires_grad_(True)
+    ref = run(p64, s64, lambda p, s: p[dst] - p[src] + s)
+    topo = Topology(src.to(device), dst.to(device), N)
+    outs = []
+    for _ in range(2):
+        pd = pos.float().to(device).requires_grad_(True)
+        sd = shift.float().to(device).requires_grad_(True)
+        outs.append(run(pd, sd, lambda p, s: edge_vectors(p, s, topo)))
+    for o, r in zip(outs[0], ref):
+        if r.numel():
+            assert rel_err(o, r) < 1e-5
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a, b)
