@@ -15,6 +15,12 @@ component order (component k of degree l sits at l*l + m):
   dx    dx[i] += sum_p gw[p] sum C_p y[m2] go[k]
   dy    dy[j] += sum_p gw[p] sum C_p x[m1] go[k]
   dg    dg[p]  = sum_k go[k] sum C_p x[m1] y[m2]
+  dydg  dy and dg of the same x in one pass
+
+The sums are grouped so that the lane-varying operand meets the CG literal
+first: B_jk = sum_i C x[i] costs one VALU op per nonzero, and the per-edge
+harmonics y (wave-uniform, in SGPRs) enter once per (j, k) pair.  dydg
+shares each B_jk between the two adjoints.
 
 and ``Sh<L>`` with the component-normalised direction harmonics, their
 Jacobian-transpose product (bwd), Jacobian product (jvp) and the
@@ -31,6 +37,10 @@ sys.path.insert(0, os.path.dirname(_HERE))
 from ictc_o3.basis import tables  # noqa: E402
 
 LMAX = 3
+# Scheduling fence after each output slot of the contractions: without it the
+# scheduler interleaves the independent B_jk products of many slots and the
+# register demand of the degree-3 kernels doubles.
+SB = ""
 
 
 def f(v: float) -> str:
@@ -52,7 +62,20 @@ def tp_struct(li, le, lo):
         for (m1, m2, m3, v) in T.nonzeros(p):
             ent.append((p, l1 * l1 + m1, l2 * l2 + m2, T.out_component(p, m3), v))
     lines.append(f"  static constexpr int NNZ = {len(ent)};")
-    # forward
+    path_of = {}
+    by_kj = {}    # output slot k -> edge component j -> [(i, coef)]
+    for p, i, j, k, v in ent:
+        path_of[k] = p
+        by_kj.setdefault(k, {}).setdefault(j, []).append((i, v))
+
+    def b_expr(x, terms):
+        # B_jk = sum_i C x[i]: lane-varying operand times a literal, one VALU op per nonzero
+        return " + ".join(f"{f(v)} * {x}[{i}]" for i, v in terms)
+
+    def t_expr(x, y, js):
+        return " + ".join(f"{y}[{j}] * ({b_expr(x, terms)})" for j, terms in sorted(js.items()))
+
+    # forward: o[k] += gw[p] sum_j y[j] B_jk(x)
     lines.append("  __device__ __forceinline__ static void fwd(const float* __restrict__ x, const float* __restrict__ y,"
                  " const float* __restrict__ gw, float* __restrict__ o) {")
     by_out = {}
@@ -62,36 +85,48 @@ def tp_struct(li, le, lo):
         expr = " + ".join(f"{f(v)} * (x[{i}] * y[{j}])" for i, j, v in terms)
         lines.append(f"    o[{k}] = fmaf(gw[{p}], {expr}, o[{k}]);")
     lines.append("  }")
-    # dx
+    # dx: d[i] += sum_j y[j] sum_p gw[p] sum_{k in p} C go[k]
     lines.append("  __device__ __forceinline__ static void dx(const float* __restrict__ y, const float* __restrict__ gw,"
                  " const float* __restrict__ go, float* __restrict__ d) {")
-    by_x = {}
+    by_ij = {}
     for p, i, j, k, v in ent:
-        by_x.setdefault(i, []).append((p, j, k, v))
-    for i, terms in sorted(by_x.items()):
-        expr = " + ".join(f"{f(v)} * (gw[{p}] * (y[{j}] * go[{k}]))" for p, j, k, v in terms)
-        lines.append(f"    d[{i}] += {expr};")
+        by_ij.setdefault(i, {}).setdefault(j, {}).setdefault(p, []).append((k, v))
+    for i, js in sorted(by_ij.items()):
+        parts = []
+        for j, ps in sorted(js.items()):
+            inner = " + ".join(f"gw[{p}] * ({' + '.join(f'{f(v)} * go[{k}]' for k, v in ks)})"
+                               for p, ks in sorted(ps.items()))
+            parts.append(f"y[{j}] * ({inner})")
+        lines.append(f"    d[{i}] += {' + '.join(parts)};")
     lines.append("  }")
-    # dy
+    # dy: d[j] += sum_k (gw[p] go[k]) B_jk(x)
     lines.append("  __device__ __forceinline__ static void dy(const float* __restrict__ x, const float* __restrict__ gw,"
                  " const float* __restrict__ go, float* __restrict__ d) {")
-    by_y = {}
-    for p, i, j, k, v in ent:
-        by_y.setdefault(j, []).append((p, i, k, v))
-    for j, terms in sorted(by_y.items()):
-        expr = " + ".join(f"{f(v)} * (gw[{p}] * (x[{i}] * go[{k}]))" for p, i, k, v in terms)
-        lines.append(f"    d[{j}] += {expr};")
+    for k, js in sorted(by_kj.items()):
+        lines.append(f"    {{ const float w = gw[{path_of[k]}] * go[{k}];")
+        for j, terms in sorted(js.items()):
+            lines.append(f"      d[{j}] = fmaf(w, {b_expr('x', terms)}, d[{j}]);")
+        lines.append(f"    }}{SB}")
     lines.append("  }")
-    # dg
+    # dg: d[p] = sum_{k in p} go[k] sum_j y[j] B_jk(x)
     lines.append("  __device__ __forceinline__ static void dg(const float* __restrict__ x, const float* __restrict__ y,"
                  " const float* __restrict__ go, float* __restrict__ d) {")
-    by_p = {}
-    for p, i, j, k, v in ent:
-        by_p.setdefault(p, []).append((i, j, k, v))
-    for p in range(P):
-        terms = by_p.get(p, [])
-        expr = " + ".join(f"{f(v)} * (x[{i}] * (y[{j}] * go[{k}]))" for i, j, k, v in terms) or "0.f"
-        lines.append(f"    d[{p}] = {expr};")
+    lines.append(f"#pragma unroll\n    for (int p = 0; p < {P}; ++p) d[p] = 0.f;")
+    for k, js in sorted(by_kj.items()):
+        lines.append(f"    d[{path_of[k]}] = fmaf(go[{k}], {t_expr('x', 'y', js)}, d[{path_of[k]}]);{SB}")
+    lines.append("  }")
+    # dy and dg of one x together: each B_jk(x) feeds both
+    lines.append("  __device__ __forceinline__ static void dydg(const float* __restrict__ x, const float* __restrict__ y,"
+                 " const float* __restrict__ gw, const float* __restrict__ go, float* __restrict__ dyv,"
+                 " float* __restrict__ d) {")
+    lines.append(f"#pragma unroll\n    for (int p = 0; p < {P}; ++p) d[p] = 0.f;")
+    for k, js in sorted(by_kj.items()):
+        p = path_of[k]
+        lines.append(f"    {{ const float w = gw[{p}] * go[{k}]; float t = 0.f;")
+        for j, terms in sorted(js.items()):
+            lines.append(f"      {{ const float b = {b_expr('x', terms)}; dyv[{j}] = fmaf(w, b, dyv[{j}]);"
+                         f" t = fmaf(y[{j}], b, t); }}")
+        lines.append(f"      d[{p}] = fmaf(go[{k}], t, d[{p}]); }}{SB}")
     lines.append("  }")
     lines.append("};")
     return "\n".join(lines)

@@ -205,10 +205,11 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
       T::dx(y, gw, go, d);
       store_row<T::NX>(dx + e * (int64_t)(T::NX * C), C, c, d);
     }
-    if (dsh) T::dy(xv, gw, go, dyv);
+    float d[T::P];
+    if (dsh && dgates) T::dydg(xv, y, gw, go, dyv, d);
+    else if (dsh) T::dy(xv, gw, go, dyv);
+    else if (dgates) T::dg(xv, y, go, d);
     if (dgates) {
-      float d[T::P];
-      T::dg(xv, y, go, d);
       if (a.weight) {
 #pragma unroll
         for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
@@ -366,10 +367,11 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
         float xv[T::NX], gw[T::P];
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
         load_gw<T>(a, e, c, m, gw);
-        if (dsh) T::dy(xv, gw, go, dyv);
+        float d[T::P];
+        if (dsh && dgates) T::dydg(xv, y, gw, go, dyv, d);
+        else if (dsh) T::dy(xv, gw, go, dyv);
+        else if (dgates) T::dg(xv, y, go, d);
         if (dgates) {
-          float d[T::P];
-          T::dg(xv, y, go, d);
 #pragma unroll
           for (int p = 0; p < T::P; ++p) d[p] *= m;
           if (a.weight) {

@@ -61,6 +61,21 @@ __device__ __forceinline__ void store_dsh(float* __restrict__ out, int64_t e, co
   if (lane_id() < T::NY) out[e * T::NY + lane_id()] = mine;
 }
 
+// dyv += dy(x, w, go) when want_dy; dacc += dg(x, y, go) when want_dg; one
+// pass over the CG entries when both are wanted.
+template <class T>
+__device__ __forceinline__ void dy_dg_add(bool want_dy, bool want_dg, const float* x, const float* y,
+                                          const float* w, const float* go, float* dyv, float* dacc) {
+  float d2[T::P];
+  if (want_dy && want_dg) T::dydg(x, y, w, go, dyv, d2);
+  else if (want_dy) T::dy(x, w, go, dyv);
+  else if (want_dg) T::dg(x, y, go, d2);
+  if (want_dg) {
+#pragma unroll
+    for (int p = 0; p < T::P; ++p) dacc[p] += d2[p];
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Per-edge TP: one wave per (edge, channel group); every output optional.
 // ---------------------------------------------------------------------------
@@ -106,23 +121,11 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeSecond, T::LI, T::LE, T::LO
         if (t.gates) T::dx(y, tg, go, d);
         store_row<T::NX>(dx + xo, C, c, d);
       }
-      if (dsh) {
-        if (t.x) T::dy(tx, gw, go, dyv);
-        if (t.gates) T::dy(xv, tg, go, dyv);
-      }
+      float d[T::P];
+      zero<T::P>(d);
+      if (t.x) dy_dg_add<T>(dsh != nullptr, dgates != nullptr, tx, y, gw, go, dyv, d);
+      dy_dg_add<T>(dsh && t.gates, dgates && t.sh, xv, ty, tg, go, dyv, d);
       if (dgates) {
-        float d[T::P], d2[T::P];
-        zero<T::P>(d);
-        if (t.x) {
-          T::dg(tx, y, go, d2);
-#pragma unroll
-          for (int p = 0; p < T::P; ++p) d[p] += d2[p];
-        }
-        if (t.sh) {
-          T::dg(xv, ty, go, d2);
-#pragma unroll
-          for (int p = 0; p < T::P; ++p) d[p] += d2[p];
-        }
         if (a.weight) {
 #pragma unroll
           for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
@@ -246,31 +249,21 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge2, T::LI, T::LE, T::L
         else zero<T::NX>(xv);
         if (need_tx) load_row<T::NX>(t.x + xo, C, c, tx);
         else zero<T::NX>(tx);
-        if (dsh) {
-          if (t.x) {
-            float gw[T::P];
-            load_gates<T>(a.gates, a, e, c, m, gw);
-            T::dy(tx, gw, go, dyv);
-          }
-          if (t.gates) {
-            float tg[T::P];
-            load_gates<T>(t.gates, a, e, c, m, tg);
-            T::dy(xv, tg, go, dyv);
-          }
+        float d[T::P];
+        zero<T::P>(d);
+        if (t.x) {
+          float gw[T::P];
+          if (dsh) load_gates<T>(a.gates, a, e, c, m, gw);
+          else zero<T::P>(gw);
+          dy_dg_add<T>(dsh != nullptr, dgates != nullptr, tx, y, gw, go, dyv, d);
+        }
+        {
+          float tg[T::P];
+          if (dsh && t.gates) load_gates<T>(t.gates, a, e, c, m, tg);
+          else zero<T::P>(tg);
+          dy_dg_add<T>(dsh && t.gates, dgates && t.sh, xv, ty, tg, go, dyv, d);
         }
         if (dgates) {
-          float d[T::P], d2[T::P];
-          zero<T::P>(d);
-          if (t.x) {
-            T::dg(tx, y, go, d2);
-#pragma unroll
-            for (int p = 0; p < T::P; ++p) d[p] += d2[p];
-          }
-          if (t.sh) {
-            T::dg(xv, ty, go, d2);
-#pragma unroll
-            for (int p = 0; p < T::P; ++p) d[p] += d2[p];
-          }
 #pragma unroll
           for (int p = 0; p < T::P; ++p) d[p] *= m;
           if (a.weight) {
