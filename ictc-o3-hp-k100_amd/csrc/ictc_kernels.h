@@ -29,24 +29,59 @@ constexpr int kBlock = kWave * kWavesPerBlock;
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
-// Sum over the 64 lanes of a wave, returned wave-uniform.  Within each row of
-// 16 lanes the sum is formed with DPP moves (quad xor 1, quad xor 2, half-row
-// mirror, row mirror: VALU only, no LDS traffic); the four row sums are then
-// read with readlane and added in a fixed order (deterministic).
+// DPP move within rows of 16 lanes (all rows and banks enabled).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_mov<0x141>(v);  // row_half_mirror
-  v += dpp_mov<0x140>(v);  // row_mirror
-  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-  return (r0 + r1) + (r2 + r3);
+
+// Sums over the wave of v[0..N) (N <= 16) by reduce-scatter: a permlane32
+// swap pairs component k with k+8 across the wave halves, a permlane16 swap
+// pairs k with k+4 across rows, so row r ends up with partial sums of
+// components 4r .. 4r+3 over 4 lanes each; four DPP row rotations (8, 4, 2, 1)
+// finish each row sum.  About 3 VALU ops per component instead of a full wave
+// reduction per component.  Lane 16r + k (k < 4) returns the total of
+// component 4r + k (wave_sums_slot); the addition order is fixed.
+template <int N>
+__device__ __forceinline__ float wave_sums(const float* v) {
+  static_assert(N >= 1 && N <= 16, "wave_sums covers up to 16 components");
+  float w[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    if (k < N || k + 8 < N) {
+      const float a = k < N ? v[k] : 0.f, b = k + 8 < N ? v[k + 8] : 0.f;
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+      w[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+      w[k] = 0.f;
+    }
+  }
+  float u[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (k < N || k + 4 < N || k + 8 < N || k + 12 < N) {
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(w[k]), __float_as_uint(w[k + 4]), false, false);
+      u[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+      u[k] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u[k] += dpp_mov<0x128>(u[k]);   // row_ror:8
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u[k] += dpp_mov<0x124>(u[k]);   // row_ror:4
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u[k] += dpp_mov<0x122>(u[k]);   // row_ror:2
+#pragma unroll
+  for (int k = 0; k < 4; ++k) u[k] += dpp_mov<0x121>(u[k]);   // row_ror:1
+  const int q = lane_id() & 3;
+  return q == 0 ? u[0] : (q == 1 ? u[1] : (q == 2 ? u[2] : u[3]));
+}
+
+// Component whose total wave_sums returns in this lane, or -1.
+__device__ __forceinline__ int wave_sums_slot() {
+  const int l = lane_id();
+  return (l & 15) < 4 ? 4 * (l >> 4) + (l & 15) : -1;
 }
 
 struct Operands {
@@ -219,14 +254,9 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
   }
   if (!dsh) return;
   float* out = group_target(dsh, dsh_part, rg.group, a.rows, T::NY);
-  // lane j (< NY) ends up holding this group's sum of component j
-  float mine = 0.f;
-#pragma unroll
-  for (int j = 0; j < T::NY; ++j) {
-    const float s = wave_sum(dyv[j]);
-    mine = lane_id() == j ? s : mine;
-  }
-  if (lane_id() < T::NY) out[e * T::NY + lane_id()] = mine;
+  const float mine = wave_sums<T::NY>(dyv);
+  const int j = wave_sums_slot();
+  if (j >= 0 && j < T::NY) out[e * T::NY + j] = mine;
 }
 
 // ---------------------------------------------------------------------------
@@ -350,9 +380,6 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
     const int32_t count = min(end - pos, kWave);
     Chunk<T> ch;
     stage_chunk<T>(a, src, csr.order, pos, count, ch);
-    float acc[T::NY];  // lane i: this group's harmonic gradient of the chunk's edge i
-#pragma unroll
-    for (int j = 0; j < T::NY; ++j) acc[j] = 0.f;
     for (int i = 0; i < count; ++i) {
       const int64_t e = lane_i(ch.e, i);
       const int64_t s = lane_i(ch.peer, i);
@@ -382,16 +409,11 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
         }
       }
       if (dsh) {
-#pragma unroll
-        for (int j = 0; j < T::NY; ++j) {
-          const float v = wave_sum(dyv[j]);
-          acc[j] = lane_id() == i ? v : acc[j];
-        }
+        // this group's harmonic gradient of edge e, one component per slot lane
+        const float v = wave_sums<T::NY>(dyv);
+        const int j = wave_sums_slot();
+        if (j >= 0 && j < T::NY) dsh_g[e * T::NY + j] = v;
       }
-    }
-    if (dsh && lane_id() < count) {
-#pragma unroll
-      for (int j = 0; j < T::NY; ++j) dsh_g[(int64_t)ch.e * T::NY + j] = acc[j];
     }
   }
 }

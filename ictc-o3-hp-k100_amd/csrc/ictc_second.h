@@ -52,13 +52,9 @@ __device__ __forceinline__ void zero(float* v) {
 // the output; group g > 0: its workspace slab, summed by launch_group_sum).
 template <class T>
 __device__ __forceinline__ void store_dsh(float* __restrict__ out, int64_t e, const float* dyv) {
-  float mine = 0.f;
-#pragma unroll
-  for (int j = 0; j < T::NY; ++j) {
-    const float s = wave_sum(dyv[j]);
-    mine = lane_id() == j ? s : mine;
-  }
-  if (lane_id() < T::NY) out[e * T::NY + lane_id()] = mine;
+  const float mine = wave_sums<T::NY>(dyv);
+  const int j = wave_sums_slot();
+  if (j >= 0 && j < T::NY) out[e * T::NY + j] = mine;
 }
 
 // dyv += dy(x, w, go) when want_dy; dacc += dg(x, y, go) when want_dg; one
@@ -229,8 +225,6 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge2, T::LI, T::LE, T::L
     stage_chunk<T>(a, src, csr.order, pos, count, ch);
     float tys[T::NY];
     stage_tangent<T>(t.sh, ch, count, tys);
-    float acc[T::NY];
-    zero<T::NY>(acc);
     for (int i = 0; i < count; ++i) {
       const int64_t e = lane_i(ch.e, i);
       const int64_t s = lane_i(ch.peer, i);
@@ -274,16 +268,11 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge2, T::LI, T::LE, T::L
         }
       }
       if (dsh) {
-#pragma unroll
-        for (int j = 0; j < T::NY; ++j) {
-          const float v = wave_sum(dyv[j]);
-          acc[j] = lane_id() == i ? v : acc[j];
-        }
+        // this group's harmonic gradient of edge e, one component per slot lane
+        const float v = wave_sums<T::NY>(dyv);
+        const int j = wave_sums_slot();
+        if (j >= 0 && j < T::NY) dsh_g[e * T::NY + j] = v;
       }
-    }
-    if (dsh && lane_id() < count) {
-#pragma unroll
-      for (int j = 0; j < T::NY; ++j) dsh_g[(int64_t)ch.e * T::NY + j] = acc[j];
     }
   }
 }
