@@ -102,14 +102,37 @@ __device__ __forceinline__ void load_harmonics(const float* __restrict__ sh, int
   for (int j = 0; j < T::NY; ++j) y[j] = p[j];
 }
 
+template <int N>
+__device__ __forceinline__ void load_row(const float* __restrict__ base, int C, int c, float* v) {
+  // wave-uniform row pointer stepped on the scalar unit + a 32-bit lane byte offset: the loads take
+  // the SGPR-base form with no per-load 64-bit vector address arithmetic.  The empty asm keeps the
+  // offset's zero extension next to the loads (hoisted out of a loop it hides the pattern).
+  uint32_t off = (uint32_t)c * 4u;
+  asm volatile("" : "+v"(off));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    v[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off);
+    base += C;
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c, const float* v) {
+  uint32_t off = (uint32_t)c * 4u;
+  asm volatile("" : "+v"(off));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + off) = v[i];
+    base += C;
+  }
+}
+
 // Gates of edge e for channel c, times the per-path weight (if any) and `scale`.
 // All P gate loads are issued before any use so they are in flight together;
 // the optional weight is a separate uniform branch after them.
 template <class T>
 __device__ __forceinline__ void load_gw(const Operands& a, int64_t e, int c, float scale, float* gw) {
-  const float* g = a.gates + e * (int64_t)(T::P * a.channels) + c;
-#pragma unroll
-  for (int p = 0; p < T::P; ++p) gw[p] = g[p * a.channels];
+  load_row<T::P>(a.gates + e * (int64_t)(T::P * a.channels), a.channels, c, gw);
   if (a.weight) {
     float w[T::P];
 #pragma unroll
@@ -119,18 +142,6 @@ __device__ __forceinline__ void load_gw(const Operands& a, int64_t e, int c, flo
   }
 #pragma unroll
   for (int p = 0; p < T::P; ++p) gw[p] *= scale;
-}
-
-template <int N>
-__device__ __forceinline__ void load_row(const float* __restrict__ base, int C, int c, float* v) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = base[i * C + c];
-}
-
-template <int N>
-__device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c, const float* v) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) base[i * C + c] = v[i];
 }
 
 // ---------------------------------------------------------------------------

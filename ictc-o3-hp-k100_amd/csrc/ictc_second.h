@@ -28,9 +28,7 @@ struct Tangents {
 template <class T>
 __device__ __forceinline__ void load_gates(const float* __restrict__ base, const Operands& a, int64_t e, int c,
                                            float scale, float* gw) {
-  const float* g = base + e * (int64_t)(T::P * a.channels) + c;
-#pragma unroll
-  for (int p = 0; p < T::P; ++p) gw[p] = g[p * a.channels];
+  load_row<T::P>(base + e * (int64_t)(T::P * a.channels), a.channels, c, gw);
   if (a.weight) {
     float w[T::P];
 #pragma unroll
