@@ -122,10 +122,13 @@ def sc_struct(li, lt, corr):
     L.append(f"  static constexpr int TERMS = {nterms};")
 
     def load_weights():
-        s = ["    const int64_t sb = s;"]
-        for (Lo, nu, p) in wq:
+        # species row of each weight block (wave-uniform) + the lane's byte offset: SGPR-base loads
+        s = ["    const int64_t sb = s;", "    const uint32_t off = sc_lane_offset(c);"]
+        for (Lo, nu) in sorted({(Lo, nu) for (Lo, nu, p) in wq}):
             P = counts[(Lo, nu)]
-            s.append(f"    const float w{Lo}_{nu}_{p} = t.w[{Lo}][{nu - 1}][(sb * {P} + {p}) * C + c];")
+            s.append(f"    const float* __restrict__ wb{Lo}_{nu} = t.w[{Lo}][{nu - 1}] + sb * {P} * C;")
+        for (Lo, nu, p) in wq:
+            s.append(f"    const float w{Lo}_{nu}_{p} = sc_load(wb{Lo}_{nu} + {p} * C, off);")
         return s
 
     # forward
@@ -247,6 +250,15 @@ def generate(path):
     parts = ["// Generated by csrc/gen_sc.py from the frozen ICTC basis and the e3nn/MACE coupling. Do not edit.",
              "#pragma once", "#include <stdint.h>", "namespace ictc {",
              "struct ScWeights { const float* w[4][3]; };",
+             "// Lane byte offset kept opaque so that its zero extension stays next to each load.",
+             "__device__ __forceinline__ uint32_t sc_lane_offset(int c) {",
+             "  uint32_t off = (uint32_t)c * 4u;",
+             "  asm volatile(\"\" : \"+v\"(off));",
+             "  return off;",
+             "}",
+             "__device__ __forceinline__ float sc_load(const float* __restrict__ row, uint32_t off) {",
+             "  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(row) + off);",
+             "}",
              "template <int LI, int LT, int CORR> struct Sc;"]
     cfgs = []
     for li, lt in CONFIGS:

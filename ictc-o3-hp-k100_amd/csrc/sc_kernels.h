@@ -28,13 +28,15 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 
 template <int N>
 __device__ __forceinline__ void load(const float* __restrict__ b, int C, int c, float* v) {
+  const uint32_t off = sc_lane_offset(c);
 #pragma unroll
-  for (int i = 0; i < N; ++i) v[i] = b[i * C + c];
+  for (int i = 0; i < N; ++i) v[i] = sc_load(b + (int64_t)i * C, off);
 }
 template <int N>
 __device__ __forceinline__ void store(float* __restrict__ b, int C, int c, const float* v) {
+  const uint32_t off = sc_lane_offset(c);
 #pragma unroll
-  for (int i = 0; i < N; ++i) b[i * C + c] = v[i];
+  for (int i = 0; i < N; ++i) *reinterpret_cast<float*>(reinterpret_cast<char*>(b + (int64_t)i * C) + off) = v[i];
 }
 
 struct Args {
