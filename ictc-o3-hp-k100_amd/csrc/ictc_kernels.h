@@ -292,6 +292,17 @@ __device__ __forceinline__ int64_t visit_row(const Csr& csr, int64_t slot, int64
   return n >= 0 && n < rows ? n : -1;
 }
 
+// Part `part` of `parts` equal shares of row n's CSR segment (receiver-owned
+// kernels whose outputs are per edge split long rows over several waves when
+// the graph has too few rows to fill the GPU).  False when the share is empty.
+__device__ __forceinline__ bool row_part(const Csr& csr, int64_t n, int part, int parts, int32_t& beg, int32_t& end) {
+  const int32_t b = csr.ptr[n], e = csr.ptr[n + 1];
+  const int32_t per = (e - b + parts - 1) / parts;
+  beg = b + part * per;
+  end = min(e, beg + per);
+  return beg < end;
+}
+
 // Edge metadata of a chunk of up to 64 consecutive CSR positions, staged one
 // edge per lane with coalesced loads; the edge loop then reads it with
 // readlane (wave-uniform SGPR values, no memory latency inside the loop).
@@ -371,11 +382,14 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO>::value)) void msg_bwd_edge_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad, float* __restrict__ dsh,
-    float* __restrict__ dsh_part, float* __restrict__ dgates) {
+    float* __restrict__ dsh_part, float* __restrict__ dgates, int parts) {
   const RowGroup rg = row_group_y_xcd();
-  if (rg.row > a.rows) return;
-  const int64_t n = visit_row(csr, rg.row, a.rows);
+  const int64_t slot = rg.row / parts;
+  if (slot > a.rows) return;
+  const int64_t n = visit_row(csr, slot, a.rows);
   if (n < 0) return;
+  int32_t beg, end;
+  if (!row_part(csr, n, (int)(rg.row % parts), parts, beg, end)) return;
   const bool tail = n == a.rows;
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
@@ -386,7 +400,6 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
 #pragma unroll
     for (int k = 0; k < T::NO; ++k) go[k] = 0.f;
   }
-  const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
   for (int32_t pos = beg; pos < end; pos += kWave) {
     const int32_t count = min(end - pos, kWave);
     Chunk<T> ch;

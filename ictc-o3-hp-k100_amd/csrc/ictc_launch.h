@@ -48,4 +48,14 @@ hipError_t dispatch_tp(const TpShape& s, F&& f) {
 
 inline unsigned blocks_for(int64_t waves) { return (unsigned)((waves + kWavesPerBlock - 1) / kWavesPerBlock); }
 
+// Waves per row for the receiver-owned per-edge kernels: enough shares of
+// each row's edges to give about 32k waves when the graph has few rows (up to
+// 8 per row; 1 for large graphs).
+inline int row_parts(int64_t row_slots, int groups) {
+  const int64_t waves = row_slots * groups;
+  if (waves <= 0) return 1;
+  const int64_t p = (32768 + waves - 1) / waves;
+  return (int)(p < 1 ? 1 : (p > 8 ? 8 : p));
+}
+
 }  // namespace ictc

@@ -202,11 +202,14 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd2, T::LI, T::LE, T::LO>::
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge2, T::LI, T::LE, T::LO>::value)) void msg_bwd_edge2_kernel(
     Operands a, Tangents t, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad,
-    float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates) {
+    float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates, int parts) {
   const RowGroup rg = row_group_y_xcd();
-  if (rg.row > a.rows) return;
-  const int64_t n = visit_row(csr, rg.row, a.rows);
+  const int64_t slot = rg.row / parts;
+  if (slot > a.rows) return;
+  const int64_t n = visit_row(csr, slot, a.rows);
   if (n < 0) return;
+  int32_t beg, end;
+  if (!row_part(csr, n, (int)(rg.row % parts), parts, beg, end)) return;
   const bool tail = n == a.rows;
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
@@ -216,7 +219,6 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge2, T::LI, T::LE, T::L
   else zero<T::NO>(go);
   const bool need_x = (dsh && t.gates) || (dgates && t.sh);
   const bool need_tx = t.x != nullptr;
-  const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
   for (int32_t pos = beg; pos < end; pos += kWave) {
     const int32_t count = min(end - pos, kWave);
     Chunk<T> ch;

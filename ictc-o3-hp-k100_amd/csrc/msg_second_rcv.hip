@@ -23,8 +23,9 @@ struct MsgSecondRcv {
       if (err != hipSuccess) return err;
     }
     if (dsh || dg) {
-      hipLaunchKernelGGL((msg_bwd_edge2_kernel<T>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock), 0, st, a, t, src,
-                         csr, grad, dsh, ws, dg);
+      const int parts = row_parts(a.rows + 1, G);
+      hipLaunchKernelGGL((msg_bwd_edge2_kernel<T>), dim3(blocks_for((a.rows + 1) * parts), G), dim3(kBlock), 0, st,
+                         a, t, src, csr, grad, dsh, ws, dg, parts);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess || !dsh) return err;
       return launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st);
