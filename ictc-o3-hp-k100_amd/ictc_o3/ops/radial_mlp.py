@@ -67,17 +67,22 @@ def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a^T b over edge rows: the split-reduction kernel while the output alone cannot fill the GPU
+    (up to 16 tiles of 64 x 64), the library GEMM otherwise."""
+    tiles = -(-a.shape[1] // 64) * -(-b.shape[1] // 64)
+    if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda and tiles <= 16:
+        return _gemm_tn(a, b)
+    return a.t() @ b
+
+
 class _WeightGrad(torch.autograd.Function):
     """a^T b over edge rows (a weight gradient); differentiable in a and b."""
 
     @staticmethod
     def forward(ctx, a, b):
         ctx.save_for_backward(a, b)
-        tiles = -(-a.shape[1] // 64) * -(-b.shape[1] // 64)
-        # the split pays off while the output alone cannot fill the GPU (up to 16 tiles of 64 x 64)
-        if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda and tiles <= 16:
-            return _gemm_tn(a, b)
-        return a.t() @ b
+        return weight_grad(a, b)
 
     @staticmethod
     def backward(ctx, h):
@@ -198,7 +203,7 @@ class _RadialGates(torch.autograd.Function):
             nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
                      nat.ptr(W2), nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
             R = _radial(0, r, None, None, 8, cutoff, poly_p)
-            dW = [dz1.t() @ R, dz2.t() @ a1, dz3.t() @ a2, dg.t() @ a3]
+            dW = [weight_grad(dz1, R), weight_grad(dz2, a1), weight_grad(dz3, a2), weight_grad(dg, a3)]
         return (dr if needs[0] else None, *[d if n else None for d, n in zip(dW, needs[1:5])], None, None, None)
 
 
