@@ -6,7 +6,8 @@ site).  Shapes (C channels, N nodes):
   path_linear    out[n, l*l+m, :] = scale * W_l @ concat_k msg[n, l, k, m, :] (message_linear / avg_num_neighbors)
   species_linear out[n, :] = W[s_n] @ x[n, :]                               (element-conditioned self-connection)
 The composable forms below are FP32 GEMMs through the ROCm BLAS library (TF32
-off) and stay differentiable to any order; ``degree_linear_fast`` /
+off) whose weight gradients over the tall row dimension run on the
+split-reduction kernel (``edge_linear``); they stay differentiable to any order; ``degree_linear_fast`` /
 ``path_linear_fast`` run the same maps on the hand-written MFMA kernel
 (``ictc_packed_linear``) for first-derivative callers (energy + forces).
 """
@@ -16,6 +17,8 @@ from typing import Dict, List
 
 import torch
 
+from ictc_o3.ops.radial_mlp import edge_linear
+
 
 def degree_linear(x: torch.Tensor, weights: List[torch.Tensor], C: int, lmax: int, scale: float = 1.0):
     N = x.shape[0]
@@ -23,7 +26,7 @@ def degree_linear(x: torch.Tensor, weights: List[torch.Tensor], C: int, lmax: in
     for l in range(lmax + 1):
         blk = x[:, l * l * C:(l + 1) ** 2 * C].reshape(N * (2 * l + 1), C)
         w = weights[l] if scale == 1.0 else weights[l] * scale
-        parts.append(torch.matmul(blk, w.t()).reshape(N, (2 * l + 1) * C))
+        parts.append(edge_linear(blk, w).reshape(N, (2 * l + 1) * C))
     return torch.cat(parts, 1)
 
 
@@ -35,7 +38,7 @@ def path_linear(m: torch.Tensor, weights: List[torch.Tensor], counts: Dict[int, 
         k, w = counts.get(l, 0), 2 * l + 1
         blk = m[:, off:off + k * w * C].reshape(N, k, w, C).transpose(1, 2).reshape(N * w, k * C)
         off += k * w * C
-        parts.append(torch.matmul(blk, (weights[l] * scale).t()).reshape(N, w * C))
+        parts.append(edge_linear(blk, weights[l] * scale).reshape(N, w * C))
     return torch.cat(parts, 1)
 
 
