@@ -588,7 +588,8 @@ def run_cfg5(args):
     dt = (time.perf_counter() - t0) / args.steps
     log(f"cfg5: N={N} E={E} step={dt * 1e3:.2f} ms loss={float(loss):.4f}")
     kern, nbytes = layer_message_kernels(model, src, dst, N, None, reps=10)
-    achieved = nbytes["msg_fwd"] / kern["msg_fwd"] / 1e9
+    dom = max(kern, key=kern.get)   # the layer-1 message kernel with the largest time
+    achieved = nbytes[dom] / kern[dom] / 1e9
     result = {
         "metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": dt * 1e3, "higher_is_better": True, "scaling": "weak",
@@ -601,7 +602,7 @@ def run_cfg5(args):
                    "atoms": N, "edges": E, "channels": 128,
                    "kernel_us_layer1": {k: round(t * 1e6, 2) for k, t in kern.items()},
                    "kernel_algorithmic_MB_layer1": {k: round(v / 1e6, 2) for k, v in nbytes.items()}},
-        "roofline": {"bound": "hbm", "kernel": "msg_fwd (layer 1, P17 C128)",
+        "roofline": {"bound": "hbm", "kernel": f"{dom} (layer 1, P17 C128)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": None},
     }
