@@ -16,6 +16,13 @@
 // interleaved over 16 waves, the 16 wave sums combined in wave order), so the
 // result does not depend on scheduling.
 //
+// Wide outputs (more than 16 tiles, e.g. the 2,176 x 64 gradient of a gate
+// projection) are MFMA-bound in FP32 (about 65 TFLOP/s measured); they run
+// the same tiling on bf16 MFMA with the three-way operand split (six
+// v_mfma_f32_16x16x32_bf16 per 16x16x32 step, FP32-level accuracy): each
+// 32-row slab is split once while it is staged, into hi / mid / lo planes
+// stored reduction-index-contiguous, so every operand is one 16-byte LDS read.
+//
 // Block order: the tiles of one chunk are consecutive logical blocks, and the
 // logical range is split contiguously over the 8 XCDs, so the chunk's rows of
 // the shared operand are fetched into one XCD's L2 and reused by its tiles.
@@ -24,6 +31,7 @@
 #include <stdio.h>
 
 #include "../../include/ictc_mi355x.h"
+#include "split_bf16.h"
 
 namespace ictc {
 int set_error(int code, const char* msg);
@@ -55,7 +63,7 @@ int cu_count() {
 
 struct Plan {
   int mt, nt, chunks;
-  int64_t rows;      // reduction rows per chunk (multiple of kSlab)
+  int64_t rows;      // reduction rows per chunk (multiple of 32)
   int64_t blocks;    // launched blocks (logical count rounded up to a multiple of kXcds)
 };
 
@@ -66,13 +74,16 @@ Plan plan_for(int64_t K, int M, int N) {
   const int64_t tiles = (int64_t)p.mt * p.nt;
   const int64_t want = (int64_t)cu_count() * 8;          // about 8 blocks (32 waves) per CU
   int64_t chunks = (want + tiles - 1) / tiles;
+  // Wide outputs: every tile of a chunk re-reads the chunk's rows of B, so keep the chunks an XCD runs at
+  // once (about 160 blocks, i.e. 160 / tiles chunks) within its 4 MB L2: about 2,048 rows per chunk.
+  if (tiles > 16 && chunks < (K + 2047) / 2048) chunks = (K + 2047) / 2048;
   const int64_t max_chunks = (K + 63) / 64;               // at least 64 rows per chunk
   if (chunks > max_chunks) chunks = max_chunks;
   if (chunks > 1024) chunks = 1024;
   if (chunks < 1) chunks = 1;
   int64_t rows = (K + chunks - 1) / chunks;
-  rows = (rows + kSlab - 1) / kSlab * kSlab;
-  if (rows < kSlab) rows = kSlab;
+  rows = (rows + 31) / 32 * 32;   // whole slabs of both kernels (16 and 32 rows)
+  if (rows < 32) rows = 32;
   chunks = K > 0 ? (K + rows - 1) / rows : 1;
   p.chunks = (int)chunks;
   p.rows = rows;
@@ -154,6 +165,94 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __res
   }
 }
 
+constexpr int kSlabB = 32;     // reduction rows per stage of the bf16 kernel (one MFMA K)
+constexpr int kPlanePitch = 40;  // bf16 per plane row: 32 + 8 (80 bytes: 16-byte reads of 8 rows hit distinct banks)
+
+__device__ __forceinline__ v4f mfma16(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* __restrict__ A, int64_t K, int M,
+                                                                   int64_t lda, const float* __restrict__ B, int N,
+                                                                   int64_t ldb, float* __restrict__ part, int mt,
+                                                                   int nt, int chunks, int64_t rows, int64_t blocks) {
+  const int64_t per = blocks / kXcds;
+  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
+  const int64_t tiles = (int64_t)mt * nt;
+  if (logical >= tiles * chunks) return;
+  const int tile = (int)(logical % tiles);
+  const int chunk = (int)(logical / tiles);
+  const int m0 = (tile % mt) * kTile, n0 = (tile / mt) * kTile;
+  const int64_t k0 = (int64_t)chunk * rows;
+  const int64_t k1 = k0 + rows < K ? k0 + rows : K;
+
+  // planes[operand][part][column][k]: column = m (A) or n (B) within the tile
+  __shared__ __attribute__((aligned(16))) __bf16 planes[2][3][kTile][kPlanePitch];
+  const int t = threadIdx.x, col = t & 63, r0 = t >> 6;   // staging: column col, slab rows 8 r0 .. 8 r0 + 7
+  const int lane = t & 63, wave = t >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const bool a_col = m0 + col < M, b_col = n0 + col < N;
+  const float* __restrict__ Ap = A + m0 + col;
+  const float* __restrict__ Bp = B + n0 + col;
+
+  float ra[8], rb[8];
+  auto load = [&](int64_t k) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t kr = k + 8 * r0 + e;
+      const bool in = kr < k1;
+      ra[e] = (in && a_col) ? Ap[kr * lda] : 0.f;
+      rb[e] = (in && b_col) ? Bp[kr * ldb] : 0.f;
+    }
+  };
+
+  v4f acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+  if (k0 < k1) load(k0);
+  for (int64_t k = k0; k < k1; k += kSlabB) {
+    const Split sa = split8(ra), sb = split8(rb);
+    __syncthreads();
+    *reinterpret_cast<bf16x8*>(&planes[0][0][col][8 * r0]) = sa.hi;
+    *reinterpret_cast<bf16x8*>(&planes[0][1][col][8 * r0]) = sa.mid;
+    *reinterpret_cast<bf16x8*>(&planes[0][2][col][8 * r0]) = sa.lo;
+    *reinterpret_cast<bf16x8*>(&planes[1][0][col][8 * r0]) = sb.hi;
+    *reinterpret_cast<bf16x8*>(&planes[1][1][col][8 * r0]) = sb.mid;
+    *reinterpret_cast<bf16x8*>(&planes[1][2][col][8 * r0]) = sb.lo;
+    __syncthreads();
+    if (k + kSlabB < k1) load(k + kSlabB);
+    // A operand: row m = 16 wave + li, reduction rows 8 lg .. 8 lg + 7 of the slab
+    const int am = 16 * wave + li;
+    const bf16x8 ahi = *reinterpret_cast<const bf16x8*>(&planes[0][0][am][8 * lg]);
+    const bf16x8 amid = *reinterpret_cast<const bf16x8*>(&planes[0][1][am][8 * lg]);
+    const bf16x8 alo = *reinterpret_cast<const bf16x8*>(&planes[0][2][am][8 * lg]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int bn = 16 * j + li;
+      const bf16x8 bhi = *reinterpret_cast<const bf16x8*>(&planes[1][0][bn][8 * lg]);
+      const bf16x8 bmid = *reinterpret_cast<const bf16x8*>(&planes[1][1][bn][8 * lg]);
+      const bf16x8 blo = *reinterpret_cast<const bf16x8*>(&planes[1][2][bn][8 * lg]);
+      acc[j] = mfma16(alo, bhi, acc[j]);
+      acc[j] = mfma16(ahi, blo, acc[j]);
+      acc[j] = mfma16(amid, bmid, acc[j]);
+      acc[j] = mfma16(amid, bhi, acc[j]);
+      acc[j] = mfma16(ahi, bmid, acc[j]);
+      acc[j] = mfma16(ahi, bhi, acc[j]);
+    }
+  }
+
+  float* __restrict__ P = part + (int64_t)chunk * M * N;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 16 * j + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 16 * wave + 4 * lg + r;
+      if (m < M && n < N) P[(int64_t)m * N + n] = acc[j][r];
+    }
+  }
+}
+
 // out[i] = sum over chunks of part[c][i]: wave w of a block adds chunks
 // w, w + 16, ... for 64 consecutive outputs; the wave sums meet in LDS and
 // are added in wave order.
@@ -196,8 +295,12 @@ int ictc_gemm_tn(const float* a, int64_t k, int64_t m, int64_t lda, const float*
     return fail(ICTC_ERR_ARGUMENT, "gemm_tn: workspace smaller than ictc_gemm_tn_workspace_bytes");
   float* part = static_cast<float*>(workspace);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(gemm_tn_partial_kernel, dim3((unsigned)p.blocks), dim3(256), 0, st, a, k, (int)m, lda, b,
-                     (int)n, ldb, part, p.mt, p.nt, p.chunks, p.rows, p.blocks);
+  if ((int64_t)p.mt * p.nt > 16)
+    hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel, dim3((unsigned)p.blocks), dim3(256), 0, st, a, k, (int)m, lda, b,
+                       (int)n, ldb, part, p.mt, p.nt, p.chunks, p.rows, p.blocks);
+  else
+    hipLaunchKernelGGL(gemm_tn_partial_kernel, dim3((unsigned)p.blocks), dim3(256), 0, st, a, k, (int)m, lda, b,
+                       (int)n, ldb, part, p.mt, p.nt, p.chunks, p.rows, p.blocks);
   const int64_t total = m * n;
   hipLaunchKernelGGL(gemm_tn_sum_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64 * kSumWaves), 0, st, part,
                      total, p.chunks, out);
