@@ -23,6 +23,7 @@
 #include <stdio.h>
 
 #include "../../include/ictc_mi355x.h"
+#include "split_bf16.h"
 
 namespace ictc {
 int set_error(int code, const char* msg);
@@ -37,37 +38,6 @@ constexpr int kK = 64;           // hidden width (reduction length)
 constexpr int kEdgesPerBlock = 256;
 constexpr int kTiles = kEdgesPerBlock / 16;
 
-union Bf8 {
-  bf16x8 v;
-  uint16_t u[8];
-};
-
-struct Split {
-  bf16x8 hi, mid, lo;
-};
-
-// bf16 (as the upper half of an FP32 bit pattern) nearest to x, ties to even.
-__device__ __forceinline__ uint32_t round_bf16(float x) {
-  uint32_t u = __float_as_uint(x);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u & 0xFFFF0000u;
-}
-
-__device__ __forceinline__ Split split8(const float* v) {
-  Bf8 h, m, l;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint32_t hb = round_bf16(v[e]);
-    const float r1 = v[e] - __uint_as_float(hb);
-    const uint32_t mb = round_bf16(r1);
-    const float r2 = r1 - __uint_as_float(mb);
-    const uint32_t lb = round_bf16(r2);
-    h.u[e] = (uint16_t)(hb >> 16);
-    m.u[e] = (uint16_t)(mb >> 16);
-    l.u[e] = (uint16_t)(lb >> 16);
-  }
-  return {h.v, m.v, l.v};
-}
 
 __device__ __forceinline__ v4f mfma(bf16x8 a, bf16x8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);

@@ -68,10 +68,9 @@ def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """a^T b over edge rows: the split-reduction kernel while the output alone cannot fill the GPU
-    (up to 16 tiles of 64 x 64), the library GEMM otherwise."""
-    tiles = -(-a.shape[1] // 64) * -(-b.shape[1] // 64)
-    if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda and tiles <= 16:
+    """a^T b over edge rows on the split-reduction kernel (FP32 MFMA up to 16 output tiles of 64 x 64,
+    split-bf16 MFMA beyond); the library GEMM below _TN_MIN_ROWS rows."""
+    if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda:
         return _gemm_tn(a, b)
     return a.t() @ b
 
