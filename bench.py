@@ -459,9 +459,9 @@ def run_cfg3(args):
     species = torch.randint(0, S, (N,), device=dev, generator=g)
     go = torch.randn(N, 4 * C, device=dev, generator=g)
 
-    def step():
+    def step():   # SC forward + feature adjoint (dx returned, not accumulated into x.grad)
         out = mod.contract(x, species)
-        torch.autograd.backward(out, go)
+        return torch.autograd.grad(out, x, go)
 
     for _ in range(max(args.warmup, 3)):
         step()
