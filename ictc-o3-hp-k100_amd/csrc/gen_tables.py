@@ -85,6 +85,13 @@ def tp_struct(li, le, lo):
         expr = " + ".join(f"{f(v)} * (x[{i}] * y[{j}])" for i, j, v in terms)
         lines.append(f"    o[{k}] = fmaf(gw[{p}], {expr}, o[{k}]);")
     lines.append("  }")
+    # forward grouped like the adjoints (o[k] += gw[p] sum_j y[j] B_jk(x)): fewer VALU ops, more live
+    # values; used where a single forward is the kernel's only contraction
+    lines.append("  __device__ __forceinline__ static void fwd_b(const float* __restrict__ x, const float* __restrict__ y,"
+                 " const float* __restrict__ gw, float* __restrict__ o) {")
+    for k, js in sorted(by_kj.items()):
+        lines.append(f"    o[{k}] = fmaf(gw[{path_of[k]}], {t_expr('x', 'y', js)}, o[{k}]);")
+    lines.append("  }")
     # dx: d[i] += sum_j y[j] sum_p gw[p] sum_{k in p} C go[k]
     lines.append("  __device__ __forceinline__ static void dx(const float* __restrict__ y, const float* __restrict__ gw,"
                  " const float* __restrict__ go, float* __restrict__ d) {")

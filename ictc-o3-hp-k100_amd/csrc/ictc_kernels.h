@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
         float xv[T::NX], gw[T::P];
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
         load_gw<T>(a, e, c, m, gw);
-        T::fwd(xv, y, gw, o);
+        T::fwd_b(xv, y, gw, o);
       }
     }
   }
