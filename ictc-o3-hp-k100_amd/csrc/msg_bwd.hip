@@ -31,8 +31,8 @@ struct MsgBwd {
     if (dsh || dg) {
       // rows + 1 row slots: the last one zero-fills the out-of-range tail segment.
       const int parts = row_parts(a.rows + 1, G);
-      hipLaunchKernelGGL((msg_bwd_edge_kernel<T>), dim3(blocks_for((a.rows + 1) * parts), G), dim3(kBlock), 0, st,
-                         a, src, dcsr, grad, dsh, ws, dg, parts);
+      hipLaunchKernelGGL((msg_bwd_edge_kernel<T>), dim3(blocks_for((a.rows + 1) * parts), G), dim3(kBlock), 0,
+                         st, a, src, dcsr, grad, dsh, ws, dg, parts);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
       if (dsh && (err = launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st)) != hipSuccess) return err;

@@ -487,6 +487,16 @@ int cu_count() {
   return cached[dev];
 }
 
+// Blocks of `kernel` resident per CU (LDS, registers), at most `want`: the
+// persistent kernels below size their grid to what runs at once, so that no
+// block waits for a second round on a half-empty GPU.
+template <class K>
+int resident_per_cu(K kernel, int threads, int want) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess || n <= 0) n = 1;
+  return n < want ? n : want;
+}
+
 unsigned grid_for(int64_t edges, int waves, int blocks_per_cu) {
   const int64_t tiles = (edges + 15) / 16, need = (tiles + waves - 1) / waves;
   const int64_t cap = (int64_t)cu_count() * blocks_per_cu;
@@ -506,7 +516,8 @@ int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden
   if (edges == 0) return ICTC_OK;
   if (!r || !W1 || !W2 || !W3 || !a3) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
   if (!aligned16(a3)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: a3 must be 16-byte aligned");
-  hipLaunchKernelGGL(mlp_fwd_kernel, dim3(grid_for(edges, FWD_WAVES, 3)), dim3(FWD_WAVES * 64), 0,
+  const int fwd_per_cu = resident_per_cu(mlp_fwd_kernel, FWD_WAVES * 64, 3);
+  hipLaunchKernelGGL(mlp_fwd_kernel, dim3(grid_for(edges, FWD_WAVES, fwd_per_cu)), dim3(FWD_WAVES * 64), 0,
                      (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, a3);
   return launch_status("ictc_radial_mlp_fwd launch");
 }
@@ -533,7 +544,7 @@ int ictc_radial_gates_fwd(const float* r, int64_t edges, int num_basis, int hidd
                      (bf16x8*)workspace);
   if (int rc = launch_status("ictc_radial_gates_fwd split")) return rc;
   const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
-  const int64_t cap = (int64_t)cu_count() * 3;
+  const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel, GATE_TILES * 64, 3);
   hipLaunchKernelGGL(gates_fwd_kernel, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0, st, r,
                      edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates, out);
   return launch_status("ictc_radial_gates_fwd launch");
@@ -549,7 +560,8 @@ int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden
   for (const float* p : {da3, (const float*)dz1, (const float*)dz2, (const float*)dz3, (const float*)a1,
                          (const float*)a2})
     if (p && !aligned16(p)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: [E, 64] operands must be 16-byte aligned");
-  hipLaunchKernelGGL(mlp_bwd_kernel, dim3(grid_for(edges, BWD_WAVES, 1)), dim3(BWD_WAVES * 64), 0,
+  const int bwd_per_cu = resident_per_cu(mlp_bwd_kernel, BWD_WAVES * 64, 1);
+  hipLaunchKernelGGL(mlp_bwd_kernel, dim3(grid_for(edges, BWD_WAVES, bwd_per_cu)), dim3(BWD_WAVES * 64), 0,
                      (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, dr, dz1, dz2, dz3,
                      a1, a2);
   return launch_status("ictc_radial_mlp_bwd launch");
