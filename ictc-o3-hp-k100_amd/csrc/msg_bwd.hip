@@ -38,8 +38,8 @@ struct MsgBwd {
       if (dsh && (err = launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st)) != hipSuccess) return err;
     }
     if (dx) {
-      hipLaunchKernelGGL((msg_bwd_x_kernel<T>), dim3(blocks_for(a.rows), G), dim3(kBlock), bwd_x_lds_cap<T>(a.rows), st, a,
-                         dst, scsr, grad, dx);
+      hipLaunchKernelGGL((msg_bwd_x_kernel<T>), dim3(blocks_for(a.rows), G), dim3(kBlock), bwd_x_lds_cap<T>(a.rows),
+                         st, a, dst, scsr, grad, dx);
       return hipGetLastError();
     }
     return hipSuccess;
