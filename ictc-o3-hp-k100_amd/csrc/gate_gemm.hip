@@ -248,10 +248,15 @@ int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float*
     return fail(ICTC_ERR_ARGUMENT, "gate adjoint: operands must be 16-byte aligned");
   const int S = gates / 64;
   const int64_t tiles = (edges + 15) / 16;
-  const int per_cu = S >= 8 ? 1 : (S >= 4 ? 2 : 4);
+  const size_t lds = sizeof(float) * 2 * S * 16 * kRedRow;
+  // persistent blocks: as many as are resident at once (LDS and registers), so none waits for a second round
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_gemm_nn_kernel, 64 * S, lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  if (per_cu > 4) per_cu = 4;
   const int64_t want = (int64_t)cu_count() * per_cu;
   const unsigned blocks = (unsigned)(tiles < want ? tiles : want);
-  const size_t lds = sizeof(float) * 2 * S * 16 * kRedRow;
   hipLaunchKernelGGL(gate_gemm_nn_kernel, dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream, grad, edges, weight,
                      gates, dhidden);
   hipError_t e = hipGetLastError();
