@@ -13,36 +13,26 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-union Bf8 {
-  bf16x8 v;
-  uint16_t u[8];
-};
-
 struct Split {
   bf16x8 hi, mid, lo;
 };
 
-// bf16 (as the upper half of an FP32 bit pattern) nearest to x, ties to even.
-__device__ __forceinline__ uint32_t round_bf16(float x) {
-  uint32_t u = __float_as_uint(x);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u & 0xFFFF0000u;
-}
-
+// The conversions use gfx950's f32 -> bf16 convert (v_cvt_pk_bf16_f32, round
+// to nearest even): the same parts as rounding the bit pattern by hand, in
+// about a third of the VALU operations.
 __device__ __forceinline__ Split split8(const float* v) {
-  Bf8 h, m, l;
+  bf16x8 h, m, l;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const uint32_t hb = round_bf16(v[e]);
-    const float r1 = v[e] - __uint_as_float(hb);
-    const uint32_t mb = round_bf16(r1);
-    const float r2 = r1 - __uint_as_float(mb);
-    const uint32_t lb = round_bf16(r2);
-    h.u[e] = (uint16_t)(hb >> 16);
-    m.u[e] = (uint16_t)(mb >> 16);
-    l.u[e] = (uint16_t)(lb >> 16);
+    const __bf16 hb = (__bf16)v[e];
+    const float r1 = v[e] - (float)hb;
+    const __bf16 mb = (__bf16)r1;
+    const float r2 = r1 - (float)mb;
+    h[e] = hb;
+    m[e] = mb;
+    l[e] = (__bf16)r2;
   }
-  return {h.v, m.v, l.v};
+  return {h, m, l};
 }
 
 }  // namespace
