@@ -98,9 +98,8 @@ class _EdgeLinear(torch.autograd.Function):
     def forward(ctx, x, W):
         ctx.save_for_backward(x, W)
         ctx.inputs = (x, W)
-        if (x.is_cuda and x.shape[0] >= _TN_MIN_ROWS and x.shape[1] == 64 and W.shape[0] % 16 == 0
-                and W.shape[0] > 64):
-            return gate_projection(x, W)   # the wide gate projection: split-bf16 MFMA, FP32-level accuracy
+        if x.is_cuda and x.shape[0] >= _TN_MIN_ROWS and x.shape[1] == 64 and W.shape[0] % 16 == 0:
+            return gate_projection(x, W)   # split-bf16 MFMA, FP32-level accuracy (hidden layers and projection)
         return x @ W.t()
 
     @staticmethod
@@ -122,7 +121,7 @@ class _EdgeLinearT(torch.autograd.Function):
         ctx.save_for_backward(u, W)
         ctx.inputs = (u, W)
         M = W.shape[0]
-        if u.is_cuda and u.shape[0] >= _TN_MIN_ROWS and W.shape[1] == 64 and M % 64 == 0 and 64 < M <= 768:
+        if u.is_cuda and u.shape[0] >= _TN_MIN_ROWS and W.shape[1] == 64 and M % 64 == 0 and M <= 768:
             return gate_projection_adjoint(u, W)   # split-bf16 MFMA, FP32-level accuracy
         return u @ W
 
