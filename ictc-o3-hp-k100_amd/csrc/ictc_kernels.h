@@ -117,6 +117,12 @@ __device__ __forceinline__ void load_row(const float* __restrict__ base, int C, 
 }
 
 template <int N>
+__device__ __forceinline__ void zero_row(float* v) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = 0.f;
+}
+
+template <int N>
 __device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c, const float* v) {
   uint32_t off = (uint32_t)c * 4u;
   asm volatile("" : "+v"(off));
@@ -160,7 +166,9 @@ constexpr int kMaxGroups = 4;
 // Minimum waves per SIMD requested for each (kernel, degree triple): the
 // highest of 4, 3, 2, 1 at which the kernel compiles without register spills,
 // found by tune_occupancy.py and recorded in ictc_occupancy.h.
-enum KernelKind { kEdgeFwd, kEdgeBwd, kMsgFwd, kMsgBwdEdge, kMsgBwdX, kEdgeSecond, kMsgFwd2, kMsgBwdEdge2, kMsgBwdX2 };
+enum KernelKind {
+  kEdgeFwd, kEdgeBwd, kMsgFwd, kMsgBwdEdge, kMsgBwdX, kEdgeSecond, kMsgFwd2, kMsgBwdEdge2, kMsgBwdX2, kMsgBwdSrc
+};
 template <int K, int LI, int LE, int LO>
 struct Occupancy {
 #ifdef ICTC_OCCUPANCY_PROBE
@@ -477,6 +485,73 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::
     }
   }
   if (active) store_row<T::NX>(dx + n * (int64_t)(T::NX * C), C, c, d);
+}
+
+// Source-owned complete adjoint: the feature gradient of each source row and,
+// on the way, the gate and harmonic gradients of its out-edges (per-edge
+// outputs, so any owner may write them).  One pass reads the gate stream once
+// and gathers only the receiver cotangent rows the feature gradient needs;
+// the sender's own features are loaded once per row.  Row slot `rows` covers
+// the out-of-range tail segment of the source CSR and writes zero gate and
+// harmonic gradients for it (no feature row).
+template <class T>
+__global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value)) void msg_bwd_src_kernel(
+    Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx,
+    float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates) {
+  const RowGroup rg = row_group_y_xcd();
+  if (rg.row > a.rows) return;
+  const int64_t n = visit_row(scsr, rg.row, a.rows);
+  if (n < 0) return;
+  const bool tail = n == a.rows;
+  const int C = a.channels, c = 64 * rg.group + lane_id();
+  const bool active = c < C;
+  float* dsh_g = group_target(dsh, dsh_part, rg.group, a.edges, T::NY);
+  float xv[T::NX], d[T::NX];
+  if (active && !tail) load_row<T::NX>(a.x + n * (int64_t)(T::NX * C), C, c, xv);
+  else zero_row<T::NX>(xv);
+  zero_row<T::NX>(d);
+  const int32_t beg = scsr.ptr[n], end = scsr.ptr[n + 1];
+  // An out-of-range receiver contributes zero (mask 0, row 0 read).
+  for (int32_t pos = beg; pos < end; pos += kWave) {
+    const int32_t count = min(end - pos, kWave);
+    Chunk<T> ch;
+    stage_chunk<T>(a, dst, scsr.order, pos, count, ch);
+    for (int i = 0; i < count; ++i) {
+      const int64_t e = lane_i(ch.e, i);
+      const int64_t r = lane_i(ch.peer, i);
+      const float m = lane_f(ch.m, i);
+      float y[T::NY], dyv[T::NY];
+#pragma unroll
+      for (int j = 0; j < T::NY; ++j) {
+        y[j] = lane_f(ch.y[j], i);
+        dyv[j] = 0.f;
+      }
+      if (active) {
+        float go[T::NO], gw[T::P], dg[T::P];
+        load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
+        load_gw<T>(a, e, c, m, gw);
+        if (!tail) T::dx(y, gw, go, d);
+        if (dsh && dgates) T::dydg(xv, y, gw, go, dyv, dg);
+        else if (dsh) T::dy(xv, gw, go, dyv);
+        else if (dgates) T::dg(xv, y, go, dg);
+        if (dgates) {
+#pragma unroll
+          for (int p = 0; p < T::P; ++p) dg[p] *= m;
+          if (a.weight) {
+#pragma unroll
+            for (int p = 0; p < T::P; ++p) dg[p] *= a.weight[p * C + c];
+          }
+          store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, dg);
+        }
+      }
+      if (dsh) {
+        const float v = wave_sums<T::NY>(dyv);
+        const int j = wave_sums_slot();
+        if (j >= 0 && j < T::NY) dsh_g[e * T::NY + j] = v;
+      }
+    }
+  }
+  if (active && !tail && dx) store_row<T::NX>(dx + n * (int64_t)(T::NX * C), C, c, d);
 }
 
 // ---------------------------------------------------------------------------
