@@ -32,7 +32,7 @@ struct MsgBwd {
     // keeps 2 waves per SIMD; the P17 shapes need the register room of two separate passes.
     if (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value >= 2 && dx && (dsh || dg)) {
       hipLaunchKernelGGL((msg_bwd_src_kernel<T>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock),
-                         bwd_x_lds_cap<T>(a.rows), st, a, dst, scsr, grad, dx, dsh, ws, dg);
+                         0, st, a, dst, scsr, grad, dx, dsh, ws, dg);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
       if (dsh) return launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st);
