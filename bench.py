@@ -45,7 +45,7 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # `bench.py --workload probe`, each scaled by the counter's reading for a 1 GiB copy (FETCH x2.0,
 # WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.
 MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 20.07e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
-                    ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 52.71e9}
+                    ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9}
 
 
 def log(*a):
