@@ -22,9 +22,12 @@ from ictc_o3.ops.radial_mlp import edge_linear
 
 def degree_linear(x: torch.Tensor, weights: List[torch.Tensor], C: int, lmax: int, scale: float = 1.0):
     N = x.shape[0]
+    # one split (its adjoint is a single concatenation) rather than per-degree
+    # slices, whose adjoints each materialise a zero-filled full-width gradient
+    blocks = torch.split(x, [(2 * l + 1) * C for l in range(lmax + 1)], 1)
     parts = []
     for l in range(lmax + 1):
-        blk = x[:, l * l * C:(l + 1) ** 2 * C].reshape(N * (2 * l + 1), C)
+        blk = blocks[l].reshape(N * (2 * l + 1), C)
         w = weights[l] if scale == 1.0 else weights[l] * scale
         parts.append(edge_linear(blk, w).reshape(N, (2 * l + 1) * C))
     return torch.cat(parts, 1)
@@ -33,11 +36,13 @@ def degree_linear(x: torch.Tensor, weights: List[torch.Tensor], C: int, lmax: in
 def path_linear(m: torch.Tensor, weights: List[torch.Tensor], counts: Dict[int, int], C: int, lmax: int,
                 scale: float = 1.0):
     N = m.shape[0]
-    parts, off = [], 0
+    sizes = [counts.get(l, 0) * (2 * l + 1) * C for l in range(lmax + 1)]
+    tail = m.shape[1] - sum(sizes)
+    blocks = torch.split(m, sizes + [tail] if tail else sizes, 1)
+    parts = []
     for l in range(lmax + 1):
         k, w = counts.get(l, 0), 2 * l + 1
-        blk = m[:, off:off + k * w * C].reshape(N, k, w, C).transpose(1, 2).reshape(N * w, k * C)
-        off += k * w * C
+        blk = blocks[l].reshape(N, k, w, C).transpose(1, 2).reshape(N * w, k * C)
         parts.append(edge_linear(blk, weights[l] * scale).reshape(N, w * C))
     return torch.cat(parts, 1)
 

@@ -190,7 +190,10 @@ class Product(nn.Module):
     def forward(self, message, sc, species, first_order=False):
         out = self.linear(self.symmetric_contractions.contract(message, species), first_order)
         C = self.channels
-        return torch.cat([out[:, :C] + sc, out[:, C:]], 1) if out.shape[1] > C else out + sc
+        if out.shape[1] == C:
+            return out + sc
+        head, rest = torch.split(out, [C, out.shape[1] - C], 1)
+        return torch.cat([head + sc, rest], 1)
 
 
 class ScalarReadout(nn.Module):
