@@ -45,7 +45,8 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # `bench.py --workload probe`, each scaled by the counter's reading for a 1 GiB copy (FETCH x2.0,
 # WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.
 MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 20.07e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
-                    ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9}
+                    ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9,
+                    ("msg_bwd_tan", 131072, 5262704, 64): 66.70e9}
 
 
 def log(*a):
@@ -91,7 +92,10 @@ def message_bytes(N, E, C, NX, NY, P, NO):
     # the complete adjoint (dx, dsh, dg) of one source-owned pass: every operand read once, every output written once
     bwd = N * NO * C * 4 + N * NX * C * 4 + E * NY * 4 + E * P * C * 4 + idx + E * NY * 4 + E * P * C * 4 \
         + N * NX * C * 4
-    return {"msg_fwd": fwd, "msg_bwd_edge": bwd_edge, "msg_bwd_x": bwd_x, "msg_bwd": bwd}
+    # gate-tangent form of the complete adjoint (energy + forces): gdot [E, P*C] read in place of dg written,
+    # plus dr [E]
+    bwd_tan = bwd + E * 4
+    return {"msg_fwd": fwd, "msg_bwd_edge": bwd_edge, "msg_bwd_x": bwd_x, "msg_bwd": bwd, "msg_bwd_tan": bwd_tan}
 
 
 def time_launches(fn, reps, stream):
@@ -345,10 +349,16 @@ def layer_message_kernels(model, src, dst, N, pos, reps=5):
     # the model's backward asks for dx, dsh and dg together: one fused source-owned kernel where the library fuses
     t_bwd = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, True, True)), reps,
                           stream)
+    # energy + forces (the model's forces_only route): dx, dsh and dr = sum dg * d gates / dr
+    gdot = torch.randn_like(gates)
+    t_tan = time_launches(lambda: tpo._msg_bwd_tangent_raw(spec, topo, x, Y, gates, gdot, None, go, (True, True)),
+                          reps, stream)
+    del gdot
     nbytes = message_bytes(N, src.numel(), C, NX, NY, spec.num_paths, spec.out_components)
     kern = {"msg_fwd": t_fwd, "msg_bwd_edge": t_bwd_e, "msg_bwd_x": t_bwd_x}
     if t_bwd < 0.9 * (t_bwd_e + t_bwd_x):   # fused (one launch); otherwise it is the two kernels above
         kern["msg_bwd"] = t_bwd
+        kern["msg_bwd_tan"] = t_tan
     else:
         log(f"  last-layer full adjoint {t_bwd * 1e6:.1f} us: the two kernels above (not fused at this shape)")
     for k, t in kern.items():
@@ -662,7 +672,7 @@ def cpu_baseline_train(model, budget_s=25.0):
 
 
 def run_probe(args):
-    """Counter-collection workload: the cfg4 layer-1 message kernels and gate projection, then a 1 GiB copy.
+    """Counter-collection workload: the cfg4 layer-1 message kernels and gate kernels, then a 1 GiB copy.
 
     Run under ``rocprofv3 --pmc FETCH_SIZE`` (and separately ``WRITE_SIZE``): the
     copy (1 GiB read, 1 GiB written) calibrates the counters, the message
@@ -694,12 +704,18 @@ def run_probe(args):
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True))
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, False, False))
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, True, True))
-    from ictc_o3.ops.radial_mlp import gate_projection_adjoint, radial_gates
+    gdot = torch.randn_like(gates)
+    for _ in range(args.steps):
+        tpo._msg_bwd_tangent_raw(spec, topo, x, Y, gates, gdot, None, go, (True, True))
+    del gdot
+    from ictc_o3.ops.radial_mlp import gate_projection_adjoint, radial_gates, radial_gates_tangent
     lin = [m for m in inter.fc if isinstance(m, torch.nn.Linear)]
     with torch.no_grad():
         for _ in range(args.steps):
             radial_gates(r, inter.fc, model.max_radius, model.polynomial_cutoff_p, 1.6791767923989418)
             gate_projection_adjoint(gates, lin[-1].weight.detach())
+            radial_gates_tangent(r, [m.weight for m in lin], model.max_radius, model.polynomial_cutoff_p,
+                                 1.6791767923989418)
     a = torch.empty(1 << 28, device=dev)
     b = torch.randn(1 << 28, device=dev)
     for _ in range(args.steps):

@@ -369,6 +369,41 @@ int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh,
                    "ictc_msg_bwd launch");
 }
 
+int64_t ictc_msg_bwd_tangent_workspace_bytes(int edge_lmax, int C, int64_t E) {
+  const int G = ictc::channel_groups(C);
+  if (G == 0 || E < 0) return -1;
+  return G > 1 ? (int64_t)(G - 1) * E * ((edge_lmax + 1) * (edge_lmax + 1) + 1) * (int64_t)sizeof(float) : 0;
+}
+
+int ictc_msg_bwd_tangent(int li, int le, int lo, int C, const float* x, const float* sh, const float* g,
+                         const float* w, const float* mask, const int64_t* src, const int64_t* dst, int64_t N,
+                         int64_t E, const int32_t* dptr, const int32_t* dorder, const int32_t* sptr,
+                         const int32_t* sorder, const int32_t* dst_rows, const int32_t* src_rows, const float* grad,
+                         const float* gdot, float* dx, float* dsh, float* dr, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
+  if (int rc = check_shape(li, le, lo, C)) return rc;
+  if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
+  if (!dr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: dr is required");
+  if (E == 0) {
+    const int64_t n = dx ? N * (int64_t)(C * (li + 1) * (li + 1)) : 0;
+    if (n == 0) return ICTC_OK;
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, dx, n);
+    return check_hip(hipGetLastError(), "dx fill");
+  }
+  if (!x || !sh || !g || !gdot || !src || !dst || !grad || !dptr)
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: null operand");
+  if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: dfeatures needs the source CSR");
+  const int64_t need = ictc_msg_bwd_tangent_workspace_bytes(le, C, E);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: %d channels need a workspace of %lld bytes", C,
+                (long long)need);
+  const ictc::TpShape s{li, le, lo, C};
+  return check_hip(ictc::launch_msg_bwd_tangent(s, operands(x, sh, g, w, mask, N, E, C), src, dst,
+                                                ictc::Csr{dptr, dorder, dst_rows}, ictc::Csr{sptr, sorder, src_rows},
+                                                grad, gdot, dx, dsh, dr, (float*)workspace, (hipStream_t)stream),
+                   "ictc_msg_bwd_tangent launch");
+}
+
 int ictc_tp_second(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
                    const float* grad, const float* tx, const float* tsh, const float* tg, int64_t E, float* dgrad,
                    float* dx, float* dsh, float* dg, void* workspace, int64_t workspace_bytes, void* stream) {

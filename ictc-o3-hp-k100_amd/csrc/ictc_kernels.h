@@ -384,13 +384,59 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
   if (active) store_row<T::NO>(out + n * (int64_t)(T::NO * C), C, c, o);
 }
 
+// Gate-tangent mode of the first adjoint: per edge, the harmonic gradient (when
+// dsh_g) and dr = sum over paths and channels of dgates * gdot, reduced over the
+// wave's 64 channels in one wave_sums where the components fit.
+template <int NY>
+__device__ __forceinline__ void store_dsh_dr(float* __restrict__ dsh_g, float* __restrict__ dr_g, int64_t e,
+                                             const float* dyv, float dgt) {
+  const int j = wave_sums_slot();
+  if constexpr (NY + 1 <= 16) {
+    if (dsh_g) {
+      float v[NY + 1];
+#pragma unroll
+      for (int k = 0; k < NY; ++k) v[k] = dyv[k];
+      v[NY] = dgt;
+      const float t = wave_sums<NY + 1>(v);
+      if (j >= 0 && j < NY) dsh_g[e * NY + j] = t;
+      else if (j == NY) dr_g[e] = t;
+      return;
+    }
+  } else {
+    if (dsh_g) {
+      const float t = wave_sums<NY>(dyv);
+      if (j >= 0 && j < NY) dsh_g[e * NY + j] = t;
+    }
+  }
+  const float t = wave_sums<1>(&dgt);
+  if (j == 0) dr_g[e] = t;
+}
+
+// This lane's share of the gate-tangent dot: sum_p dg[p] w[p] gdot[p] (dg unweighted, unmasked).
+template <class T>
+__device__ __forceinline__ float gate_tangent_dot(const Operands& a, const float* __restrict__ gdot, int64_t e, int c,
+                                                  const float* gt, const float* dg) {
+  float t = 0.f;
+  if (a.weight) {
+#pragma unroll
+    for (int p = 0; p < T::P; ++p) t += dg[p] * a.weight[p * a.channels + c] * gt[p];
+  } else {
+#pragma unroll
+    for (int p = 0; p < T::P; ++p) t += dg[p] * gt[p];
+  }
+  return t;
+}
+
 // Receiver-owned adjoint: per-edge gate and harmonic gradients.  Waves of
 // row `rows` own the out-of-range tail segment ptr[rows]..ptr[rows+1] and
 // write zero gradients for it (mask 0, zero cotangent).
-template <class T>
+// With TAN, gdot [E, P*C] (d gates / dr) replaces the gate gradient output:
+// dr[e] = sum dgates * gdot is written instead (group g > 0: slab g-1 of dr_part).
+template <class T, bool TAN>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO>::value)) void msg_bwd_edge_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad, float* __restrict__ dsh,
-    float* __restrict__ dsh_part, float* __restrict__ dgates, int parts) {
+    float* __restrict__ dsh_part, float* __restrict__ dgates, int parts, const float* __restrict__ gdot,
+    float* __restrict__ dr, float* __restrict__ dr_part) {
   const RowGroup rg = row_group_y_xcd();
   const int64_t slot = rg.row / parts;
   if (slot > a.rows) return;
@@ -402,6 +448,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
   float* dsh_g = group_target(dsh, dsh_part, rg.group, a.edges, T::NY);
+  float* dr_g = rg.group > 0 ? dr_part + (int64_t)(rg.group - 1) * a.edges : dr;
   float go[T::NO];
   if (active && !tail) load_row<T::NO>(grad + n * (int64_t)(T::NO * C), C, c, go);
   else {
@@ -421,6 +468,20 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO
       for (int j = 0; j < T::NY; ++j) {
         y[j] = lane_f(ch.y[j], i);
         dyv[j] = 0.f;
+      }
+      float dgt = 0.f;
+      if (TAN && active) {
+        float xv[T::NX], gw[T::P], gt[T::P], d[T::P];
+        load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
+        load_gw<T>(a, e, c, m, gw);
+        load_row<T::P>(gdot + e * (int64_t)(T::P * C), C, c, gt);
+        if (dsh) T::dydg(xv, y, gw, go, dyv, d);
+        else T::dg(xv, y, go, d);
+        dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, d);
+      }
+      if (TAN) {
+        store_dsh_dr<T::NY>(dsh_g, dr_g, e, dyv, dgt);
+        continue;
       }
       if (active) {
         float xv[T::NX], gw[T::P];
@@ -494,10 +555,12 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::
 // the sender's own features are loaded once per row.  Row slot `rows` covers
 // the out-of-range tail segment of the source CSR and writes zero gate and
 // harmonic gradients for it (no feature row).
-template <class T>
+// TAN: as in msg_bwd_edge_kernel, dr from gdot in place of the gate gradient.
+template <class T, bool TAN>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value)) void msg_bwd_src_kernel(
     Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx,
-    float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates) {
+    float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates, const float* __restrict__ gdot,
+    float* __restrict__ dr, float* __restrict__ dr_part) {
   const RowGroup rg = row_group_y_xcd();
   if (rg.row > a.rows) return;
   const int64_t n = visit_row(scsr, rg.row, a.rows);
@@ -506,6 +569,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>
   const int C = a.channels, c = 64 * rg.group + lane_id();
   const bool active = c < C;
   float* dsh_g = group_target(dsh, dsh_part, rg.group, a.edges, T::NY);
+  float* dr_g = rg.group > 0 ? dr_part + (int64_t)(rg.group - 1) * a.edges : dr;
   float xv[T::NX], d[T::NX];
   if (active && !tail) load_row<T::NX>(a.x + n * (int64_t)(T::NX * C), C, c, xv);
   else zero_row<T::NX>(xv);
@@ -525,6 +589,21 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>
       for (int j = 0; j < T::NY; ++j) {
         y[j] = lane_f(ch.y[j], i);
         dyv[j] = 0.f;
+      }
+      float dgt = 0.f;
+      if (TAN && active) {
+        float go[T::NO], gw[T::P], gt[T::P], dg[T::P];
+        load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
+        load_gw<T>(a, e, c, m, gw);
+        load_row<T::P>(gdot + e * (int64_t)(T::P * C), C, c, gt);
+        if (!tail) T::dx(y, gw, go, d);
+        if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
+        else T::dg(xv, y, go, dg);
+        dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, dg);
+      }
+      if (TAN) {
+        store_dsh_dr<T::NY>(dsh_g, dr_g, e, dyv, dgt);
+        continue;
       }
       if (active) {
         float go[T::NO], gw[T::P], dg[T::P];

@@ -22,8 +22,25 @@ hipError_t launch_edge_bwd(const TpShape& s, const Operands& a, const float* gra
                            float* ws, hipStream_t st);
 hipError_t launch_msg_fwd(const TpShape& s, const Operands& a, const int64_t* src, Csr dcsr, float* out,
                           hipStream_t st);
+// The source-owned feature adjoint gathers a 9 KB receiver cotangent row per
+// edge; with more rows in flight than the L2 holds, the re-reads grow faster
+// than the latency hiding gains.  Unused dynamic LDS caps the resident blocks
+// per CU (160 KB / cap bytes).  Measured on the cfg4 layer-1 shape: 2 blocks
+// (8 waves) per CU 4.85 ms and 31.7 GB fetched, 3 blocks 4.94 ms / 36.4 GB,
+// uncapped (16 waves) 5.19 ms / 39.5 GB.  The receiver-owned kernels lose
+// more latency hiding than they save (msg_fwd 3.50 -> 3.95 ms when capped).
+// Small graphs (cfg2's 4,096 rows) fit the L2 and keep every wave.
+template <class T>
+inline size_t bwd_x_lds_cap(int64_t rows) {
+  return (T::LI == 2 && T::LE == 2 && T::LO == 2 && rows >= 65536) ? 72 * 1024 : 0;
+}
+
 hipError_t launch_msg_bwd(const TpShape& s, const Operands& a, const int64_t* src, const int64_t* dst, Csr dcsr,
                           Csr scsr, const float* grad, float* dx, float* dsh, float* dg, float* ws, hipStream_t st);
+
+hipError_t launch_msg_bwd_tangent(const TpShape& s, const Operands& a, const int64_t* src, const int64_t* dst,
+                                  Csr dcsr, Csr scsr, const float* grad, const float* gdot, float* dx, float* dsh,
+                                  float* dr, float* ws, hipStream_t st);
 
 hipError_t launch_edge_second(const TpShape& s, const Operands& a, const Tangents& t, const float* grad, float* dgrad,
                               float* dx, float* dsh, float* dg, float* ws, hipStream_t st);

@@ -5,19 +5,6 @@
 namespace ictc {
 
 namespace {
-// The source-owned feature adjoint gathers a 9 KB receiver cotangent row per
-// edge; with more rows in flight than the L2 holds, the re-reads grow faster
-// than the latency hiding gains.  Unused dynamic LDS caps the resident blocks
-// per CU (160 KB / cap bytes).  Measured on the cfg4 layer-1 shape: 2 blocks
-// (8 waves) per CU 4.85 ms and 31.7 GB fetched, 3 blocks 4.94 ms / 36.4 GB,
-// uncapped (16 waves) 5.19 ms / 39.5 GB.  The receiver-owned kernels lose
-// more latency hiding than they save (msg_fwd 3.50 -> 3.95 ms when capped).
-// Small graphs (cfg2's 4,096 rows) fit the L2 and keep every wave.
-template <class T>
-size_t bwd_x_lds_cap(int64_t rows) {
-  return (T::LI == 2 && T::LE == 2 && T::LO == 2 && rows >= 65536) ? 72 * 1024 : 0;
-}
-
 struct MsgBwd {
   const Operands& a;
   const int64_t *src, *dst;
@@ -31,8 +18,8 @@ struct MsgBwd {
     // One source-owned pass for all three (rows + 1 slots: the last covers the out-of-range tail) where it
     // keeps 2 waves per SIMD; the P17 shapes need the register room of two separate passes.
     if (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value >= 2 && dx && (dsh || dg)) {
-      hipLaunchKernelGGL((msg_bwd_src_kernel<T>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock),
-                         0, st, a, dst, scsr, grad, dx, dsh, ws, dg);
+      hipLaunchKernelGGL((msg_bwd_src_kernel<T, false>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock),
+                         0, st, a, dst, scsr, grad, dx, dsh, ws, dg, nullptr, nullptr, nullptr);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
       if (dsh) return launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st);
@@ -41,8 +28,8 @@ struct MsgBwd {
     if (dsh || dg) {
       // rows + 1 row slots: the last one zero-fills the out-of-range tail segment.
       const int parts = row_parts(a.rows + 1, G);
-      hipLaunchKernelGGL((msg_bwd_edge_kernel<T>), dim3(blocks_for((a.rows + 1) * parts), G), dim3(kBlock), 0,
-                         st, a, src, dcsr, grad, dsh, ws, dg, parts);
+      hipLaunchKernelGGL((msg_bwd_edge_kernel<T, false>), dim3(blocks_for((a.rows + 1) * parts), G), dim3(kBlock),
+                         0, st, a, src, dcsr, grad, dsh, ws, dg, parts, nullptr, nullptr, nullptr);
       hipError_t err = hipGetLastError();
       if (err != hipSuccess) return err;
       if (dsh && (err = launch_group_sum(dsh, ws, a.edges * T::NY, G - 1, st)) != hipSuccess) return err;

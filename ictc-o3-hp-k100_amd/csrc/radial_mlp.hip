@@ -274,6 +274,67 @@ __device__ __forceinline__ void forward_tile(const FwdWeights& w, const Radial& 
   act<KEEP>(z, s, a3, s3);
 }
 
+// gemm6 for two B operands that share the A operand reads (values and tangents).
+__device__ __forceinline__ void gemm6_pair(const bf16x8 (*A)[4][2][64], const Split* B, const Split* Bt, v4f* acc,
+                                           v4f* acct) {
+  const int l = threadIdx.x & 63;
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) acc[nb] = acct[nb] = v4f{0.f, 0.f, 0.f, 0.f};
+#define ICTC_STEP(PA, PB, KS)                                          \
+  _Pragma("unroll") for (int nb = 0; nb < 4; ++nb) {                   \
+    const bf16x8 a = A[PA][nb][KS][l];                                 \
+    acc[nb] = mfma16(a, B[KS].p[PB], acc[nb]);                         \
+    acct[nb] = mfma16(a, Bt[KS].p[PB], acct[nb]);                      \
+  }
+  ICTC_STEP(2, 0, 0) ICTC_STEP(0, 2, 0) ICTC_STEP(1, 1, 0)
+  ICTC_STEP(2, 0, 1) ICTC_STEP(0, 2, 1) ICTC_STEP(1, 1, 1)
+  ICTC_STEP(1, 0, 0) ICTC_STEP(0, 1, 0) ICTC_STEP(1, 0, 1)
+  ICTC_STEP(0, 1, 1) ICTC_STEP(0, 0, 0) ICTC_STEP(0, 0, 1)
+#undef ICTC_STEP
+}
+
+// a <- s silu(z), t <- s silu'(z) * tz (forward-mode derivative of the activation).
+__device__ __forceinline__ void act_tangent(const v4f* z, const v4f* tz, float s, v4f* a, v4f* t) {
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float x = z[nb][k], g = sigm(x);
+      a[nb][k] = s * x * g;
+      t[nb][k] = s * g * (1.f + x * (1.f - g)) * tz[nb][k];
+    }
+}
+
+// The MLP of one tile and its forward-mode derivative along r, layer by layer
+// (each slope is used as soon as it is formed): a3 and t3 = d a3 / dr.
+__device__ __forceinline__ void forward_tangent_tile(const FwdWeights& w, const Radial& q, float x, float s, v4f* a3,
+                                                     v4f* t3) {
+  const int l = threadIdx.x & 63, g = l >> 4;
+  float b[2], db[2];
+  radial_one(q, x, 2 * g + 1, b[0], db[0]);
+  radial_one(q, x, 2 * g + 2, b[1], db[1]);
+  v4f z[4], tz[4], a[4], t[4];
+#pragma unroll
+  for (int jb = 0; jb < 4; ++jb) {
+    z[jb] = tz[jb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      z[jb] = mfma32(w.w1f[jb][ks][l], b[ks], z[jb]);
+      tz[jb] = mfma32(w.w1f[jb][ks][l], db[ks], tz[jb]);
+    }
+  }
+  act_tangent(z, tz, s, a, t);
+  Split B[2], Bt[2];
+  split_units(a, B);
+  split_units(t, Bt);
+  gemm6_pair(w.wf[0], B, Bt, z, tz);
+  act_tangent(z, tz, s, a, t);
+  split_units(a, B);
+  split_units(t, Bt);
+  gemm6_pair(w.wf[1], B, Bt, z, tz);
+  act_tangent(z, tz, s, a3, t3);
+}
+
 // Forward: a3 = s silu(W3 s silu(W2 s silu(W1 R(r)))), written to a3 [E, 64].
 __global__ __launch_bounds__(FWD_WAVES * 64) void mlp_fwd_kernel(const float* __restrict__ r, int64_t E, float rc,
                                                                  int p, const float* __restrict__ W1,
@@ -322,10 +383,14 @@ __global__ void gates_split_kernel(const float* __restrict__ W4, int M, bf16x8* 
   for (int p = 0; p < 3; ++p) ws[((int64_t)(rb * 2 + ks) * 3 + p) * 64 + l] = sp.p[p];
 }
 
-__global__ __launch_bounds__(GATE_TILES * 64) void gates_fwd_kernel(
+// With TAN each wave also runs the MLP's forward-mode derivative along r for
+// its tile, and the block projects twice per group: the gates, then (the
+// waves' tangent splits swapped into the same LDS tiles) d gates / dr.
+template <bool TAN>
+__global__ __launch_bounds__(GATE_TILES * 64, 2) void gates_fwd_kernel(
     const float* __restrict__ r, int64_t E, float rc, int p, const float* __restrict__ W1,
     const float* __restrict__ W2, const float* __restrict__ W3, float s, const bf16x8* __restrict__ w4s, int M,
-    float* __restrict__ gates) {
+    float* __restrict__ gates, float* __restrict__ gdot) {
   __shared__ FwdWeights ws;
   __shared__ bf16x8 bsh[GATE_TILES][2][3][64];
   stage_fwd(ws, W1, W2, W3);
@@ -336,6 +401,7 @@ __global__ __launch_bounds__(GATE_TILES * 64) void gates_fwd_kernel(
   const int nrb = M / 16;
   for (int64_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
     const int64_t e0 = 16 * GATE_TILES * grp;
+    Split T[2];  // TAN: this wave's tangent split, projected in the second pass
     {
       const FwdWeights& wf = *opaque(&ws);
       const int64_t e = e0 + 16 * w + i;
@@ -343,7 +409,13 @@ __global__ __launch_bounds__(GATE_TILES * 64) void gates_fwd_kernel(
       const float x = ok ? r[e] : 2.f * rc;
       v4f a[4];
       float db[2];
-      forward_tile<false>(wf, q, x, s, a, nullptr, nullptr, nullptr, db, nullptr, nullptr, e, ok);
+      if (TAN) {
+        v4f t3[4];
+        forward_tangent_tile(wf, q, x, s, a, t3);
+        split_units(t3, T);
+      } else {
+        forward_tile<false>(wf, q, x, s, a, nullptr, nullptr, nullptr, db, nullptr, nullptr, e, ok);
+      }
       Split B[2];
       split_units(a, B);
 #pragma unroll
@@ -351,50 +423,60 @@ __global__ __launch_bounds__(GATE_TILES * 64) void gates_fwd_kernel(
 #pragma unroll
         for (int pt = 0; pt < 3; ++pt) bsh[w][ks][pt][l] = B[ks].p[pt];
     }
-    __syncthreads();
-    Split Bt[GATE_TILES][2];
-#pragma unroll
-    for (int t = 0; t < GATE_TILES; ++t)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int pt = 0; pt < 3; ++pt) Bt[t][ks].p[pt] = bsh[t][ks][pt][l];
-    // A operands of the wave's next row block are in flight while the current one multiplies
-    bf16x8 An[2][3];
-    if (w < nrb) {
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int pt = 0; pt < 3; ++pt) An[ks][pt] = w4s[((int64_t)w * 6 + ks * 3 + pt) * 64 + l];
-    }
-    for (int rb = w; rb < nrb; rb += GATE_TILES) {
-      bf16x8 Aop[2][3];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int pt = 0; pt < 3; ++pt) Aop[ks][pt] = An[ks][pt];
-      if (rb + GATE_TILES < nrb) {
+    for (int pass = 0; pass < (TAN ? 2 : 1); ++pass) {
+      if (TAN && pass == 1) {
+        __syncthreads();  // every wave holds the first pass's tiles in registers
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-          for (int pt = 0; pt < 3; ++pt)
-            An[ks][pt] = w4s[((int64_t)(rb + GATE_TILES) * 6 + ks * 3 + pt) * 64 + l];
+          for (int pt = 0; pt < 3; ++pt) bsh[w][ks][pt][l] = T[ks].p[pt];
       }
-      v4f acc[GATE_TILES];
+      __syncthreads();
+      float* __restrict__ out = pass ? gdot : gates;
+      Split Bt[GATE_TILES][2];
 #pragma unroll
-      for (int t = 0; t < GATE_TILES; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+      for (int t = 0; t < GATE_TILES; ++t)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int pt = 0; pt < 3; ++pt) Bt[t][ks].p[pt] = bsh[t][ks][pt][l];
+      // A operands of the wave's next row block are in flight while the current one multiplies
+      bf16x8 An[2][3];
+      if (w < nrb) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int pt = 0; pt < 3; ++pt) An[ks][pt] = w4s[((int64_t)w * 6 + ks * 3 + pt) * 64 + l];
+      }
+      for (int rb = w; rb < nrb; rb += GATE_TILES) {
+        bf16x8 Aop[2][3];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int pt = 0; pt < 3; ++pt) Aop[ks][pt] = An[ks][pt];
+        if (rb + GATE_TILES < nrb) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int pt = 0; pt < 3; ++pt)
+              An[ks][pt] = w4s[((int64_t)(rb + GATE_TILES) * 6 + ks * 3 + pt) * 64 + l];
+        }
+        v4f acc[GATE_TILES];
+#pragma unroll
+        for (int t = 0; t < GATE_TILES; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 #define ICTC_STEP(PA, PB, KS) \
   _Pragma("unroll") for (int t = 0; t < GATE_TILES; ++t) acc[t] = mfma16(Aop[KS][PA], Bt[t][KS].p[PB], acc[t]);
-      ICTC_STEP(2, 0, 0) ICTC_STEP(0, 2, 0) ICTC_STEP(1, 1, 0)
-      ICTC_STEP(2, 0, 1) ICTC_STEP(0, 2, 1) ICTC_STEP(1, 1, 1)
-      ICTC_STEP(1, 0, 0) ICTC_STEP(0, 1, 0) ICTC_STEP(1, 0, 1)
-      ICTC_STEP(0, 1, 1) ICTC_STEP(0, 0, 0) ICTC_STEP(0, 0, 1)
+        ICTC_STEP(2, 0, 0) ICTC_STEP(0, 2, 0) ICTC_STEP(1, 1, 0)
+        ICTC_STEP(2, 0, 1) ICTC_STEP(0, 2, 1) ICTC_STEP(1, 1, 1)
+        ICTC_STEP(1, 0, 0) ICTC_STEP(0, 1, 0) ICTC_STEP(1, 0, 1)
+        ICTC_STEP(0, 1, 1) ICTC_STEP(0, 0, 0) ICTC_STEP(0, 0, 1)
 #undef ICTC_STEP
-      // D: lane holds edge i of tile t, outputs 16 rb + 4 g + r
+        // D: lane holds edge i of tile t, outputs 16 rb + 4 g + r
 #pragma unroll
-      for (int t = 0; t < GATE_TILES; ++t) {
-        const int64_t e = e0 + 16 * t + i;
-        if (e < E) *reinterpret_cast<v4f*>(gates + e * M + 16 * rb + 4 * g) = acc[t];
+        for (int t = 0; t < GATE_TILES; ++t) {
+          const int64_t e = e0 + 16 * t + i;
+          if (e < E) *reinterpret_cast<v4f*>(out + e * M + 16 * rb + 4 * g) = acc[t];
+        }
       }
     }
     __syncthreads();  // bsh is rewritten by the next group
@@ -533,10 +615,38 @@ int ictc_radial_gates_fwd(const float* r, int64_t edges, int num_basis, int hidd
                      (bf16x8*)workspace);
   if (int rc = launch_status("ictc_radial_gates_fwd split")) return rc;
   const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
-  const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel, GATE_TILES * 64, 3);
-  hipLaunchKernelGGL(gates_fwd_kernel, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0, st, r,
-                     edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates, out);
+  const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel<false>, GATE_TILES * 64, 3);
+  hipLaunchKernelGGL(gates_fwd_kernel<false>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0,
+                     st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates, out,
+                     nullptr);
   return launch_status("ictc_radial_gates_fwd launch");
+}
+
+int ictc_radial_gates_tangent_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                                  const float* W1, const float* W2, const float* W3, const float* W4, int gates,
+                                  float silu_scale, float* out, float* tangent, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
+  if (edges < 0 || !(cutoff > 0.f) || poly_p < 2 || gates <= 0 || gates % 16)
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: invalid arguments (gates must be a positive multiple of 16)");
+  if (edges == 0) return ICTC_OK;
+  if (!r || !W1 || !W2 || !W3 || !W4 || !out || !tangent || !workspace)
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: null operand");
+  if (workspace_bytes < ictc_radial_gates_workspace_bytes(gates))
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: workspace too small");
+  if (!aligned16(out) || !aligned16(tangent) || !aligned16(workspace))
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: operands must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  const int split_threads = (gates / 16) * 2 * 64;
+  hipLaunchKernelGGL(gates_split_kernel, dim3((split_threads + 255) / 256), dim3(256), 0, st, W4, gates,
+                     (bf16x8*)workspace);
+  if (int rc = launch_status("ictc_radial_gates_tangent_fwd split")) return rc;
+  const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
+  const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel<true>, GATE_TILES * 64, 3);
+  hipLaunchKernelGGL(gates_fwd_kernel<true>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0,
+                     st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates, out,
+                     tangent);
+  return launch_status("ictc_radial_gates_tangent_fwd launch");
 }
 
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,

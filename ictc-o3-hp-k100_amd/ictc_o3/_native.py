@@ -38,6 +38,9 @@ _SIGNATURES = {
     "ictc_msg_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
     "ictc_msg_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
                           _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "ictc_msg_bwd_tangent_workspace_bytes": (_i64, [_i, _i, _i64]),
+    "ictc_msg_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
+                                  _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_sh_fwd": (_i, [_p, _i64, _i, _p, _p]),
     "ictc_sh_bwd": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_jvp": (_i, [_p, _p, _i64, _i, _p, _p]),
@@ -52,6 +55,8 @@ _SIGNATURES = {
     "ictc_radial_gates_workspace_bytes": (_i64, [_i]),
     "ictc_radial_gates_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, _p, _i, ctypes.c_float, _p, _p,
                                    _i64, _p]),
+    "ictc_radial_gates_tangent_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, _p, _i,
+                                           ctypes.c_float, _p, _p, _p, _i64, _p]),
     "ictc_gate_gemm_bwd": (_i, [_p, _i64, _i, _p, _i, _p, _p]),
     "ictc_gemm_tn_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "ictc_gemm_tn": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p]),

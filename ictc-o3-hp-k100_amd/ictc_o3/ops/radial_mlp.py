@@ -180,29 +180,49 @@ class _RadialGates(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, dg):
         r, W1, W2, W3, W4 = ctx.saved_tensors
-        cutoff, poly_p, scale = ctx.cfg
-        dg = _c(dg)
-        E = r.shape[0]
         from ictc_o3.autograd import required_gradients
         needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:5]) if ctx.inputs else ctx.needs_input_grad[:5]
         ctx.inputs = None
-        need_w = any(needs[1:5])
-        da3 = gate_projection_adjoint(dg, W4)
-        dr = r.new_empty(E)
-        extra = [r.new_empty(E, 64) for _ in range(5)] if need_w else [None] * 5   # dz1, dz2, dz3, a1, a2
-        nat.call("ictc_radial_mlp_bwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
-                 nat.ptr(W3), float(scale), nat.ptr(da3), nat.ptr(dr), *[nat.ptr(t) for t in extra],
-                 nat.stream_of(r))
-        dW = [None] * 4
-        if need_w:
-            from ictc_o3.ops.activation import _radial
-            dz1, dz2, dz3, a1, a2 = extra
-            a3 = r.new_empty(E, 64)   # recomputed: the forward kept it on chip
-            nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
-                     nat.ptr(W2), nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
-            R = _radial(0, r, None, None, 8, cutoff, poly_p)
-            dW = [weight_grad(dz1, R), weight_grad(dz2, a1), weight_grad(dz3, a2), weight_grad(dg, a3)]
-        return (dr if needs[0] else None, *[d if n else None for d, n in zip(dW, needs[1:5])], None, None, None)
+        dr, dW = radial_gates_adjoint(r, (W1, W2, W3, W4), ctx.cfg, _c(dg), needs)
+        return (dr, *dW, None, None, None)
+
+
+def radial_gates_adjoint(r, weights, cfg, dg, needs):
+    """Adjoint of the fused radial gates for cotangent dg [E, M]: (dr or None, [dW1..dW4 or None])."""
+    W1, W2, W3, W4 = weights
+    cutoff, poly_p, scale = cfg
+    E = r.shape[0]
+    need_w = any(needs[1:5])
+    da3 = gate_projection_adjoint(dg, W4)
+    dr = r.new_empty(E)
+    extra = [r.new_empty(E, 64) for _ in range(5)] if need_w else [None] * 5   # dz1, dz2, dz3, a1, a2
+    nat.call("ictc_radial_mlp_bwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
+             nat.ptr(W3), float(scale), nat.ptr(da3), nat.ptr(dr), *[nat.ptr(t) for t in extra],
+             nat.stream_of(r))
+    dW = [None] * 4
+    if need_w:
+        from ictc_o3.ops.activation import _radial
+        dz1, dz2, dz3, a1, a2 = extra
+        a3 = r.new_empty(E, 64)   # recomputed: the forward kept it on chip
+        nat.call("ictc_radial_mlp_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
+                 nat.ptr(W2), nat.ptr(W3), float(scale), nat.ptr(a3), nat.stream_of(r))
+        R = _radial(0, r, None, None, 8, cutoff, poly_p)
+        dW = [weight_grad(dz1, R), weight_grad(dz2, a1), weight_grad(dz3, a2), weight_grad(dg, a3)]
+    return (dr if needs[0] else None), [d if n else None for d, n in zip(dW, needs[1:5])]
+
+
+def radial_gates_tangent(r, weights, cutoff, poly_p, scale):
+    """Fused radial gates [E, M] and their derivative along r, d gates / dr [E, M] (no autograd)."""
+    W1, W2, W3, W4 = (_c(w.detach()) for w in weights)
+    r = _c(r.detach())
+    E, M = r.shape[0], W4.shape[0]
+    gates, gdot = r.new_empty(E, M), r.new_empty(E, M)
+    ws_bytes = int(nat.lib().ictc_radial_gates_workspace_bytes(M))
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=r.device)
+    nat.call("ictc_radial_gates_tangent_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
+             nat.ptr(W2), nat.ptr(W3), nat.ptr(W4), M, float(scale), nat.ptr(gates), nat.ptr(gdot), nat.ptr(ws),
+             ws_bytes, nat.stream_of(r))
+    return gates, gdot
 
 
 def fused_supported(fc: torch.nn.Sequential) -> bool:

@@ -26,6 +26,7 @@ import torch
 
 from ictc_o3 import _native as nat
 from ictc_o3.autograd import required_gradients
+from torch.autograd.function import once_differentiable
 
 
 @dataclass(frozen=True)
@@ -353,6 +354,77 @@ class Message(torch.autograd.Function):
             return (None,) * 6
         dx, dsh, dg = MessageAdjoint.apply(x, sh, g, _c(go), ctx.spec, ctx.topo, ctx.mask, need)
         return dx, dsh, dg, None, None, None
+
+
+def _msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, mask, go, need):
+    """First adjoint with the gate gradient contracted against gdot = d gates / dr: (dx, dsh, dr)."""
+    N, E = x.shape[0], sh.shape[0]
+    dx = torch.empty_like(x) if need[0] else None
+    dsh = torch.empty_like(sh) if need[1] else None
+    dr = sh.new_empty(E)
+    sp = topo.by_src if need[0] else None
+    nbytes = int(nat.lib().ictc_msg_bwd_tangent_workspace_bytes(spec.le, spec.channels, E))
+    ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=x.device) if nbytes > 0 else None
+    nat.call("ictc_msg_bwd_tangent", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+             _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
+             nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
+             nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
+             nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(gdot),
+             nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr), nat.ptr(ws), max(nbytes, 0), nat.stream_of(x))
+    return dx, dsh, dr
+
+
+class RadialMessage(torch.autograd.Function):
+    """message(x, sh, radial_gates(r, fc)) for first-derivative (energy + forces) callers.
+
+    The forward also writes d gates / dr (forward mode through the radial MLP), so
+    a backward that needs no weight gradient forms dE/dr = sum dgates * d gates/dr
+    inside the message adjoint: the gate gradient [E, P*C], its projection onto the
+    hidden layer and the MLP adjoint are never run.  A backward that does need the
+    weight gradients takes the ordinary route (message adjoint, then radial adjoint).
+    """
+
+    @staticmethod
+    def forward(ctx, x, sh, r, W1, W2, W3, W4, spec, topo, mask, cfg):
+        from ictc_o3.ops.radial_mlp import radial_gates_tangent
+        ctx.set_materialize_grads(False)
+        ctx.inputs = (x, sh, r, W1, W2, W3, W4)
+        ctx.spec, ctx.topo, ctx.mask, ctx.cfg = spec, topo, mask, cfg
+        x, sh = _c(x), _c(sh)
+        gates, gdot = radial_gates_tangent(r, (W1, W2, W3, W4), *cfg)
+        ctx.save_for_backward(x, sh, _c(r), *(_c(w) for w in (W1, W2, W3, W4)), gates, gdot)
+        return _msg_fwd_raw(spec, topo, x, sh, gates, mask)
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, go):
+        from ictc_o3.ops.radial_mlp import radial_gates_adjoint
+        if go is None:
+            return (None,) * 11
+        x, sh, r, W1, W2, W3, W4, gates, gdot = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:7])
+        ctx.inputs = None
+        spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
+        go = _c(go)
+        dW = [None] * 4
+        if any(needs[3:7]):
+            dx, dsh, dg = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], True))
+            dr, dW = radial_gates_adjoint(r, (W1, W2, W3, W4), ctx.cfg, dg, (needs[2], *needs[3:7]))
+        elif needs[2]:
+            dx, dsh, dr = _msg_bwd_tangent_raw(spec, topo, x, sh, gates, gdot, mask, go, needs[:2])
+        elif needs[0] or needs[1]:
+            dx, dsh, _ = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], False))
+            dr = None
+        else:
+            return (None,) * 11
+        return (dx, dsh, dr, *dW, None, None, None, None)
+
+
+def radial_message(x, sh, r, fc, spec, topo, mask, cfg):
+    """message() with the fused radial gates of `fc` (see RadialMessage); cfg = (cutoff, poly_p, silu_scale)."""
+    lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
+    return RadialMessage.apply(x, sh, r, *(m.weight for m in lin), spec, topo, mask,
+                               (float(cfg[0]), int(cfg[1]), float(cfg[2])))
 
 
 def message(x, sh, g, spec, topo, mask=None):

@@ -161,18 +161,21 @@ class Interaction(nn.Module):
             self._spec = tpo.make_spec(self.input_lmax, self.lmax, self.lmax, self.channels, None)
         return self._spec
 
-    def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None):
+    def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None, forces_only=False):
         """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path)."""
         C = self.channels
         first_order = radial is None
         x = self.linear_up(h, first_order)
-        if radial is None:
-            from ictc_o3.ops.radial_mlp import radial_gates
-            gates = radial_gates(r, self.fc, *radial_cfg)
+        if radial is None and forces_only:
+            m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg)
         else:
-            from ictc_o3.ops.radial_mlp import radial_mlp
-            gates = radial_mlp(radial, self.fc)
-        m = tpo.message(x, Y, gates, self.spec(), topo, mask)
+            if radial is None:
+                from ictc_o3.ops.radial_mlp import radial_gates
+                gates = radial_gates(r, self.fc, *radial_cfg)
+            else:
+                from ictc_o3.ops.radial_mlp import radial_mlp
+                gates = radial_mlp(radial, self.fc)
+            m = tpo.message(x, Y, gates, self.spec(), topo, mask)
         message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8), first_order)
         sc = self.self_connection.forward_l0(h[:, :C], species)
         return message, sc
@@ -262,8 +265,16 @@ class PureCartesianICTDFix(nn.Module):
         from ictc_o3.ops.activation import radial_embedding
         return radial_embedding(r, self.max_radius, self.number_of_basis, self.polynomial_cutoff_p)
 
-    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, topology=None, second_order=True):
+    def forward(self, pos, A, batch, edge_src, edge_dst, edge_shifts, cell, *, topology=None, second_order=True,
+                forces_only=False):
         """Per-atom energies [N, 1].
+
+        forces_only=True (with second_order=False) tells the fused path that the
+        backward will ask for position gradients and no parameter gradients: the
+        radial gates are then written with their derivative along r, and the
+        message adjoint forms dE/dr without the gate gradient.  A backward that
+        does ask for parameter gradients stays correct (it takes the ordinary
+        route), only slower.
 
         second_order=False allows the fused radial-MLP kernel, whose adjoint
         supports first derivatives only (forces, parameter gradients); the
@@ -302,7 +313,7 @@ class PureCartesianICTDFix(nn.Module):
         h = self.node_embedding.weight.t().index_select(0, species)
         energy = None
         for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
-            message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg)
+            message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only)
             h = prod(message, sc, species, first_order=radial is None)
             if i < self.num_interaction - 1:
                 e = self.layer_energy_readouts[i](h[:, :self.channels])

@@ -73,7 +73,7 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
     with torch.enable_grad():
         pos = positions if positions.requires_grad else positions.detach().requires_grad_(True)
         output = model(pos, atomic_numbers, batch, edge_src, edge_dst, edge_shifts, cell, topology=topology,
-                       second_order=training)
+                       second_order=training, forces_only=not training)
         atomic = (output[0] if isinstance(output, tuple) else output).reshape(n)
         selected = atomic if owned_mask is None else atomic * owned_mask.to(atomic)
         # per-graph sums in FP64 without atomics (deterministic, contention free)

@@ -145,6 +145,25 @@ int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                  float* dfeatures, float* dharmonics, float* dgates, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* ictc_msg_bwd for a caller that holds gtangent [E, P*C] = d gates / d r
+ * (ictc_radial_gates_tangent_fwd) and wants the edge-length gradient rather
+ * than the gate gradient: dr [E] (required) = sum over paths and channels of
+ * dgates * gtangent, formed in registers, so dgates is never written.
+ * dfeatures / dharmonics (NULL = skipped) are bitwise those of ictc_msg_bwd.
+ * More than 64 channels need ictc_msg_bwd_tangent_workspace_bytes bytes of
+ * workspace.  Same reference boundary as ictc_msg_bwd (_first,
+ * ops/rematerialized_message.py:25-83) composed with the radial adjoint the
+ * reference's force autograd runs through `fc` (layers.py:826-835).          */
+int64_t ictc_msg_bwd_tangent_workspace_bytes(int edge_lmax, int channels, int64_t edges);
+int ictc_msg_bwd_tangent(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                         const float* features, const float* harmonics, const float* gates,
+                         const float* weight, const float* mask, const int64_t* src, const int64_t* dst,
+                         int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                         const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
+                         const int32_t* src_rows, const float* grad, const float* gtangent,
+                         float* dfeatures, float* dharmonics, float* dr, void* workspace,
+                         int64_t workspace_bytes, void* stream);
+
 /* Mixed second derivative of ictc_msg_bwd along tangents of its outputs
  * (tfeatures [nodes, C*(LI+1)^2], tharmonics [E, NY], tgates [E, P*C]; NULL =
  * zero tangent); replaces generated_second (graph mode,
@@ -315,6 +334,18 @@ int64_t ictc_radial_gates_workspace_bytes(int gates);
 int ictc_radial_gates_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                           const float* W1, const float* W2, const float* W3, const float* W4, int gates,
                           float silu_scale, float* out, void* workspace, int64_t workspace_bytes, void* stream);
+/* ictc_radial_gates_fwd that also writes tangent [E, gates] = d out / d r
+ * (forward mode through the MLP, same split-bf16 arithmetic).  For
+ * energy-and-forces callers that need no weight gradient: the force term of
+ * the gates is then sum over gates of dout * tangent per edge, which
+ * ictc_msg_bwd_tangent forms inside the message adjoint, so neither the gate
+ * gradient [E, gates] nor the MLP adjoint is materialised.  No single
+ * reference counterpart: it replaces the autograd pass through `fc`
+ * (layers.py:826-835) that the reference's force computation runs.          */
+int ictc_radial_gates_tangent_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                                  const float* W1, const float* W2, const float* W3, const float* W4, int gates,
+                                  float silu_scale, float* out, float* tangent, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
                         float* dr, float* dz1, float* dz2, float* dz3, float* a1, float* a2, void* stream);
