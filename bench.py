@@ -611,7 +611,7 @@ def run_cfg5(args):
         loss = step()
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
-    log(f"cfg5: N={N} E={E} step={dt * 1e3:.2f} ms loss={float(loss):.4f}")
+    log(f"cfg5: N={N} E={E} step={dt * 1e3:.2f} ms loss={float(loss.detach()):.4f}")
     kern, nbytes = layer_message_kernels(model, src, dst, N, None, reps=10)
     dom = max(kern, key=kern.get)   # the layer-1 message kernel with the largest time
     achieved = nbytes[dom] / kern[dom] / 1e9

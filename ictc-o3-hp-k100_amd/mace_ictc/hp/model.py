@@ -195,8 +195,9 @@ class Product(nn.Module):
         C = self.channels
         if out.shape[1] == C:
             return out + sc
-        head, rest = torch.split(out, [C, out.shape[1] - C], 1)
-        return torch.cat([head + sc, rest], 1)
+        # in place on the linear's fresh output (no backward saves it): no concatenation copy
+        out[:, :C] += sc
+        return out
 
 
 class ScalarReadout(nn.Module):
