@@ -46,7 +46,7 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.
 MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 20.07e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
                     ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9,
-                    ("msg_bwd_tan", 131072, 5262704, 64): 66.70e9}
+                    ("msg_bwd_tan", 131072, 5262704, 64): 53.10e9}
 
 
 def log(*a):

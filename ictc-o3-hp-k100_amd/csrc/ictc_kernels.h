@@ -555,9 +555,20 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::
 // the sender's own features are loaded once per row.  Row slot `rows` covers
 // the out-of-range tail segment of the source CSR and writes zero gate and
 // harmonic gradients for it (no feature row).
+// Waves per SIMD of the source-owned adjoint.  The gate-tangent form streams the
+// tangent rows as well; where the table allows 3 it runs better at 2, with fewer
+// receiver rows in flight (cfg4 layer-1 shape: 8.62 ms at 2, 9.6 ms at 3 with 13
+// spilled VGPRs).
+template <class T, bool TAN>
+constexpr int src_adjoint_waves() {
+  return (TAN && Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value == 3)
+             ? 2
+             : Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value;
+}
+
 // TAN: as in msg_bwd_edge_kernel, dr from gdot in place of the gate gradient.
 template <class T, bool TAN>
-__global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value)) void msg_bwd_src_kernel(
+__global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd_src_kernel(
     Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx,
     float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates, const float* __restrict__ gdot,
     float* __restrict__ dr, float* __restrict__ dr_part) {
