@@ -430,10 +430,20 @@ __device__ __forceinline__ float gate_tangent_dot(const Operands& a, const float
 // Receiver-owned adjoint: per-edge gate and harmonic gradients.  Waves of
 // row `rows` own the out-of-range tail segment ptr[rows]..ptr[rows+1] and
 // write zero gradients for it (mask 0, zero cotangent).
+// Waves per SIMD of the receiver-owned adjoint: the gate-tangent form holds the
+// tangent row besides the gate row and the full dy/dg contraction, so it asks
+// for one wave per SIMD fewer than the table (at the table's level up to 113
+// VGPRs spill, e.g. Tp<2,3,3>; one fewer leaves at most 5).
+template <class T, bool TAN>
+constexpr int edge_adjoint_waves() {
+  constexpr int w = Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO>::value;
+  return (TAN && w > 1) ? w - 1 : w;
+}
+
 // With TAN, gdot [E, P*C] (d gates / dr) replaces the gate gradient output:
 // dr[e] = sum dgates * gdot is written instead (group g > 0: slab g-1 of dr_part).
 template <class T, bool TAN>
-__global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdEdge, T::LI, T::LE, T::LO>::value)) void msg_bwd_edge_kernel(
+__global__ __launch_bounds__(kBlock, (edge_adjoint_waves<T, TAN>())) void msg_bwd_edge_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, const float* __restrict__ grad, float* __restrict__ dsh,
     float* __restrict__ dsh_part, float* __restrict__ dgates, int parts, const float* __restrict__ gdot,
     float* __restrict__ dr, float* __restrict__ dr_part) {
