@@ -300,7 +300,10 @@ def run_cfg4(args):
 
     src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
     kern, nbytes = layer_message_kernels(model, src, dst, N, pos)
-    dom = max(kern, key=kern.get)   # the message kernel with the largest time
+    # the step's own message kernels (energy + forces: the forward and the gate-tangent adjoint); the other
+    # adjoint forms are timed for reference only
+    in_step = [k for k in ("msg_fwd", "msg_bwd_tan") if k in kern] if "msg_bwd_tan" in kern else list(kern)
+    dom = max(in_step, key=kern.get)   # the step's message kernel with the largest time
     achieved = nbytes[dom] / kern[dom] / 1e9
     result = {
         "metric": METRIC,
@@ -349,16 +352,15 @@ def layer_message_kernels(model, src, dst, N, pos, reps=5):
     # the model's backward asks for dx, dsh and dg together: one fused source-owned kernel where the library fuses
     t_bwd = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, True, True)), reps,
                           stream)
-    # energy + forces (the model's forces_only route): dx, dsh and dr = sum dg * d gates / dr
-    gdot = torch.randn_like(gates)
-    t_tan = time_launches(lambda: tpo._msg_bwd_tangent_raw(spec, topo, x, Y, gates, gdot, None, go, (True, True)),
-                          reps, stream)
-    del gdot
     nbytes = message_bytes(N, src.numel(), C, NX, NY, spec.num_paths, spec.out_components)
     kern = {"msg_fwd": t_fwd, "msg_bwd_edge": t_bwd_e, "msg_bwd_x": t_bwd_x}
     if t_bwd < 0.9 * (t_bwd_e + t_bwd_x):   # fused (one launch); otherwise it is the two kernels above
         kern["msg_bwd"] = t_bwd
-        kern["msg_bwd_tan"] = t_tan
+        # energy + forces (the model's forces_only route): dx, dsh and dr = sum dg * d gates / dr
+        gdot = torch.randn_like(gates)
+        kern["msg_bwd_tan"] = time_launches(
+            lambda: tpo._msg_bwd_tangent_raw(spec, topo, x, Y, gates, gdot, None, go, (True, True)), reps, stream)
+        del gdot
     else:
         log(f"  last-layer full adjoint {t_bwd * 1e6:.1f} us: the two kernels above (not fused at this shape)")
     for k, t in kern.items():
