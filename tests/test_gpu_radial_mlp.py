@@ -47,3 +47,28 @@ def test_fused_radial_gates(device, E, out):
     assert rel_err(rd.grad, rr.grad) < 1e-5
     for m, W in zip([m for m in fc if isinstance(m, torch.nn.Linear)], Wr):
         assert rel_err(m.weight.grad, W.grad) < 1e-5
+
+
+@pytest.mark.parametrize("n,offset", [(4096, 0), (1001, 0), (4096, 1)])
+def test_normalized_silu_derivatives(device, n, offset):
+    """normalized SiLU, its first and second derivatives (16-byte vector path when n % 4 == 0 and the
+    operands are aligned, scalar path otherwise) vs float64 autograd, 1e-5 relative."""
+    from ictc_o3.ops.activation import normalized_silu
+    g = torch.Generator().manual_seed(n + offset)
+    x64 = torch.randn(n + offset, generator=g, dtype=torch.float64)[offset:] * 4
+    v64 = torch.randn(n, generator=g, dtype=torch.float64)
+    w64 = torch.randn(n, generator=g, dtype=torch.float64)
+
+    def run(x, v, w, f):
+        x = x.clone().requires_grad_(True)
+        y = f(x)
+        (d1,) = torch.autograd.grad(y, x, v, create_graph=True)
+        (d2,) = torch.autograd.grad(d1, x, w)
+        return y, d1, d2
+
+    ref = run(x64, v64, w64, lambda t: torch.nn.functional.silu(t) * mo.SILU)
+    xd = torch.randn(n + offset, generator=g).to(device)[offset:]
+    xd.copy_(x64.float().to(device))
+    got = run(xd, v64.float().to(device), w64.float().to(device), lambda t: normalized_silu(t, mo.SILU))
+    for a, b in zip(got, ref):
+        assert rel_err(a, b) < 1e-5
