@@ -352,13 +352,13 @@ int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh,
                  void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
-  if (E == 0 && dx) {
-    const int64_t n = N * (int64_t)(C * (li + 1) * (li + 1));
+  if (E == 0) {
+    // no edges: dsh and dg are empty, dx is zero
+    const int64_t n = dx ? N * (int64_t)(C * (li + 1) * (li + 1)) : 0;
     if (n == 0) return ICTC_OK;
     hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, dx, n);
     return check_hip(hipGetLastError(), "dx fill");
   }
-  if (N == 0 && E == 0) return ICTC_OK;
   if (!x || !sh || !g || !src || !dst || !grad || !dptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: null operand");
   if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: dfeatures needs the source CSR");
   if (int rc = check_ws(dsh, (const float*)workspace, workspace_bytes, le, C, E, "ictc_msg_bwd")) return rc;
@@ -383,13 +383,14 @@ int ictc_msg_bwd_tangent(int li, int le, int lo, int C, const float* x, const fl
                          int64_t workspace_bytes, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
-  if (!dr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: dr is required");
   if (E == 0) {
+    // no edges: dsh and dr are empty, dx is zero
     const int64_t n = dx ? N * (int64_t)(C * (li + 1) * (li + 1)) : 0;
     if (n == 0) return ICTC_OK;
     hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, dx, n);
     return check_hip(hipGetLastError(), "dx fill");
   }
+  if (!dr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: dr is required");
   if (!x || !sh || !g || !gdot || !src || !dst || !grad || !dptr)
     return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: null operand");
   if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: dfeatures needs the source CSR");

@@ -282,7 +282,23 @@ class PureCartesianICTDFix(nn.Module):
         default keeps every operator differentiable to second order.
         """
         N = pos.shape[0]
-        species = self.atomic_number_to_index[A.long()]
+        A_long = A.long()
+        # species validation of backbone.py:996-1009 (skip_input_validation drops its two host syncs)
+        if not getattr(self, "skip_input_validation", False) and A_long.numel() > 0:
+            top = int(A_long.max().item())
+            if top >= self.atomic_number_to_index.numel():
+                raise ValueError(
+                    f"Encountered atomic number {top}, but compact mapping supports only up to "
+                    f"{self.atomic_number_to_index.numel() - 1}. atomic_numbers={self.atomic_numbers}")
+            if int(A_long.min().item()) < 0:
+                bad = torch.unique(A_long[A_long < 0]).tolist()
+                raise ValueError(f"Encountered atomic numbers without compact mapping: {bad}. "
+                                 f"Configured atomic_numbers={self.atomic_numbers}")
+        species = self.atomic_number_to_index[A_long]
+        if not getattr(self, "skip_input_validation", False) and bool(torch.any(species < 0)):
+            bad = torch.unique(A_long[species < 0]).tolist()
+            raise ValueError(f"Encountered atomic numbers without compact mapping: {bad}. "
+                             f"Configured atomic_numbers={self.atomic_numbers}")
         if topology is None:
             # spatial row order for one periodic system; batched graphs keep index order (their
             # atoms are contiguous per graph, and the graphs' coordinates overlap)

@@ -234,3 +234,19 @@ def test_message_row_order_bitwise_identical(device, li, le, lo, C):
     for other in results[1:]:
         for a, b in zip(results[0], other):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("which", [(1, 2), (0,), (0, 1, 2)])
+def test_message_backward_without_edges(device, which):
+    """E = 0: any subset of gradients comes back correctly shaped (dx zero, dsh and dg empty)."""
+    from ictc_o3 import PackedGraphMessage
+    op = PackedGraphMessage.create(channels=64, input_lmax=2, edge_lmax=2, output_lmax=2, device=device)
+    x = torch.randn(7, 64 * 9, device=device, requires_grad=0 in which)
+    sh = torch.zeros(0, 9, device=device, requires_grad=1 in which)
+    g = torch.zeros(0, op.gate_width, device=device, requires_grad=2 in which)
+    e = torch.zeros(0, dtype=torch.long, device=device)
+    out = op(x, sh, g, e, e)
+    assert out.shape == (7, op.output_width) and float(out.abs().max()) == 0.0
+    grads = torch.autograd.grad(out.sum(), [t for t in (x, sh, g) if t.requires_grad], allow_unused=True)
+    for t, d in zip([t for t in (x, sh, g) if t.requires_grad], grads):
+        assert d is None or (d.shape == t.shape and (d.numel() == 0 or float(d.abs().max()) == 0.0))

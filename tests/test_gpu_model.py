@@ -88,3 +88,25 @@ def test_configure_model_contract(device):
         configure_model(model, layout="bogus")
     with pytest.raises(ValueError):
         configure_model(model, training=True, gate_cache_bytes=10)
+
+
+@pytest.mark.parametrize("training", [False, True])
+def test_energy_and_forces_without_edges(device, training):
+    """Atoms farther apart than the cutoff (runtime.py:107 keeps zero-edge graphs differentiable):
+    energies from the node embedding alone, zero forces, on both the first-order and the training route."""
+    from mace_ictc.hp import create_model, energy_and_forces
+    torch.manual_seed(4)
+    model = create_model(channels=16, lmax=2, atomic_numbers=(1, 6, 8), cutoff=4.5, device=device)
+    pos = torch.tensor([[0.0, 0.0, 0.0], [10.0, 0.0, 0.0], [0.0, 10.0, 0.0]], dtype=torch.float64)
+    Z = torch.tensor([1, 6, 8])
+    batch = torch.zeros(3, dtype=torch.long)
+    cell = (torch.eye(3, dtype=torch.float64) * 30.0)[None]
+    src = dst = torch.zeros(0, dtype=torch.long)
+    sh = torch.zeros(0, 3)
+    E0, F0, A0 = mo.energy_and_forces(model.state_dict(), mo.config_of(model), pos, Z, batch, src, dst,
+                                      sh.double(), cell, 1)
+    out = energy_and_forces(model, pos.float().to(device), Z.to(device), batch.to(device), src.to(device),
+                            dst.to(device), sh.to(device), cell.float().to(device), training=training)
+    assert abs(float(out["energy"][0]) - float(E0[0])) <= 1e-6 * float(A0.abs().sum())
+    assert float(out["forces"].abs().max()) == 0.0
+    assert rel_err(out["atomic_energy"], A0) < 1e-5

@@ -99,3 +99,13 @@ def test_geometry_oracle_gradcheck():
     vec = pos[dst] - pos[src] + shift
     assert torch.allclose((n * n).sum(1), torch.ones(8, dtype=torch.float64))
     assert torch.allclose((n * vec).sum(1), r)
+
+
+@pytest.mark.parametrize("bad_z", [200, 2])
+def test_unknown_atomic_number_raises_before_any_kernel(bad_z):
+    """backbone.py:996-1009: an atomic number past the map or without a species is a ValueError (host-side check)."""
+    model, pos, Z, batch, cell, src, dst, sh = _model_and_system()
+    Z = Z.clone()
+    Z[3] = bad_z
+    with pytest.raises(ValueError, match="atomic number"):
+        model(pos.float(), Z, batch, src, dst, sh, cell.float())

@@ -217,3 +217,49 @@ def test_oracle_gradcheck_tiny():
         return orc.edge_tp_packed(x, sh, gg, 1, 1, 1, C)
     assert torch.autograd.gradcheck(f, (feats, n, gates))
     assert torch.autograd.gradgradcheck(f, (feats, n, gates))
+
+
+def _cg0(l1, l2, l3):
+    """<l1 0 l2 0 | l3 0> from sympy (Racah's closed form), float."""
+    from sympy.physics.quantum.cg import CG
+    return float(CG(l1, 0, l2, 0, l3, 0).doit())
+
+
+def _coupling_identity_error(cg, l1, l2, l3, seed):
+    """max |sum_{m1 m2} C[m1,m2,m3] Y_l1(n)[m1] Y_l2(n)[m2] - s Y_l3(n)[m3]| with
+    s = +sqrt((2l1+1)(2l2+1)/(2l3+1)) |<l1 0 l2 0|l3 0>|.
+
+    The reference's coupling tensor is the harmonic projection of the product
+    polynomial (ictd_irreps.py:1245-1304), scaled by a positive factor
+    (:151-157), so contracting it with two harmonics of the same direction
+    returns a positive multiple of Y_l3: this fixes the sign and the magnitude
+    of every path, which equivariance and the Frobenius norm leave open.
+    """
+    n = unit_vectors(16, seed)
+    Y = orc.direction_harmonics(n, max(l1, l2, l3))
+    lhs = torch.einsum("ei,ej,ijk->ek", Y[l1], Y[l2], torch.as_tensor(cg, dtype=torch.float64))
+    s = math.sqrt((2 * l1 + 1) * (2 * l2 + 1) / (2 * l3 + 1)) * abs(_cg0(l1, l2, l3))
+    return float((lhs - s * Y[l3]).abs().max())
+
+
+@pytest.mark.parametrize("path", orc.natural_paths(3, 3, 3))
+def test_cg_sign_and_magnitude_pinned_by_harmonic_product(path):
+    l1, l2, l3 = path
+    assert _coupling_identity_error(orc.cg_component(l1, l2, l3), l1, l2, l3, 20 + l1 + 4 * l2 + 16 * l3) < 1e-10
+
+
+@pytest.mark.parametrize("path", orc.natural_paths(3, 3, 3))
+def test_product_coupling_tables_pinned_by_harmonic_product(path):
+    """The tables the kernels are generated from (ictc_o3/basis/tables.py) obey the same identity."""
+    from ictc_o3.basis import tables
+    l1, l2, l3 = path
+    assert _coupling_identity_error(tables.coupling_component(l1, l2, l3), l1, l2, l3, 7 + l1 + 4 * l2) < 1e-10
+
+
+def test_coupling_identity_detects_a_sign_flip():
+    """A single path with its sign flipped fails the identity (the check is not vacuous)."""
+    C = -orc.cg_component(1, 1, 2)
+    assert _coupling_identity_error(C, 1, 1, 2, 3) > 0.1
+    C = orc.cg_component(2, 2, 2).copy()
+    C[..., 0] *= -1     # one flipped m3 column
+    assert _coupling_identity_error(C, 2, 2, 2, 3) > 0.1
