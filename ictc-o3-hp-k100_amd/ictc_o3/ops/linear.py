@@ -50,8 +50,33 @@ def path_linear(m: torch.Tensor, weights: List[torch.Tensor], counts: Dict[int, 
 def species_linear(x: torch.Tensor, weight: torch.Tensor, species: torch.Tensor):
     """weight [S, Cout, Cin]: all species products in one GEMM, then select per node."""
     S, Co, Ci = weight.shape
-    allp = torch.matmul(x, weight.reshape(S * Co, Ci).t()).reshape(x.shape[0], S, Co)
+    allp = edge_linear(x, weight.reshape(S * Co, Ci)).reshape(x.shape[0], S, Co)
     return allp.gather(1, species.view(-1, 1, 1).expand(-1, 1, Co)).squeeze(1)
+
+
+class _SpeciesRows(torch.autograd.Function):
+    """rows[n] = table[species[n]] (table [S, C]); the table gradient one_hot^T . drows runs on the
+    split-reduction kernel in a fixed order (an index_select adjoint would add rows with atomics)."""
+
+    @staticmethod
+    def forward(ctx, table, species):
+        ctx.save_for_backward(species)
+        ctx.S = table.shape[0]
+        return table.index_select(0, species)
+
+    @staticmethod
+    def backward(ctx, drows):
+        from ictc_o3.ops.radial_mlp import _WeightGrad
+        (species,) = ctx.saved_tensors
+        if drows is None or not ctx.needs_input_grad[0]:
+            return None, None
+        onehot = torch.nn.functional.one_hot(species, ctx.S).to(drows.dtype)
+        return _WeightGrad.apply(onehot, drows), None
+
+
+def species_rows(table: torch.Tensor, species: torch.Tensor) -> torch.Tensor:
+    """table[species] with a deterministic table gradient (node embedding, backbone.py:1016-1020)."""
+    return _SpeciesRows.apply(table, species)
 
 
 def channel_linear(features: torch.Tensor, weight: torch.Tensor, bias=None):

@@ -69,7 +69,8 @@ def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 def weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """a^T b over edge rows on the split-reduction kernel (FP32 MFMA up to 16 output tiles of 64 x 64,
-    split-bf16 MFMA beyond); the library GEMM below _TN_MIN_ROWS rows."""
+    split-bf16 MFMA beyond; chunk partials added in a fixed order); the library GEMM below
+    _TN_MIN_ROWS rows."""
     if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda:
         return _gemm_tn(a, b)
     return a.t() @ b

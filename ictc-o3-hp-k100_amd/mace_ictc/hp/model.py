@@ -32,6 +32,8 @@ from ictc_o3.basis import tables
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops import tensor_product as tpo
 from ictc_o3.ops.harmonics import harmonics_packed
+from ictc_o3.ops.linear import species_rows
+from ictc_o3.ops.radial_mlp import edge_linear
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
 SILU_SCALE = 1.6791767923989418   # _Normalize2MomSiLU (layers.py:307-314)
@@ -209,7 +211,7 @@ class ScalarReadout(nn.Module):
         nn.init.normal_(self.readout.weight, mean=0.0, std=1.0 / math.sqrt(channels))
 
     def forward(self, h0):
-        return F.linear(h0, self.readout.weight)
+        return edge_linear(h0, self.readout.weight)
 
 
 class MACEStyleReadout(nn.Module):
@@ -224,7 +226,7 @@ class MACEStyleReadout(nn.Module):
         _mace_linear_init(self.linear_2)
 
     def forward(self, h0):
-        return F.linear(self.activation(F.linear(h0, self.linear_1.weight)), self.linear_2.weight)
+        return edge_linear(self.activation(edge_linear(h0, self.linear_1.weight)), self.linear_2.weight)
 
 
 class PureCartesianICTDFix(nn.Module):
@@ -327,7 +329,7 @@ class PureCartesianICTDFix(nn.Module):
                  and all(fused_supported(inter.fc) for inter in self.interactions))
         radial = None if fused else self.radial_embedding(r)
         radial_cfg = (self.max_radius, self.polynomial_cutoff_p, SILU_SCALE)
-        h = self.node_embedding.weight.t().index_select(0, species)
+        h = species_rows(self.node_embedding.weight.t(), species)
         energy = None
         for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
             message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only)

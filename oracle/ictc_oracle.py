@@ -249,16 +249,16 @@ def edge_tp_blocks(x: Dict[int, torch.Tensor], Y: Dict[int, torch.Tensor], gates
     cgs, offsets, count = path_tables(paths)
     E, C = gates.shape[0], gates.shape[2]
     lmax_out = max(l3 for _, _, l3 in paths) if lmax_out is None else lmax_out
-    out = {l: torch.zeros(E, count.get(l, 0) * C, 2 * l + 1, dtype=gates.dtype) for l in range(lmax_out + 1)}
+    blocks: Dict[int, list] = {l: [None] * count.get(l, 0) for l in range(lmax_out + 1)}
     for p, (l1, l2, l3) in enumerate(paths):
         cg = torch.tensor(cgs[p], dtype=gates.dtype)
-        seg = torch.einsum("ecm,en,mnk->eck", x[l1], Y[l2], cg)
+        seg = torch.einsum("ecm,emk->eck", x[l1], torch.einsum("en,mnk->emk", Y[l2], cg))
         if weight is not None:
             seg = seg * weight[p].view(1, C, 1)
         seg = seg * gates[:, p, :].unsqueeze(-1)
-        o = offsets[p] * C
-        out[l3] = out[l3].index_add(1, torch.arange(o, o + C), seg)
-    return out
+        blocks[l3][offsets[p]] = seg          # channel block offsets[p]*C .. +C of out[l3]
+    # offsets are the running count per l3, so the blocks tile out[l3] in order
+    return {l: (torch.cat(b, 1) if b else torch.zeros(E, 0, 2 * l + 1, dtype=gates.dtype)) for l, b in blocks.items()}
 
 
 def pack_ir_mul(blocks: Dict[int, torch.Tensor], lmax: int) -> torch.Tensor:

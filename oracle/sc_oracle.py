@@ -140,9 +140,9 @@ def u_ictc(lmax, l_out, nu):
     letters = "abcdefgh"
     if l_out == 0:
         spec = ",".join(f"{letters[k]}{'ijk'[k]}" for k in range(nu)) + "," + "ijk"[:nu] + "p->" + letters[:nu] + "p"
-        return np.einsum(spec, *([qin] * nu), U)
+        return np.einsum(spec, *([qin] * nu), U, optimize="optimal")
     spec = "ro," + ",".join(f"{letters[k]}{'ijk'[k]}" for k in range(nu)) + ",o" + "ijk"[:nu] + "p->r" + letters[:nu] + "p"
-    return np.einsum(spec, q_block(l_out), *([qin] * nu), U)
+    return np.einsum(spec, q_block(l_out), *([qin] * nu), U, optimize="optimal")
 
 
 def contraction(x, species, weights, lmax, l_out, corr):
@@ -150,19 +150,32 @@ def contraction(x, species, weights, lmax, l_out, corr):
 
     x [N, C, dim] (ICTC basis), species [N] int64, weights[nu] [S, P_nu, C] for nu = 1..corr.
     Returns [N, C * (2 l_out + 1)] (channel-major, as the reference reshapes).
+
+    The reference selects each node's weights (index_select by species) and
+    runs the Horner recursion out = ((c3 x + c2) x + c1) x on per-node
+    coefficients c_nu = U_nu . W_nu[s_n].  The same recursion here runs per
+    species on that species' nodes, so the coefficient tensors are formed once
+    per species instead of once per node (identical arithmetic per node).
     """
-    def coeff(nu):
-        W = weights[nu].index_select(0, species)                      # [N, P, C]
-        U = torch.tensor(u_ictc(lmax, l_out, nu), dtype=x.dtype)
+    N, C = x.shape[0], x.shape[1]
+    U = {nu: torch.tensor(u_ictc(lmax, l_out, nu), dtype=x.dtype) for nu in range(1, corr + 1)}
+
+    def coeff(nu, s):
+        W = weights[nu][s]                                             # [P, C]
         if l_out == 0:
-            return torch.einsum("...p,npc->nc...", U, W)
-        return torch.einsum("m...p,npc->ncm...", U, W)
-    out = coeff(corr)
-    for nu in range(corr - 1, 0, -1):
-        out = torch.einsum("nc...i,nci->nc...", out, x)
-        out = out + coeff(nu)
-    out = torch.einsum("nc...i,nci->nc...", out, x)
-    return out.reshape(out.shape[0], -1)
+            return torch.einsum("...p,pc->c...", U[nu], W)
+        return torch.einsum("m...p,pc->cm...", U[nu], W)
+
+    out = x.new_zeros(N, C * (2 * l_out + 1))
+    for s in torch.unique(species).tolist():
+        idx = torch.nonzero(species == s).flatten()
+        xs = x.index_select(0, idx)
+        o = torch.einsum("c...i,nci->nc...", coeff(corr, s), xs)
+        for nu in range(corr - 1, 0, -1):
+            o = o + coeff(nu, s)
+            o = torch.einsum("nc...i,nci->nc...", o, xs)
+        out = out.index_copy(0, idx, o.reshape(o.shape[0], -1))
+    return out
 
 
 def symmetric_contraction(x, species, weights_by_L, lmax, target_lmax, corr):

@@ -151,3 +151,123 @@ def test_cfg1_edge_tp_at_2_pow_20(device):
     rows = torch.randint(0, E, (1024,), generator=g)
     ref = orc.edge_tp_packed(x[rows].double(), Y[rows].double(), gates[rows].double(), 2, 2, 2, C)
     assert rel_err(out[rows], ref) < 1e-5
+
+
+def _oracle_gates(r, Ws, cutoff):
+    """Bessel x polynomial cutoff (p = 5) -> 8-64-64-64-M MLP with normalized SiLU, float64 (layers.py:826-835)."""
+    t = mo.radial(r, cutoff, 8, 5)
+    for i, W in enumerate(Ws):
+        t = t @ W.t()
+        if i < len(Ws) - 1:
+            t = mo._silu(t)
+    return t
+
+
+def test_cfg2_full_size_backward_with_radial_gates(device):
+    """cfg2 forward + backward at full size with the gates from the fused Bessel + MLP kernel.
+
+    Per-edge gradients (harmonics, edge length through the gates) of sampled
+    edges, feature gradients of sampled sender rows, and receiver rows of the
+    output, each against the float64 oracle evaluated on exactly the edges those
+    rows depend on; the MLP weight gradients at full size against the oracle's
+    MLP adjoint fed the same gate cotangent (itself checked on the sampled edges).
+    """
+    from ictc_o3 import PackedGraphMessage, direction_harmonics
+    from ictc_o3.ops.radial_mlp import _RadialGates
+    from mace_ictc.hp import radius_graph_pbc
+    g = torch.Generator().manual_seed(4321)
+    Lb = (4096 / 0.1) ** (1 / 3)
+    N, C, cutoff = 4096, 64, 4.5
+    pos = torch.rand(N, 3, generator=g, dtype=torch.float64) * Lb
+    cell = torch.eye(3, dtype=torch.float64) * Lb
+    src, dst, shf = radius_graph_pbc(pos.float().to(device), cell.float().to(device), cutoff)
+    s, d = src.cpu(), dst.cpu()
+    E = s.numel()
+    assert 140000 < E < 175000
+    vec = (pos[d] - pos[s] + shf.double().cpu() @ cell).float().double()     # FP32-exact inputs
+    r = vec.norm(dim=1)
+    op = PackedGraphMessage.create(channels=C, input_lmax=2, edge_lmax=2, output_lmax=2, device=device)
+    P = op.tp.num_paths
+    widths = [8, 64, 64, 64, P * C]
+    Ws = [(torch.randn(o, i, generator=g, dtype=torch.float64) / i ** 0.5).float().double()
+          for i, o in zip(widths[:-1], widths[1:])]
+    x = torch.randn(N, 9 * C, generator=g).double()
+    go = torch.randn(N, op.output_width, generator=g).double()
+    # product: harmonics of the edge directions, fused radial gates, message; all gradients
+    xd = x.float().to(device).requires_grad_(True)
+    nd = (vec / r[:, None]).float().to(device)
+    Yd = torch.cat(direction_harmonics(nd, 2), -1).detach().requires_grad_(True)
+    rd = r.float().to(device).requires_grad_(True)
+    Wd = [W.float().to(device).requires_grad_(True) for W in Ws]
+    gates_d = _RadialGates.apply(rd, *Wd, cutoff, 5, mo.SILU)
+    gates_d.retain_grad()
+    out = op(xd, Yd, gates_d, src, dst)
+    out.backward(go.float().to(device))
+    Y = Yd.detach().double().cpu()
+    # receiver rows of the output and per-edge gradients of the edges ending there
+    rows = torch.tensor([0, 5, 777, 2048, 4095])
+    sel = torch.isin(d, rows)
+    rs = r[sel].clone().requires_grad_(True)
+    Ys = Y[sel].clone().requires_grad_(True)
+    Wl = [W.clone().requires_grad_(True) for W in Ws]
+    gs = _oracle_gates(rs, Wl, cutoff)
+    ref = orc.message_packed(x, Ys, gs, s[sel], d[sel], None, 2, 2, 2, C)
+    assert rel_err(out.detach()[rows.to(device)], ref[rows]) < 1e-5
+    torch.autograd.backward(ref, go)
+    idx = torch.nonzero(sel).flatten().to(device)
+    assert rel_err(Yd.grad[idx], Ys.grad) < 1e-5
+    assert rel_err(rd.grad[idx], rs.grad) < 1e-5
+    # feature gradients of sampled sender rows: every edge leaving them
+    senders = torch.tensor([1, 100, 2049, 3000, 4094])
+    ssel = torch.isin(s, senders)
+    xs = x.clone().requires_grad_(True)
+    ref2 = orc.message_packed(xs, Y[ssel], _oracle_gates(r[ssel], Ws, cutoff), s[ssel], d[ssel], None, 2, 2, 2, C)
+    torch.autograd.backward(ref2, go)
+    assert rel_err(xd.grad[senders.to(device)], xs.grad[senders]) < 1e-5
+    # full-size MLP weight gradients: oracle adjoint of the gates fed the product's gate cotangent
+    dg = gates_d.grad.double().cpu()
+    Wf = [W.clone().requires_grad_(True) for W in Ws]
+    torch.autograd.backward(_oracle_gates(r, Wf, cutoff), dg)
+    for a, b in zip(Wd, Wf):
+        assert float((a.grad.double().cpu() - b.grad).norm() / b.grad.norm()) < 3e-5
+
+
+def test_cfg3_full_size_sc_backward(device):
+    """cfg3 feature gradient on sampled nodes vs the oracle; weight gradients at full size as the
+    sum of the weight gradients of two disjoint halves of the nodes (row-additivity)."""
+    from ictc_o3 import create_symmetric_contraction
+    N, C, S = 32768, 64, 4
+    torch.manual_seed(11)
+    mod = create_symmetric_contraction(num_elements=S, lmax=2, target_lmax=1, channels=C, correlation=3,
+                                       device=device)
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(N, C, 9, generator=g, dtype=torch.float64)
+    species = torch.randint(0, S, (N,), generator=g)
+    go = torch.randn(N, 4 * C, generator=g, dtype=torch.float64)
+    xp = x.transpose(1, 2).reshape(N, -1).float().to(device).requires_grad_(True)
+    sd, god = species.to(device), go.float().to(device)
+    out = mod.contract(xp, sd)
+    params = [p for p in mod.parameters() if p.requires_grad]
+    grads = torch.autograd.grad(out, [xp, *params], god)
+    dx = grads[0].double().cpu()
+    rows = torch.randint(0, N, (512,), generator=g)
+    W = {L: {nu: c.weight_for(nu).detach().double().cpu() for nu in range(1, 4)}
+         for L, c in enumerate(mod.symmetric_contractions.contractions)}
+    xr = x[rows].clone().requires_grad_(True)
+    ref = so.symmetric_contraction(xr, species[rows], W, 2, 1, 3)
+    # the product's output and cotangent are component-major per degree; the oracle's channel-major
+    parts, off = [], 0
+    for L in range(2):
+        w = C * (2 * L + 1)
+        parts.append(go[rows][:, off:off + w].reshape(-1, 2 * L + 1, C).transpose(1, 2).reshape(-1, w))
+        off += w
+    torch.autograd.backward(ref, torch.cat(parts, -1))
+    dx_ref = xr.grad.transpose(1, 2).reshape(len(rows), -1)
+    assert rel_err(dx[rows], dx_ref) < 1e-5
+    half = torch.randperm(N, generator=g)[: N // 2].to(device)
+    mask = torch.zeros(N, dtype=torch.bool, device=device)
+    mask[half] = True
+    ga = torch.autograd.grad(mod.contract(xp, sd), params, god * mask[:, None])
+    gb = torch.autograd.grad(mod.contract(xp, sd), params, god * (~mask)[:, None])
+    for full, a, b in zip(grads[1:], ga, gb):
+        assert float((full - (a + b)).norm() / full.norm()) < 1e-5
