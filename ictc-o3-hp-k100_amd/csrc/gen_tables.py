@@ -139,6 +139,85 @@ def tp_struct(li, le, lo):
     return "\n".join(lines)
 
 
+def tp_group_struct(li, le, lo, l1):
+    """``TpG<LI,LE,LO,L1>``: the paths of ``Tp<LI,LE,LO>`` with input degree l1 only.
+
+    Paths are enumerated l1 outer, so a group is the contiguous range
+    P0 .. P0+PG-1 of path indices (and of gate rows).  Operands are the group's
+    views: x[NXG] the degree-l1 block (component m1), gw[PG] the group's gates,
+    o / go[NOG] the group's output slots, whose packed output components are
+    SLOT[0..NOG) in ascending order.  Same term grouping as ``Tp``.
+    """
+    paths = tables.natural_paths(li, le, lo)
+    group = [p for p, path in enumerate(paths) if path[0] == l1]
+    if not group:
+        return None
+    T = tables.PathTable(paths, lmax_out=lo)
+    p0, PG = group[0], len(group)
+    assert group == list(range(p0, p0 + PG))
+    slots = sorted({T.out_component(p, m3) for p in group for m3 in range(2 * paths[p][2] + 1)})
+    local = {k: n for n, k in enumerate(slots)}
+    ent = []
+    for p in group:
+        for (m1, m2, m3, v) in T.nonzeros(p):
+            ent.append((p - p0, m1, paths[p][1] ** 2 + m2, local[T.out_component(p, m3)], v))
+    NY = (le + 1) ** 2
+    lines = [f"template <> struct TpG<{li}, {le}, {lo}, {l1}> {{",
+             f"  static constexpr int LI = {li}, LE = {le}, LO = {lo}, L1 = {l1};",
+             f"  static constexpr int NXG = {2 * l1 + 1}, X0 = {l1 * l1}, NY = {NY}, P0 = {p0}, PG = {PG}, "
+             f"NOG = {len(slots)}, NO = {T.out_components};",
+             f"  static constexpr int SLOT[{len(slots)}] = {{{', '.join(map(str, slots))}}};"]
+    path_of, by_kj = {}, {}
+    for p, i, j, k, v in ent:
+        path_of[k] = p
+        by_kj.setdefault(k, {}).setdefault(j, []).append((i, v))
+
+    def b_expr(x, terms):
+        return " + ".join(f"{f(v)} * {x}[{i}]" for i, v in terms)
+
+    def t_expr(x, y, js):
+        return " + ".join(f"{y}[{j}] * ({b_expr(x, terms)})" for j, terms in sorted(js.items()))
+
+    lines.append("  __device__ __forceinline__ static void fwd_b(const float* __restrict__ x, const float* __restrict__ y,"
+                 " const float* __restrict__ gw, float* __restrict__ o) {")
+    for k, js in sorted(by_kj.items()):
+        lines.append(f"    o[{k}] = fmaf(gw[{path_of[k]}], {t_expr('x', 'y', js)}, o[{k}]);")
+    lines.append("  }")
+    lines.append("  __device__ __forceinline__ static void dx(const float* __restrict__ y, const float* __restrict__ gw,"
+                 " const float* __restrict__ go, float* __restrict__ d) {")
+    by_ij = {}
+    for p, i, j, k, v in ent:
+        by_ij.setdefault(i, {}).setdefault(j, {}).setdefault(p, []).append((k, v))
+    for i, js in sorted(by_ij.items()):
+        parts = []
+        for j, ps in sorted(js.items()):
+            inner = " + ".join(f"gw[{p}] * ({' + '.join(f'{f(v)} * go[{k}]' for k, v in ks)})"
+                               for p, ks in sorted(ps.items()))
+            parts.append(f"y[{j}] * ({inner})")
+        lines.append(f"    d[{i}] += {' + '.join(parts)};")
+    lines.append("  }")
+    lines.append("  __device__ __forceinline__ static void dydg(const float* __restrict__ x, const float* __restrict__ y,"
+                 " const float* __restrict__ gw, const float* __restrict__ go, float* __restrict__ dyv,"
+                 " float* __restrict__ d) {")
+    lines.append(f"#pragma unroll\n    for (int p = 0; p < {PG}; ++p) d[p] = 0.f;")
+    for k, js in sorted(by_kj.items()):
+        p = path_of[k]
+        lines.append(f"    {{ const float w = gw[{p}] * go[{k}]; float t = 0.f;")
+        for j, terms in sorted(js.items()):
+            lines.append(f"      {{ const float b = {b_expr('x', terms)}; dyv[{j}] = fmaf(w, b, dyv[{j}]);"
+                         f" t = fmaf(y[{j}], b, t); }}")
+        lines.append(f"      d[{p}] = fmaf(go[{k}], t, d[{p}]); }}")
+    lines.append("  }")
+    lines.append("  __device__ __forceinline__ static void dg(const float* __restrict__ x, const float* __restrict__ y,"
+                 " const float* __restrict__ go, float* __restrict__ d) {")
+    lines.append(f"#pragma unroll\n    for (int p = 0; p < {PG}; ++p) d[p] = 0.f;")
+    for k, js in sorted(by_kj.items()):
+        lines.append(f"    d[{path_of[k]}] = fmaf(go[{k}], {t_expr('x', 'y', js)}, d[{path_of[k]}]);")
+    lines.append("  }")
+    lines.append("};")
+    return "\n".join(lines)
+
+
 def sh_struct(L):
     N = (L + 1) ** 2
     lines = [f"template <> struct Sh<{L}> {{", f"  static constexpr int N = {N};",
@@ -259,6 +338,12 @@ def generate(path):
                 if s is not None:
                     parts.append(s)
                     configs.append((li, le, lo))
+    parts.append("template <int LI, int LE, int LO, int L1> struct TpG;")
+    for li, le, lo in configs:
+        for l1 in range(li + 1):
+            g = tp_group_struct(li, le, lo, l1)
+            if g is not None:
+                parts.append(g)
     for L in range(LMAX + 1):
         parts.append(sh_struct(L))
     parts.append("}  // namespace ictc")
