@@ -29,6 +29,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/ictc_mi355x.h"
 
 namespace ictc {
@@ -635,6 +637,77 @@ unsigned grid_for(int64_t edges, int waves, int blocks_per_cu) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+
+// Argument checks shared by the two gate-tangent entry points: a negative
+// error code, 1 when there is nothing to do (no edges), 0 to launch.
+int gates_tangent_check(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                        const float* W1, const float* W2, const float* W3, const float* W4, int gates,
+                        const float* out, const float* tangent) {
+  if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
+  if (edges < 0 || !(cutoff > 0.f) || poly_p < 2 || gates <= 0 || gates % 16)
+    return fail(ICTC_ERR_ARGUMENT, "radial gates: invalid arguments (gates must be a positive multiple of 16)");
+  if (edges == 0) return 1;
+  if (!r || !W1 || !W2 || !W3 || !W4 || !out || !tangent) return fail(ICTC_ERR_ARGUMENT, "radial gates: null operand");
+  if (!aligned16(out) || !aligned16(tangent)) return fail(ICTC_ERR_ARGUMENT, "radial gates: operands must be 16-byte aligned");
+  return 0;
+}
+
+// W4 split into MFMA operand order in `ws`, then the gates and their r tangents.
+int gates_tangent_launch(const float* r, int64_t edges, float cutoff, int poly_p, const float* W1, const float* W2,
+                         const float* W3, const float* W4, int gates, float silu_scale, float* out, float* tangent,
+                         bf16x8* ws, hipStream_t st) {
+  const int split_threads = (gates / 16) * 2 * 64;
+  hipLaunchKernelGGL(gates_split_kernel, dim3((split_threads + 255) / 256), dim3(256), 0, st, W4, gates, ws);
+  if (int rc = launch_status("ictc_radial_gates_tangent_fwd split")) return rc;
+  if (gates <= SMALL_MAX_GATES) {
+    const size_t lds = (size_t)(gates / 16) * 6 * 64 * sizeof(bf16x8);
+    const int64_t tiles = (edges + 15) / 16, cap = (int64_t)cu_count() * SMALL_WAVES;
+    const int64_t blocks = (tiles + SMALL_WAVES - 1) / SMALL_WAVES;
+    hipLaunchKernelGGL(gates_small_kernel<true>, dim3((unsigned)(blocks < cap / SMALL_WAVES ? blocks : cap / SMALL_WAVES)),
+                       dim3(SMALL_WAVES * 64), lds, st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale,
+                       (const bf16x8*)ws, gates, out, tangent);
+    return launch_status("ictc_radial_gates_tangent_fwd launch");
+  }
+  const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
+  const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel<true>, GATE_TILES * 64, 3);
+  hipLaunchKernelGGL(gates_fwd_kernel<true>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0,
+                     st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)ws, gates, out,
+                     tangent);
+  return launch_status("ictc_radial_gates_tangent_fwd launch");
+}
+
+// ---- static scratch of the no-alloc entry point ----------------------------
+// The split W4 of ictc_radial_gates_tangent_fwd_noalloc lives in this
+// file-scope device array (ICTC_NOALLOC_MAX_GATES * 384 bytes, held by every
+// GPU the library runs on until the process ends).  Host code never passes
+// the array's name to a kernel: its device address is looked up once per
+// device with hipGetSymbolAddress and kept per device.
+constexpr int kNoallocWords = ICTC_NOALLOC_MAX_GATES * 24;   // bf16x8 words (384 bytes per gate)
+static __device__ __align__(256) bf16x8 scratch[kNoallocWords];
+
+constexpr int kMaxDevices = 64;
+bf16x8* g_scratch[kMaxDevices] = {};
+std::mutex g_scratch_mu;
+
+int noalloc_scratch(bf16x8** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(ICTC_ERR_RUNTIME, "radial gates (no-alloc): no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      char buf[256];
+      snprintf(buf, sizeof(buf), "radial gates (no-alloc): hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return fail(ICTC_ERR_RUNTIME, buf);
+    }
+    g_scratch[dev] = static_cast<bf16x8*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return ICTC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -685,36 +758,28 @@ int ictc_radial_gates_tangent_fwd(const float* r, int64_t edges, int num_basis, 
                                   const float* W1, const float* W2, const float* W3, const float* W4, int gates,
                                   float silu_scale, float* out, float* tangent, void* workspace,
                                   int64_t workspace_bytes, void* stream) {
-  if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
-  if (edges < 0 || !(cutoff > 0.f) || poly_p < 2 || gates <= 0 || gates % 16)
-    return fail(ICTC_ERR_ARGUMENT, "radial gates: invalid arguments (gates must be a positive multiple of 16)");
-  if (edges == 0) return ICTC_OK;
-  if (!r || !W1 || !W2 || !W3 || !W4 || !out || !tangent || !workspace)
-    return fail(ICTC_ERR_ARGUMENT, "radial gates: null operand");
+  if (int rc = gates_tangent_check(r, edges, num_basis, hidden, cutoff, poly_p, W1, W2, W3, W4, gates, out, tangent))
+    return rc > 0 ? ICTC_OK : rc;
+  if (!workspace) return fail(ICTC_ERR_ARGUMENT, "radial gates: null operand");
   if (workspace_bytes < ictc_radial_gates_workspace_bytes(gates))
     return fail(ICTC_ERR_ARGUMENT, "radial gates: workspace too small");
-  if (!aligned16(out) || !aligned16(tangent) || !aligned16(workspace))
-    return fail(ICTC_ERR_ARGUMENT, "radial gates: operands must be 16-byte aligned");
-  hipStream_t st = (hipStream_t)stream;
-  const int split_threads = (gates / 16) * 2 * 64;
-  hipLaunchKernelGGL(gates_split_kernel, dim3((split_threads + 255) / 256), dim3(256), 0, st, W4, gates,
-                     (bf16x8*)workspace);
-  if (int rc = launch_status("ictc_radial_gates_tangent_fwd split")) return rc;
-  if (gates <= SMALL_MAX_GATES) {
-    const size_t lds = (size_t)(gates / 16) * 6 * 64 * sizeof(bf16x8);
-    const int64_t tiles = (edges + 15) / 16, cap = (int64_t)cu_count() * SMALL_WAVES;
-    const int64_t blocks = (tiles + SMALL_WAVES - 1) / SMALL_WAVES;
-    hipLaunchKernelGGL(gates_small_kernel<true>, dim3((unsigned)(blocks < cap / SMALL_WAVES ? blocks : cap / SMALL_WAVES)),
-                       dim3(SMALL_WAVES * 64), lds, st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale,
-                       (const bf16x8*)workspace, gates, out, tangent);
-    return launch_status("ictc_radial_gates_tangent_fwd launch");
-  }
-  const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
-  const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel<true>, GATE_TILES * 64, 3);
-  hipLaunchKernelGGL(gates_fwd_kernel<true>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0,
-                     st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates, out,
-                     tangent);
-  return launch_status("ictc_radial_gates_tangent_fwd launch");
+  if (!aligned16(workspace)) return fail(ICTC_ERR_ARGUMENT, "radial gates: operands must be 16-byte aligned");
+  return gates_tangent_launch(r, edges, cutoff, poly_p, W1, W2, W3, W4, gates, silu_scale, out, tangent,
+                              (bf16x8*)workspace, (hipStream_t)stream);
+}
+
+int ictc_radial_gates_tangent_fwd_noalloc(const float* r, int64_t edges, int num_basis, int hidden, float cutoff,
+                                          int poly_p, const float* W1, const float* W2, const float* W3,
+                                          const float* W4, int gates, float silu_scale, float* out, float* tangent,
+                                          void* stream) {
+  if (gates > ICTC_NOALLOC_MAX_GATES)
+    return fail(ICTC_ERR_ARGUMENT, "radial gates (no-alloc): more gates than the static scratch holds");
+  if (int rc = gates_tangent_check(r, edges, num_basis, hidden, cutoff, poly_p, W1, W2, W3, W4, gates, out, tangent))
+    return rc > 0 ? ICTC_OK : rc;
+  bf16x8* ws = nullptr;
+  if (int rc = noalloc_scratch(&ws)) return rc;
+  return gates_tangent_launch(r, edges, cutoff, poly_p, W1, W2, W3, W4, gates, silu_scale, out, tangent, ws,
+                              (hipStream_t)stream);
 }
 
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,

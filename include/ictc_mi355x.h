@@ -346,6 +346,19 @@ int ictc_radial_gates_tangent_fwd(const float* r, int64_t edges, int num_basis, 
                                   const float* W1, const float* W2, const float* W3, const float* W4, int gates,
                                   float silu_scale, float* out, float* tangent, void* workspace,
                                   int64_t workspace_bytes, void* stream);
+/* ictc_radial_gates_tangent_fwd without a workspace argument and without any
+ * allocation: the split W4 goes to a static device array of
+ * ICTC_NOALLOC_MAX_GATES * 384 bytes (1.5 MiB) that each GPU holds until the
+ * process ends.  No counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses
+ * that forbid hipMalloc); gates above ICTC_NOALLOC_MAX_GATES fail with
+ * ICTC_ERR_ARGUMENT.  All calls on one GPU share the array: calls that
+ * overlap in time on one GPU (different streams or threads) race.            */
+#define ICTC_NOALLOC_MAX_GATES 4096
+int ictc_radial_gates_tangent_fwd_noalloc(const float* r, int64_t edges, int num_basis, int hidden, float cutoff,
+                                          int poly_p, const float* W1, const float* W2, const float* W3,
+                                          const float* W4, int gates, float silu_scale, float* out, float* tangent,
+                                          void* stream);
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
                         float* dr, float* dz1, float* dz2, float* dz3, float* a1, float* a2, void* stream);
