@@ -16,10 +16,13 @@ One step = radial MLP -> gates -> CSR message forward -> backward to
 (features, harmonics, gates, radial weights), all on the GPU.  Inputs are
 resident in HBM before the timed region.
 
-Roofline: the dominant message kernel is timed live with HIP events on the
-stream it runs on (torch's current stream), averaged over repeated launches;
-its algorithmic bytes (compulsory traffic: each operand read once, each output
+Roofline: the step's layer-1 kernels (radial gates with their r tangents,
+message forward, gate-tangent message adjoint) are timed live with HIP events
+on the stream they run on (torch's current stream), averaged over repeated
+launches; the one with the largest time is the roofline kernel: its
+algorithmic bytes (compulsory traffic: each operand read once, each output
 written once, index arrays included, gathers not counted) / time vs 8 TB/s.
+``roofline_kernels`` lists all of them.
 
 CPU baseline: the FP32 torch-eager restatement of the reference path
 (oracle/: gather, per-path CG einsum, gate, index_add, SC recursion, linears,
@@ -46,7 +49,7 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.
 MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 20.07e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
                     ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9,
-                    ("msg_bwd_tan", 131072, 5262704, 64): 53.10e9}
+                    ("msg_bwd_tan", 131072, 5262704, 64): 53.10e9, ("gates_tan", 131072, 5262704, 64): 31.50e9}
 
 
 def log(*a):
@@ -300,10 +303,12 @@ def run_cfg4(args):
 
     src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
     kern, nbytes = layer_message_kernels(model, src, dst, N, pos)
-    # the step's own message kernels (energy + forces: the forward and the gate-tangent adjoint); the other
-    # adjoint forms are timed for reference only
-    in_step = [k for k in ("msg_fwd", "msg_bwd_tan") if k in kern] if "msg_bwd_tan" in kern else list(kern)
-    dom = max(in_step, key=kern.get)   # the step's message kernel with the largest time
+    # the layer-1 radial gates with their r tangents (the step's largest kernel), timed the same way
+    kern["gates_tan"], nbytes["gates_tan"] = layer_gate_kernel(model, src.numel())
+    # the step's own layer-1 kernels (energy + forces: radial gates with tangents, message forward,
+    # gate-tangent adjoint); the other adjoint forms are timed for reference only
+    in_step = [k for k in ("gates_tan", "msg_fwd", "msg_bwd_tan") if k in kern]
+    dom = max(in_step, key=kern.get)   # the step's kernel with the largest time
     achieved = nbytes[dom] / kern[dom] / 1e9
     result = {
         "metric": METRIC,
@@ -320,8 +325,31 @@ def run_cfg4(args):
         "roofline": {"bound": "hbm", "kernel": f"{dom} (layer 1, P11 C64)", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": MEASURED_TRAFFIC.get((dom, N, E, 64))},
+        # every layer-1 kernel of the step, largest first (the first is the roofline kernel above)
+        "roofline_kernels": [{"kernel": k, "time_us": round(kern[k] * 1e6, 1),
+                              "algorithmic_GB": round(nbytes[k] / 1e9, 3),
+                              "achieved": nbytes[k] / kern[k] / 1e9, "frac": nbytes[k] / kern[k] / 1e9 / HBM_PEAK_GBS,
+                              "traffic": MEASURED_TRAFFIC.get((k, N, E, 64))}
+                             for k in sorted(in_step, key=kern.get, reverse=True)],
     }
     return result, model
+
+
+def layer_gate_kernel(model, E, reps=5):
+    """HIP-event time of the layer-1 radial gates with their r tangents (ictc_radial_gates_tangent_fwd: W4
+    split, then the MLP, both projections and both stores) and its algorithmic bytes: the edge lengths read,
+    gates and tangents [E, M] written (weights: under 0.3 MB)."""
+    import torch
+    from ictc_o3.ops.radial_mlp import radial_gates_tangent
+    inter = model.interactions[-1]
+    dev = next(model.parameters()).device
+    lin = [m.weight for m in inter.fc if isinstance(m, torch.nn.Linear)]
+    M = lin[-1].shape[0]
+    r = torch.rand(E, device=dev, generator=torch.Generator(device=dev).manual_seed(4)) * 3 + 1.5
+    t = time_launches(lambda: radial_gates_tangent(r, lin, model.max_radius, model.polynomial_cutoff_p,
+                                                   1.6791767923989418), reps, torch.cuda.current_stream(dev))
+    log(f"  last-layer gates_tan: {t * 1e6:.1f} us  {(E * 4 + 2 * E * M * 4) / t / 1e9:.0f} GB/s")
+    return t, E * 4 + 2 * E * M * 4
 
 
 def layer_message_kernels(model, src, dst, N, pos, reps=5):

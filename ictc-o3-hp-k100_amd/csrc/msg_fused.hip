@@ -1,0 +1,631 @@
+// Fused radial-gate graph message for energy + forces: the gates
+// g[e, p, c] = sum_k h3[e, k] W4[p C + c, k] (the last Linear of the radial MLP
+// `fc`, layers.py:826-835) are formed tile by tile inside the message kernels
+// from the MLP's last hidden activation h3 [E, 64] and never written to HBM
+// (the reference's streamed gate message, ictc_o3/ops/streamed_gate_message.py:
+// 51-57 and _StreamedGate :87-223, which tiles the projection with the TP the
+// same way for frozen-weight force inference).  The adjoint rebuilds the
+// gates and their r tangents gdot = sum_k t3[e, k] W4[p C + c, k] (t3 =
+// d h3 / dr) per tile and forms dE/dr = sum dgates * gdot in registers.
+//
+// Path groups.  The projection matrix of 11 paths x 64 channels (64 x 704,
+// 270 KB as the three bf16 parts below) does not fit the 160 KB LDS, so a
+// launch covers the paths of one input degree l1 (a contiguous range of path
+// indices: paths are enumerated l1 outer), whose W4 rows (PG x 64 x 64, split:
+// PG x 24 KB) stay in LDS for a persistent block.  Such a group reads only
+// the degree-l1 block of the gathered features and writes only its own
+// output slots, so the groups' launches together gather each feature row
+// once; the per-edge harmonic gradient and dr are sums over all paths and
+// accumulate over the group launches in launch order (deterministic, no
+// atomics).  Each launch also covers one channel group of 64.
+//
+// Projection on bf16 MFMA with the three-way operand split (split_bf16.h):
+// A = h3 rows of a 16-edge tile (edge = MFMA row), B = W4^T columns of 16
+// channels, v_mfma_f32_16x16x32_bf16, six products per 16x16x32 block,
+// FP32-level accuracy.  The result D[edge][channel] (lane (q, j) holds edges
+// 4q .. 4q+3 of channel 16 cb + j) is transposed to one channel per lane
+// (lane 16 b + j holds edges 0 .. 15 of channel 16 b + j) by a 4 x 4 block
+// transpose across the lane rows: one v_permlane32_swap and one
+// v_permlane16_swap stage.  The edge loop then runs the generated group
+// contraction TpG on wave-uniform harmonics exactly like the materialised-gate
+// kernels.  The adjoint's tiles are 8 edges: rows 0..7 carry h3 and rows
+// 8..15 t3 of the same edges, so one MFMA pass yields gates and tangents.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ictc_mi355x.h"
+#include "ictc_launch.h"
+#include "split_bf16.h"
+
+namespace ictc {
+int set_error(int code, const char* msg);
+}
+
+namespace ictc {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Waves per block (one block per CU: the W4 slice fills the LDS): 16 where the
+// kernel fits 128 VGPRs (input degree 0 groups), else 8.
+template <class TG>
+constexpr int fused_waves() { return TG::L1 == 0 ? 16 : 8; }
+constexpr int kSlice = 4 * 2 * 3 * 64;       // bf16x8 words of one path's split W4 for one channel group (24 KB)
+
+__device__ __forceinline__ v4f mfma_bf16(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Split projection: ws[((p G + cg) 4 + cb) 2 + ks][part][lane] = part of
+// W4[p C + 64 cg + 16 cb + l%16][32 ks + 8 (l/16) + e] * w[p, 64 cg + 16 cb + l%16]
+// (e = 0..7; w the TP path weight, nullptr = 1): the B operand of the 16x16x32 MFMA.
+__global__ void fused_split_kernel(const float* __restrict__ W4, const float* __restrict__ tpw, int P, int C,
+                                   bf16x8* __restrict__ ws) {
+  const int G = C / 64;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (int64_t)P * G * 4 * 2 * 64) return;
+  const int l = (int)(t & 63), ks = (int)((t >> 6) & 1), cb = (int)((t >> 7) & 3);
+  const int64_t pg = t >> 9;
+  const int p = (int)(pg / G), cg = (int)(pg % G);
+  const int c = 64 * cg + 16 * cb + (l & 15);
+  const float scale = tpw ? tpw[(int64_t)p * C + c] : 1.f;
+  float v[8];
+  const float* row = W4 + ((int64_t)p * C + c) * 64 + 32 * ks + 8 * (l >> 4);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = row[e] * scale;
+  const Split s = split8(v);
+  bf16x8* o = ws + (t >> 6) * 3 * 64 + l;
+  o[0] = s.hi;
+  o[64] = s.mid;
+  o[128] = s.lo;
+}
+
+__global__ void fused_zero_kernel(float* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+
+// Block-wide copy of the group's W4 slices (paths P0 .. P0+PG-1, channel group cg) into LDS.
+template <int PG, int P0>
+__device__ __forceinline__ void stage_slice(const bf16x8* __restrict__ ws, int G, int cg, bf16x8* lds) {
+  for (int t = threadIdx.x; t < PG * kSlice; t += blockDim.x) {
+    const int p = t / kSlice, rest = t - p * kSlice;
+    lds[t] = ws[((int64_t)(P0 + p) * G + cg) * kSlice + rest];
+  }
+}
+
+// 4 x 4 block transpose across the lane rows (16 lanes each) of four 4-vectors:
+// lane (q, j) register [b][r]  ->  lane (b, j) register [q][r].
+__device__ __forceinline__ void transpose_rows(v4f* D) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(D[b][r]), __float_as_uint(D[b + 2][r]), false,
+                                                      false);
+      D[b][r] = __uint_as_float(s[0]);
+      D[b + 2][r] = __uint_as_float(s[1]);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; b += 2) {
+      const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(D[b][r]), __float_as_uint(D[b + 1][r]), false,
+                                                      false);
+      D[b][r] = __uint_as_float(s[0]);
+      D[b + 1][r] = __uint_as_float(s[1]);
+    }
+  }
+}
+
+// Gates of one 16-row tile for every path of the group: A[ks] is the split
+// row block (row l%16, k = 32 ks + 8 (l/16) + e); on return Gt[p][i] holds row
+// i's gate of path p for this lane's channel.
+template <int PG>
+__device__ __forceinline__ void project_tile(const bf16x8* __restrict__ w4l, const Split* A, float (*Gt)[16]) {
+  const int l = lane_id();
+#pragma unroll
+  for (int p = 0; p < PG; ++p) {
+    v4f D[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const bf16x8* b = w4l + (p * 4 + cb) * 2 * 3 * 64 + l;
+      const bf16x8 b0h = b[0], b0m = b[64], b0l = b[128], b1h = b[192], b1m = b[256], b1l = b[320];
+      v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+      // the six products of each k-step, smallest first: lo*hi, hi*lo, mid*mid, mid*hi, hi*mid, hi*hi
+      acc = mfma_bf16(A[0].lo, b0h, acc);
+      acc = mfma_bf16(A[0].hi, b0l, acc);
+      acc = mfma_bf16(A[0].mid, b0m, acc);
+      acc = mfma_bf16(A[1].lo, b1h, acc);
+      acc = mfma_bf16(A[1].hi, b1l, acc);
+      acc = mfma_bf16(A[1].mid, b1m, acc);
+      acc = mfma_bf16(A[0].mid, b0h, acc);
+      acc = mfma_bf16(A[0].hi, b0m, acc);
+      acc = mfma_bf16(A[1].mid, b1h, acc);
+      acc = mfma_bf16(A[1].hi, b1m, acc);
+      acc = mfma_bf16(A[0].hi, b0h, acc);
+      acc = mfma_bf16(A[1].hi, b1h, acc);
+      D[cb] = acc;
+    }
+    transpose_rows(D);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Gt[p][4 * q + r] = D[q][r];
+  }
+}
+
+// Split A operand of one row: 16 floats of row `row` (k = 32 ks + 8 (l/16) .. +7), zero when !ok.
+__device__ __forceinline__ void load_a(const float* __restrict__ h, int64_t row, bool ok, Split* A) {
+  const int g = lane_id() >> 4;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    float v[8];
+    if (ok) {
+      const v4f* p = reinterpret_cast<const v4f*>(h + row * 64 + 32 * ks + 8 * g);
+      const v4f a = p[0], b = p[1];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = a[e];
+        v[4 + e] = b[e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    A[ks] = split8(v);
+  }
+}
+
+// Edge metadata of up to 64 consecutive CSR positions, one edge per lane.
+template <int NY>
+struct FChunk {
+  int32_t e, peer;
+  float m;
+  float y[NY];
+};
+
+template <int NY>
+__device__ __forceinline__ void stage(const float* __restrict__ sh, const float* __restrict__ mask,
+                                      const int64_t* __restrict__ peer_ids, const int32_t* __restrict__ order,
+                                      int64_t rows, int32_t pos, int32_t count, FChunk<NY>& ch) {
+  const int l = lane_id();
+  ch.e = 0;
+  ch.peer = 0;
+  ch.m = 0.f;
+#pragma unroll
+  for (int j = 0; j < NY; ++j) ch.y[j] = 0.f;
+  if (l < count) {
+    const int32_t e = order ? order[pos + l] : pos + l;
+    const int64_t p = peer_ids[e];
+    const bool ok = p >= 0 && p < rows;
+    ch.e = e;
+    ch.peer = ok ? (int32_t)p : 0;
+    ch.m = ok ? (mask ? mask[e] : 1.f) : 0.f;
+#pragma unroll
+    for (int j = 0; j < NY; ++j) ch.y[j] = sh[(int64_t)e * NY + j];
+  }
+}
+
+// Rows of a persistent block.  Block b runs on XCD b % 8; XCD x owns a
+// contiguous share of the row slots, and its blocks stride through that share
+// together (block i of the XCD, wave w: slots begin + i W + w, then + nbx W),
+// so at any time the XCD's waves work on one window of nbx * W consecutive
+// rows and the neighbour rows they gather stay in that XCD's L2.
+struct RowRange {
+  int64_t first, end, stride;
+};
+template <int W>
+__device__ __forceinline__ RowRange block_rows(int64_t slots) {
+  const int64_t nb = gridDim.x, x = blockIdx.x % kXcds, i = blockIdx.x / kXcds;
+  const int64_t q = nb / kXcds, rem = nb % kXcds;
+  const int64_t nbx = q + (x < rem ? 1 : 0);                  // blocks on this XCD
+  const int64_t before = x * q + (x < rem ? x : rem);         // blocks on lower XCDs
+  const int64_t b0 = slots * before / nb, b1 = slots * (before + nbx) / nb;
+  return {b0 + i * W + wave_id(), b1, nbx * W};
+}
+
+// dsh[e, 0..NY) and dr[e] from this lane's shares (dyv, dgt), reduced over the
+// wave's channels; `acc` adds to what the earlier group launches wrote.
+template <int NY>
+__device__ __forceinline__ void put_dsh_dr(float* __restrict__ dsh, float* __restrict__ dr, int64_t e, const float* dyv,
+                                           float dgt, bool acc) {
+  const int j = wave_sums_slot();
+  if constexpr (NY + 1 <= 16) {
+    if (dsh) {
+      float v[NY + 1];
+#pragma unroll
+      for (int k = 0; k < NY; ++k) v[k] = dyv[k];
+      v[NY] = dgt;
+      const float t = wave_sums<NY + 1>(v);
+      if (j >= 0 && j < NY) {
+        float* q = dsh + e * NY + j;
+        *q = acc ? *q + t : t;
+      } else if (j == NY) {
+        dr[e] = acc ? dr[e] + t : t;
+      }
+      return;
+    }
+  } else {
+    if (dsh) {
+      const float t = wave_sums<NY>(dyv);
+      if (j >= 0 && j < NY) {
+        float* q = dsh + e * NY + j;
+        *q = acc ? *q + t : t;
+      }
+    }
+  }
+  const float t = wave_sums<1>(&dgt);
+  if (j == 0) dr[e] = acc ? dr[e] + t : t;
+}
+
+struct FusedArgs {
+  const float* x;       // node features [N, NX*C]
+  const float* sh;      // [E, NY]
+  const float* h;       // h3 [E, 64]
+  const float* t;       // t3 = d h3 / dr [E, 64] (adjoint only)
+  const bf16x8* w4s;    // split projection (fused_split_kernel)
+  const float* mask;    // [E] or nullptr
+  const int64_t* peer;  // src (receiver-owned kernels) or dst (source-owned)
+  int64_t rows, edges;
+  int C, cg;            // channels, channel group of this launch
+  Csr csr;
+};
+
+// Forward: out[n, SLOT[k], c] for the group's slots (receiver-owned).
+template <class TG>
+__global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_fwd_kernel(FusedArgs a, float* __restrict__ out) {
+  extern __shared__ bf16x8 w4l[];
+  constexpr int NX = (TG::LI + 1) * (TG::LI + 1);
+  stage_slice<TG::PG, TG::P0>(a.w4s, a.C / 64, a.cg, w4l);
+  __syncthreads();
+  const int C = a.C, l = lane_id(), c = 64 * a.cg + l;
+  const RowRange rr = block_rows<fused_waves<TG>()>(a.rows);
+  for (int64_t slot = rr.first; slot < rr.end; slot += rr.stride) {
+    const int64_t n = visit_row(a.csr, slot, a.rows);
+    if (n < 0) continue;
+    float o[TG::NOG];
+#pragma unroll
+    for (int k = 0; k < TG::NOG; ++k) o[k] = 0.f;
+    const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+    for (int32_t pos = beg; pos < end; pos += 64) {
+      const int32_t count = min(end - pos, 64);
+      FChunk<TG::NY> ch;
+      stage<TG::NY>(a.sh, a.mask, a.peer, a.csr.order, a.rows, pos, count, ch);
+      for (int t0 = 0; t0 < count; t0 += 16) {
+        const int ci = t0 + (l & 15);
+        const int32_t ea = __shfl(ch.e, ci);
+        Split A[2];
+        load_a(a.h, ea, ci < count, A);
+        float Gt[TG::PG][16];
+        project_tile<TG::PG>(w4l, A, Gt);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          if (t0 + i < count) {
+            const int64_t s = lane_i(ch.peer, t0 + i);
+            const float m = lane_f(ch.m, t0 + i);
+            float y[TG::NY], xv[TG::NXG], gw[TG::PG];
+#pragma unroll
+            for (int j = 0; j < TG::NY; ++j) y[j] = lane_f(ch.y[j], t0 + i);
+            load_row<TG::NXG>(a.x + s * (int64_t)(NX * C) + TG::X0 * C, C, c, xv);
+#pragma unroll
+            for (int p = 0; p < TG::PG; ++p) gw[p] = Gt[p][i] * m;
+            TG::fwd_b(xv, y, gw, o);
+          }
+        }
+      }
+    }
+    float* row = out + n * (int64_t)(TG::NO * C) + c;
+#pragma unroll
+    for (int k = 0; k < TG::NOG; ++k) row[(int64_t)TG::SLOT[k] * C] = o[k];
+  }
+}
+
+// Gate-tangent adjoint, source-owned (sender rows of the source-sorted CSR, the
+// tail slot `rows` holding edges whose sender is out of range): dx of the
+// group's input block, and the group's shares of dsh and dr per edge.
+template <class TG>
+__global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_bwd_src_kernel(FusedArgs a,
+                                                                                const float* __restrict__ grad,
+                                                                                float* __restrict__ dx,
+                                                                                float* __restrict__ dsh,
+                                                                                float* __restrict__ dr, int acc) {
+  extern __shared__ bf16x8 w4l[];
+  constexpr int NX = (TG::LI + 1) * (TG::LI + 1);
+  stage_slice<TG::PG, TG::P0>(a.w4s, a.C / 64, a.cg, w4l);
+  __syncthreads();
+  const int C = a.C, l = lane_id(), c = 64 * a.cg + l;
+  const RowRange rr = block_rows<fused_waves<TG>()>(a.rows + 1);
+  for (int64_t slot = rr.first; slot < rr.end; slot += rr.stride) {
+    const int64_t n = visit_row(a.csr, slot, a.rows);
+    if (n < 0) continue;
+    const bool tail = n == a.rows;
+    float xv[TG::NXG], d[TG::NXG];
+    if (!tail) load_row<TG::NXG>(a.x + n * (int64_t)(NX * C) + TG::X0 * C, C, c, xv);
+    else zero_row<TG::NXG>(xv);
+    zero_row<TG::NXG>(d);
+    const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+    for (int32_t pos = beg; pos < end; pos += 64) {
+      const int32_t count = min(end - pos, 64);
+      FChunk<TG::NY> ch;
+      stage<TG::NY>(a.sh, a.mask, a.peer, a.csr.order, a.rows, pos, count, ch);
+      for (int t0 = 0; t0 < count; t0 += 8) {
+        // rows 0..7: h3 of the tile's edges, rows 8..15: their r tangents
+        const int ci = t0 + (l & 7);
+        const int32_t ea = __shfl(ch.e, ci);
+        Split A[2];
+        load_a((l & 8) ? a.t : a.h, ea, ci < count, A);
+        float Gt[TG::PG][16];
+        project_tile<TG::PG>(w4l, A, Gt);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (t0 + i < count) {
+            const int64_t e = lane_i(ch.e, t0 + i);
+            const int64_t r = lane_i(ch.peer, t0 + i);
+            const float m = lane_f(ch.m, t0 + i);
+            float y[TG::NY], dyv[TG::NY], go[TG::NOG], gw[TG::PG], dg[TG::PG];
+#pragma unroll
+            for (int j = 0; j < TG::NY; ++j) {
+              y[j] = lane_f(ch.y[j], t0 + i);
+              dyv[j] = 0.f;
+            }
+            const float* grow = grad + r * (int64_t)(TG::NO * C) + c;
+#pragma unroll
+            for (int k = 0; k < TG::NOG; ++k) go[k] = grow[(int64_t)TG::SLOT[k] * C];
+#pragma unroll
+            for (int p = 0; p < TG::PG; ++p) gw[p] = Gt[p][i] * m;
+            if (!tail) TG::dx(y, gw, go, d);
+            if (dsh) TG::dydg(xv, y, gw, go, dyv, dg);
+            else TG::dg(xv, y, go, dg);
+            float dgt = 0.f;
+#pragma unroll
+            for (int p = 0; p < TG::PG; ++p) dgt = fmaf(dg[p], Gt[p][8 + i], dgt);
+            put_dsh_dr<TG::NY>(dsh, dr, e, dyv, m * dgt, acc != 0);
+          }
+          // two edges' loads in flight at most: hoisting all eight edges' cotangent rows spills
+          if (i & 1) __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    if (!tail && dx) {
+      float* row = dx + n * (int64_t)(NX * C) + TG::X0 * C + c;
+#pragma unroll
+      for (int i = 0; i < TG::NXG; ++i) row[(int64_t)i * C] = d[i];
+    }
+  }
+}
+
+// Gate-tangent adjoint without the feature gradient, receiver-owned: the
+// receiver's cotangent row is read once per row; the tail slot `rows` holds
+// edges whose receiver is out of range (zero gradients).
+template <class TG>
+__global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_bwd_rcv_kernel(FusedArgs a,
+                                                                                const float* __restrict__ grad,
+                                                                                float* __restrict__ dsh,
+                                                                                float* __restrict__ dr, int acc) {
+  extern __shared__ bf16x8 w4l[];
+  constexpr int NX = (TG::LI + 1) * (TG::LI + 1);
+  stage_slice<TG::PG, TG::P0>(a.w4s, a.C / 64, a.cg, w4l);
+  __syncthreads();
+  const int C = a.C, l = lane_id(), c = 64 * a.cg + l;
+  const RowRange rr = block_rows<fused_waves<TG>()>(a.rows + 1);
+  for (int64_t slot = rr.first; slot < rr.end; slot += rr.stride) {
+    const int64_t n = visit_row(a.csr, slot, a.rows);
+    if (n < 0) continue;
+    const bool tail = n == a.rows;
+    float go[TG::NOG];
+    if (!tail) {
+      const float* grow = grad + n * (int64_t)(TG::NO * C) + c;
+#pragma unroll
+      for (int k = 0; k < TG::NOG; ++k) go[k] = grow[(int64_t)TG::SLOT[k] * C];
+    } else {
+#pragma unroll
+      for (int k = 0; k < TG::NOG; ++k) go[k] = 0.f;
+    }
+    const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+    for (int32_t pos = beg; pos < end; pos += 64) {
+      const int32_t count = min(end - pos, 64);
+      FChunk<TG::NY> ch;
+      stage<TG::NY>(a.sh, a.mask, a.peer, a.csr.order, a.rows, pos, count, ch);
+      for (int t0 = 0; t0 < count; t0 += 8) {
+        const int ci = t0 + (l & 7);
+        const int32_t ea = __shfl(ch.e, ci);
+        Split A[2];
+        load_a((l & 8) ? a.t : a.h, ea, ci < count, A);
+        float Gt[TG::PG][16];
+        project_tile<TG::PG>(w4l, A, Gt);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          if (t0 + i < count) {
+            const int64_t e = lane_i(ch.e, t0 + i);
+            const int64_t s = lane_i(ch.peer, t0 + i);
+            const float m = tail ? 0.f : lane_f(ch.m, t0 + i);
+            float y[TG::NY], dyv[TG::NY], xv[TG::NXG], gw[TG::PG], dg[TG::PG];
+#pragma unroll
+            for (int j = 0; j < TG::NY; ++j) {
+              y[j] = lane_f(ch.y[j], t0 + i);
+              dyv[j] = 0.f;
+            }
+            load_row<TG::NXG>(a.x + s * (int64_t)(NX * C) + TG::X0 * C, C, c, xv);
+#pragma unroll
+            for (int p = 0; p < TG::PG; ++p) gw[p] = Gt[p][i] * m;
+            if (dsh) TG::dydg(xv, y, gw, go, dyv, dg);
+            else TG::dg(xv, y, go, dg);
+            float dgt = 0.f;
+#pragma unroll
+            for (int p = 0; p < TG::PG; ++p) dgt = fmaf(dg[p], Gt[p][8 + i], dgt);
+            put_dsh_dr<TG::NY>(dsh, dr, e, dyv, m * dgt, acc != 0);
+          }
+        }
+      }
+    }
+  }
+}
+
+int fail(int code, const char* msg) { return set_error(code, msg); }
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return ICTC_OK;
+  char buf[256];
+  snprintf(buf, sizeof(buf), "%s: %s", what, hipGetErrorString(e));
+  return fail(ICTC_ERR_RUNTIME, buf);
+}
+
+int cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+enum class Pass { kFwd, kBwdSrc, kBwdRcv };
+
+struct Launch {
+  Pass pass;
+  FusedArgs a;
+  const float* grad;
+  float *out, *dx, *dsh, *dr;
+  int acc;
+  hipStream_t st;
+};
+
+template <class TG>
+int launch_group(const Launch& L) {
+  const size_t lds = (size_t)TG::PG * kSlice * sizeof(bf16x8);
+  const dim3 grid((unsigned)cus()), block(fused_waves<TG>() * 64);
+  switch (L.pass) {
+    case Pass::kFwd:
+      hipLaunchKernelGGL(msg_fused_fwd_kernel<TG>, grid, block, lds, L.st, L.a, L.out);
+      break;
+    case Pass::kBwdSrc:
+      hipLaunchKernelGGL(msg_fused_bwd_src_kernel<TG>, grid, block, lds, L.st, L.a, L.grad, L.dx, L.dsh, L.dr, L.acc);
+      break;
+    case Pass::kBwdRcv:
+      hipLaunchKernelGGL(msg_fused_bwd_rcv_kernel<TG>, grid, block, lds, L.st, L.a, L.grad, L.dsh, L.dr, L.acc);
+      break;
+  }
+  return launch_status("fused message launch");
+}
+
+// Path groups of the compiled degree triples, in launch order (l1 ascending).
+#define ICTC_FUSED_SHAPES(X) \
+  X(0, 2, 2) X(1, 2, 2) X(2, 2, 2)
+
+template <int LI, int LE, int LO, int L1>
+int run_groups(Launch L, int first) {
+  if constexpr (L1 > LI) {
+    return ICTC_OK;
+  } else {
+    L.acc = first ? 0 : 1;
+    if (int rc = launch_group<TpG<LI, LE, LO, L1>>(L)) return rc;
+    return run_groups<LI, LE, LO, L1 + 1>(L, 0);
+  }
+}
+
+int run_all(int li, int le, int lo, const Launch& L, int first) {
+#define ICTC_CASE(A, B, C) \
+  if (li == A && le == B && lo == C) return run_groups<A, B, C, 0>(L, first);
+  ICTC_FUSED_SHAPES(ICTC_CASE)
+#undef ICTC_CASE
+  return fail(ICTC_ERR_UNSUPPORTED, "fused message: degree triple not compiled");
+}
+
+bool fused_shape(int li, int le, int lo) {
+#define ICTC_CASE(A, B, C) \
+  if (li == A && le == B && lo == C) return true;
+  ICTC_FUSED_SHAPES(ICTC_CASE)
+#undef ICTC_CASE
+  return false;
+}
+
+int check(int li, int le, int lo, int C, int64_t N, int64_t E) {
+  if (!fused_shape(li, le, lo)) return fail(ICTC_ERR_UNSUPPORTED, "fused message: degree triple not compiled");
+  if (C <= 0 || C % 64 || C > 64 * kMaxGroups)
+    return fail(ICTC_ERR_UNSUPPORTED, "fused message: channels must be a multiple of 64 up to 256");
+  if (N < 0 || E < 0 || N > INT32_MAX || E > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "fused message: bad sizes");
+  return ICTC_OK;
+}
+
+}  // namespace
+}  // namespace ictc
+
+using namespace ictc;
+
+extern "C" {
+
+int ictc_fused_supported(int input_lmax, int edge_lmax, int output_lmax, int channels) {
+  return fused_shape(input_lmax, edge_lmax, output_lmax) && channels > 0 && channels % 64 == 0 &&
+         channels <= 64 * kMaxGroups;
+}
+
+int64_t ictc_fused_weight_bytes(int paths, int channels) {
+  if (paths <= 0 || channels <= 0 || channels % 64) return -1;
+  return (int64_t)paths * (channels / 64) * kSlice * (int64_t)sizeof(bf16x8);
+}
+
+int ictc_fused_weight_split(const float* W4, const float* tp_weight, int paths, int channels, void* out,
+                            int64_t out_bytes, void* stream) {
+  const int64_t need = ictc_fused_weight_bytes(paths, channels);
+  if (need < 0) return fail(ICTC_ERR_ARGUMENT, "fused weight split: paths > 0 and channels a multiple of 64");
+  if (!W4 || !out) return fail(ICTC_ERR_ARGUMENT, "fused weight split: null operand");
+  if (out_bytes < need) return fail(ICTC_ERR_ARGUMENT, "fused weight split: output smaller than ictc_fused_weight_bytes");
+  if (reinterpret_cast<uintptr_t>(out) & 15) return fail(ICTC_ERR_ARGUMENT, "fused weight split: output not 16-byte aligned");
+  const int64_t threads = (int64_t)paths * (channels / 64) * 4 * 2 * 64;
+  hipLaunchKernelGGL(fused_split_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     W4, tp_weight, paths, channels, (bf16x8*)out);
+  return launch_status("ictc_fused_weight_split launch");
+}
+
+int ictc_msg_fused_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* h3,
+                       const void* w4split, const float* mask, const int64_t* src, int64_t N, int64_t E,
+                       const int32_t* dptr, const int32_t* dorder, const int32_t* dst_rows, float* out, void* stream) {
+  if (int rc = check(li, le, lo, C, N, E)) return rc;
+  if (N == 0) return ICTC_OK;
+  if (!x || !out || !dptr || (E > 0 && (!sh || !h3 || !w4split || !src)))
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_fwd: null operand");
+  if ((reinterpret_cast<uintptr_t>(h3) | reinterpret_cast<uintptr_t>(w4split)) & 15)
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_fwd: h3 and the split weight must be 16-byte aligned");
+  Launch L{Pass::kFwd,
+           FusedArgs{x, sh, h3, nullptr, (const bf16x8*)w4split, mask, src, N, E, C, 0, Csr{dptr, dorder, dst_rows}},
+           nullptr, out, nullptr, nullptr, nullptr, 0, (hipStream_t)stream};
+  for (int cg = 0; cg < C / 64; ++cg) {
+    L.a.cg = cg;
+    if (int rc = run_all(li, le, lo, L, 1)) return rc;
+  }
+  return ICTC_OK;
+}
+
+int ictc_msg_fused_bwd_tangent(int li, int le, int lo, int C, const float* x, const float* sh, const float* h3,
+                               const float* t3, const void* w4split, const float* mask, const int64_t* src,
+                               const int64_t* dst, int64_t N, int64_t E, const int32_t* dptr, const int32_t* dorder,
+                               const int32_t* sptr, const int32_t* sorder, const int32_t* dst_rows,
+                               const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dr,
+                               void* stream) {
+  if (int rc = check(li, le, lo, C, N, E)) return rc;
+  if (E == 0) {
+    // no edges: dsh and dr are empty, dx is zero
+    const int64_t n = dx ? N * (int64_t)(C * (li + 1) * (li + 1)) : 0;
+    if (n == 0) return ICTC_OK;
+    hipLaunchKernelGGL(fused_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, dx, n);
+    return launch_status("ictc_msg_fused_bwd_tangent dx fill");
+  }
+  if (!dr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_bwd_tangent: dr is required");
+  if (!x || !sh || !h3 || !t3 || !w4split || !src || !dst || !grad || !dptr)
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_bwd_tangent: null operand");
+  if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_bwd_tangent: dfeatures needs the source CSR");
+  if ((reinterpret_cast<uintptr_t>(h3) | reinterpret_cast<uintptr_t>(t3) | reinterpret_cast<uintptr_t>(w4split)) & 15)
+    return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_bwd_tangent: h3, t3 and the split weight must be 16-byte aligned");
+  const bool src_owned = dx != nullptr;
+  Launch L{src_owned ? Pass::kBwdSrc : Pass::kBwdRcv,
+           FusedArgs{x, sh, h3, t3, (const bf16x8*)w4split, mask, src_owned ? dst : src, N, E, C, 0,
+                     src_owned ? Csr{sptr, sorder, src_rows} : Csr{dptr, dorder, dst_rows}},
+           grad, nullptr, dx, dsh, dr, 0, (hipStream_t)stream};
+  for (int cg = 0; cg < C / 64; ++cg) {
+    L.a.cg = cg;
+    if (int rc = run_all(li, le, lo, L, cg == 0)) return rc;
+  }
+  return ICTC_OK;
+}
+
+}  // extern "C"

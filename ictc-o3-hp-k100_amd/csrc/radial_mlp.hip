@@ -361,6 +361,31 @@ __global__ __launch_bounds__(FWD_WAVES * 64) void mlp_fwd_kernel(const float* __
   }
 }
 
+// Forward with the forward-mode derivative along r: a3 and t3 = d a3 / dr,
+// both [E, 64] (the hidden state the fused radial-gate message projects).
+__global__ __launch_bounds__(FWD_WAVES * 64) void mlp_tan_kernel(const float* __restrict__ r, int64_t E, float rc,
+                                                                 int p, const float* __restrict__ W1,
+                                                                 const float* __restrict__ W2,
+                                                                 const float* __restrict__ W3, float s,
+                                                                 float* __restrict__ a3, float* __restrict__ t3) {
+  __shared__ FwdWeights ws;
+  stage_fwd(ws, W1, W2, W3);
+  __syncthreads();
+  const Radial q = radial_consts(rc, p);
+  const int waves = blockDim.x >> 6;
+  const int64_t tiles = (E + 15) / 16, stride = (int64_t)gridDim.x * waves;
+  for (int64_t t = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6); t < tiles; t += stride) {
+    const int64_t e = 16 * t + (threadIdx.x & 15);
+    const bool ok = e < E;
+    const float x = ok ? r[e] : 2.f * rc;
+    const FwdWeights& w = *opaque(&ws);
+    v4f a[4], tg[4];
+    forward_tangent_tile(w, q, x, s, a, tg);
+    store_units(a3, e, ok, a);
+    store_units(t3, e, ok, tg);
+  }
+}
+
 // ---- fused radial gates: MLP forward + gate projection ----------------------
 // gates[E, M] = s silu(...) (the MLP's last activation a3) . W4^T, W4 [M, 64]
 // (the last Linear of `fc`).  a3 never leaves the chip: each wave runs the MLP
@@ -723,6 +748,20 @@ int ictc_radial_mlp_fwd(const float* r, int64_t edges, int num_basis, int hidden
   hipLaunchKernelGGL(mlp_fwd_kernel, dim3(grid_for(edges, FWD_WAVES, fwd_per_cu)), dim3(FWD_WAVES * 64), 0,
                      (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, a3);
   return launch_status("ictc_radial_mlp_fwd launch");
+}
+
+int ictc_radial_mlp_tangent_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                                const float* W1, const float* W2, const float* W3, float silu_scale, float* a3,
+                                float* t3, void* stream) {
+  if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
+  if (edges < 0 || !(cutoff > 0.f) || poly_p < 2) return fail(ICTC_ERR_ARGUMENT, "radial MLP: invalid arguments");
+  if (edges == 0) return ICTC_OK;
+  if (!r || !W1 || !W2 || !W3 || !a3 || !t3) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
+  if (!aligned16(a3) || !aligned16(t3)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: a3 and t3 must be 16-byte aligned");
+  const int per_cu = resident_per_cu(mlp_tan_kernel, FWD_WAVES * 64, 3);
+  hipLaunchKernelGGL(mlp_tan_kernel, dim3(grid_for(edges, FWD_WAVES, per_cu)), dim3(FWD_WAVES * 64), 0,
+                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, a3, t3);
+  return launch_status("ictc_radial_mlp_tangent_fwd launch");
 }
 
 int64_t ictc_radial_gates_workspace_bytes(int gates) {

@@ -41,6 +41,12 @@ _SIGNATURES = {
     "ictc_msg_bwd_tangent_workspace_bytes": (_i64, [_i, _i, _i64]),
     "ictc_msg_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
                                   _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "ictc_fused_supported": (_i, [_i, _i, _i, _i]),
+    "ictc_fused_weight_bytes": (_i64, [_i, _i]),
+    "ictc_fused_weight_split": (_i, [_p, _p, _i, _i, _p, _i64, _p]),
+    "ictc_msg_fused_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
+    "ictc_msg_fused_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
+                                        _p, _p, _p, _p, _p, _p, _p]),
     "ictc_sh_fwd": (_i, [_p, _i64, _i, _p, _p]),
     "ictc_sh_bwd": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_jvp": (_i, [_p, _p, _i64, _i, _p, _p]),
@@ -66,6 +72,8 @@ _SIGNATURES = {
     "ictc_edge_geometry_bwd": (_i, [_p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "ictc_edge_vector_bwd": (_i, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_radial_mlp_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p]),
+    "ictc_radial_mlp_tangent_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p,
+                                         _p]),
     "ictc_radial_mlp_bwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p,
                                  _p, _p, _p, _p]),
     "ictc_sc_terms": (_i, [_i, _i, _i]),

@@ -420,11 +420,110 @@ class RadialMessage(torch.autograd.Function):
         return (dx, dsh, dr, *dW, None, None, None, None)
 
 
+# Where the fused radial-gate message (FusedRadialMessage) replaces the materialised-gate RadialMessage:
+# "auto" = the compiled shapes with input degree 0 (cfg4 layer 0, P3 C64: 5.3 against 6.0 ms for the
+# layer's radial gates + message forward + adjoint); with input degree 2 (P11) the three path-group
+# launches of the adjoint measure slower than reading materialised gates (22.8 against 20.7 ms);
+# "always" = every compiled shape; "never" = nowhere.
+FUSED_GATES = "auto"
+
+
+def _fused_weight(fc, W4, spec):
+    """W4 folded with the path weight and split into the fused kernels' MFMA operand layout, cached on `fc`
+    per (storage, version) of the weights (the reference's _folded_weights, streamed_gate_message.py:23-47)."""
+    tpw = spec.weight
+    key = (W4.data_ptr(), W4._version, str(W4.device),
+           None if tpw is None else (tpw.data_ptr(), tpw._version))
+    cached = getattr(fc, "_ictc_fused_w4", None)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    W = _c(W4.detach())
+    nbytes = int(nat.lib().ictc_fused_weight_bytes(spec.num_paths, spec.channels))
+    out = torch.empty(nbytes // 4, dtype=torch.float32, device=W.device)
+    nat.call("ictc_fused_weight_split", nat.ptr(W), None if tpw is None else nat.ptr(_c(tpw.detach())),
+             spec.num_paths, spec.channels, nat.ptr(out), nbytes, nat.stream_of(W))
+    fc._ictc_fused_w4 = (key, out)
+    return out
+
+
+def _fused_ok(spec, x):
+    if FUSED_GATES == "never" or (FUSED_GATES == "auto" and spec.li != 0):
+        return False
+    return (x.is_cuda and x.dtype == torch.float32
+            and bool(nat.lib().ictc_fused_supported(spec.li, spec.le, spec.lo, spec.channels)))
+
+
+class FusedRadialMessage(torch.autograd.Function):
+    """message(x, sh, radial_gates(r, fc)) for energy + forces without materialised gates.
+
+    The forward writes the MLP's last hidden activation h3 and its r tangent
+    t3 = d h3 / dr ([E, 64] each) and the message kernels project the gates
+    (and, in the adjoint, their r tangents) per edge tile from them
+    (streamed_gate_message.py:87-223).  A backward that needs weight
+    gradients rebuilds the gates [E, P*C] from h3 and takes the ordinary
+    message and radial adjoints.
+    """
+
+    @staticmethod
+    def forward(ctx, x, sh, r, W1, W2, W3, W4, spec, topo, mask, cfg, w4s):
+        ctx.set_materialize_grads(False)
+        ctx.inputs = (x, sh, r, W1, W2, W3, W4)
+        ctx.spec, ctx.topo, ctx.mask, ctx.cfg, ctx.w4s = spec, topo, mask, cfg, w4s
+        x, sh, rc = _c(x), _c(sh), _c(r.detach())
+        Ws = [_c(w.detach()) for w in (W1, W2, W3, W4)]
+        E = rc.shape[0]
+        h3, t3 = rc.new_empty(E, 64), rc.new_empty(E, 64)
+        nat.call("ictc_radial_mlp_tangent_fwd", nat.ptr(rc), E, 8, 64, float(cfg[0]), int(cfg[1]),
+                 nat.ptr(Ws[0]), nat.ptr(Ws[1]), nat.ptr(Ws[2]), float(cfg[2]), nat.ptr(h3), nat.ptr(t3),
+                 nat.stream_of(rc))
+        N = x.shape[0]
+        out = x.new_empty(N, spec.out_components * spec.channels)
+        nat.call("ictc_msg_fused_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh),
+                 nat.ptr(h3), nat.ptr(w4s), nat.ptr(mask), nat.ptr(topo.src), N, E, nat.ptr(topo.by_dst.ptr),
+                 nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.stream_of(x))
+        ctx.save_for_backward(x, sh, rc, *Ws, h3, t3)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, go):
+        from ictc_o3.ops.radial_mlp import gate_projection, radial_gates_adjoint
+        if go is None:
+            return (None,) * 12
+        x, sh, r, W1, W2, W3, W4, h3, t3 = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:7])
+        ctx.inputs = None
+        spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
+        go = _c(go)
+        if any(needs[3:7]):
+            gates = gate_projection(h3, W4)   # unweighted: the message kernels apply the path weight
+            dx, dsh, dg = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], True))
+            dr, dW = radial_gates_adjoint(r, (W1, W2, W3, W4), ctx.cfg, dg, (needs[2], *needs[3:7]))
+            return (dx, dsh, dr, *dW, None, None, None, None, None)
+        if not any(needs[:3]):
+            return (None,) * 12
+        N, E = x.shape[0], sh.shape[0]
+        dx = torch.empty_like(x) if needs[0] else None
+        dsh = torch.empty_like(sh) if needs[1] else None
+        dr = sh.new_empty(E)
+        sp = topo.by_src if needs[0] else None
+        nat.call("ictc_msg_fused_bwd_tangent", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh),
+                 nat.ptr(h3), nat.ptr(t3), nat.ptr(ctx.w4s), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst),
+                 N, E, nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
+                 nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
+                 nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr), nat.stream_of(x))
+        return (dx, dsh, dr if needs[2] else None, None, None, None, None, None, None, None, None, None)
+
+
 def radial_message(x, sh, r, fc, spec, topo, mask, cfg):
-    """message() with the fused radial gates of `fc` (see RadialMessage); cfg = (cutoff, poly_p, silu_scale)."""
+    """message() with the fused radial gates of `fc` (FusedRadialMessage where the library compiles the
+    shape, else RadialMessage); cfg = (cutoff, poly_p, silu_scale)."""
     lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
-    return RadialMessage.apply(x, sh, r, *(m.weight for m in lin), spec, topo, mask,
-                               (float(cfg[0]), int(cfg[1]), float(cfg[2])))
+    cfg = (float(cfg[0]), int(cfg[1]), float(cfg[2]))
+    if _fused_ok(spec, x):
+        w4s = _fused_weight(fc, lin[-1].weight, spec)
+        return FusedRadialMessage.apply(x, sh, r, *(m.weight for m in lin), spec, topo, mask, cfg, w4s)
+    return RadialMessage.apply(x, sh, r, *(m.weight for m in lin), spec, topo, mask, cfg)
 
 
 def message(x, sh, g, spec, topo, mask=None):

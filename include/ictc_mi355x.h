@@ -164,6 +164,38 @@ int ictc_msg_bwd_tangent(int input_lmax, int edge_lmax, int output_lmax, int cha
                          float* dfeatures, float* dharmonics, float* dr, void* workspace,
                          int64_t workspace_bytes, void* stream);
 
+/* ---- Fused radial-gate message (energy + forces) ---------------------------
+ * Replaces the reference's streamed gate message for frozen-weight force
+ * inference (ictc_o3/ops/streamed_gate_message.py:51-57, _StreamedGate
+ * :87-223): the gates [E, P*C] = h3 . W4^T are formed per edge tile inside the
+ * message kernels from the radial MLP's last hidden activation h3 [E, 64]
+ * (ictc_radial_mlp_tangent_fwd) and never materialised.  W4 [P*C, 64] is the
+ * last Linear of `fc` (layers.py:826-835), folded with the TP path weight
+ * [P, C] (may be NULL = ones) and split once into the MFMA operand layout
+ * (ictc_fused_weight_split, ictc_fused_weight_bytes bytes, 16-byte aligned).
+ * Compiled degree triples: ictc_fused_supported (input <= 2, edge = output
+ * = 2; channels a multiple of 64 up to 256); others return
+ * ICTC_ERR_UNSUPPORTED.  ictc_msg_fused_fwd writes out [N, NO*C] exactly as
+ * ictc_msg_fwd with gates = h3 . W4^T.  ictc_msg_fused_bwd_tangent is
+ * ictc_msg_bwd_tangent with gtangent = t3 . W4^T (t3 = d h3 / dr): dr [E]
+ * (required), dharmonics [E, NY] and dfeatures (NULL = skipped; with
+ * dfeatures NULL the receiver-owned pass runs and the source CSR is unused).  */
+int ictc_fused_supported(int input_lmax, int edge_lmax, int output_lmax, int channels);
+int64_t ictc_fused_weight_bytes(int paths, int channels);
+int ictc_fused_weight_split(const float* W4, const float* tp_weight, int paths, int channels, void* out,
+                            int64_t out_bytes, void* stream);
+int ictc_msg_fused_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels, const float* features,
+                       const float* harmonics, const float* h3, const void* w4split, const float* mask,
+                       const int64_t* src, int64_t nodes, int64_t edges, const int32_t* dst_ptr,
+                       const int32_t* dst_order, const int32_t* dst_rows, float* out, void* stream);
+int ictc_msg_fused_bwd_tangent(int input_lmax, int edge_lmax, int output_lmax, int channels, const float* features,
+                               const float* harmonics, const float* h3, const float* t3, const void* w4split,
+                               const float* mask, const int64_t* src, const int64_t* dst, int64_t nodes,
+                               int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                               const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
+                               const int32_t* src_rows, const float* grad, float* dfeatures, float* dharmonics,
+                               float* dr, void* stream);
+
 /* Mixed second derivative of ictc_msg_bwd along tangents of its outputs
  * (tfeatures [nodes, C*(LI+1)^2], tharmonics [E, NY], tgates [E, P*C]; NULL =
  * zero tangent); replaces generated_second (graph mode,
@@ -359,6 +391,12 @@ int ictc_radial_gates_tangent_fwd_noalloc(const float* r, int64_t edges, int num
                                           int poly_p, const float* W1, const float* W2, const float* W3,
                                           const float* W4, int gates, float silu_scale, float* out, float* tangent,
                                           void* stream);
+/* ictc_radial_mlp_fwd that also writes t3 [E, 64] = d a3 / dr (forward mode
+ * through the MLP): the hidden state and tangent the fused radial-gate
+ * message projects (the `fc` of layers.py:826-835 without its last Linear).  */
+int ictc_radial_mlp_tangent_fwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                                const float* W1, const float* W2, const float* W3, float silu_scale, float* a3,
+                                float* t3, void* stream);
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
                         float* dr, float* dz1, float* dz2, float* dz3, float* a1, float* a2, void* stream);
