@@ -236,8 +236,13 @@ def fused_supported(fc: torch.nn.Sequential) -> bool:
             and lin[3].weight.shape[0] % 16 == 0)
 
 
-def radial_gates(r: torch.Tensor, fc: torch.nn.Sequential, cutoff: float, poly_p: int, scale: float):
-    """[E] edge lengths -> [E, P*C] gates through the fused kernel (first derivatives only)."""
+def radial_gates(r: torch.Tensor, fc: torch.nn.Sequential, cutoff: float, poly_p: int, scale: float,
+                 basis_scale: float = 1.0):
+    """[E] edge lengths -> [E, P*C] gates through the fused kernel (first derivatives only).
+
+    basis_scale multiplies the radial basis (the historical sqrt(num_basis) norm,
+    radial_basis.py:87-91); it is folded into the first Linear's weight."""
     lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
-    return _RadialGates.apply(r, lin[0].weight, lin[1].weight, lin[2].weight, lin[3].weight, float(cutoff),
+    W1 = lin[0].weight if basis_scale == 1.0 else lin[0].weight * basis_scale
+    return _RadialGates.apply(r, W1, lin[1].weight, lin[2].weight, lin[3].weight, float(cutoff),
                               int(poly_p), float(scale))

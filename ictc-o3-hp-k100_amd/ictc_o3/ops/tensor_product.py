@@ -515,15 +515,18 @@ class FusedRadialMessage(torch.autograd.Function):
         return (dx, dsh, dr if needs[2] else None, None, None, None, None, None, None, None, None, None)
 
 
-def radial_message(x, sh, r, fc, spec, topo, mask, cfg):
+def radial_message(x, sh, r, fc, spec, topo, mask, cfg, basis_scale=1.0):
     """message() with the fused radial gates of `fc` (FusedRadialMessage where the library compiles the
-    shape, else RadialMessage); cfg = (cutoff, poly_p, silu_scale)."""
-    lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
+    shape, else RadialMessage); cfg = (cutoff, poly_p, silu_scale); basis_scale multiplies the radial
+    basis (folded into the first Linear's weight)."""
+    W = [m.weight for m in fc if isinstance(m, torch.nn.Linear)]
+    if basis_scale != 1.0:
+        W[0] = W[0] * basis_scale
     cfg = (float(cfg[0]), int(cfg[1]), float(cfg[2]))
     if _fused_ok(spec, x):
-        w4s = _fused_weight(fc, lin[-1].weight, spec)
-        return FusedRadialMessage.apply(x, sh, r, *(m.weight for m in lin), spec, topo, mask, cfg, w4s)
-    return RadialMessage.apply(x, sh, r, *(m.weight for m in lin), spec, topo, mask, cfg)
+        w4s = _fused_weight(fc, W[-1], spec)
+        return FusedRadialMessage.apply(x, sh, r, *W, spec, topo, mask, cfg, w4s)
+    return RadialMessage.apply(x, sh, r, *W, spec, topo, mask, cfg)
 
 
 def message(x, sh, g, spec, topo, mask=None):

@@ -1,0 +1,195 @@
+"""Checkpoint reconstruction for the MACE-ICTC baseline (reference: mace_ictc/checkpoints/loader.py:87-1211).
+
+Scope: checkpoints of the ``pure-cartesian-ictd-fix`` baseline backbone that
+``create_model`` builds (mace_ictc/hp/runtime.py:6-83) -- the architecture
+the MI355X kernels implement.  The reference reads every other backbone
+variant (spherical, sparse, o3) and the optional fusion / attention /
+long-range / dispersion / tensor-output heads through the same function;
+here those raise ValueError naming the unsupported option.
+
+Differences kept on purpose:
+* the file is read with ``torch.load(..., weights_only=True)``, which runs no
+  code from the file (the reference unpickles); a checkpoint whose metadata
+  holds arbitrary Python objects is refused with a ValueError;
+* the reference's log lines are not printed.
+"""
+from __future__ import annotations
+
+import math
+import warnings
+from typing import Any, List, Mapping, Optional
+
+import torch
+
+from mace_ictc.checkpoints.adapters import AtomForcesWrapper
+
+_BASELINE = "pure-cartesian-ictd-fix"
+
+
+def get_checkpoint_e3_state_dict(checkpoint: Mapping[str, Any] | None, *, prefer_ema: bool = True):
+    """(state_dict, source) with source in {"raw", "ema", "swa"} (mace_ictc/utils/checkpoint_metadata.py:202-244):
+    an explicit ``default_state_source`` wins; otherwise EMA when present (prefer_ema), then raw, SWA, EMA."""
+    if not isinstance(checkpoint, Mapping):
+        raise ValueError("Checkpoint must be a mapping to resolve e3trans weights.")
+    states = {"raw": checkpoint.get("e3trans_state_dict"), "ema": checkpoint.get("e3trans_ema_state_dict"),
+              "swa": checkpoint.get("e3trans_swa_state_dict")}
+    default = str(checkpoint.get("default_state_source", "") or "").lower()
+    if default in states and isinstance(states[default], Mapping):
+        return states[default], default
+    order = ("ema", "raw", "swa") if prefer_ema else ("raw", "swa", "ema")
+    for key in order:
+        if isinstance(states[key], Mapping):
+            return states[key], key
+    raise KeyError("Checkpoint does not contain e3trans_state_dict, e3trans_ema_state_dict, "
+                   "or e3trans_swa_state_dict.")
+
+
+class LoadedPotential:
+    """Loaded model and E0 buffers, independent of any simulation engine (loader.py:66-83)."""
+
+    def __init__(self, model, element_types, max_radius, atomic_energy_keys, atomic_energy_values, device="cpu",
+                 dtype=torch.float32):
+        self.device, self.dtype = device, dtype
+        self.element_types, self.max_radius = list(element_types), max_radius
+        self.wrapper = AtomForcesWrapper(model, atomic_energy_keys, atomic_energy_values).to(device)
+
+    @property
+    def model(self):
+        return self.wrapper.model
+
+
+def _meta(ckpt, arch, name, default=None):
+    if name in ckpt:
+        return ckpt[name]
+    return arch.get(name, default)
+
+
+def _infer_correlation(sd) -> int:
+    """Correlation order from the first product's contraction weights: weights_max plus weights.0 .. weights.{nu-2}."""
+    prefix = "products.0.symmetric_contractions.symmetric_contractions.contractions.0."
+    if prefix + "weights_max" not in sd:
+        raise ValueError("checkpoint has no symmetric-contraction weights of the baseline product")
+    return 1 + sum(1 for k in sd if k.startswith(prefix + "weights."))
+
+
+def _unsupported(ckpt, arch, sd):
+    """Names of reference options outside the baseline create_model architecture that the checkpoint uses."""
+    bad = []
+    checks = {
+        "ictd_fix_route": ("baseline",), "long_range_mode": ("none",), "angular_basis": ("ictd",),
+        "long_range_dispersion_mode": ("none",), "ictd_fix_interaction_attn_heads": (0,),
+        "ictd_fix_fusion_heads": (1, None), "energy_output_scale_enabled": (False,),
+        "energy_output_shift_enabled": (False,), "ictd_fix_use_reduced_cg": (False,),
+    }
+    for name, ok in checks.items():
+        v = _meta(ckpt, arch, name, ok[0])
+        if v not in ok:
+            bad.append(f"{name}={v!r}")
+    for key in sd:
+        if (key.startswith(("multiple_contraction_mix", "fusion_head", "long_range", "dispersion", "zbl"))
+                or ".attn_" in key or key in ("energy_output_scale", "energy_output_shift", "mace_first_layer_sc0")):
+            bad.append(f"state entry {key}")
+            break
+    if arch.get("physical_tensor_outputs") or ckpt.get("physical_tensor_outputs"):
+        bad.append("physical_tensor_outputs")
+    if arch.get("external_tensor_rank") is not None or ckpt.get("external_tensor_rank") is not None:
+        bad.append("external_tensor_rank")
+    if arch.get("zbl") or arch.get("use_zbl"):
+        bad.append("zbl")
+    return bad
+
+
+def load_checkpoint(checkpoint_path: str, element_types: List[str], max_radius: Optional[float] = None,
+                    atomic_energy_keys: Optional[List[int]] = None, atomic_energy_values: Optional[List[float]] = None,
+                    device: str = "cpu", embed_size: Optional[List[int]] = None, output_size: Optional[int] = None,
+                    tensor_product_mode: Optional[str] = None, num_interaction: Optional[int] = None,
+                    ictd_tp_path_policy: Optional[str] = None, ictd_tp_max_rank_other: Optional[int] = None,
+                    avg_num_neighbors: Optional[float] = None, torchscript: bool = False, force_naive: bool = False,
+                    ictd_tp_backend: Optional[str] = None, operator_plan: str = "auto",
+                    generated_layout: str = "packed", *, _potential_class=LoadedPotential) -> LoadedPotential:
+    """Rebuild a baseline MACE-ICTC checkpoint (loader.py:87-1211, the pure-cartesian-ictd-fix route).
+
+    Hyperparameters resolve as in the reference: explicit argument, then the
+    checkpoint's top-level entry, then ``model_hyperparameters``, then the
+    reference's historical defaults (max_radius 5.0, polynomial cutoff p = 6,
+    sqrt(num_basis) radial norm on, 2 interactions); channels, radial basis
+    size, species count and correlation are read from the weights' shapes.
+    avg_num_neighbors is required for correct energies: without it the
+    reference's 14.38 fallback is used with a RuntimeWarning (loader.py:372-394).
+    """
+    from mace_ictc.hp.model import PureCartesianICTDFix
+    try:
+        ckpt = torch.load(checkpoint_path, map_location="cpu", weights_only=True)
+    except Exception as exc:   # the safe loader refuses pickled Python objects
+        raise ValueError(f"checkpoint {checkpoint_path!r} cannot be read with weights_only=True "
+                         f"(it holds objects other than tensors and plain containers): {exc}") from exc
+    if not isinstance(ckpt, Mapping):
+        raise ValueError("checkpoint must be a dictionary")
+    sd, _source = get_checkpoint_e3_state_dict(ckpt)
+    sd = dict(sd)
+    arch = dict(ckpt.get("model_hyperparameters", {}) or {})
+    mode = str(tensor_product_mode or ckpt.get("tensor_product_mode", "spherical"))
+    if mode != _BASELINE:
+        raise ValueError(f"tensor_product_mode {mode!r} is not built here: the MI355X build reconstructs "
+                         f"{_BASELINE!r} checkpoints (the create_model architecture)")
+    if force_naive or torchscript:
+        raise ValueError("force_naive / torchscript reconstruction routes are not part of the MI355X build")
+    bad = _unsupported(ckpt, arch, sd)
+    if bad:
+        raise ValueError("checkpoint uses options outside the baseline architecture: " + ", ".join(bad))
+
+    dtype_raw = ckpt.get("dtype", arch.get("dtype", torch.float64))
+    if isinstance(dtype_raw, str):
+        dtype = torch.float64 if dtype_raw in ("float64", "double") else torch.float32
+    else:
+        dtype = dtype_raw
+    radius = float(ckpt.get("max_radius", max_radius if max_radius is not None else 5.0))
+    if num_interaction is None:
+        num_interaction = int(arch.get("num_interaction", 2))
+    avg = avg_num_neighbors if avg_num_neighbors is not None else (
+        ckpt.get("avg_num_neighbors") or arch.get("avg_num_neighbors"))
+    if avg is None:
+        warnings.warn("avg_num_neighbors is NOT in the checkpoint and was not passed explicitly; falling back "
+                      "to 14.38. The model divides messages by this constant, so if training used a different "
+                      "value the energies/forces are WRONG.", RuntimeWarning)
+        avg = 14.38
+    poly_p = _meta(ckpt, arch, "polynomial_cutoff_p", 6)
+    if poly_p is None:
+        raise ValueError("a radial basis without polynomial cutoff is not part of the MI355X build")
+    sqrt_norm = bool(_meta(ckpt, arch, "radial_sqrt_num_basis", True))
+    function_type = str(arch.get("function_type", "bessel"))
+    if function_type != "bessel":
+        raise ValueError(f"radial function_type {function_type!r} is not built here (Bessel only)")
+    lmax = int(arch.get("lmax", 2))
+    edge_lmax = _meta(ckpt, arch, "ictd_fix_edge_lmax", None)
+    edge_lmax = lmax if edge_lmax is None else int(edge_lmax)
+    readout_hidden = int(_meta(ckpt, arch, "ictd_fix_readout_hidden_channels", 16) or 16)
+    emb = sd.get("node_embedding.weight")
+    if emb is None or emb.dim() != 2:
+        raise ValueError("checkpoint has no node_embedding.weight [channels, species]")
+    channels, n_species = int(emb.shape[0]), int(emb.shape[1])
+    n_basis = int(sd["interactions.0.fc.0.weight"].shape[1])
+    correlation = _infer_correlation(sd)
+
+    if atomic_energy_keys is not None and atomic_energy_values is not None:
+        aek = torch.as_tensor(atomic_energy_keys, dtype=torch.long)
+        aev = torch.as_tensor(atomic_energy_values, dtype=torch.float64)
+    elif ckpt.get("atomic_energy_keys") is not None and ckpt.get("atomic_energy_values") is not None:
+        aek = torch.as_tensor(ckpt["atomic_energy_keys"]).detach().cpu().long()
+        aev = torch.as_tensor(ckpt["atomic_energy_values"]).detach().cpu().double()
+    else:
+        raise ValueError("atomic_energy_keys / atomic_energy_values are neither passed nor in the checkpoint "
+                         "(the reference's fitted_E0.csv fallback is not part of this build)")
+    atomic_numbers = aek.tolist()
+    if len(set(atomic_numbers)) != n_species:
+        raise ValueError(f"{len(set(atomic_numbers))} atomic energy keys but the embedding has {n_species} species")
+
+    model = PureCartesianICTDFix(channels=channels, lmax=lmax, edge_lmax=edge_lmax, num_interactions=num_interaction,
+                                 correlation=correlation, atomic_numbers=atomic_numbers, cutoff=radius,
+                                 avg_num_neighbors=float(avg), number_of_basis=n_basis, polynomial_cutoff_p=int(poly_p),
+                                 readout_hidden=readout_hidden, radial_sqrt_num_basis=sqrt_norm)
+    state = {k: (v.to(torch.float32) if torch.is_tensor(v) and v.is_floating_point() else v) for k, v in sd.items()}
+    model.load_state_dict(state, strict=True)
+    model = model.to(device)
+    return _potential_class(model=model, element_types=element_types, max_radius=radius, atomic_energy_keys=aek,
+                            atomic_energy_values=aev, device=device, dtype=torch.float32)

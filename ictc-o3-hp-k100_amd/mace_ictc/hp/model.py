@@ -164,17 +164,19 @@ class Interaction(nn.Module):
             self._spec = tpo.make_spec(self.input_lmax, self.lmax, self.lmax, self.channels, None)
         return self._spec
 
-    def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None, forces_only=False):
-        """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path)."""
+    def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None, forces_only=False,
+                basis_scale=1.0):
+        """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path;
+        basis_scale multiplies the radial basis there)."""
         C = self.channels
         first_order = radial is None
         x = self.linear_up(h, first_order)
         if radial is None and forces_only:
-            m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg)
+            m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg, basis_scale)
         else:
             if radial is None:
                 from ictc_o3.ops.radial_mlp import radial_gates
-                gates = radial_gates(r, self.fc, *radial_cfg)
+                gates = radial_gates(r, self.fc, *radial_cfg, basis_scale=basis_scale)
             else:
                 from ictc_o3.ops.radial_mlp import radial_mlp
                 gates = radial_mlp(radial, self.fc)
@@ -235,8 +237,11 @@ class PureCartesianICTDFix(nn.Module):
 
     def __init__(self, *, channels=64, lmax=2, edge_lmax=None, num_interactions=2, correlation=3,
                  atomic_numbers=(1, 6, 8), cutoff=5.0, avg_num_neighbors=50.0, number_of_basis=8,
-                 polynomial_cutoff_p=5, readout_hidden=16):
+                 polynomial_cutoff_p=5, readout_hidden=16, radial_sqrt_num_basis=False):
         super().__init__()
+        # the historical sqrt(num_basis) radial norm (radial_basis.py:87-91); create_model leaves it off
+        self.radial_sqrt_num_basis = bool(radial_sqrt_num_basis)
+        self.radial_basis_scale = math.sqrt(number_of_basis) if radial_sqrt_num_basis else 1.0
         edge_lmax = lmax if edge_lmax is None else edge_lmax
         self.channels, self.lmax, self.ictd_fix_edge_lmax = channels, lmax, edge_lmax
         self.num_interaction, self.max_radius = num_interactions, float(cutoff)
@@ -336,11 +341,14 @@ class PureCartesianICTDFix(nn.Module):
         fused = (not second_order and self.number_of_basis == 8
                  and all(fused_supported(inter.fc) for inter in self.interactions))
         radial = None if fused else self.radial_embedding(r)
+        if radial is not None and self.radial_basis_scale != 1.0:
+            radial = radial * self.radial_basis_scale
         radial_cfg = (self.max_radius, self.polynomial_cutoff_p, SILU_SCALE)
         h = species_rows(self.node_embedding.weight.t(), species)
         energy = None
         for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
-            message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only)
+            message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only,
+                                self.radial_basis_scale)
             h = prod(message, sc, species, first_order=radial is None)
             if i < self.num_interaction - 1:
                 e = self.layer_energy_readouts[i](h[:, :self.channels])

@@ -63,7 +63,9 @@ def forward(sd, cfg, pos, A, batch, src, dst, shifts, cell, dtype=torch.float64)
     shift_vec = torch.einsum("ni,nij->nj", shifts.to(dtype), cell[batch[src]].to(dtype))
     r, n, mask = edge_geometry(pos, src, dst, shift_vec, cfg["cutoff"])
     Y = orc.direction_harmonics(n, Le)
-    rad = radial(r, cfg["cutoff"], 8, 5)
+    rad = radial(r, cfg["cutoff"], cfg.get("num_basis", 8), cfg.get("poly_p", 5))
+    if cfg.get("radial_sqrt", False):      # historical sqrt(num_basis) norm (radial_basis.py:87-91)
+        rad = rad * math.sqrt(cfg.get("num_basis", 8))
     N, E = pos.shape[0], src.numel()
     h = {0: g("node_embedding.weight").t()[species][:, :, None]}
     energy = torch.zeros(N, dtype=dtype)
@@ -129,4 +131,6 @@ def config_of(model):
     return {"channels": model.channels, "lmax": model.lmax, "edge_lmax": model.ictd_fix_edge_lmax,
             "num_elements": model.num_elements, "z_table": model.atomic_number_to_index.cpu(),
             "num_interactions": model.num_interaction, "cutoff": model.max_radius,
-            "avg": model.avg_num_neighbors, "correlation": model.products[0].symmetric_contractions.correlation}
+            "avg": model.avg_num_neighbors, "correlation": model.products[0].symmetric_contractions.correlation,
+            "num_basis": model.number_of_basis, "poly_p": model.polynomial_cutoff_p,
+            "radial_sqrt": bool(getattr(model, "radial_sqrt_num_basis", False))}
