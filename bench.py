@@ -301,6 +301,8 @@ def run_cfg4(args):
     dt = (time.perf_counter() - t0) / args.steps
     log(f"cfg4: N={N} E={E} step={dt * 1e3:.2f} ms energy={float(out['energy'][0]):.6f}")
 
+    if args.no_kernel_timing:
+        return {"metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "ms_per_step": dt * 1e3}, model
     src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
     kern, nbytes = layer_message_kernels(model, src, dst, N, pos)
     # the layer-1 radial gates with their r tangents (the step's largest kernel), timed the same way
@@ -642,6 +644,8 @@ def run_cfg5(args):
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / args.steps
     log(f"cfg5: N={N} E={E} step={dt * 1e3:.2f} ms loss={float(loss.detach()):.4f}")
+    if args.no_kernel_timing:
+        return {"metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "ms_per_step": dt * 1e3}, model
     kern, nbytes = layer_message_kernels(model, src, dst, N, None, reps=10)
     dom = max(kern, key=kern.get)   # the layer-1 message kernel with the largest time
     achieved = nbytes[dom] / kern[dom] / 1e9
@@ -764,6 +768,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="cfg4", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "probe"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-timing", action="store_true",
+                    help="skip the per-kernel HIP-event timings after the timed steps (clean profiles of the step)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one-GPU hot path by design); "

@@ -133,20 +133,22 @@ __global__ __launch_bounds__(256, 2) void gate_gemm_nt_kernel(const float* __res
 constexpr int kMaxSlices = 12;  // up to 768 gates: 12 waves per block leave 170 VGPRs per lane
 constexpr int kRedRow = 68;  // LDS row pitch (floats) of a partial 16 x 64 tile
 
-__device__ __forceinline__ void load_dg(const float* __restrict__ dg, int64_t e, int64_t E, int M, int s, float* v) {
+__device__ __forceinline__ void load_dg(const float* __restrict__ dg, int64_t e, int64_t E, int64_t ldg, int s,
+                                        float* v) {
   const int g = (threadIdx.x & 63) >> 4;
   if (e < E) {
-    load8(dg + e * M + 64 * s + 8 * g, v);
-    load8(dg + e * M + 64 * s + 32 + 8 * g, v + 8);
+    load8(dg + e * ldg + 64 * s + 8 * g, v);
+    load8(dg + e * ldg + 64 * s + 32 + 8 * g, v + 8);
   } else {
 #pragma unroll
     for (int q = 0; q < 16; ++q) v[q] = 0.f;
   }
 }
 
-__global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const float* __restrict__ dg, int64_t E,
-                                                                       const float* __restrict__ W, int M,
-                                                                       float* __restrict__ dh) {
+// dg rows have pitch ldg (a column block of a wider gradient); accumulate != 0 adds to dh.
+__global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const float* __restrict__ dg, int64_t ldg,
+                                                                       int64_t E, const float* __restrict__ W, int M,
+                                                                       float* __restrict__ dh, int accumulate) {
   extern __shared__ float red[];  // [2][S][16][kRedRow]
   const int l = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int i = l & 15, g = l >> 4;
@@ -164,12 +166,12 @@ __global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const flo
   const int64_t tiles = (E + 15) / 16;
   float next[16];
   int64_t t = blockIdx.x;
-  if (t < tiles) load_dg(dg, 16 * t + i, E, M, s, next);
+  if (t < tiles) load_dg(dg, 16 * t + i, E, ldg, s, next);
   for (int buf = 0; t < tiles; t += gridDim.x, buf ^= 1) {
     float cur[16];
 #pragma unroll
     for (int q = 0; q < 16; ++q) cur[q] = next[q];
-    if (t + gridDim.x < tiles) load_dg(dg, 16 * (t + gridDim.x) + i, E, M, s, next);
+    if (t + gridDim.x < tiles) load_dg(dg, 16 * (t + gridDim.x) + i, E, ldg, s, next);
     const Split B0 = split8(cur), B1 = split8(cur + 8);
     v4f acc[4];
 #pragma unroll
@@ -192,7 +194,10 @@ __global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const flo
       v4f sum = *reinterpret_cast<const v4f*>(src);
       for (int w = 1; w < S; ++w) sum += *reinterpret_cast<const v4f*>(src + (int64_t)w * 16 * kRedRow);
       const int64_t e = 16 * t + edge;
-      if (e < E) *reinterpret_cast<v4f*>(dh + e * kK + 4 * kq) = sum;
+      if (e < E) {
+        v4f* o = reinterpret_cast<v4f*>(dh + e * kK + 4 * kq);
+        *o = accumulate ? *o + sum : sum;
+      }
     }
   }
 }
@@ -239,9 +244,15 @@ int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, con
 
 int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float* weight, int hidden_width,
                        float* dhidden, void* stream) {
+  return ictc_gate_gemm_bwd_strided(grad, gates, edges, gates, weight, hidden_width, dhidden, 0, stream);
+}
+
+int ictc_gate_gemm_bwd_strided(const float* grad, int64_t grad_pitch, int64_t edges, int gates, const float* weight,
+                               int hidden_width, float* dhidden, int accumulate, void* stream) {
   if (hidden_width != kK) return fail(ICTC_ERR_UNSUPPORTED, "gate adjoint is compiled for a 64-wide hidden layer");
   if (edges < 0 || gates <= 0 || gates % 64 != 0 || gates > 64 * kMaxSlices)
     return fail(ICTC_ERR_UNSUPPORTED, "gate adjoint: gates must be a positive multiple of 64, at most 768");
+  if (grad_pitch < gates || grad_pitch % 4) return fail(ICTC_ERR_ARGUMENT, "gate adjoint: grad pitch >= gates, a multiple of 4");
   if (edges == 0) return ICTC_OK;
   if (!grad || !weight || !dhidden) return fail(ICTC_ERR_ARGUMENT, "gate adjoint: null operand");
   if ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(dhidden)) & 15)
@@ -257,8 +268,8 @@ int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float*
   if (per_cu > 4) per_cu = 4;
   const int64_t want = (int64_t)cu_count() * per_cu;
   const unsigned blocks = (unsigned)(tiles < want ? tiles : want);
-  hipLaunchKernelGGL(gate_gemm_nn_kernel, dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream, grad, edges, weight,
-                     gates, dhidden);
+  hipLaunchKernelGGL(gate_gemm_nn_kernel, dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream, grad, grad_pitch,
+                     edges, weight, gates, dhidden, accumulate);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char buf[256];

@@ -1,0 +1,180 @@
+// General channel-linear GEMM and the per-graph energy sum.
+//
+// C[M, N] (+)= A[M, K] . B[N, K]^T, row-major operands with leading
+// dimensions, FP32 in and out, products and sums on FP32 MFMA
+// (v_mfma_f32_16x16x4f32: the precision of an FP32 library GEMM with TF32
+// off).  This is every `x W^T` / `u W` of the training path's channel
+// linears and readouts that the wider kernels (gate_gemm.hip: 64-wide inputs;
+// gemm_tn.hip: weight gradients) do not take: the per-degree and
+// per-path channel maps (layers.py:317-355, ictd_irreps.py:207-227), the
+// species-selected self connection (layers.py:21-87) and the readouts
+// (heads.py:12-27), forward and input adjoint.
+//
+// Tiling: a block of 4 waves computes a 128 x 64 output tile; each K step
+// stages a 128 x 32 slab of A and a 64 x 32 slab of B through LDS (reduction
+// index outer, so every MFMA operand is one LDS read; 16-byte global loads
+// along K where pitch and alignment allow), and wave w multiplies its rows
+// 32 w .. 32 w + 31 (two 16-row blocks) against the four 16-column blocks:
+// 8 MFMAs per 6 LDS reads.  Thin shapes (N = 1 readouts) are HBM-bound and
+// read A once.
+//
+// Per-graph energy sum: out[b] = sum over atoms n with batch[n] == b of
+// values[n] in FP64, one block per graph scanning the atoms in index order and
+// adding the thread sums in a fixed tree: deterministic without atomics.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/ictc_mi355x.h"
+
+namespace ictc {
+int set_error(int code, const char* msg);
+}
+
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kTM = 128;  // output tile rows (4 waves x 32)
+constexpr int kTN = 64;   // output tile columns
+constexpr int kK = 32;    // K per LDS stage
+
+int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+// Stage rows [r0, r0 + R) x k [k0, k0 + kK) of a row-major operand into lds[k][row] (zero outside).
+// Thread t covers (R * kK / 256) entries as float4 runs along k when the pitch and base allow it.
+template <int R, bool VEC>
+__device__ __forceinline__ void stage(const float* __restrict__ X, int64_t rows, int64_t K, int64_t ld, int64_t r0,
+                                      int64_t k0, float (*lds)[R + 4]) {
+  constexpr int per = R * kK / 256;   // entries per thread (16 for R = 128, 8 for R = 64)
+  constexpr int runs = per / 4;
+#pragma unroll
+  for (int q = 0; q < runs; ++q) {
+    const int idx = threadIdx.x + 256 * q;      // run index: row = idx / (kK / 4), k = 4 (idx % (kK / 4))
+    const int row = idx / (kK / 4), kq = 4 * (idx % (kK / 4));
+    const int64_t r = r0 + row, k = k0 + kq;
+    float v[4];
+    if (VEC && r < rows && k + 3 < K) {
+      const v4f x = *reinterpret_cast<const v4f*>(X + r * ld + k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = x[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = (r < rows && k + e < K) ? X[r * ld + k + e] : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) lds[kq + e][row] = v[e];
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t lda,
+                                                      const float* __restrict__ B, int64_t N, int64_t ldb,
+                                                      float* __restrict__ C, int64_t ldc, int accumulate,
+                                                      int64_t n_tiles) {
+  __shared__ float As[kK][kTM + 4];
+  __shared__ float Bs[kK][kTN + 4];
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t bm = blockIdx.x / n_tiles, bn = blockIdx.x % n_tiles;
+  const int64_t m0 = bm * kTM, n0 = bn * kTN;
+  v4f acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int64_t k0 = 0; k0 < K; k0 += kK) {
+    stage<kTM, VEC>(A, M, K, lda, m0, k0, As);
+    stage<kTN, VEC>(B, N, K, ldb, n0, k0, Bs);
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < kK; kk += 4) {
+      const int k = kk + (l >> 4);
+      const float a0 = As[k][32 * w + (l & 15)], a1 = As[k][32 * w + 16 + (l & 15)];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float b = Bs[k][16 * j + (l & 15)];
+        acc[0][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, b, acc[0][j], 0, 0, 0);
+        acc[1][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, b, acc[1][j], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  // D: lane holds rows 4 (l/16) + r of each 16-row block, column l % 16 of each 16-column block
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = n0 + 16 * j + (l & 15);
+    if (n >= N) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + 32 * w + 16 * i + 4 * (l >> 4) + r;
+        if (m < M) {
+          float* c = C + m * ldc + n;
+          *c = accumulate ? *c + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+  }
+}
+
+constexpr int kSumThreads = 256;
+
+__global__ __launch_bounds__(kSumThreads) void graph_sum_kernel(const float* __restrict__ values,
+                                                                const int64_t* __restrict__ batch, int64_t n,
+                                                                double* __restrict__ out) {
+  __shared__ double part[kSumThreads];
+  const int64_t b = blockIdx.x;
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += kSumThreads)
+    if (batch[i] == b) s += (double)values[i];
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int h = kSumThreads / 2; h > 0; h >>= 1) {
+    if ((int)threadIdx.x < h) part[threadIdx.x] += part[threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[b] = part[0];
+}
+
+int launch_status(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e == hipSuccess) return ICTC_OK;
+  char buf[256];
+  snprintf(buf, sizeof(buf), "%s: %s", what, hipGetErrorString(e));
+  return fail(ICTC_ERR_RUNTIME, buf);
+}
+
+}  // namespace
+
+extern "C" {
+
+int ictc_gemm_nt(const float* a, int64_t m, int64_t k, int64_t lda, const float* b, int64_t n, int64_t ldb, float* c,
+                 int64_t ldc, int accumulate, void* stream) {
+  if (m < 0 || n < 0 || k < 0 || lda < k || ldb < k || ldc < n)
+    return fail(ICTC_ERR_ARGUMENT, "gemm_nt: need m, n, k >= 0, lda >= k, ldb >= k, ldc >= n");
+  if (m == 0 || n == 0) return ICTC_OK;
+  if (!c || (k > 0 && (!a || !b))) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: null operand");
+  const int64_t mt = (m + kTM - 1) / kTM, nt = (n + kTN - 1) / kTN;
+  if (mt * nt > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: too many output tiles");
+  const bool vec = lda % 4 == 0 && ldb % 4 == 0 &&
+                   ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(gemm_nt_kernel<true>, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k,
+                       lda, b, n, ldb, c, ldc, accumulate, nt);
+  else
+    hipLaunchKernelGGL(gemm_nt_kernel<false>, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k,
+                       lda, b, n, ldb, c, ldc, accumulate, nt);
+  return launch_status("ictc_gemm_nt launch");
+}
+
+int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, double* out, void* stream) {
+  if (n < 0 || graphs < 0) return fail(ICTC_ERR_ARGUMENT, "graph_sum: negative size");
+  if (graphs == 0) return ICTC_OK;
+  if (!out || (n > 0 && (!values || !batch))) return fail(ICTC_ERR_ARGUMENT, "graph_sum: null operand");
+  if (graphs > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "graph_sum: too many graphs");
+  hipLaunchKernelGGL(graph_sum_kernel, dim3((unsigned)graphs), dim3(kSumThreads), 0, (hipStream_t)stream, values,
+                     batch, n, out);
+  return launch_status("ictc_graph_sum launch");
+}
+
+}  // extern "C"

@@ -79,6 +79,33 @@ def species_rows(table: torch.Tensor, species: torch.Tensor) -> torch.Tensor:
     return _SpeciesRows.apply(table, species)
 
 
+class _GraphSum(torch.autograd.Function):
+    """out[b] = sum_{batch[n] == b} values[n] in FP64 (ictc_graph_sum: fixed order, no atomics); the adjoint
+    is the gather grad[batch], differentiable to any order."""
+
+    @staticmethod
+    def forward(ctx, values, batch, graphs):
+        from ictc_o3 import _native as nat
+        values = values if values.is_contiguous() else values.contiguous()
+        batch = batch if batch.is_contiguous() else batch.contiguous()
+        out = torch.empty(graphs, dtype=torch.float64, device=values.device)
+        nat.call("ictc_graph_sum", nat.ptr(values), nat.ptr(batch), values.numel(), graphs, nat.ptr(out),
+                 nat.stream_of(values))
+        ctx.save_for_backward(batch)
+        ctx.dtype = values.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, grad):
+        (batch,) = ctx.saved_tensors
+        return grad.index_select(0, batch).to(ctx.dtype), None, None
+
+
+def graph_sum(values: torch.Tensor, batch: torch.Tensor, graphs: int) -> torch.Tensor:
+    """Per-graph FP64 sums of per-atom values (batch int64 graph ids in [0, graphs))."""
+    return _GraphSum.apply(values, batch, int(graphs))
+
+
 def channel_linear(features: torch.Tensor, weight: torch.Tensor, bias=None):
     """[*, Cin, m] x [Cout, Cin] -> [*, Cout, m] (operators.py:609-628)."""
     angular = features.movedim(-2, -1).contiguous()
@@ -143,9 +170,11 @@ class _PackedLinear(torch.autograd.Function):
                 dws.append(None)
                 continue
             k, m = pin[l], 2 * l + 1
-            xin = x[:, in_off[l]:in_off[l] + k * m * Ci].reshape(N, k, m, Ci)
-            dl = dout[:, out_off[l]:out_off[l] + m * Co].reshape(N, m, Co)
-            dws.append(scales[l] * torch.einsum("nmo,nkmc->okc", dl, xin).reshape(Co, k * Ci))
+            xin = x[:, in_off[l]:in_off[l] + k * m * Ci].reshape(N, k, m, Ci).transpose(1, 2).reshape(N * m, k * Ci)
+            dl = dout[:, out_off[l]:out_off[l] + m * Co].reshape(N * m, Co)
+            # dW[o, (k, c)] = sum_{n, m} dl[n, m, o] x[n, k, m, c] on the split-reduction kernel
+            from ictc_o3.ops.radial_mlp import weight_grad
+            dws.append(scales[l] * weight_grad(dl, xin))
         return (dx, None, *dws)
 
 

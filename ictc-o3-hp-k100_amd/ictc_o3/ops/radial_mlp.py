@@ -15,6 +15,8 @@ tiles only the small output.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 from torch.autograd.function import once_differentiable
 
@@ -41,15 +43,35 @@ def gate_projection_adjoint(dg: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
     E, M = dg.shape[0], W.shape[0]
     if dg.dim() != 2 or dg.shape[1] != M or W.shape[1] != 64:
         raise ValueError("gate adjoint needs dg [E, M] and W [M, 64]")
-    if M % 64 or M > 768:
-        return torch.mm(dg, W)   # shapes outside the kernel's register budget: library GEMM (TF32 off)
+    if M % 64:
+        return gemm_nt(dg, W.t())   # outside the split-bf16 kernel's column blocks: FP32 MFMA
     dg, W = _c(dg), _c(W)
     out = dg.new_empty(E, 64)
-    nat.call("ictc_gate_gemm_bwd", nat.ptr(dg), E, M, nat.ptr(W), 64, nat.ptr(out), nat.stream_of(dg))
+    # column blocks of at most 768 gates (the kernel's register budget), accumulated in column order
+    for c0 in range(0, M, 768):
+        mc = min(768, M - c0)
+        nat.call("ictc_gate_gemm_bwd_strided", ctypes.c_void_p(dg.data_ptr() + 4 * c0), M, E, mc,
+                 ctypes.c_void_p(W.data_ptr() + 4 * c0 * 64), 64, nat.ptr(out), int(c0 > 0), nat.stream_of(dg))
     return out
 
 
 _TN_MIN_ROWS = 16384   # below this the library GEMM's output tiling is enough
+
+
+def gemm_nt(x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
+    """x [M, K] . W^T ([N, K]) on the FP32-MFMA channel-linear kernel (ictc_gemm_nt)."""
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    W = _c(W.detach())
+    M, K, N = x.shape[0], x.shape[1], W.shape[0]
+    out = x.new_empty(M, N)
+    nat.call("ictc_gemm_nt", nat.ptr(x), M, K, x.stride(0), nat.ptr(W), N, K, nat.ptr(out), N, 0,
+             nat.stream_of(x))
+    return out
+
+
+def _own_gemm(x: torch.Tensor) -> bool:
+    return x.is_cuda and x.dtype == torch.float32 and x.dim() == 2
 
 
 def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
@@ -68,10 +90,9 @@ def _gemm_tn(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def weight_grad(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """a^T b over edge rows on the split-reduction kernel (FP32 MFMA up to 16 output tiles of 64 x 64,
-    split-bf16 MFMA beyond; chunk partials added in a fixed order); the library GEMM below
-    _TN_MIN_ROWS rows."""
-    if a.shape[0] >= _TN_MIN_ROWS and a.is_cuda:
+    """a^T b over rows on the split-reduction kernel (FP32 MFMA up to 16 output tiles of 64 x 64,
+    split-bf16 MFMA beyond; chunk partials added in a fixed order, so the result is bitwise repeatable)."""
+    if a.is_cuda and a.dtype == torch.float32 and b.dtype == torch.float32:
         return _gemm_tn(a, b)
     return a.t() @ b
 
@@ -87,6 +108,11 @@ class _WeightGrad(torch.autograd.Function):
     @staticmethod
     def backward(ctx, h):
         a, b = ctx.saved_tensors
+        if _own_gemm(a) and _own_gemm(b):
+            h = _c(h)
+            da = _EdgeLinear.apply(b, h) if ctx.needs_input_grad[0] else None        # b h^T
+            db = _EdgeLinearT.apply(a, h) if ctx.needs_input_grad[1] else None       # a h
+            return da, db
         da = b @ h.t() if ctx.needs_input_grad[0] else None
         db = a @ h if ctx.needs_input_grad[1] else None
         return da, db
@@ -101,6 +127,8 @@ class _EdgeLinear(torch.autograd.Function):
         ctx.inputs = (x, W)
         if x.is_cuda and x.shape[0] >= _TN_MIN_ROWS and x.shape[1] == 64 and W.shape[0] % 16 == 0:
             return gate_projection(x, W)   # split-bf16 MFMA, FP32-level accuracy (hidden layers and projection)
+        if _own_gemm(x):
+            return gemm_nt(x, W)
         return x @ W.t()
 
     @staticmethod
@@ -122,8 +150,10 @@ class _EdgeLinearT(torch.autograd.Function):
         ctx.save_for_backward(u, W)
         ctx.inputs = (u, W)
         M = W.shape[0]
-        if u.is_cuda and u.shape[0] >= _TN_MIN_ROWS and W.shape[1] == 64 and M % 64 == 0 and M <= 768:
+        if u.is_cuda and u.shape[0] >= _TN_MIN_ROWS and W.shape[1] == 64 and M % 64 == 0:
             return gate_projection_adjoint(u, W)   # split-bf16 MFMA, FP32-level accuracy
+        if _own_gemm(u):
+            return gemm_nt(u, W.t())
         return u @ W
 
     @staticmethod

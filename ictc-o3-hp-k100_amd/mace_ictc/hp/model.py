@@ -319,8 +319,8 @@ class PureCartesianICTDFix(nn.Module):
             # atoms are contiguous per graph, and the graphs' coordinates overlap)
             topology = tpo.Topology(edge_src, edge_dst, N, positions=pos if cell.shape[0] == 1 else None)
         shifts = edge_shifts.to(pos.dtype)
-        if cell.shape[0] == 1:
-            shift_vec = shifts @ cell[0]
+        if cell.shape[0] == 1:   # [E, 3] x [3, 3] as three broadcast products (no library GEMM)
+            shift_vec = (shifts.unsqueeze(-1) * cell[0].to(shifts.dtype)).sum(1)
         else:  # per-edge cell rows without a batched 1x3x3 GEMM per edge
             cells = cell[batch[edge_src]]
             shift_vec = (shifts.unsqueeze(-1) * cells).sum(1)

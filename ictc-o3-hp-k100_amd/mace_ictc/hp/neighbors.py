@@ -60,11 +60,16 @@ def radius_graph_pbc(pos: torch.Tensor, cell: torch.Tensor, cutoff: float):
     return _radius_graph_torch(pos, cell, cutoff)
 
 
+def _mat3(x: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
+    """x [..., 3] . m [3, 3] as broadcast products (no library GEMM for these thin shapes)."""
+    return (x.unsqueeze(-1) * m).sum(-2)
+
+
 def _radius_graph_torch(pos: torch.Tensor, cell: torch.Tensor, cutoff: float):
     """The same edge list with torch device ops (CPU tensors, non-FP32 positions, few cells)."""
     dev = pos.device
     inv = torch.linalg.inv(cell.double())
-    frac = pos.double() @ inv
+    frac = _mat3(pos.double(), inv)
     k = torch.floor(frac)
     fw = frac - k
     lengths = cell.double().norm(dim=1)
@@ -102,8 +107,8 @@ def _cell_list(pos, cell, cutoff, fw, k, ncell):
     valid = cand >= 0
     j = cand.clamp(min=0)
     cellf = cell.double()
-    posw = fw @ cellf                                                                  # wrapped positions
-    img = wrap.double() @ cellf                                                        # [N,27,3]
+    posw = _mat3(fw, cellf)                                                            # wrapped positions
+    img = _mat3(wrap.double(), cellf)                                                  # [N,27,3]
     # vec = pos_w[i] - (pos_w[j] + img)
     vec = posw[:, None, None, :] - (posw[j] + img[:, :, None, :])
     r2 = (vec * vec).sum(-1)
@@ -121,13 +126,13 @@ def _all_pairs(pos, cell, cutoff, fw, k, widths):
     reps = torch.ceil(cutoff / widths).long().tolist()
     imgs = torch.tensor(list(itertools.product(*[range(-r, r + 1) for r in reps])), device=dev, dtype=torch.double)
     cellf = cell.double()
-    posw = fw @ cellf
+    posw = _mat3(fw, cellf)
     src_l, dst_l, sh_l = [], [], []
     N = pos.shape[0]
     chunk = max(1, int(4e7 // max(1, N * imgs.shape[0])))
     for s in range(0, N, chunk):
         i = torch.arange(s, min(N, s + chunk), device=dev)
-        vec = posw[i, None, None, :] - (posw[None, :, None, :] + (imgs @ cellf)[None, None])
+        vec = posw[i, None, None, :] - (posw[None, :, None, :] + _mat3(imgs, cellf)[None, None])
         r2 = (vec * vec).sum(-1)
         keep = (r2 < cutoff * cutoff) & (r2 > 1e-20)
         a, b, c = torch.nonzero(keep, as_tuple=True)

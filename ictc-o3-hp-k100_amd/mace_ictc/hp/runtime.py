@@ -79,6 +79,9 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
         # per-graph sums in FP64 without atomics (deterministic, contention free)
         if cell.shape[0] == 1:
             energy64 = selected.double().sum().reshape(1)
+        elif selected.is_cuda:
+            from ictc_o3.ops.linear import graph_sum
+            energy64 = graph_sum(selected, batch, cell.shape[0])
         else:
             onehot = torch.nn.functional.one_hot(batch, cell.shape[0]).to(torch.float64)
             energy64 = onehot.t() @ selected.double()

@@ -287,6 +287,27 @@ int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, con
  * per-slice partial sums are added in a fixed order (deterministic).          */
 int ictc_gate_gemm_bwd(const float* grad, int64_t edges, int gates, const float* weight, int hidden_width,
                        float* dhidden, void* stream);
+/* ictc_gate_gemm_bwd over a column block of a wider gradient: grad rows have
+ * pitch grad_pitch (>= gates, a multiple of 4), weight holds the block's
+ * `gates` rows; accumulate != 0 adds to dhidden.  Wider projections (more than
+ * 768 gates, e.g. 17 paths x 128 channels) run as blocks of at most 768
+ * columns accumulated in column order (deterministic).                        */
+int ictc_gate_gemm_bwd_strided(const float* grad, int64_t grad_pitch, int64_t edges, int gates, const float* weight,
+                               int hidden_width, float* dhidden, int accumulate, void* stream);
+
+/* Channel-linear GEMM: c [m, n] = a [m, k] . b [n, k]^T (accumulate != 0: c +=),
+ * row-major with row pitches lda, ldb, ldc, FP32 MFMA products and sums.
+ * Replaces the library GEMMs torch runs for the channel linears' forward and
+ * input adjoint in the training path and for the readouts: the per-degree and
+ * per-path maps (layers.py:317-355, ictd_irreps.py:207-227 linear_up), the
+ * element-conditioned self connection (layers.py:21-87) and the readouts
+ * (heads.py:12-27; pure_cartesian_ictd_layers.py:89-115).                      */
+int ictc_gemm_nt(const float* a, int64_t m, int64_t k, int64_t lda, const float* b, int64_t n, int64_t ldb, float* c,
+                 int64_t ldc, int accumulate, void* stream);
+/* Per-graph energy: out [graphs] (FP64) = sum of values [n] over atoms with
+ * batch [n] == graph, a fixed-order reduction (deterministic, no atomics);
+ * replaces the per-graph scatter of hp/runtime.py:86-113.                     */
+int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, double* out, void* stream);
 
 /* Weight gradient of a per-edge linear (replaces the library GEMM dW = dy^T x
  * that autograd runs for every Linear of the radial MLP fc in the force-loss

@@ -8,6 +8,8 @@ edge counts that end inside a 16-edge tile and inside a 256-edge block.
 import pytest
 import torch
 
+from helpers import rel_err
+
 pytestmark = pytest.mark.gpu
 
 
@@ -71,3 +73,16 @@ def test_gate_adjoint_range_and_determinism(device):
     a = _check_adjoint(device, 5000, 704, scale=20, seed=3)
     b = _check_adjoint(device, 5000, 704, scale=20, seed=3)
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("E,M", [(5000, 2176), (777, 1600), (300, 832)])
+def test_wide_gate_adjoint_column_blocks(device, E, M):
+    """Projections wider than 768 gates: the split-bf16 adjoint over column blocks of at most 768, accumulated
+    in column order, against float64 (1e-5) and bitwise repeatable."""
+    from ictc_o3.ops.radial_mlp import gate_projection_adjoint
+    g = torch.Generator().manual_seed(E + M)
+    dg = torch.randn(E, M, generator=g, dtype=torch.float64)
+    W = torch.randn(M, 64, generator=g, dtype=torch.float64) / 8
+    out = gate_projection_adjoint(dg.float().to(device), W.float().to(device))
+    assert rel_err(out, dg @ W) < 1e-5
+    assert torch.equal(out, gate_projection_adjoint(dg.float().to(device), W.float().to(device)))

@@ -68,3 +68,35 @@ def test_fast_linear_refuses_second_order(device):
     out = degree_linear_fast(x, W, 64, 0)
     with pytest.raises(RuntimeError):
         torch.autograd.grad(out.square().sum(), x, create_graph=True)
+
+
+@pytest.mark.parametrize("M,K,N,lda,acc", [(1000, 64, 1, 64, 0), (131, 8, 64, 8, 0), (517, 128, 1280, 200, 0),
+                                           (64, 2176, 64, 2176, 1), (3, 5, 7, 9, 1), (8192, 16, 64, 16, 0)])
+def test_gemm_nt_against_float64(device, M, K, N, lda, acc):
+    """ictc_gemm_nt: c (+)= a . b^T with row pitches, odd sizes, thin readout shapes (FP32-MFMA sums, 1e-5)."""
+    from ictc_o3 import _native as nat
+    g = torch.Generator().manual_seed(M + K + N)
+    a = torch.randn(M, lda, generator=g, dtype=torch.float64)
+    b = torch.randn(N, K, generator=g, dtype=torch.float64)
+    c0 = torch.randn(M, N, generator=g, dtype=torch.float64)
+    ref = a[:, :K] @ b.t() + (c0 if acc else 0)
+    ad, bd, cd = a.float().to(device), b.float().to(device), c0.float().to(device)
+    nat.call("ictc_gemm_nt", nat.ptr(ad), M, K, lda, nat.ptr(bd), N, K, nat.ptr(cd), N, acc,
+             torch.cuda.current_stream(device).cuda_stream)
+    torch.cuda.synchronize()
+    assert rel_err(cd, ref) < 1e-5
+
+
+def test_graph_sum_exact_and_repeatable(device):
+    from ictc_o3.ops.linear import graph_sum
+    g = torch.Generator().manual_seed(4)
+    v = torch.randn(50000, generator=g)
+    batch = torch.randint(0, 37, (50000,), generator=g)
+    ref = torch.zeros(37, dtype=torch.float64).index_add(0, batch, v.double())
+    vd = v.to(device).requires_grad_(True)
+    out = graph_sum(vd, batch.to(device), 37)
+    assert out.dtype == torch.float64 and float((out.cpu() - ref).abs().max()) < 1e-9
+    assert torch.equal(out, graph_sum(vd, batch.to(device), 37))
+    w = torch.randn(37, generator=g, dtype=torch.float64)
+    (gv,) = torch.autograd.grad((out * w.to(device)).sum(), vd)
+    assert torch.equal(gv.cpu(), w[batch].float())
