@@ -705,6 +705,48 @@ def cpu_baseline_train(model, budget_s=25.0):
 
 
 
+def run_layers(args):
+    """Fused against materialised radial gates, per cfg4 layer: one message forward + energy-and-forces adjoint
+    (features, harmonics, edge lengths) including the layer's radial gates, HIP-event timed (ms per pass)."""
+    import torch
+    from mace_ictc.hp import create_model, radius_graph_pbc
+    from ictc_o3.ops import tensor_product as tpo
+    dev = torch.device("cuda:0")
+    torch.manual_seed(2024)
+    model = create_model(channels=64, lmax=2, num_interactions=2, correlation=3, atomic_numbers=(1, 6, 8),
+                         cutoff=4.5, avg_num_neighbors=42.0, device=dev)
+    pos, Z, cell, a = fcc_system(32, 0.1, 0.3, 1234, 3, dev)
+    N = pos.shape[0]
+    src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
+    E = src.numel()
+    topo = tpo.Topology(src, dst, N, positions=pos)
+    topo.by_src
+    g = torch.Generator(device=dev).manual_seed(3)
+    r = (torch.rand(E, device=dev, generator=g) * 3 + 1.5).requires_grad_(True)
+    Y = torch.randn(E, 9, device=dev, generator=g).requires_grad_(True)
+    cfg = (4.5, 5, 1.6791767923989418)
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    for li, inter in ((0, model.interactions[0]), (2, model.interactions[1])):
+        spec = inter.spec()
+        x = torch.randn(N, (li + 1) ** 2 * 64, device=dev, generator=g).requires_grad_(li > 0)
+        go = torch.randn(N, spec.out_components * 64, device=dev, generator=g)
+        wrt = [t for t in (x, Y, r) if t.requires_grad]
+        for mode in ("always", "never"):
+            tpo.FUSED_GATES = mode
+
+            def step():
+                o = tpo.radial_message(x, Y, r, inter.fc, spec, topo, None, cfg)
+                torch.autograd.grad(o, wrt, go)
+            t = time_launches(step, args.steps, stream)
+            out[f"layer{li}_{'fused' if mode == 'always' else 'materialised'}_ms"] = round(t * 1e3, 3)
+            log(f"  input degree {li}, {mode}: {t * 1e3:.2f} ms")
+    tpo.FUSED_GATES = "auto"
+    print(json.dumps({"workload": "cfg4 layers: radial gates + message forward + energy-and-forces adjoint",
+                      "atoms": N, "edges": E, **out}), flush=True)
+    return None, None
+
+
 def run_probe(args):
     """Counter-collection workload: the cfg4 layer-1 message kernels and gate kernels, then a 1 GiB copy.
 
@@ -766,7 +808,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="cfg4", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "probe"])
+    ap.add_argument("--workload", default="cfg4", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5", "probe", "layers"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="skip the per-kernel HIP-event timings after the timed steps (clean profiles of the step)")
@@ -780,6 +822,9 @@ def main():
                "cfg5": (run_cfg5, cpu_baseline_train)}
     if args.workload == "probe":
         run_probe(args)
+        return
+    if args.workload == "layers":
+        run_layers(args)
         return
     run, cpu = runners[args.workload]
     result, data = run(args)
