@@ -122,3 +122,31 @@ def test_receiver_row_order_choice():
     inv = torch.empty_like(perm)
     inv[perm] = torch.arange(perm.numel())
     assert _index_order_scattered(shuffled, inv[rows.long()].int())
+
+
+def test_fused_and_gemm_entry_points_host_checks():
+    """Coverage queries and argument checks of the fused message and GEMM entry points (no device work)."""
+    from ictc_o3 import _native
+    if not os.path.exists(_native.library_path()):
+        pytest.skip("library not built")
+    lib = _native.lib()
+    assert lib.ictc_fused_supported(2, 2, 2, 64) == 1 and lib.ictc_fused_supported(0, 2, 2, 128) == 1
+    assert lib.ictc_fused_supported(2, 3, 3, 64) == 0 and lib.ictc_fused_supported(2, 2, 2, 48) == 0
+    assert lib.ictc_fused_weight_bytes(11, 64) == 11 * 24 * 1024
+    assert lib.ictc_fused_weight_bytes(11, 48) < 0
+    with pytest.raises(ValueError, match="not compiled"):
+        _native.call("ictc_msg_fused_fwd", 2, 3, 3, 64, None, None, None, None, None, None, 10, 10, None, None, None,
+                     None, None)
+    with pytest.raises(ValueError, match="multiple of 64"):
+        _native.call("ictc_msg_fused_fwd", 2, 2, 2, 96, None, None, None, None, None, None, 10, 10, None, None, None,
+                     None, None)
+    with pytest.raises(ValueError, match="dr is required"):
+        _native.call("ictc_msg_fused_bwd_tangent", 2, 2, 2, 64, None, None, None, None, None, None, None, None, 10,
+                     10, None, None, None, None, None, None, None, None, None, None, None)
+    with pytest.raises(ValueError, match="lda >= k"):
+        _native.call("ictc_gemm_nt", None, 4, 8, 4, None, 4, 8, None, 4, 0, None)
+    with pytest.raises(ValueError, match="pitch"):
+        _native.call("ictc_gate_gemm_bwd_strided", None, 100, 10, 128, None, 64, None, 0, None)
+    with pytest.raises(ValueError, match="static scratch"):
+        _native.call("ictc_radial_gates_tangent_fwd_noalloc", None, 10, 8, 64, 4.5, 5, None, None, None, None,
+                     4096 + 16, 1.0, None, None, None)

@@ -144,3 +144,25 @@ def test_fused_message_weight_gradient_route(device):
     assert rel_err(out, ref.detach()) < TOL
     for a, b in zip(grads, [xr.grad, shr.grad, rr.grad] + [W.grad for W in Wl]):
         assert rel_err(a, b) < TOL
+
+
+@pytest.mark.parametrize("li", [0, 2])
+def test_fused_message_without_edges(device, li):
+    """E = 0: zero output rows, zero feature gradient, empty harmonic and edge-length gradients."""
+    from ictc_o3.ops import tensor_product as tpo
+    N, C = 9, 64
+    P = len(orc.natural_paths(li, 2, 2))
+    sizes = [8, 64, 64, 64, P * C]
+    Ws = [torch.randn(o, i, dtype=torch.float64) / math.sqrt(i) for i, o in zip(sizes, sizes[1:])]
+    fc = _fc(P * C, Ws, device)
+    spec = tpo.make_spec(li, 2, 2, C)
+    e = torch.zeros(0, dtype=torch.long, device=device)
+    topo = tpo.Topology(e, e, N)
+    x = torch.randn(N, C * (li + 1) ** 2, device=device, requires_grad=True)
+    sh = torch.zeros(0, 9, device=device, requires_grad=True)
+    r = torch.zeros(0, device=device, requires_grad=True)
+    out = tpo.radial_message(x, sh, r, fc, spec, topo, None, CFG)
+    assert type(out.grad_fn).__name__.startswith("FusedRadialMessage")
+    assert out.shape == (N, spec.out_components * C) and float(out.abs().max()) == 0.0
+    dx, dsh, dr = torch.autograd.grad(out, [x, sh, r], torch.ones_like(out))
+    assert float(dx.abs().max()) == 0.0 and dsh.shape == (0, 9) and dr.shape == (0,)
