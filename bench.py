@@ -46,10 +46,11 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # HBM bytes per launch of the cfg4 layer-1 message kernels (P11, C64, E=5,262,704; msg_bwd_x in
 # the Morton source order the model uses), from rocprofv3 FETCH_SIZE + WRITE_SIZE runs of
 # `bench.py --workload probe`, each scaled by the counter's reading for a 1 GiB copy (FETCH x2.0,
-# WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.
-MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 20.07e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
+# WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.  msg_fwd, msg_bwd_tan and gates_tan are the step's
+# forms: gates shared by each edge and its reverse (2,631,352 gate rows).
+MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 19.81e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
                     ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9,
-                    ("msg_bwd_tan", 131072, 5262704, 64): 53.10e9, ("gates_tan", 131072, 5262704, 64): 31.50e9}
+                    ("msg_bwd_tan", 131072, 5262704, 64): 53.13e9, ("gates_tan", 131072, 5262704, 64): 15.79e9}
 
 
 def log(*a):
@@ -87,17 +88,20 @@ def radial_basis(r, r_max, n_basis=8, p=5):
     return emb * (env * (r < r_max))[:, None]
 
 
-def message_bytes(N, E, C, NX, NY, P, NO):
+def message_bytes(N, E, C, NX, NY, P, NO, G=None):
+    """Algorithmic HBM bytes of the message kernels; G = rows of gates shared through gate_rows (None = E, one
+    row per edge; otherwise the gate-reading forms read G rows plus the int32 gate_rows map)."""
     idx = E * 8 + (N + 2) * 4 + E * 4
-    fwd = N * NX * C * 4 + E * NY * 4 + E * P * C * 4 + idx + N * NO * C * 4
+    gread = E * P * C * 4 if G is None else G * P * C * 4 + E * 4
+    fwd = N * NX * C * 4 + E * NY * 4 + gread + idx + N * NO * C * 4
     bwd_edge = N * NO * C * 4 + N * NX * C * 4 + E * NY * 4 + E * P * C * 4 + idx + E * NY * 4 + E * P * C * 4
     bwd_x = N * NO * C * 4 + E * NY * 4 + E * P * C * 4 + idx + N * NX * C * 4
     # the complete adjoint (dx, dsh, dg) of one source-owned pass: every operand read once, every output written once
     bwd = N * NO * C * 4 + N * NX * C * 4 + E * NY * 4 + E * P * C * 4 + idx + E * NY * 4 + E * P * C * 4 \
         + N * NX * C * 4
-    # gate-tangent form of the complete adjoint (energy + forces): gdot [E, P*C] read in place of dg written,
-    # plus dr [E]
-    bwd_tan = bwd + E * 4
+    # gate-tangent form of the complete adjoint (energy + forces): gates and gdot read (G rows each, through one
+    # gate_rows map), dr [E] written, no dg
+    bwd_tan = bwd - 2 * E * P * C * 4 + (2 * E * P * C * 4 if G is None else 2 * G * P * C * 4 + E * 4) + E * 4
     return {"msg_fwd": fwd, "msg_bwd_edge": bwd_edge, "msg_bwd_x": bwd_x, "msg_bwd": bwd, "msg_bwd_tan": bwd_tan}
 
 
@@ -303,10 +307,10 @@ def run_cfg4(args):
 
     if args.no_kernel_timing:
         return {"metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "ms_per_step": dt * 1e3}, model
-    src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
-    kern, nbytes = layer_message_kernels(model, src, dst, N, pos)
-    # the layer-1 radial gates with their r tangents (the step's largest kernel), timed the same way
-    kern["gates_tan"], nbytes["gates_tan"] = layer_gate_kernel(model, src.numel())
+    src, dst, sh = radius_graph_pbc(pos, cell[0], 4.5)
+    kern, nbytes, G = layer_message_kernels(model, src, dst, N, pos, sh)
+    # the layer-1 radial gates with their r tangents over the step's gate rows, timed the same way
+    kern["gates_tan"], nbytes["gates_tan"] = layer_gate_kernel(model, G)
     # the step's own layer-1 kernels (energy + forces: radial gates with tangents, message forward,
     # gate-tangent adjoint); the other adjoint forms are timed for reference only
     in_step = [k for k in ("gates_tan", "msg_fwd", "msg_bwd_tan") if k in kern]
@@ -320,7 +324,7 @@ def run_cfg4(args):
         "data": "synthetic (seeded jittered FCC positions, uniform species, random-init weights)",
         "config": {"workload": "cfg4: MACE-ICTC E+F, 131072 atoms FCC 32^3 at 0.1/A^3 +-0.3 A, rc 4.5 A, "
                                "C64 lmax2, 2 interactions, correlation 3, 8 Bessel, neighbour list rebuilt each step",
-                   "atoms": N, "edges": E, "channels": 64, "lmax": 2,
+                   "atoms": N, "edges": E, "gate_rows": G, "channels": 64, "lmax": 2,
                    "tp_edges_per_s": 2 * E / dt,
                    "kernel_us_layer1": {k: round(t * 1e6, 2) for k, t in kern.items()},
                    "kernel_algorithmic_MB_layer1": {k: round(v / 1e6, 2) for k, v in nbytes.items()}},
@@ -340,7 +344,8 @@ def run_cfg4(args):
 def layer_gate_kernel(model, E, reps=5):
     """HIP-event time of the layer-1 radial gates with their r tangents (ictc_radial_gates_tangent_fwd: W4
     split, then the MLP, both projections and both stores) and its algorithmic bytes: the edge lengths read,
-    gates and tangents [E, M] written (weights: under 0.3 MB)."""
+    gates and tangents [E, M] written (weights: under 0.3 MB).  E = the gate rows of the step (one per
+    undirected edge pair)."""
     import torch
     from ictc_o3.ops.radial_mlp import radial_gates_tangent
     inter = model.interactions[-1]
@@ -354,14 +359,22 @@ def layer_gate_kernel(model, E, reps=5):
     return t, E * 4 + 2 * E * M * 4
 
 
-def layer_message_kernels(model, src, dst, N, pos, reps=5):
+def layer_message_kernels(model, src, dst, N, pos, shifts=None, pair=True, reps=5):
     """Live HIP-event timing of the last interaction's message kernels (fwd, bwd_edge, bwd_x) at the run's shapes,
-    visiting rows in the spatial order the model uses (and, for the log only, in index order)."""
+    visiting rows in the spatial order the model uses (and, for the log only, in index order).  The step's own
+    forms (msg_fwd, msg_bwd_tan) read the gates shared by each edge and its reverse, as the model does; the
+    other adjoint forms (timed for reference) read one gate row per edge.  pair=False (the second-order
+    training route, which keeps per-edge gates) times every form on per-edge rows.  Returns (times, bytes,
+    gate rows)."""
     import torch
     from ictc_o3.ops import tensor_product as tpo
     dev = src.device
     stream = torch.cuda.current_stream(dev)
     topo = tpo.Topology(src, dst, N, positions=pos)
+    if pair:
+        topo.pair_edges(shifts)
+    rows = topo.gate_rows
+    G = src.numel() if rows is None else topo.gate_reps.numel()
     inter = model.interactions[-1]
     spec = inter.spec()
     C = spec.channels
@@ -372,8 +385,9 @@ def layer_message_kernels(model, src, dst, N, pos, reps=5):
     with torch.no_grad():
         r = torch.rand(src.numel(), device=dev, generator=g) * 3 + 1.5
         gates = inter.fc(model.radial_embedding(r))
+    shared = gates[:G]
     go = torch.randn(N, spec.out_components * C, device=dev, generator=g)
-    t_fwd = time_launches(lambda: tpo._msg_fwd_raw(spec, topo, x, Y, gates, None), reps, stream)
+    t_fwd = time_launches(lambda: tpo._msg_fwd_raw(spec, topo, x, Y, shared, None, rows), reps, stream)
     t_bwd_e = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True)), reps,
                             stream)
     topo.by_src
@@ -383,13 +397,16 @@ def layer_message_kernels(model, src, dst, N, pos, reps=5):
     t_bwd = time_launches(lambda: tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, True, True)), reps,
                           stream)
     nbytes = message_bytes(N, src.numel(), C, NX, NY, spec.num_paths, spec.out_components)
+    paired = message_bytes(N, src.numel(), C, NX, NY, spec.num_paths, spec.out_components, None if rows is None else G)
+    nbytes["msg_fwd"], nbytes["msg_bwd_tan"] = paired["msg_fwd"], paired["msg_bwd_tan"]
     kern = {"msg_fwd": t_fwd, "msg_bwd_edge": t_bwd_e, "msg_bwd_x": t_bwd_x}
     if t_bwd < 0.9 * (t_bwd_e + t_bwd_x):   # fused (one launch); otherwise it is the two kernels above
         kern["msg_bwd"] = t_bwd
         # energy + forces (the model's forces_only route): dx, dsh and dr = sum dg * d gates / dr
-        gdot = torch.randn_like(gates)
+        gdot = torch.randn_like(shared)
         kern["msg_bwd_tan"] = time_launches(
-            lambda: tpo._msg_bwd_tangent_raw(spec, topo, x, Y, gates, gdot, None, go, (True, True)), reps, stream)
+            lambda: tpo._msg_bwd_tangent_raw(spec, topo, x, Y, shared, gdot, None, go, (True, True), rows), reps,
+            stream)
         del gdot
     else:
         log(f"  last-layer full adjoint {t_bwd * 1e6:.1f} us: the two kernels above (not fused at this shape)")
@@ -403,8 +420,9 @@ def layer_message_kernels(model, src, dst, N, pos, reps=5):
                            stream),
              time_launches(lambda: tpo._msg_bwd_raw(spec, plain, x, Y, gates, None, go, (True, False, False)), reps,
                            stream)]
-    log("  index-order rows: " + ", ".join(f"{k} {t * 1e6:.1f} us" for k, t in zip(kern, t_idx)))
-    return kern, nbytes
+    log("  index-order rows (one gate row per edge): " + ", ".join(f"{k} {t * 1e6:.1f} us"
+                                                                 for k, t in zip(kern, t_idx)))
+    return kern, nbytes, G
 
 
 def run_cfg1(args):
@@ -646,7 +664,7 @@ def run_cfg5(args):
     log(f"cfg5: N={N} E={E} step={dt * 1e3:.2f} ms loss={float(loss.detach()):.4f}")
     if args.no_kernel_timing:
         return {"metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "ms_per_step": dt * 1e3}, model
-    kern, nbytes = layer_message_kernels(model, src, dst, N, None, reps=10)
+    kern, nbytes, _ = layer_message_kernels(model, src, dst, N, None, pair=False, reps=10)
     dom = max(kern, key=kern.get)   # the layer-1 message kernel with the largest time
     achieved = nbytes[dom] / kern[dom] / 1e9
     result = {
@@ -763,7 +781,7 @@ def run_probe(args):
                          cutoff=4.5, avg_num_neighbors=42.0, device=dev)
     pos, Z, cell, a = fcc_system(32, 0.1, 0.3, 1234, 3, dev)
     N = pos.shape[0]
-    src, dst, _ = radius_graph_pbc(pos, cell[0], 4.5)
+    src, dst, sh = radius_graph_pbc(pos, cell[0], 4.5)
     topo = tpo.Topology(src, dst, N, positions=pos)
     inter = model.interactions[-1]
     spec = inter.spec()
@@ -780,9 +798,16 @@ def run_probe(args):
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (False, True, True))
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, False, False))
         tpo._msg_bwd_raw(spec, topo, x, Y, gates, None, go, (True, True, True))
-    gdot = torch.randn_like(gates)
+    # the energy + forces step's forms: gates (and gdot) shared by each edge and its reverse
+    paired = tpo.Topology(src, dst, N, positions=pos)
+    paired.pair_edges(sh)
+    G = paired.gate_reps.numel() if paired.gate_rows is not None else src.numel()
+    shared = gates[:G]
+    gdot = torch.randn_like(shared)
+    paired.by_src
     for _ in range(args.steps):
-        tpo._msg_bwd_tangent_raw(spec, topo, x, Y, gates, gdot, None, go, (True, True))
+        tpo._msg_fwd_raw(spec, paired, x, Y, shared, None, paired.gate_rows)
+        tpo._msg_bwd_tangent_raw(spec, paired, x, Y, shared, gdot, None, go, (True, True), paired.gate_rows)
     del gdot
     from ictc_o3.ops.radial_mlp import gate_projection_adjoint, radial_gates, radial_gates_tangent
     lin = [m for m in inter.fc if isinstance(m, torch.nn.Linear)]
@@ -790,7 +815,7 @@ def run_probe(args):
         for _ in range(args.steps):
             radial_gates(r, inter.fc, model.max_radius, model.polynomial_cutoff_p, 1.6791767923989418)
             gate_projection_adjoint(gates, lin[-1].weight.detach())
-            radial_gates_tangent(r, [m.weight for m in lin], model.max_radius, model.polynomial_cutoff_p,
+            radial_gates_tangent(r[:G], [m.weight for m in lin], model.max_radius, model.polynomial_cutoff_p,
                                  1.6791767923989418)
     a = torch.empty(1 << 28, device=dev)
     b = torch.randn(1 << 28, device=dev)
@@ -798,7 +823,9 @@ def run_probe(args):
         a.copy_(b)
     torch.cuda.synchronize()
     nbytes = message_bytes(N, src.numel(), 64, 9, 9, spec.num_paths, spec.out_components)
-    log(f"probe: N={N} E={src.numel()} algorithmic bytes {nbytes}; copy {4 << 28} bytes each way")
+    pb = message_bytes(N, src.numel(), 64, 9, 9, spec.num_paths, spec.out_components, G)
+    log(f"probe: N={N} E={src.numel()} gate rows {G} algorithmic bytes {nbytes}; paired msg_fwd "
+        f"{pb['msg_fwd']} msg_bwd_tan {pb['msg_bwd_tan']}; copy {4 << 28} bytes each way")
     return None, None
 
 

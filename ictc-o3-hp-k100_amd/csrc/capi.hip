@@ -56,8 +56,9 @@ int check_shape(int li, int le, int lo, int C) {
 }
 
 ictc::Operands operands(const float* x, const float* sh, const float* g, const float* w, const float* mask,
-                        int64_t rows, int64_t edges, int C) {
+                        int64_t rows, int64_t edges, int C, const int32_t* gate_rows = nullptr) {
   ictc::Operands a;
+  a.grow = gate_rows;
   a.x = x;
   a.sh = sh;
   a.gates = g;
@@ -333,14 +334,14 @@ int ictc_morton_order(const float* pos, int64_t N, float spacing, int32_t* order
 
 int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
                  const float* mask, const int64_t* src, int64_t N, int64_t E, const int32_t* dptr,
-                 const int32_t* dorder, const int32_t* dst_rows, float* out, void* stream) {
+                 const int32_t* dorder, const int32_t* dst_rows, float* out, const int32_t* gate_rows, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
   if (N == 0) return ICTC_OK;
   if (!x || !out || !dptr || (E > 0 && (!sh || !g || !src)))
     return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fwd: null operand");
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(route_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C), src, ictc::Csr{dptr, dorder, dst_rows}, out,
+  return check_hip(route_msg_fwd(s, operands(x, sh, g, w, mask, N, E, C, gate_rows), src, ictc::Csr{dptr, dorder, dst_rows}, out,
                                         (hipStream_t)stream),
                    "ictc_msg_fwd launch");
 }
@@ -380,7 +381,7 @@ int ictc_msg_bwd_tangent(int li, int le, int lo, int C, const float* x, const fl
                          int64_t E, const int32_t* dptr, const int32_t* dorder, const int32_t* sptr,
                          const int32_t* sorder, const int32_t* dst_rows, const int32_t* src_rows, const float* grad,
                          const float* gdot, float* dx, float* dsh, float* dr, void* workspace,
-                         int64_t workspace_bytes, void* stream) {
+                         int64_t workspace_bytes, const int32_t* gate_rows, void* stream) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
   if (E == 0) {
@@ -399,7 +400,7 @@ int ictc_msg_bwd_tangent(int li, int le, int lo, int C, const float* x, const fl
     return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_tangent: %d channels need a workspace of %lld bytes", C,
                 (long long)need);
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(ictc::launch_msg_bwd_tangent(s, operands(x, sh, g, w, mask, N, E, C), src, dst,
+  return check_hip(ictc::launch_msg_bwd_tangent(s, operands(x, sh, g, w, mask, N, E, C, gate_rows), src, dst,
                                                 ictc::Csr{dptr, dorder, dst_rows}, ictc::Csr{sptr, sorder, src_rows},
                                                 grad, gdot, dx, dsh, dr, (float*)workspace, (hipStream_t)stream),
                    "ictc_msg_bwd_tangent launch");

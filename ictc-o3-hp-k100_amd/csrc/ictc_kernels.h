@@ -93,7 +93,13 @@ struct Operands {
   int64_t rows;         // E (edge TP) or N (message)
   int64_t edges;
   int channels;
+  // Gate row of each edge ([E], nullptr = the edge itself): the radial gates depend on the edge length
+  // only, and an edge and its reverse have bitwise-equal lengths, so one row can serve both.
+  const int32_t* grow = nullptr;
 };
+
+// Row of the gate (and gate-tangent) arrays that edge e reads.
+__device__ __forceinline__ int64_t gate_row(const Operands& a, int64_t e) { return a.grow ? (int64_t)a.grow[e] : e; }
 
 template <class T>
 __device__ __forceinline__ void load_harmonics(const float* __restrict__ sh, int64_t e, float* y) {
@@ -138,7 +144,7 @@ __device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c
 // the optional weight is a separate uniform branch after them.
 template <class T>
 __device__ __forceinline__ void load_gw(const Operands& a, int64_t e, int c, float scale, float* gw) {
-  load_row<T::P>(a.gates + e * (int64_t)(T::P * a.channels), a.channels, c, gw);
+  load_row<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * a.channels), a.channels, c, gw);
   if (a.weight) {
     float w[T::P];
 #pragma unroll
@@ -484,7 +490,7 @@ __global__ __launch_bounds__(kBlock, (edge_adjoint_waves<T, TAN>())) void msg_bw
         float xv[T::NX], gw[T::P], gt[T::P], d[T::P];
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
         load_gw<T>(a, e, c, m, gw);
-        load_row<T::P>(gdot + e * (int64_t)(T::P * C), C, c, gt);
+        load_row<T::P>(gdot + gate_row(a, e) * (int64_t)(T::P * C), C, c, gt);
         if (dsh) T::dydg(xv, y, gw, go, dyv, d);
         else T::dg(xv, y, go, d);
         dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, d);
@@ -616,7 +622,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
         float go[T::NO], gw[T::P], gt[T::P], dg[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
         load_gw<T>(a, e, c, m, gw);
-        load_row<T::P>(gdot + e * (int64_t)(T::P * C), C, c, gt);
+        load_row<T::P>(gdot + gate_row(a, e) * (int64_t)(T::P * C), C, c, gt);
         if (!tail) T::dx(y, gw, go, d);
         if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
         else T::dg(xv, y, go, dg);

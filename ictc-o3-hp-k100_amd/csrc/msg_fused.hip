@@ -269,7 +269,10 @@ struct FusedArgs {
   int64_t rows, edges;
   int C, cg;            // channels, channel group of this launch
   Csr csr;
+  const int32_t* grow;  // row of h / t for each edge ([E], nullptr = the edge itself)
 };
+
+__device__ __forceinline__ int64_t hrow(const FusedArgs& a, int32_t e) { return a.grow ? (int64_t)a.grow[e] : e; }
 
 // Forward: out[n, SLOT[k], c] for the group's slots (receiver-owned).
 template <class TG>
@@ -295,7 +298,7 @@ __global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_fwd_kerne
         const int ci = t0 + (l & 15);
         const int32_t ea = __shfl(ch.e, ci);
         Split A[2];
-        load_a(a.h, ea, ci < count, A);
+        load_a(a.h, ci < count ? hrow(a, ea) : 0, ci < count, A);
         float Gt[TG::PG][16];
         project_tile<TG::PG>(w4l, A, Gt);
 #pragma unroll
@@ -353,7 +356,7 @@ __global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_bwd_src_k
         const int ci = t0 + (l & 7);
         const int32_t ea = __shfl(ch.e, ci);
         Split A[2];
-        load_a((l & 8) ? a.t : a.h, ea, ci < count, A);
+        load_a((l & 8) ? a.t : a.h, ci < count ? hrow(a, ea) : 0, ci < count, A);
         float Gt[TG::PG][16];
         project_tile<TG::PG>(w4l, A, Gt);
 #pragma unroll
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_bwd_rcv_k
         const int ci = t0 + (l & 7);
         const int32_t ea = __shfl(ch.e, ci);
         Split A[2];
-        load_a((l & 8) ? a.t : a.h, ea, ci < count, A);
+        load_a((l & 8) ? a.t : a.h, ci < count ? hrow(a, ea) : 0, ci < count, A);
         float Gt[TG::PG][16];
         project_tile<TG::PG>(w4l, A, Gt);
 #pragma unroll
@@ -579,7 +582,8 @@ int ictc_fused_weight_split(const float* W4, const float* tp_weight, int paths, 
 
 int ictc_msg_fused_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* h3,
                        const void* w4split, const float* mask, const int64_t* src, int64_t N, int64_t E,
-                       const int32_t* dptr, const int32_t* dorder, const int32_t* dst_rows, float* out, void* stream) {
+                       const int32_t* dptr, const int32_t* dorder, const int32_t* dst_rows, float* out,
+                       const int32_t* gate_rows, void* stream) {
   if (int rc = check(li, le, lo, C, N, E)) return rc;
   if (N == 0) return ICTC_OK;
   if (!x || !out || !dptr || (E > 0 && (!sh || !h3 || !w4split || !src)))
@@ -587,7 +591,8 @@ int ictc_msg_fused_fwd(int li, int le, int lo, int C, const float* x, const floa
   if ((reinterpret_cast<uintptr_t>(h3) | reinterpret_cast<uintptr_t>(w4split)) & 15)
     return fail(ICTC_ERR_ARGUMENT, "ictc_msg_fused_fwd: h3 and the split weight must be 16-byte aligned");
   Launch L{Pass::kFwd,
-           FusedArgs{x, sh, h3, nullptr, (const bf16x8*)w4split, mask, src, N, E, C, 0, Csr{dptr, dorder, dst_rows}},
+           FusedArgs{x, sh, h3, nullptr, (const bf16x8*)w4split, mask, src, N, E, C, 0, Csr{dptr, dorder, dst_rows},
+                     gate_rows},
            nullptr, out, nullptr, nullptr, nullptr, 0, (hipStream_t)stream};
   for (int cg = 0; cg < C / 64; ++cg) {
     L.a.cg = cg;
@@ -601,7 +606,7 @@ int ictc_msg_fused_bwd_tangent(int li, int le, int lo, int C, const float* x, co
                                const int64_t* dst, int64_t N, int64_t E, const int32_t* dptr, const int32_t* dorder,
                                const int32_t* sptr, const int32_t* sorder, const int32_t* dst_rows,
                                const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dr,
-                               void* stream) {
+                               const int32_t* gate_rows, void* stream) {
   if (int rc = check(li, le, lo, C, N, E)) return rc;
   if (E == 0) {
     // no edges: dsh and dr are empty, dx is zero
@@ -619,7 +624,7 @@ int ictc_msg_fused_bwd_tangent(int li, int le, int lo, int C, const float* x, co
   const bool src_owned = dx != nullptr;
   Launch L{src_owned ? Pass::kBwdSrc : Pass::kBwdRcv,
            FusedArgs{x, sh, h3, t3, (const bf16x8*)w4split, mask, src_owned ? dst : src, N, E, C, 0,
-                     src_owned ? Csr{sptr, sorder, src_rows} : Csr{dptr, dorder, dst_rows}},
+                     src_owned ? Csr{sptr, sorder, src_rows} : Csr{dptr, dorder, dst_rows}, gate_rows},
            grad, nullptr, dx, dsh, dr, 0, (hipStream_t)stream};
   for (int cg = 0; cg < C / 64; ++cg) {
     L.a.cg = cg;

@@ -35,18 +35,20 @@ _SIGNATURES = {
     "ictc_csr_build": (_i, [_p, _i64, _i64, _p, _p, _p, _i64, _p]),
     "ictc_morton_workspace_bytes": (_i64, [_i64]),
     "ictc_morton_order": (_i, [_p, _i64, ctypes.c_float, _p, _p, _i64, _p]),
-    "ictc_msg_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
+    "ictc_msg_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_msg_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
                           _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_msg_bwd_tangent_workspace_bytes": (_i64, [_i, _i, _i64]),
     "ictc_msg_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
-                                  _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
+                                  _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p]),
     "ictc_fused_supported": (_i, [_i, _i, _i, _i]),
     "ictc_fused_weight_bytes": (_i64, [_i, _i]),
     "ictc_fused_weight_split": (_i, [_p, _p, _i, _i, _p, _i64, _p]),
-    "ictc_msg_fused_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p]),
+    "ictc_msg_fused_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_msg_fused_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
-                                        _p, _p, _p, _p, _p, _p, _p]),
+                                        _p, _p, _p, _p, _p, _p, _p, _p]),
+    "ictc_edge_pairs_workspace_bytes": (_i64, [_i64]),
+    "ictc_edge_pairs": (_i, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_sh_fwd": (_i, [_p, _i64, _i, _p, _p]),
     "ictc_sh_bwd": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_jvp": (_i, [_p, _p, _i64, _i, _p, _p]),

@@ -19,6 +19,7 @@ a differentiable torch path, operators.py:85-103).
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 from typing import Optional
 
@@ -281,6 +282,49 @@ class Topology:
         self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None
         if self.src_rows is not None and nodes > 1 and _index_order_scattered(positions, self.src_rows):
             self.dst_rows = self.src_rows
+        self.gate_rows = None     # int32 [E]: row of the shared radial gates each edge reads (pair_edges)
+        self.gate_reps = None     # int64 [rows]: the edge whose length fills each gate row
+        self._pairs_of = None
+
+    def pair_edges(self, shifts: torch.Tensor | None):
+        """Share one radial-gate row between every edge and its reverse (same length, bitwise).
+
+        The reverse of (s -> d, shift S) is an edge (d -> s, shift -S); shifts
+        [E, 3] are compared exactly (None = no periodic images).  Computed once
+        per live shifts tensor and version (one host sync for the row count).
+        Where no edge has a reverse the rows stay per edge (gate_rows None).
+        """
+        key = None if shifts is None else (shifts._version, tuple(shifts.shape))
+        seen = self._pairs_of
+        if seen is not None and (seen[0] is None if shifts is None else seen[0] is not None and seen[0]() is shifts) \
+                and seen[1] == key:
+            return
+        E = self.src.numel()
+        self.gate_rows = self.gate_reps = None
+        if E > 0:
+            sh = None if shifts is None else _c(shifts.detach().to(torch.float32))
+            if sh is not None and tuple(sh.shape) != (E, 3):
+                raise ValueError("edge shifts must be [E, 3]")
+            dev = self.src.device
+            rows = torch.empty(E, dtype=torch.int32, device=dev)
+            reps = torch.empty(E, dtype=torch.int32, device=dev)
+            count = torch.empty(1, dtype=torch.int32, device=dev)
+            ws_bytes = int(nat.lib().ictc_edge_pairs_workspace_bytes(E))
+            if ws_bytes < 0:
+                raise ValueError("too many edges to pair (2^30 or more)")
+            ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+            nat.call("ictc_edge_pairs", nat.ptr(self.src), nat.ptr(self.dst), nat.ptr(sh), self.nodes, E,
+                     nat.ptr(self.by_dst.ptr), nat.ptr(self.by_dst.order), nat.ptr(rows), nat.ptr(reps),
+                     nat.ptr(count), nat.ptr(ws), ws_bytes, nat.stream_of(self.src))
+            n = int(count.item())
+            if n < E:
+                self.gate_rows, self.gate_reps = rows, reps[:n].long()
+        self._pairs_of = (None if shifts is None else weakref.ref(shifts), key)
+
+    def gate_input(self, r: torch.Tensor) -> torch.Tensor:
+        """The edge lengths of the gate rows (r itself when the rows are per edge)."""
+        return r if self.gate_reps is None else r.index_select(0, self.gate_reps)
+
 
     @property
     def by_src(self):
@@ -289,12 +333,18 @@ class Topology:
         return self._by_src
 
 
-def _msg_fwd_raw(spec, topo, x, sh, g, mask):
+def _expand_gates(g, gate_rows):
+    """Per-edge gate rows [E, ...] from rows shared through gate_rows (None = already per edge)."""
+    return g if gate_rows is None else g.index_select(0, gate_rows)
+
+
+def _msg_fwd_raw(spec, topo, x, sh, g, mask, gate_rows=None):
     N, E = x.shape[0], sh.shape[0]
     out = x.new_empty(N, spec.out_components * spec.channels)
     nat.call("ictc_msg_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), N, E, nat.ptr(topo.by_dst.ptr),
-             nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.stream_of(x))
+             nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.ptr(gate_rows),
+             nat.stream_of(x))
     return out
 
 
@@ -356,7 +406,7 @@ class Message(torch.autograd.Function):
         return dx, dsh, dg, None, None, None
 
 
-def _msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, mask, go, need):
+def _msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, mask, go, need, gate_rows=None):
     """First adjoint with the gate gradient contracted against gdot = d gates / dr: (dx, dsh, dr)."""
     N, E = x.shape[0], sh.shape[0]
     dx = torch.empty_like(x) if need[0] else None
@@ -370,7 +420,8 @@ def _msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, mask, go, need):
              nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
              nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
              nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(gdot),
-             nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr), nat.ptr(ws), max(nbytes, 0), nat.stream_of(x))
+             nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr), nat.ptr(ws), max(nbytes, 0), nat.ptr(gate_rows),
+             nat.stream_of(x))
     return dx, dsh, dr
 
 
@@ -382,6 +433,8 @@ class RadialMessage(torch.autograd.Function):
     inside the message adjoint: the gate gradient [E, P*C], its projection onto the
     hidden layer and the MLP adjoint are never run.  A backward that does need the
     weight gradients takes the ordinary route (message adjoint, then radial adjoint).
+    With paired edges (Topology.pair_edges) the gates are evaluated once per
+    gate row and read through topo.gate_rows.
     """
 
     @staticmethod
@@ -391,9 +444,10 @@ class RadialMessage(torch.autograd.Function):
         ctx.inputs = (x, sh, r, W1, W2, W3, W4)
         ctx.spec, ctx.topo, ctx.mask, ctx.cfg = spec, topo, mask, cfg
         x, sh = _c(x), _c(sh)
-        gates, gdot = radial_gates_tangent(r, (W1, W2, W3, W4), *cfg)
+        ctx.rows = topo.gate_rows
+        gates, gdot = radial_gates_tangent(topo.gate_input(r), (W1, W2, W3, W4), *cfg)
         ctx.save_for_backward(x, sh, _c(r), *(_c(w) for w in (W1, W2, W3, W4)), gates, gdot)
-        return _msg_fwd_raw(spec, topo, x, sh, gates, mask)
+        return _msg_fwd_raw(spec, topo, x, sh, gates, mask, ctx.rows)
 
     @staticmethod
     @once_differentiable
@@ -408,11 +462,13 @@ class RadialMessage(torch.autograd.Function):
         go = _c(go)
         dW = [None] * 4
         if any(needs[3:7]):
+            gates = _expand_gates(gates, ctx.rows)
             dx, dsh, dg = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], True))
             dr, dW = radial_gates_adjoint(r, (W1, W2, W3, W4), ctx.cfg, dg, (needs[2], *needs[3:7]))
         elif needs[2]:
-            dx, dsh, dr = _msg_bwd_tangent_raw(spec, topo, x, sh, gates, gdot, mask, go, needs[:2])
+            dx, dsh, dr = _msg_bwd_tangent_raw(spec, topo, x, sh, gates, gdot, mask, go, needs[:2], ctx.rows)
         elif needs[0] or needs[1]:
+            gates = _expand_gates(gates, ctx.rows)
             dx, dsh, _ = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], False))
             dr = None
         else:
@@ -426,6 +482,10 @@ class RadialMessage(torch.autograd.Function):
 # launches of the adjoint measure slower than reading materialised gates (22.8 against 20.7 ms);
 # "always" = every compiled shape; "never" = nowhere.
 FUSED_GATES = "auto"
+
+# Whether callers of radial_message pair edges with their reverses (Topology.pair_edges) so that the
+# radial gates are evaluated once per undirected edge; False keeps one gate row per directed edge.
+PAIR_GATES = True
 
 
 def _fused_weight(fc, W4, spec):
@@ -459,7 +519,8 @@ class FusedRadialMessage(torch.autograd.Function):
     The forward writes the MLP's last hidden activation h3 and its r tangent
     t3 = d h3 / dr ([E, 64] each) and the message kernels project the gates
     (and, in the adjoint, their r tangents) per edge tile from them
-    (streamed_gate_message.py:87-223).  A backward that needs weight
+    (streamed_gate_message.py:87-223).  h3 and t3 have one row per gate row
+    of the topology (Topology.pair_edges).  A backward that needs weight
     gradients rebuilds the gates [E, P*C] from h3 and takes the ordinary
     message and radial adjoints.
     """
@@ -472,15 +533,18 @@ class FusedRadialMessage(torch.autograd.Function):
         x, sh, rc = _c(x), _c(sh), _c(r.detach())
         Ws = [_c(w.detach()) for w in (W1, W2, W3, W4)]
         E = rc.shape[0]
-        h3, t3 = rc.new_empty(E, 64), rc.new_empty(E, 64)
-        nat.call("ictc_radial_mlp_tangent_fwd", nat.ptr(rc), E, 8, 64, float(cfg[0]), int(cfg[1]),
+        rg = _c(topo.gate_input(rc))     # one row per edge pair
+        ctx.rows = topo.gate_rows
+        h3, t3 = rc.new_empty(rg.shape[0], 64), rc.new_empty(rg.shape[0], 64)
+        nat.call("ictc_radial_mlp_tangent_fwd", nat.ptr(rg), rg.shape[0], 8, 64, float(cfg[0]), int(cfg[1]),
                  nat.ptr(Ws[0]), nat.ptr(Ws[1]), nat.ptr(Ws[2]), float(cfg[2]), nat.ptr(h3), nat.ptr(t3),
                  nat.stream_of(rc))
         N = x.shape[0]
         out = x.new_empty(N, spec.out_components * spec.channels)
         nat.call("ictc_msg_fused_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh),
                  nat.ptr(h3), nat.ptr(w4s), nat.ptr(mask), nat.ptr(topo.src), N, E, nat.ptr(topo.by_dst.ptr),
-                 nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.stream_of(x))
+                 nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.ptr(ctx.rows),
+                 nat.stream_of(x))
         ctx.save_for_backward(x, sh, rc, *Ws, h3, t3)
         return out
 
@@ -496,7 +560,7 @@ class FusedRadialMessage(torch.autograd.Function):
         spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
         go = _c(go)
         if any(needs[3:7]):
-            gates = gate_projection(h3, W4)   # unweighted: the message kernels apply the path weight
+            gates = _expand_gates(gate_projection(h3, W4), ctx.rows)   # unweighted: the kernels apply the path weight
             dx, dsh, dg = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], True))
             dr, dW = radial_gates_adjoint(r, (W1, W2, W3, W4), ctx.cfg, dg, (needs[2], *needs[3:7]))
             return (dx, dsh, dr, *dW, None, None, None, None, None)
@@ -511,7 +575,8 @@ class FusedRadialMessage(torch.autograd.Function):
                  nat.ptr(h3), nat.ptr(t3), nat.ptr(ctx.w4s), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst),
                  N, E, nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
                  nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
-                 nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr), nat.stream_of(x))
+                 nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr),
+                 nat.ptr(ctx.rows), nat.stream_of(x))
         return (dx, dsh, dr if needs[2] else None, None, None, None, None, None, None, None, None, None)
 
 

@@ -341,6 +341,9 @@ class PureCartesianICTDFix(nn.Module):
         fused = (not second_order and self.number_of_basis == 8
                  and all(fused_supported(inter.fc) for inter in self.interactions))
         radial = None if fused else self.radial_embedding(r)
+        if fused and forces_only and tpo.PAIR_GATES:
+            # an edge and its reverse share one row of radial gates (equal lengths, bitwise)
+            topology.pair_edges(edge_shifts)
         if radial is not None and self.radial_basis_scale != 1.0:
             radial = radial * self.radial_basis_scale
         radial_cfg = (self.max_radius, self.polynomial_cutoff_p, SILU_SCALE)

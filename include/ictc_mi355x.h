@@ -119,12 +119,14 @@ int ictc_morton_order(const float* pos, int64_t rows, float spacing, int32_t* or
  * changes no result bit.  Entries outside [0, nodes) are skipped.  (When the
  * edge arrays are stored receiver-sorted, index order also streams the gate
  * rows sequentially and is the better choice.)  Deterministic: one owner per
- * output row, no floating-point atomics.                                      */
+ * output row, no floating-point atomics.  gate_rows [edges] int32 (NULL =
+ * edge e reads gate row e) maps each edge to the row of `gates` it reads:
+ * the rows shared by an edge and its reverse (ictc_edge_pairs).               */
 int ictc_msg_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                  const float* features, const float* harmonics, const float* gates,
                  const float* weight, const float* mask, const int64_t* src,
                  int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
-                 const int32_t* dst_rows, float* out, void* stream);
+                 const int32_t* dst_rows, float* out, const int32_t* gate_rows, void* stream);
 
 /* First adjoint of ictc_msg_fwd; replaces _first
  * (ops/rematerialized_message.py:25-83 -> generated_adjoint /
@@ -151,7 +153,8 @@ int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
  * dgates * gtangent, formed in registers, so dgates is never written.
  * dfeatures / dharmonics (NULL = skipped) are bitwise those of ictc_msg_bwd.
  * More than 64 channels need ictc_msg_bwd_tangent_workspace_bytes bytes of
- * workspace.  Same reference boundary as ictc_msg_bwd (_first,
+ * workspace.  gates and gtangent rows are read through gate_rows as in
+ * ictc_msg_fwd (dr stays per edge).  Same reference boundary as ictc_msg_bwd (_first,
  * ops/rematerialized_message.py:25-83) composed with the radial adjoint the
  * reference's force autograd runs through `fc` (layers.py:826-835).          */
 int64_t ictc_msg_bwd_tangent_workspace_bytes(int edge_lmax, int channels, int64_t edges);
@@ -162,14 +165,15 @@ int ictc_msg_bwd_tangent(int input_lmax, int edge_lmax, int output_lmax, int cha
                          const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
                          const int32_t* src_rows, const float* grad, const float* gtangent,
                          float* dfeatures, float* dharmonics, float* dr, void* workspace,
-                         int64_t workspace_bytes, void* stream);
+                         int64_t workspace_bytes, const int32_t* gate_rows, void* stream);
 
 /* ---- Fused radial-gate message (energy + forces) ---------------------------
  * Replaces the reference's streamed gate message for frozen-weight force
  * inference (ictc_o3/ops/streamed_gate_message.py:51-57, _StreamedGate
  * :87-223): the gates [E, P*C] = h3 . W4^T are formed per edge tile inside the
  * message kernels from the radial MLP's last hidden activation h3 [E, 64]
- * (ictc_radial_mlp_tangent_fwd) and never materialised.  W4 [P*C, 64] is the
+ * (ictc_radial_mlp_tangent_fwd) and never materialised; h3 and t3 rows are
+ * read through gate_rows as in ictc_msg_fwd (NULL = row e).  W4 [P*C, 64] is the
  * last Linear of `fc` (layers.py:826-835), folded with the TP path weight
  * [P, C] (may be NULL = ones) and split once into the MFMA operand layout
  * (ictc_fused_weight_split, ictc_fused_weight_bytes bytes, 16-byte aligned).
@@ -187,14 +191,35 @@ int ictc_fused_weight_split(const float* W4, const float* tp_weight, int paths, 
 int ictc_msg_fused_fwd(int input_lmax, int edge_lmax, int output_lmax, int channels, const float* features,
                        const float* harmonics, const float* h3, const void* w4split, const float* mask,
                        const int64_t* src, int64_t nodes, int64_t edges, const int32_t* dst_ptr,
-                       const int32_t* dst_order, const int32_t* dst_rows, float* out, void* stream);
+                       const int32_t* dst_order, const int32_t* dst_rows, float* out,
+                       const int32_t* gate_rows, void* stream);
 int ictc_msg_fused_bwd_tangent(int input_lmax, int edge_lmax, int output_lmax, int channels, const float* features,
                                const float* harmonics, const float* h3, const float* t3, const void* w4split,
                                const float* mask, const int64_t* src, const int64_t* dst, int64_t nodes,
                                int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
                                const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
                                const int32_t* src_rows, const float* grad, float* dfeatures, float* dharmonics,
-                               float* dr, void* stream);
+                               float* dr, const int32_t* gate_rows, void* stream);
+
+/* ---- Edge pairs for shared radial gates ------------------------------------
+ * No direct counterpart in the reference, which evaluates the radial MLP
+ * `fc` on every directed edge (layers.py:826-835); the gates depend on the
+ * edge length only, and an edge (s -> d, shift S) and its reverse
+ * (d -> s, shift -S) have bitwise-equal lengths, so they can share one gate
+ * row.  For each edge the reverse is looked up in the receiver CSR of its
+ * source (dst_ptr/dst_order of ictc_csr_build over dst); shifts [E, 3] (NULL
+ * = all zero) are compared exactly.  Writes gate_rows [E] (the row edge e
+ * reads, in 0..count-1), reps [E] (reps[j] = the edge whose gates fill row j,
+ * the first count entries) and count [1] int32 on the device.  An edge with
+ * src < dst (src == dst: shift zero or lexicographically positive) owns a
+ * row; any other edge reads the row of its reverse (the first in CSR order)
+ * or, without one, owns a row; owners are numbered in edge order
+ * (deterministic).  Workspace: ictc_edge_pairs_workspace_bytes(E)
+ * bytes (-1 = 2^30 edges or more).                                         */
+int64_t ictc_edge_pairs_workspace_bytes(int64_t edges);
+int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts, int64_t nodes, int64_t edges,
+                    const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps,
+                    int32_t* count, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Mixed second derivative of ictc_msg_bwd along tangents of its outputs
  * (tfeatures [nodes, C*(LI+1)^2], tharmonics [E, NY], tgates [E, P*C]; NULL =

@@ -136,13 +136,21 @@ def test_fused_and_gemm_entry_points_host_checks():
     assert lib.ictc_fused_weight_bytes(11, 48) < 0
     with pytest.raises(ValueError, match="not compiled"):
         _native.call("ictc_msg_fused_fwd", 2, 3, 3, 64, None, None, None, None, None, None, 10, 10, None, None, None,
-                     None, None)
+                     None, None, None)
     with pytest.raises(ValueError, match="multiple of 64"):
         _native.call("ictc_msg_fused_fwd", 2, 2, 2, 96, None, None, None, None, None, None, 10, 10, None, None, None,
-                     None, None)
+                     None, None, None)
     with pytest.raises(ValueError, match="dr is required"):
         _native.call("ictc_msg_fused_bwd_tangent", 2, 2, 2, 64, None, None, None, None, None, None, None, None, 10,
-                     10, None, None, None, None, None, None, None, None, None, None, None)
+                     10, None, None, None, None, None, None, None, None, None, None, None, None)
+    # edge pairs: a graph without edges writes count 0 without touching operands; E >= 2^30 is refused
+    assert lib.ictc_edge_pairs_workspace_bytes(1 << 30) < 0 and lib.ictc_edge_pairs_workspace_bytes(1000) > 12000
+    with pytest.raises(ValueError, match="negative"):
+        _native.call("ictc_edge_pairs", None, None, None, 4, -1, None, None, None, None, None, None, 0, None)
+    with pytest.raises(ValueError, match="null count"):
+        _native.call("ictc_edge_pairs", None, None, None, 4, 10, None, None, None, None, None, None, 0, None)
+    with pytest.raises(ValueError, match="null operand"):
+        _native.call("ictc_edge_pairs", None, None, None, 4, 10, None, None, None, None, 1, None, 0, None)
     with pytest.raises(ValueError, match="lda >= k"):
         _native.call("ictc_gemm_nt", None, 4, 8, 4, None, 4, 8, None, 4, 0, None)
     with pytest.raises(ValueError, match="pitch"):
