@@ -50,7 +50,7 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # forms: gates shared by each edge and its reverse (2,631,352 gate rows).
 MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 19.81e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
                     ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9,
-                    ("msg_bwd_tan", 131072, 5262704, 64): 53.13e9, ("gates_tan", 131072, 5262704, 64): 15.79e9}
+                    ("msg_bwd_tan", 131072, 5262704, 64): 42.89e9, ("gates_tan", 131072, 5262704, 64): 15.79e9}
 
 
 def log(*a):

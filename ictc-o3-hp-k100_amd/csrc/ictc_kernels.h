@@ -122,6 +122,19 @@ __device__ __forceinline__ void load_row(const float* __restrict__ base, int C, 
   }
 }
 
+// load_row for a row read once: non-temporal loads, so that the streamed row does not displace
+// the rows other waves gather again (the receiver cotangent rows of the source-owned adjoint).
+template <int N>
+__device__ __forceinline__ void load_row_stream(const float* __restrict__ base, int C, int c, float* v) {
+  uint32_t off = (uint32_t)c * 4u;
+  asm volatile("" : "+v"(off));
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    v[i] = __builtin_nontemporal_load(reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + off));
+    base += C;
+  }
+}
+
 template <int N>
 __device__ __forceinline__ void zero_row(float* v) {
 #pragma unroll
@@ -142,9 +155,10 @@ __device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c
 // Gates of edge e for channel c, times the per-path weight (if any) and `scale`.
 // All P gate loads are issued before any use so they are in flight together;
 // the optional weight is a separate uniform branch after them.
-template <class T>
+template <class T, bool STREAM = false>
 __device__ __forceinline__ void load_gw(const Operands& a, int64_t e, int c, float scale, float* gw) {
-  load_row<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * a.channels), a.channels, c, gw);
+  if (STREAM) load_row_stream<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * a.channels), a.channels, c, gw);
+  else load_row<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * a.channels), a.channels, c, gw);
   if (a.weight) {
     float w[T::P];
 #pragma unroll
@@ -355,6 +369,16 @@ __device__ __forceinline__ float lane_f(float v, int i) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
 
+// The forward keeps two edges' feature and gate rows in flight (loads of edge i + 1 issued before
+// edge i's products) where the per-lane state stays small, NX + NY + P + NO <= 64 values with input
+// degree <= 2: every such triple compiles without spills at the table's occupancy (Tp<2,2,2>: 128
+// VGPRs at 4 waves per SIMD, cfg4 layer 1 3.34 -> 3.13 ms), while (3,3,1), (3,1,3), (3,2,2) and the
+// degree-3 triples above spill.
+template <class T>
+constexpr bool msg_fwd_pipelined() {
+  return T::LI <= 2 && T::NX + T::NY + T::P + T::NO <= 64;
+}
+
 template <class T>
 __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::value)) void msg_fwd_kernel(
     Operands a, const int64_t* __restrict__ src, Csr csr, float* __restrict__ out) {
@@ -368,6 +392,45 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
 #pragma unroll
   for (int k = 0; k < T::NO; ++k) o[k] = 0.f;
   const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
+  if constexpr (msg_fwd_pipelined<T>()) {
+    for (int32_t pos = beg; pos < end; pos += kWave) {
+      const int32_t count = min(end - pos, kWave);
+      Chunk<T> ch;
+      stage_chunk<T>(a, src, csr.order, pos, count, ch);
+      float x0[T::NX], g0[T::P], x1[T::NX], g1[T::P];
+      auto fetch = [&](int i, float* xv, float* gr) {
+        const int64_t e = lane_i(ch.e, i), s = lane_i(ch.peer, i);
+        load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
+        load_row<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * C), C, c, gr);
+      };
+      auto consume = [&](int i, const float* xv, const float* gr) {
+        const float m = lane_f(ch.m, i);
+        float y[T::NY], gw[T::P];
+#pragma unroll
+        for (int j = 0; j < T::NY; ++j) y[j] = lane_f(ch.y[j], i);
+#pragma unroll
+        for (int p = 0; p < T::P; ++p) gw[p] = gr[p];
+        if (a.weight) {
+#pragma unroll
+          for (int p = 0; p < T::P; ++p) gw[p] *= a.weight[p * C + c];
+        }
+#pragma unroll
+        for (int p = 0; p < T::P; ++p) gw[p] *= m;
+        T::fwd_b(xv, y, gw, o);
+      };
+      if (!active) continue;
+      fetch(0, x0, g0);
+      for (int i = 0; i < count; i += 2) {
+        if (i + 1 < count) fetch(i + 1, x1, g1);
+        consume(i, x0, g0);
+        if (i + 1 >= count) break;
+        if (i + 2 < count) fetch(i + 2, x0, g0);
+        consume(i + 1, x1, g1);
+      }
+    }
+    if (active) store_row<T::NO>(out + n * (int64_t)(T::NO * C), C, c, o);
+    return;
+  }
   for (int32_t pos = beg; pos < end; pos += kWave) {
     const int32_t count = min(end - pos, kWave);
     Chunk<T> ch;
@@ -582,6 +645,14 @@ constexpr int src_adjoint_waves() {
              : Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value;
 }
 
+// The gate-tangent form keeps two edges' cotangent, gate and gate-tangent rows in flight where it runs
+// at 2 waves per SIMD (up to 256 VGPRs) and the second set of rows is at most 57 values per lane
+// (NO + 2 P): at 60, the (1,3,3) and (3,1,3) triples spill.
+template <class T, bool TAN>
+constexpr bool src_adjoint_pipelined() {
+  return TAN && src_adjoint_waves<T, TAN>() == 2 && T::NO + 2 * T::P <= 57;
+}
+
 // TAN: as in msg_bwd_edge_kernel, dr from gdot in place of the gate gradient.
 template <class T, bool TAN>
 __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd_src_kernel(
@@ -602,6 +673,59 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
   else zero_row<T::NX>(xv);
   zero_row<T::NX>(d);
   const int32_t beg = scsr.ptr[n], end = scsr.ptr[n + 1];
+  if constexpr (src_adjoint_pipelined<T, TAN>()) {
+    // Two edges in flight: the cotangent, gate and gate-tangent rows of edge i + 1 load while edge i
+    // computes (2 waves per SIMD leave room for the second set of rows).  Per-edge arithmetic is that
+    // of the unpipelined form, operand for operand.
+    for (int32_t pos = beg; pos < end; pos += kWave) {
+      const int32_t count = min(end - pos, kWave);
+      Chunk<T> ch;
+      stage_chunk<T>(a, dst, scsr.order, pos, count, ch);
+      float go0[T::NO], gr0[T::P], gt0[T::P], go1[T::NO], gr1[T::P], gt1[T::P];
+      auto fetch = [&](int i, float* go, float* gr, float* gt) {
+        const int64_t e = lane_i(ch.e, i), r = lane_i(ch.peer, i), row = gate_row(a, e);
+        load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
+        load_row_stream<T::P>(a.gates + row * (int64_t)(T::P * C), C, c, gr);
+        load_row_stream<T::P>(gdot + row * (int64_t)(T::P * C), C, c, gt);
+      };
+      auto consume = [&](int i, const float* go, const float* gr, const float* gt) {
+        const int64_t e = lane_i(ch.e, i);
+        const float m = lane_f(ch.m, i);
+        float y[T::NY], dyv[T::NY], gw[T::P], dg[T::P];
+#pragma unroll
+        for (int j = 0; j < T::NY; ++j) {
+          y[j] = lane_f(ch.y[j], i);
+          dyv[j] = 0.f;
+        }
+        float dgt = 0.f;
+        if (active) {
+#pragma unroll
+          for (int p = 0; p < T::P; ++p) gw[p] = gr[p];
+          if (a.weight) {
+#pragma unroll
+            for (int p = 0; p < T::P; ++p) gw[p] *= a.weight[p * C + c];
+          }
+#pragma unroll
+          for (int p = 0; p < T::P; ++p) gw[p] *= m;
+          if (!tail) T::dx(y, gw, go, d);
+          if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
+          else T::dg(xv, y, go, dg);
+          dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, dg);
+        }
+        store_dsh_dr<T::NY>(dsh_g, dr_g, e, dyv, dgt);
+      };
+      if (active) fetch(0, go0, gr0, gt0);
+      for (int i = 0; i < count; i += 2) {
+        if (active && i + 1 < count) fetch(i + 1, go1, gr1, gt1);
+        consume(i, go0, gr0, gt0);
+        if (i + 1 >= count) break;
+        if (active && i + 2 < count) fetch(i + 2, go0, gr0, gt0);
+        consume(i + 1, go1, gr1, gt1);
+      }
+    }
+    if (active && !tail && dx) store_row<T::NX>(dx + n * (int64_t)(T::NX * C), C, c, d);
+    return;
+  }
   // An out-of-range receiver contributes zero (mask 0, row 0 read).
   for (int32_t pos = beg; pos < end; pos += kWave) {
     const int32_t count = min(end - pos, kWave);
@@ -621,8 +745,8 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
       if (TAN && active) {
         float go[T::NO], gw[T::P], gt[T::P], dg[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
-        load_gw<T>(a, e, c, m, gw);
-        load_row<T::P>(gdot + gate_row(a, e) * (int64_t)(T::P * C), C, c, gt);
+        load_gw<T, true>(a, e, c, m, gw);
+        load_row_stream<T::P>(gdot + gate_row(a, e) * (int64_t)(T::P * C), C, c, gt);
         if (!tail) T::dx(y, gw, go, d);
         if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
         else T::dg(xv, y, go, dg);

@@ -151,7 +151,9 @@ int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
  * (ictc_radial_gates_tangent_fwd) and wants the edge-length gradient rather
  * than the gate gradient: dr [E] (required) = sum over paths and channels of
  * dgates * gtangent, formed in registers, so dgates is never written.
- * dfeatures / dharmonics (NULL = skipped) are bitwise those of ictc_msg_bwd.
+ * dfeatures / dharmonics (NULL = skipped) are those of ictc_msg_bwd up to FP32
+ * rounding (the same products, which the two kernels may contract into FMAs
+ * differently).
  * More than 64 channels need ictc_msg_bwd_tangent_workspace_bytes bytes of
  * workspace.  gates and gtangent rows are read through gate_rows as in
  * ictc_msg_fwd (dr stays per edge).  Same reference boundary as ictc_msg_bwd (_first,

@@ -78,9 +78,11 @@ def test_msg_bwd_tangent_matches_gate_gradient(device, N, E, C, li, le, lo, mask
     topo = tpo.Topology(src.to(device), dst.to(device), N)
     dx0, dsh0, dg0 = tpo._msg_bwd_raw(spec, topo, x, sh, g, m, go, (need_x, True, True))
     dx1, dsh1, dr = tpo._msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, m, go, (need_x, True))
-    assert torch.equal(dsh0, dsh1)
+    # the same products as the ordinary adjoint; the two kernels may contract them into FMAs differently
+    # (FP32 rounding: measured at most 7e-8 relative)
+    assert rel_err(dsh1, dsh0) < 1e-6
     if need_x:
-        assert torch.equal(dx0, dx1)
+        assert rel_err(dx1, dx0) < 1e-6
     else:
         assert dx1 is None
     ref = (dg0.double() * gdot.double()).sum(1)
