@@ -16,6 +16,7 @@ from __future__ import annotations
 from typing import Dict, List
 
 import torch
+from torch.autograd.function import once_differentiable
 
 from ictc_o3.ops.radial_mlp import edge_linear
 
@@ -155,27 +156,102 @@ class _PackedLinear(torch.autograd.Function):
         if torch.is_grad_enabled():
             raise RuntimeError("the MFMA linear path is first-order; build the model with second_order=True")
         x, *ws = ctx.saved_tensors
-        lmax, Ci, Co, pin, in_off, out_off, scales, in_cols = ctx.layout
         needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:1] + ctx.needs_input_grad[2:])
         ctx.inputs = None
-        dout = dout if dout.is_contiguous() else dout.contiguous()
-        dx = None
-        if needs[0]:
-            wt = [w.t().contiguous() for w in ws]
-            dx = _packed_call(dout, Co, Ci, lmax, [1] * (lmax + 1), out_off, pin, in_off, wt, scales, in_cols)
-        dws = []
-        N = x.shape[0]
-        for l, (w, need) in enumerate(zip(ws, needs[1:])):
-            if not need:
-                dws.append(None)
-                continue
-            k, m = pin[l], 2 * l + 1
-            xin = x[:, in_off[l]:in_off[l] + k * m * Ci].reshape(N, k, m, Ci).transpose(1, 2).reshape(N * m, k * Ci)
-            dl = dout[:, out_off[l]:out_off[l] + m * Co].reshape(N * m, Co)
-            # dW[o, (k, c)] = sum_{n, m} dl[n, m, o] x[n, k, m, c] on the split-reduction kernel
-            from ictc_o3.ops.radial_mlp import weight_grad
-            dws.append(scales[l] * weight_grad(dl, xin))
+        dx, dws = _packed_adjoint(x, ws, ctx.layout, dout, needs)
         return (dx, None, *dws)
+
+
+def _packed_adjoint(x, ws, layout, dout, needs):
+    """Input adjoint (needs[0]) and weight gradients (needs[1:]) of the packed linear for cotangent dout."""
+    lmax, Ci, Co, pin, in_off, out_off, scales, in_cols = layout
+    dout = dout if dout.is_contiguous() else dout.contiguous()
+    dx = None
+    if needs[0]:
+        wt = [w.t().contiguous() for w in ws]
+        dx = _packed_call(dout, Co, Ci, lmax, [1] * (lmax + 1), out_off, pin, in_off, wt, scales, in_cols)
+    dws = []
+    N = x.shape[0]
+    for l, (w, need) in enumerate(zip(ws, needs[1:])):
+        if not need:
+            dws.append(None)
+            continue
+        k, m = pin[l], 2 * l + 1
+        xin = x[:, in_off[l]:in_off[l] + k * m * Ci].reshape(N, k, m, Ci).transpose(1, 2).reshape(N * m, k * Ci)
+        dl = dout[:, out_off[l]:out_off[l] + m * Co].reshape(N * m, Co)
+        # dW[o, (k, c)] = sum_{n, m} dl[n, m, o] x[n, k, m, c] on the split-reduction kernel
+        from ictc_o3.ops.radial_mlp import weight_grad
+        dws.append(scales[l] * weight_grad(dl, xin))
+    return dx, dws
+
+
+class _LayerEntry(torch.autograd.Function):
+    """(degree linear of h, h[:, :C] as a contiguous [N, C] copy) for first-order callers.
+
+    The scalar columns of a layer's input feed the self connection and the
+    previous layer's energy readout; taken as slices, each slice's backward
+    would zero-fill a full [N, (L+1)^2 C] gradient and autograd would add the
+    full tensors.  Here the backward forms the linear's input adjoint and adds
+    the scalar columns' (small) gradient into its first C columns in place.
+    """
+
+    @staticmethod
+    def forward(ctx, h, layout, C, *weights):
+        lmax, Ci, Co, pin, in_off, out_off, scales, in_cols = layout
+        ctx.layout, ctx.C = layout, C
+        ctx.inputs = (h, *weights)
+        x = h if h.is_contiguous() else h.contiguous()
+        ws = [w.detach().contiguous() for w in weights]
+        ctx.save_for_backward(x, *ws)
+        y = _packed_call(x, Ci, Co, lmax, pin, in_off, [1] * (lmax + 1), out_off, ws, scales, (lmax + 1) ** 2 * Co)
+        return y, x[:, :C].contiguous()
+
+    @staticmethod
+    def backward(ctx, dy, ds):
+        from ictc_o3.autograd import required_gradients
+        if torch.is_grad_enabled():
+            raise RuntimeError("the MFMA linear path is first-order; build the model with second_order=True")
+        x, *ws = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:1] + ctx.needs_input_grad[3:])
+        ctx.inputs = None
+        if dy is None:
+            dy = torch.zeros(x.shape[0], (ctx.layout[0] + 1) ** 2 * ctx.layout[2], dtype=x.dtype, device=x.device)
+        dx, dws = _packed_adjoint(x, ws, ctx.layout, dy, needs)
+        if dx is not None and ds is not None:
+            dx[:, :ctx.C] += ds      # dx is this backward's own fresh tensor
+        return (dx, None, None, *dws)
+
+
+def layer_entry_fast(h, weights, C, lmax):
+    """(degree_linear(h), h[:, :C]) on the MFMA kernel with a fused input adjoint (first derivatives only)."""
+    if not _fast_ok(h, weights, C) or h.shape[1] == C:
+        return None
+    Co = weights[0].shape[0]
+    layout = (lmax, C, Co, [1] * (lmax + 1), [l * l * C for l in range(lmax + 1)],
+              [l * l * Co for l in range(lmax + 1)], [1.0] * (lmax + 1), (lmax + 1) ** 2 * C)
+    return _LayerEntry.apply(h, layout, C, *weights[:lmax + 1])
+
+
+class _AddScalars(torch.autograd.Function):
+    """out[:, :C] += s in place on a fresh tensor no backward saves; the gradient passes through without
+    the full-size clone an in-place slice update records (first-order callers)."""
+
+    @staticmethod
+    def forward(ctx, out, s):
+        C = s.shape[1]
+        out[:, :C] += s
+        ctx.mark_dirty(out)
+        ctx.C = C
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, g):
+        return g, (None if g is None else g[:, :ctx.C].contiguous())
+
+
+def add_scalars_(out, s):
+    return _AddScalars.apply(out, s)
 
 
 def _fast_ok(x, weights, C):

@@ -164,13 +164,23 @@ class Interaction(nn.Module):
             self._spec = tpo.make_spec(self.input_lmax, self.lmax, self.lmax, self.channels, None)
         return self._spec
 
+    def entry(self, h):
+        """(linear_up(h), h[:, :C]) from one first-order op whose adjoint merges both gradients, or None
+        where the input has only scalar columns or the MFMA linear does not apply."""
+        from ictc_o3.ops.linear import layer_entry_fast
+        a = self.linear_up
+        return layer_entry_fast(h, [a.adapters[str(l)].weight for l in range(a.lmax + 1)], self.channels, a.lmax)
+
     def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None, forces_only=False,
-                basis_scale=1.0):
+                basis_scale=1.0, entry=None):
         """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path;
-        basis_scale multiplies the radial basis there)."""
+        basis_scale multiplies the radial basis there).  entry: (linear_up(h), h[:, :C]) from entry()."""
         C = self.channels
         first_order = radial is None
-        x = self.linear_up(h, first_order)
+        if entry is not None:
+            x, h0 = entry
+        else:
+            x, h0 = self.linear_up(h, first_order), h[:, :C]
         if radial is None and forces_only:
             m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg, basis_scale)
         else:
@@ -182,7 +192,7 @@ class Interaction(nn.Module):
                 gates = radial_mlp(radial, self.fc)
             m = tpo.message(x, Y, gates, self.spec(), topo, mask)
         message = self.message_linear(m, 1.0 / max(self.avg_num_neighbors, 1e-8), first_order)
-        sc = self.self_connection.forward_l0(h[:, :C], species)
+        sc = self.self_connection.forward_l0(h0, species)
         return message, sc
 
 
@@ -201,6 +211,9 @@ class Product(nn.Module):
         if out.shape[1] == C:
             return out + sc
         # in place on the linear's fresh output (no backward saves it): no concatenation copy
+        if first_order:
+            from ictc_o3.ops.linear import add_scalars_
+            return add_scalars_(out, sc)
         out[:, :C] += sc
         return out
 
@@ -350,12 +363,14 @@ class PureCartesianICTDFix(nn.Module):
         h = species_rows(self.node_embedding.weight.t(), species)
         energy = None
         for i, (inter, prod) in enumerate(zip(self.interactions, self.products)):
+            # first-order route: the scalar columns come out of the next layer's entry op (one merged
+            # adjoint instead of slice gradients), so layer i - 1's energy readout is taken here, in order
+            entry = inter.entry(h) if radial is None else None
+            if i > 0:
+                e = self.layer_energy_readouts[i - 1](entry[1] if entry is not None else h[:, :self.channels])
+                energy = e if energy is None else energy + e
             message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only,
-                                self.radial_basis_scale)
+                                self.radial_basis_scale, entry=entry)
             h = prod(message, sc, species, first_order=radial is None)
-            if i < self.num_interaction - 1:
-                e = self.layer_energy_readouts[i](h[:, :self.channels])
-            else:
-                e = self.last_layer_energy_readout(h[:, :self.channels])
-            energy = e if energy is None else energy + e
-        return energy
+        e = self.last_layer_energy_readout(h if h.shape[1] == self.channels else h[:, :self.channels])
+        return e if energy is None else energy + e
