@@ -11,7 +11,7 @@
 // A degree block is a GEMM of (N rows per component m) x (paths_in * Cin) by
 // (paths_in * Cin) x (paths_out * Cout).  A wave computes 16 nodes x 64
 // output columns of one component; the block's 4 waves share the weight
-// panel (64 output columns x 64 k) staged in LDS per k-chunk.  Operand k
+// panel (64 output columns x K) staged in LDS, whole or per k-chunk.  Operand k
 // order (consistent for A and B, which is all the MFMA needs): at k-step j,
 // lane group g = l/16 supplies k = 16 g + j of the chunk, so each lane reads
 // 16 contiguous floats of its row (four 16-byte loads).
@@ -45,10 +45,17 @@ __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// WHOLE: the block's whole weight panel (64 output columns x K, K <= kWholeK) is staged in LDS once,
+// and the block loops over 64-node tiles (grid.x persistent blocks); otherwise the panel is staged
+// per 64-wide k-chunk.  MFMA operands: A = weights (M = 16 output columns), B = inputs (N = 16 nodes),
+// so each lane ends with 4 consecutive output columns of one node and stores them as one 16-byte write.
+constexpr int kWholeK = 256;
+
+template <bool WHOLE>
 __global__ __launch_bounds__(256) void packed_linear_kernel(const float* __restrict__ in, int64_t in_stride,
                                                             float* __restrict__ out, int64_t out_stride, int Ci,
-                                                            int Co, int64_t N, LinearDesc d) {
-  __shared__ float panel[64 * kPanel];
+                                                            int Co, int64_t N, LinearDesc d, int64_t node_blocks) {
+  extern __shared__ float panel[];
   // blockIdx.y enumerates the (degree, component) pairs in order.
   int l = 0, m = blockIdx.y;
   while (m >= 2 * l + 1) {
@@ -62,62 +69,72 @@ __global__ __launch_bounds__(256) void packed_linear_kernel(const float* __restr
   const float* __restrict__ W = d.w[l];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = lane & 15, g = lane >> 4;
-  const int64_t n0 = ((int64_t)blockIdx.x * 4 + wave) * 16;
-  const int64_t n = n0 + i;
-  v4f acc[4];
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int kc = 0; kc < K; kc += 64) {
-    // Stage W[col0 .. col0+64) x [kc .. kc+64) (zero outside).
-    __syncthreads();
-    for (int t = threadIdx.x; t < 64 * 16; t += 256) {
-      const int r = t >> 4, q = t & 15;
+  const int Kr = (K + 63) / 64 * 64;  // K rounded to the k-chunk; the panel is zero past K
+  const int pitch = WHOLE ? Kr + 4 : kPanel;
+  auto stage = [&](int kc, int kn) {  // W[col0 .. col0+64) x [kc .. kc+kn) -> panel[r][k - kc] (zero outside)
+    const int q4 = kn / 4;
+    for (int t = threadIdx.x; t < 64 * q4; t += 256) {
+      const int r = t / q4, q = t % q4;
       const int col = col0 + r, k = kc + 4 * q;
       float4 v = {0.f, 0.f, 0.f, 0.f};
       if (col < ncols && k < K) v = *reinterpret_cast<const float4*>(W + (int64_t)col * K + k);
-      *reinterpret_cast<float4*>(panel + r * kPanel + 4 * q) = v;
+      *reinterpret_cast<float4*>(panel + r * pitch + 4 * q) = v;
     }
+  };
+  if (WHOLE) {
+    stage(0, Kr);
     __syncthreads();
-    // A: node n, k = kc + 16 g + j (16 contiguous channels of one input path).
-    float a[16];
-    const int k0 = kc + 16 * g;
-    if (n < N && k0 < K) {
-      const int p = k0 / Ci, c = k0 % Ci;
-      const float* src = in + n * in_stride + d.in_off[l] + ((int64_t)p * w + m) * Ci + c;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
-        a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) a[j] = 0.f;
-    }
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      float b[16];
-      const float* row = panel + (16 * cb + i) * kPanel + 16 * g;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float4 v = *reinterpret_cast<const float4*>(row + 4 * q);
-        b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
-      }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) acc[cb] = mfma(a[j], b[j], acc[cb]);
-    }
   }
-  // D: lane holds output column col0 + 16 cb + i for nodes n0 + 4 g + r.
   const float s = d.scale[l];
+  for (int64_t nb = blockIdx.x; nb < node_blocks; nb += gridDim.x) {
+    const int64_t n0 = (nb * 4 + wave) * 16;
+    const int64_t n = n0 + i;
+    v4f acc[4];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
-    const int col = col0 + 16 * cb + i;
-    if (col >= ncols) continue;
-    const int p = col / Co, c = col % Co;
-    float* dst = out + d.out_off[l] + ((int64_t)p * w + m) * Co + c;
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int kc = 0; kc < K; kc += 64) {
+      if (!WHOLE) {
+        __syncthreads();
+        stage(kc, 64);
+        __syncthreads();
+      }
+      // B: node n, k = kc + 16 g + j (16 contiguous channels of one input path).
+      float a[16];
+      const int k0 = kc + 16 * g;
+      if (n < N && k0 < K) {
+        const int p = k0 / Ci, c = k0 % Ci;
+        const float* src = in + n * in_stride + d.in_off[l] + ((int64_t)p * w + m) * Ci + c;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t nn = n0 + 4 * g + r;
-      if (nn < N) dst[nn * out_stride] = s * acc[cb][r];
+        for (int q = 0; q < 4; ++q) {
+          const float4 v = *reinterpret_cast<const float4*>(src + 4 * q);
+          a[4 * q] = v.x, a[4 * q + 1] = v.y, a[4 * q + 2] = v.z, a[4 * q + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) a[j] = 0.f;
+      }
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        float b[16];
+        const float* row = panel + (16 * cb + i) * pitch + (WHOLE ? kc : 0) + 16 * g;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 v = *reinterpret_cast<const float4*>(row + 4 * q);
+          b[4 * q] = v.x, b[4 * q + 1] = v.y, b[4 * q + 2] = v.z, b[4 * q + 3] = v.w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[cb] = mfma(b[j], a[j], acc[cb]);
+      }
+    }
+    // D: lane holds output columns col0 + 16 cb + 4 g .. + 3 of node n0 + i.
+    if (n < N) {
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const int col = col0 + 16 * cb + 4 * g;
+        if (col >= ncols) continue;
+        const int p = col / Co, c = col % Co;
+        *reinterpret_cast<v4f*>(out + n * out_stride + d.out_off[l] + ((int64_t)p * w + m) * Co + c) = s * acc[cb];
+      }
     }
   }
 }
@@ -144,7 +161,8 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
   d.lmax = lmax;
   int maxcols = 0;
   for (int l = 0; l <= lmax; ++l) {
-    if (in_paths[l] < 1 || out_paths[l] < 1 || in_offsets[l] % 4 || out_offsets[l] < 0 || in_offsets[l] < 0)
+    if (in_paths[l] < 1 || out_paths[l] < 1 || in_offsets[l] % 4 || out_offsets[l] % 4 || out_offsets[l] < 0 ||
+        in_offsets[l] < 0)
       return fail(ICTC_ERR_ARGUMENT, "packed linear: bad path counts or offsets");
     if (!weights[l]) return fail(ICTC_ERR_ARGUMENT, "packed linear: null weight");
     d.w[l] = weights[l];
@@ -157,9 +175,29 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
   }
   if (nodes == 0) return ICTC_OK;
   if (!in || !out) return fail(ICTC_ERR_ARGUMENT, "packed linear: null operand");
-  const dim3 grid((unsigned)((nodes + 63) / 64), (lmax + 1) * (lmax + 1), (maxcols + 63) / 64);
-  hipLaunchKernelGGL(packed_linear_kernel, grid, dim3(256), 0, (hipStream_t)stream, in, in_stride, out, out_stride,
-                     channels_in, channels_out, nodes, d);
+  int maxk = 0;  // largest K, rounded to the 64-wide k-chunk
+  for (int l = 0; l <= lmax; ++l) {
+    const int kr = (in_paths[l] * channels_in + 63) / 64 * 64;
+    maxk = kr > maxk ? kr : maxk;
+  }
+  const int64_t node_blocks = (nodes + 63) / 64;
+  const unsigned gy = (unsigned)((lmax + 1) * (lmax + 1)), gz = (unsigned)((maxcols + 63) / 64);
+  if (maxk <= kWholeK) {
+    // persistent blocks: about 8 per CU over all (component, column block) pairs
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                 hipSuccess || cus <= 0)
+      cus = 256;
+    int64_t gx = (int64_t)8 * cus / (gy * gz);
+    gx = gx < 1 ? 1 : (gx > node_blocks ? node_blocks : gx);
+    const size_t lds = (size_t)64 * (maxk + 4) * sizeof(float);
+    hipLaunchKernelGGL(packed_linear_kernel<true>, dim3((unsigned)gx, gy, gz), dim3(256), lds, (hipStream_t)stream, in,
+                       in_stride, out, out_stride, channels_in, channels_out, nodes, d, node_blocks);
+  } else {
+    hipLaunchKernelGGL(packed_linear_kernel<false>, dim3((unsigned)node_blocks, gy, gz), dim3(256),
+                       (size_t)64 * kPanel * sizeof(float), (hipStream_t)stream, in, in_stride, out, out_stride,
+                       channels_in, channels_out, nodes, d, node_blocks);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char buf[256];
