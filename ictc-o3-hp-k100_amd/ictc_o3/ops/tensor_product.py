@@ -292,7 +292,8 @@ class Topology:
         The reverse of (s -> d, shift S) is an edge (d -> s, shift -S); shifts
         [E, 3] are compared exactly (None = no periodic images).  Computed once
         per live shifts tensor and version (one host sync for the row count).
-        Where no edge has a reverse the rows stay per edge (gate_rows None).
+        Where no edge has a reverse, or the graph is past the pairing's index range (2^30 edges), the rows
+        stay per edge (gate_rows None).
         """
         key = None if shifts is None else (shifts._version, tuple(shifts.shape))
         seen = self._pairs_of
@@ -301,7 +302,9 @@ class Topology:
             return
         E = self.src.numel()
         self.gate_rows = self.gate_reps = None
-        if E > 0:
+        ws_bytes = int(nat.lib().ictc_edge_pairs_workspace_bytes(E))
+        # pairing is an optimisation: graphs past its index range keep one gate row per edge
+        if E > 0 and ws_bytes >= 0 and self.nodes < (1 << 31) - 2:
             sh = None if shifts is None else _c(shifts.detach().to(torch.float32))
             if sh is not None and tuple(sh.shape) != (E, 3):
                 raise ValueError("edge shifts must be [E, 3]")
@@ -309,9 +312,6 @@ class Topology:
             rows = torch.empty(E, dtype=torch.int32, device=dev)
             reps = torch.empty(E, dtype=torch.int32, device=dev)
             count = torch.empty(1, dtype=torch.int32, device=dev)
-            ws_bytes = int(nat.lib().ictc_edge_pairs_workspace_bytes(E))
-            if ws_bytes < 0:
-                raise ValueError("too many edges to pair (2^30 or more)")
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
             nat.call("ictc_edge_pairs", nat.ptr(self.src), nat.ptr(self.dst), nat.ptr(sh), self.nodes, E,
                      nat.ptr(self.by_dst.ptr), nat.ptr(self.by_dst.order), nat.ptr(rows), nat.ptr(reps),
@@ -324,7 +324,6 @@ class Topology:
     def gate_input(self, r: torch.Tensor) -> torch.Tensor:
         """The edge lengths of the gate rows (r itself when the rows are per edge)."""
         return r if self.gate_reps is None else r.index_select(0, self.gate_reps)
-
 
     @property
     def by_src(self):
