@@ -97,6 +97,24 @@ __global__ void csr_ptr_kernel(const int32_t* __restrict__ sorted, int64_t E, in
   ptr[n] = (int32_t)lo;
 }
 
+// ptr of keys that are already sorted (non-decreasing, all in [0, N)): ptr[n] = first position with key >= n
+// for n in [0, N]; ptr[N+1] = E.
+__global__ void csr_ptr_sorted_kernel(const int64_t* __restrict__ keys, int64_t E, int64_t N, int32_t* __restrict__ ptr) {
+  const int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (n > N + 1) return;
+  if (n == N + 1) {
+    ptr[n] = (int32_t)E;
+    return;
+  }
+  int64_t lo = 0, hi = E;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (keys[mid] < n) lo = mid + 1;
+    else hi = mid;
+  }
+  ptr[n] = (int32_t)lo;
+}
+
 int key_bits(int64_t N) {
   int bits = 1;
   while (bits < 31 && (int64_t(1) << bits) <= N) ++bits;
@@ -278,7 +296,13 @@ int ictc_csr_build(const int64_t* keys, int64_t E, int64_t N, int32_t* ptr, int3
     hipLaunchKernelGGL(fill_zero_i32_kernel, dim3((unsigned)((N + 2 + 255) / 256)), dim3(256), 0, st, ptr, N + 2);
     return check_hip(hipGetLastError(), "csr fill");
   }
-  if (!keys || !order || !workspace) return fail(ICTC_ERR_ARGUMENT, "csr: null operand");
+  if (!keys) return fail(ICTC_ERR_ARGUMENT, "csr: null keys");
+  if (!order) {   // the caller's keys are already sorted and in range: the order is the identity
+    hipLaunchKernelGGL(csr_ptr_sorted_kernel, dim3((unsigned)((N + 2 + 255) / 256)), dim3(256), 0, st, keys, E, N,
+                       ptr);
+    return check_hip(hipGetLastError(), "csr ptr (sorted keys)");
+  }
+  if (!workspace) return fail(ICTC_ERR_ARGUMENT, "csr: null workspace");
   const int64_t need = ictc_csr_workspace_bytes(E, N);
   if (workspace_bytes < need)
     return fail(ICTC_ERR_ARGUMENT, "csr: workspace of %lld bytes, need %lld", (long long)workspace_bytes,

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
   const int lane = threadIdx.x & 63;
   float acc[3] = {0.f, 0.f, 0.f}, t[3];
   for (int32_t k = dptr[i] + lane; k < dptr[i + 1]; k += 64) {
-    const int64_t e = dord[k];
+    const int64_t e = dord ? dord[k] : k;   // dord == nullptr: edges already receiver-sorted
     edge_cotangent<VEC>(r, n, dr, dn, e, t);
 #pragma unroll
     for (int c = 0; c < 3; ++c) acc[c] += t[c];
@@ -160,7 +160,7 @@ int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, cons
                            const int32_t* src_order, float* dshift, float* dpos, void* stream) {
   if (nodes < 0 || edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge geometry: negative size");
   if (nodes == 0) return ICTC_OK;
-  if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!r || !n || !dst_order || !src_order)))
+  if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!r || !n || !src_order)))
     return fail(ICTC_ERR_ARGUMENT, "edge geometry adjoint: null operand");
   hipLaunchKernelGGL(geometry_bwd_kernel<false>, dim3((unsigned)((nodes + kBlock / 64 - 1) / (kBlock / 64))), dim3(kBlock), 0,
                      (hipStream_t)stream, r, n, dr, dn, nodes, dst_ptr, dst_order, src_ptr, src_order, dshift, dpos);
@@ -172,7 +172,7 @@ int ictc_edge_vector_bwd(const float* dvec, int64_t nodes, int64_t edges, const 
                          void* stream) {
   if (nodes < 0 || edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge vector adjoint: negative size");
   if (nodes == 0) return ICTC_OK;
-  if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!dvec || !dst_order || !src_order)))
+  if (!dpos || !dst_ptr || !src_ptr || (edges > 0 && (!dvec || !src_order)))
     return fail(ICTC_ERR_ARGUMENT, "edge vector adjoint: null operand");
   hipLaunchKernelGGL(geometry_bwd_kernel<true>, dim3((unsigned)((nodes + kBlock / 64 - 1) / (kBlock / 64))),
                      dim3(kBlock), 0, (hipStream_t)stream, nullptr, nullptr, nullptr, dvec, nodes, dst_ptr, dst_order,

@@ -214,12 +214,21 @@ class EdgeTPAdjoint(torch.autograd.Function):
 
 
 class Csr:
-    """Stable key-sorted CSR of an edge list (int32 ptr [N+2] and order [E])."""
+    """Stable key-sorted CSR of an edge list (int32 ptr [N+2] and order [E]).
 
-    def __init__(self, keys: torch.Tensor, nodes: int):
+    presorted=True: the keys are known to be in non-decreasing order and in
+    range (a receiver-sorted neighbour list); only ptr is built and order is
+    None (the identity)."""
+
+    def __init__(self, keys: torch.Tensor, nodes: int, presorted: bool = False):
         E = keys.numel()
         self.nodes = nodes
         self.ptr = torch.empty(nodes + 2, dtype=torch.int32, device=keys.device)
+        if presorted:
+            self.order = None
+            nat.call("ictc_csr_build", nat.ptr(keys), E, nodes, nat.ptr(self.ptr), None, None, 0,
+                     nat.stream_of(keys))
+            return
         self.order = torch.empty(max(E, 1), dtype=torch.int32, device=keys.device)
         ws_bytes = int(nat.lib().ictc_csr_workspace_bytes(E, nodes))
         if ws_bytes < 0:
@@ -257,6 +266,18 @@ def _index_order_scattered(positions: torch.Tensor, rows: torch.Tensor) -> bool:
     return bool(step_index > 2.0 * step_rows)
 
 
+def mark_receiver_sorted(dst: torch.Tensor, nodes: int) -> torch.Tensor:
+    """Record that `dst` (as it is now) is in non-decreasing order with every id in [0, nodes): a Topology
+    over it skips the receiver sort.  For edge lists built sorted (the neighbour list); an in-place change
+    of `dst` (a new version) or another node count clears the mark."""
+    dst._ictc_receiver_sorted = (dst._version, int(nodes))
+    return dst
+
+
+def receiver_sorted(dst: torch.Tensor, nodes: int) -> bool:
+    return getattr(dst, "_ictc_receiver_sorted", None) == (dst._version, int(nodes))
+
+
 class Topology:
     """Receiver-sorted CSR (forward, gate / harmonic adjoints) and source-sorted CSR (feature adjoint).
 
@@ -276,7 +297,7 @@ class Topology:
     def __init__(self, src: torch.Tensor, dst: torch.Tensor, nodes: int, positions: torch.Tensor | None = None,
                  spacing: float = 2.0):
         self.src, self.dst, self.nodes = _c(src), _c(dst), nodes
-        self.by_dst = Csr(self.dst, nodes)
+        self.by_dst = Csr(self.dst, nodes, presorted=receiver_sorted(self.dst, nodes))
         self._by_src = None
         self.dst_rows = None
         self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None

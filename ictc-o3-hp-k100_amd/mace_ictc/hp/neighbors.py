@@ -48,6 +48,8 @@ def _cell_list_hip(pos, cell_cpu, cutoff, ncell):
     if E:
         nat.call("ictc_neighbors_fill", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
                  nat.ptr(src), nat.ptr(dst), nat.ptr(shifts), stream)
+    from ictc_o3.ops.tensor_product import mark_receiver_sorted
+    mark_receiver_sorted(dst, N)    # emitted receiver by receiver, ids in [0, N): Topology skips the sort
     return src, dst, shifts
 
 

@@ -91,7 +91,11 @@ int ictc_tp_second(int input_lmax, int edge_lmax, int output_lmax, int channels,
  *   ptr   [nodes + 2] int32: edges of node n are order[ptr[n] .. ptr[n+1]);
  *         ptr[nodes] .. ptr[nodes+1] holds edges whose key is out of range;
  *   order [E] int32, a stable sort of edge ids by key.
- * workspace must hold ictc_csr_workspace_bytes(edges, nodes) bytes.            */
+ * workspace must hold ictc_csr_workspace_bytes(edges, nodes) bytes.  order
+ * NULL: the caller guarantees keys already in non-decreasing order with every
+ * key in [0, nodes) (a receiver-sorted edge list, e.g. the neighbour list's);
+ * only ptr is built, the order is the identity (pass NULL as dst_order), and
+ * workspace may be NULL.                                                       */
 int64_t ictc_csr_workspace_bytes(int64_t edges, int64_t nodes);
 int ictc_csr_build(const int64_t* keys, int64_t edges, int64_t nodes, int32_t* ptr,
                    int32_t* order, void* workspace, int64_t workspace_bytes, void* stream);
@@ -373,7 +377,7 @@ int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, dou
  * The adjoint takes dr [E] and dn [E,3] (either may be NULL = zero) and writes
  * dpos [N,3] = sum over incoming edges - sum over outgoing edges of d vec, as
  * a gather over the receiver- and source-sorted CSRs (ictc_csr_build over dst
- * and over src), in CSR order: deterministic, no atomics.  dshift [E,3] (may
+ * and over src; dst_order NULL = edges already receiver-sorted), in CSR order: deterministic, no atomics.  dshift [E,3] (may
  * be NULL) receives d vec per edge.  Every src/dst id must lie in [0, N).     */
 int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* src, const int64_t* dst,
                            int64_t nodes, int64_t edges, float cutoff, float* r, float* n, float* mask,

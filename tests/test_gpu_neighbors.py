@@ -47,3 +47,33 @@ def test_triclinic_against_brute_force(device):
         for a, b in torch.nonzero((r2 < 4.2 ** 2) & (r2 > 1e-20)).tolist():
             want.add((b, dst, tuple(int(x) for x in imgs[a].tolist())))
     assert got == want
+
+
+def test_receiver_sorted_mark_skips_sort(device):
+    """The neighbour list marks its dst as receiver-sorted: Topology then builds only the receiver CSR
+    pointers (order = identity), equal to the sorted build; an in-place change of dst clears the mark."""
+    from ictc_o3.ops import tensor_product as tpo
+    from mace_ictc.hp.neighbors import radius_graph_pbc
+    pos, cell = _fcc(6, 3.42, 0.3, 4)
+    s, d, _ = radius_graph_pbc(pos.to(device), cell.to(device), 4.5)
+    N = pos.shape[0]
+    assert tpo.receiver_sorted(d, N) and not tpo.receiver_sorted(d, N + 1)
+    fast = tpo.Topology(s, d, N)
+    assert fast.by_dst.order is None
+    full = tpo.Csr(d, N)
+    assert torch.equal(fast.by_dst.ptr, full.ptr)
+    assert torch.equal(full.order[:d.numel()].long().cpu(), torch.arange(d.numel()))
+    # the position adjoint of the edge geometry through the identity order is bitwise the sorted CSR's
+    from ictc_o3.ops.geometry import edge_geometry
+    slow = tpo.Topology(s, d.clone(), N)
+    assert slow.by_dst.order is not None
+    grads = []
+    for topo in (fast, slow):
+        p = pos.to(device).requires_grad_(True)
+        r, n, _ = edge_geometry(p, None, topo, 4.5)
+        (r.sum() + (n * n.flip(0)).sum()).backward()
+        grads.append(p.grad)
+    assert torch.equal(grads[0], grads[1])
+    d.add_(0)
+    assert not tpo.receiver_sorted(d, N)
+    assert tpo.Topology(s, d, N).by_dst.order is not None
