@@ -21,8 +21,11 @@ message forward, gate-tangent message adjoint) are timed live with HIP events
 on the stream they run on (torch's current stream), averaged over repeated
 launches; the one with the largest time is the roofline kernel: its
 algorithmic bytes (compulsory traffic: each operand read once, each output
-written once, index arrays included, gathers not counted) / time vs 8 TB/s.
-``roofline_kernels`` lists all of them.
+written once, index arrays included, gathers not counted; the message kernels
+counted per edge with one gate row each, the gate kernel per computed row) /
+time vs 8 TB/s.  ``frac_shared_gate_rows`` is the same time against the
+message kernels' bytes with each gate row shared by an edge and its reverse
+counted once.  ``roofline_kernels`` lists all of them.
 
 CPU baseline: the FP32 torch-eager restatement of the reference path
 (oracle/: gather, per-path CG einsum, gate, index_add, SC recursion, linears,
@@ -315,12 +318,14 @@ def run_cfg4(args):
     # gate-tangent adjoint); the other adjoint forms are timed for reference only
     in_step = [k for k in ("gates_tan", "msg_fwd", "msg_bwd_tan") if k in kern]
     dom = max(in_step, key=kern.get)   # the step's kernel with the largest time
-    achieved = nbytes[dom] / kern[dom] / 1e9
-    # the same kernels' bytes counted with one gate row per edge (the accounting of an edge list without
-    # shared gate rows), for comparison only: `achieved` counts each shared row once
-    M = 11 * 64
-    per_edge = message_bytes(N, E, 64, 9, 9, 11, 35)
-    per_edge["gates_tan"] = E * 4 + 2 * E * M * 4
+    # Algorithmic bytes per the per-unit figure of the message kernels: per edge, its gate row
+    # (P*C*4 B), harmonics, ids and mask, plus the node rows once (an edge list with one gate row per
+    # edge, the layout the reference's message kernels read).  The step shares each gate row between
+    # an edge and its reverse; `frac_shared_gate_rows` counts each of the G shared rows once instead.
+    # The gate kernel computes and writes G rows, so its unit is the shared row either way.
+    per_unit = message_bytes(N, E, 64, 9, 9, 11, 35)
+    per_unit["gates_tan"] = nbytes["gates_tan"]
+    achieved = per_unit[dom] / kern[dom] / 1e9
     result = {
         "metric": METRIC,
         "value": N / dt, "unit": "atom-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -336,13 +341,15 @@ def run_cfg4(args):
         "roofline": {"bound": "hbm", "kernel": f"{dom} (layer 1, P11 C64)", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": MEASURED_TRAFFIC.get((dom, N, E, 64)),
-                     "frac_one_gate_row_per_edge": per_edge[dom] / kern[dom] / 1e9 / HBM_PEAK_GBS},
+                     "algorithmic_GB": round(per_unit[dom] / 1e9, 3),
+                     "frac_shared_gate_rows": nbytes[dom] / kern[dom] / 1e9 / HBM_PEAK_GBS},
         # every layer-1 kernel of the step, largest first (the first is the roofline kernel above)
         "roofline_kernels": [{"kernel": k, "time_us": round(kern[k] * 1e6, 1),
-                              "algorithmic_GB": round(nbytes[k] / 1e9, 3),
-                              "achieved": nbytes[k] / kern[k] / 1e9, "frac": nbytes[k] / kern[k] / 1e9 / HBM_PEAK_GBS,
+                              "algorithmic_GB": round(per_unit[k] / 1e9, 3),
+                              "achieved": per_unit[k] / kern[k] / 1e9,
+                              "frac": per_unit[k] / kern[k] / 1e9 / HBM_PEAK_GBS,
                               "traffic": MEASURED_TRAFFIC.get((k, N, E, 64)),
-                              "frac_one_gate_row_per_edge": per_edge[k] / kern[k] / 1e9 / HBM_PEAK_GBS}
+                              "frac_shared_gate_rows": nbytes[k] / kern[k] / 1e9 / HBM_PEAK_GBS}
                              for k in sorted(in_step, key=kern.get, reverse=True)],
     }
     return result, model
