@@ -464,6 +464,285 @@ __global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_bwd_rcv_k
   }
 }
 
+// ---------------------------------------------------------------------------
+// Input degree 0 (paths (0, l, l), the model's first layer): the tensor product
+// is an outer product per edge, y[d, (l, m), c] = sum_e Y_lm(e) m_e x_s[c] g_e[l, c]
+// (times the path's CG constant), so both passes are GEMMs over an edge tile
+// on FP32 MFMA (v_mfma_f32_16x16x4f32) after the split-bf16 gate projection:
+//   forward   Out[lm][c]  += sum_e  A[lm][e] P_l[e][c],  A = Y m coef, P_l = x g_l
+//   adjoint   Q_l[e][lm]   = sum_c  P_l[e][c] go[lm][c]     (dsh = Q_l(lm), mask in P)
+//             R_l[e][lm]   = sum_c  x gdot_l[e][c] go[lm][c] (dr = sum_lm Y_lm R_l(lm))
+// The forward's projection result D[edge][channel] (lane (q, j): edges 4q + r,
+// channel j) is directly the B operand of four 16x16x4 steps (k = q, edge
+// 4q + r in step r); the adjoint projects transposed (W4 slice as the A
+// operand, h3 as B), so D[channel][edge] (lane (q, i): channels 4q + r, edge
+// i) is directly its A operand.  No lane transposes and no per-edge
+// reductions over the 64 channels: the channel sum is the MFMA's reduction.
+// ---------------------------------------------------------------------------
+// 16-edge projection tiles per LDS read of a W4 slice.  Two (12 waves per CU, 168 VGPRs) measured
+// 1.47 ms against 1.07 ms for one (16 waves) at the cfg4 layer-0 shape: ~40 edges per receiver fill
+// 63 % of two 32-edge tiles against 83 % of three 16-edge tiles, and fewer waves hide less latency.
+constexpr int kS0FwdTiles = 1;
+constexpr int kS0FwdWaves = kS0FwdTiles == 1 ? 16 : 12;
+constexpr int kS0BwdWaves = 12;  // 167 VGPRs: 3 waves per SIMD, one block per CU
+
+__device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int degree_of(int k) { return k < 1 ? 0 : k < 4 ? 1 : k < 9 ? 2 : 3; }
+
+// CG constant of output component i of a degree-0-input group (one-hot harmonic, unit gate, x = 1).
+template <class TG>
+__device__ __forceinline__ float s0_coef(int i) {
+  float x[1] = {1.f}, y[TG::NY], gw[TG::PG], o[TG::NOG];
+#pragma unroll
+  for (int k = 0; k < TG::NY; ++k) y[k] = k == i ? 1.f : 0.f;
+#pragma unroll
+  for (int p = 0; p < TG::PG; ++p) gw[p] = 1.f;
+#pragma unroll
+  for (int k = 0; k < TG::NOG; ++k) o[k] = 0.f;
+  TG::fwd_b(x, y, gw, o);
+  float c = 0.f;
+#pragma unroll
+  for (int k = 0; k < TG::NOG; ++k) c = k == i ? o[k] : c;
+  return c;
+}
+
+// The six split-bf16 W4 operands of one (path, 16-channel block), from LDS.
+struct SliceOps {
+  bf16x8 h0, m0, l0, h1, m1, l1;
+};
+__device__ __forceinline__ SliceOps slice_ops(const bf16x8* __restrict__ w4l, int p, int cb) {
+  const bf16x8* b = w4l + (p * 4 + cb) * 2 * 3 * 64 + lane_id();
+  return {b[0], b[64], b[128], b[192], b[256], b[320]};
+}
+
+// Split-bf16 projection of one (path, 16-channel block) for a 16-row tile.
+// TRANS = false: D[row][channel] (A = rows, B = W4 slice); true: D[channel][row].
+template <bool TRANS>
+__device__ __forceinline__ v4f project_block(const SliceOps& w, const Split* A) {
+  v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
+  auto mm = [&](bf16x8 a, bf16x8 b) { acc = TRANS ? mfma_bf16(b, a, acc) : mfma_bf16(a, b, acc); };
+  mm(A[0].lo, w.h0);
+  mm(A[0].hi, w.l0);
+  mm(A[0].mid, w.m0);
+  mm(A[1].lo, w.h1);
+  mm(A[1].hi, w.l1);
+  mm(A[1].mid, w.m1);
+  mm(A[0].mid, w.h0);
+  mm(A[0].hi, w.m0);
+  mm(A[1].mid, w.h1);
+  mm(A[1].hi, w.m1);
+  mm(A[0].hi, w.h0);
+  mm(A[1].hi, w.h1);
+  return acc;
+}
+
+// Edge id, sender and mask of up to 64 consecutive CSR positions, one edge per lane.
+struct S0Chunk {
+  int32_t e, s;
+  float m;
+};
+__device__ __forceinline__ S0Chunk s0_stage(const FusedArgs& a, int32_t pos, int32_t count) {
+  const int l = lane_id();
+  S0Chunk ch{0, 0, 0.f};
+  if (l < count) {
+    const int32_t e = a.csr.order ? a.csr.order[pos + l] : pos + l;
+    const int64_t p = a.peer[e];
+    const bool ok = p >= 0 && p < a.rows;
+    ch.e = e;
+    ch.s = ok ? (int32_t)p : 0;
+    ch.m = ok ? (a.mask ? a.mask[e] : 1.f) : 0.f;
+  }
+  return ch;
+}
+
+template <class TG>
+__global__ __launch_bounds__(kS0FwdWaves * 64, 1) void msg_s0_fwd_kernel(FusedArgs a, float* __restrict__ out) {
+  static_assert(TG::LI == 0 && TG::P0 == 0 && TG::NOG == TG::NY && TG::NO == TG::NY && TG::NY <= 16,
+                "degree-0 input group with one output slot per harmonic component");
+  extern __shared__ bf16x8 w4l[];
+  constexpr int NY = TG::NY, PG = TG::PG;
+  stage_slice<PG, 0>(a.w4s, a.C / 64, a.cg, w4l);
+  __syncthreads();
+  const int C = a.C, l = lane_id(), q = l >> 4, j = l & 15, c0 = 64 * a.cg;
+  const float coef = j < NY ? s0_coef<TG>(j) : 0.f;
+  const int degj = degree_of(j);
+  const RowRange rr = block_rows<kS0FwdWaves>(a.rows);
+  for (int64_t slot = rr.first; slot < rr.end; slot += rr.stride) {
+    const int64_t n = visit_row(a.csr, slot, a.rows);
+    if (n < 0) continue;
+    v4f acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+    for (int32_t pos = beg; pos < end; pos += 64) {
+      const int32_t count = min(end - pos, 64);
+      const S0Chunk ch = s0_stage(a, pos, count);
+      for (int t0 = 0; t0 < count; t0 += 16 * kS0FwdTiles) {
+        // sub-tile u: projection rows = edge t0 + 16 u + j; D-layout edges t0 + 16 u + 4q + r
+        Split A[kS0FwdTiles][2];
+        float yv[kS0FwdTiles][4], xv[kS0FwdTiles][4][4];
+#pragma unroll
+        for (int u = 0; u < kS0FwdTiles; ++u) {
+          const int ci = t0 + 16 * u + j;
+          const int32_t ei = __shfl(ch.e, ci & 63);
+          load_a(a.h, ci < count ? hrow(a, ei) : 0, ci < count, A[u]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int k = t0 + 16 * u + 4 * q + r;
+            const int32_t e = __shfl(ch.e, k & 63), s = __shfl(ch.s, k & 63);
+            const float m = __shfl(ch.m, k & 63);
+            const bool ok = k < count;
+            yv[u][r] = ok && j < NY ? coef * m * a.sh[(int64_t)e * NY + j] : 0.f;
+            const float* xs = a.x + (int64_t)s * C + c0 + j;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) xv[u][r][cb] = ok ? xs[16 * cb] : 0.f;
+          }
+        }
+#pragma unroll
+        for (int p = 0; p < PG; ++p) {
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) {
+            const SliceOps w = slice_ops(w4l, p, cb);
+#pragma unroll
+            for (int u = 0; u < kS0FwdTiles; ++u) {
+              const v4f D = project_block<false>(w, A[u]);
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                acc[cb] = mfma_f32(degj == p ? yv[u][r] : 0.f, D[r] * xv[u][r][cb], acc[cb]);
+            }
+            // one slice's LDS operands live at a time
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    }
+    // lane (q, j): component 4q + r, channel 16 cb + j
+    float* row = out + n * (int64_t)(NY * C) + c0 + j;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int k = 4 * q + r;
+      if (k < NY) {
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) row[(int64_t)k * C + 16 * cb] = acc[cb][r];
+      }
+    }
+  }
+}
+
+// Receiver-owned gate-tangent adjoint (dsh and dr; no feature gradient).  The
+// tail slot `rows` holds edges whose receiver is out of range: zero cotangent,
+// so zero gradients.  `acc` adds to what an earlier channel group wrote.
+template <class TG>
+__global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(FusedArgs a,
+                                                                           const float* __restrict__ grad,
+                                                                           float* __restrict__ dsh,
+                                                                           float* __restrict__ dr, int acc) {
+  static_assert(TG::LI == 0 && TG::P0 == 0 && TG::NOG == TG::NY && TG::NO == TG::NY && TG::NY <= 16,
+                "degree-0 input group with one output slot per harmonic component");
+  extern __shared__ bf16x8 w4l[];
+  constexpr int NY = TG::NY, PG = TG::PG;
+  stage_slice<PG, 0>(a.w4s, a.C / 64, a.cg, w4l);
+  __syncthreads();
+  const int C = a.C, l = lane_id(), q = l >> 4, j = l & 15, c0 = 64 * a.cg;
+  const float coef = j < NY ? s0_coef<TG>(j) : 0.f;
+  const int degj = degree_of(j);
+  const RowRange rr = block_rows<kS0BwdWaves>(a.rows + 1);
+  for (int64_t slot = rr.first; slot < rr.end; slot += rr.stride) {
+    const int64_t n = visit_row(a.csr, slot, a.rows);
+    if (n < 0) continue;
+    const bool tail = n == a.rows;
+    // B operand: go[component j][channel 16 cb + 4 q + r] times the component's CG constant
+    float gb[4][4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+      if (!tail && j < NY) v = *reinterpret_cast<const v4f*>(grad + n * (int64_t)(NY * C) + (int64_t)j * C + c0 + 16 * cb + 4 * q);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) gb[cb][r] = coef * v[r];
+    }
+    const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+    for (int32_t pos = beg; pos < end; pos += 64) {
+      const int32_t count = min(end - pos, 64);
+      const S0Chunk ch = s0_stage(a, pos, count);
+      for (int t0 = 0; t0 < count; t0 += 16) {
+        // projection columns and contraction rows: edge t0 + j
+        const int ci = t0 + j;
+        const bool oki = ci < count;
+        const int32_t ei = __shfl(ch.e, ci);
+        const int64_t hr = oki ? hrow(a, ei) : 0;
+        const int32_t si = __shfl(ch.s, ci);
+        const float mi = __shfl(ch.m, ci);
+        Split H[2], T[2];
+        load_a(a.h, hr, oki, H);
+        load_a(a.t, hr, oki, T);
+        // sender features of edge t0 + j at channels 16 cb + 4 q .. + 3, times the mask
+        float xv[4][4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+          v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+          if (oki) v = *reinterpret_cast<const v4f*>(a.x + (int64_t)si * C + c0 + 16 * cb + 4 * q);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xv[cb][r] = mi * v[r];
+        }
+        v4f Q[PG], R[PG];
+#pragma unroll
+        for (int p = 0; p < PG; ++p) {
+          Q[p] = v4f{0.f, 0.f, 0.f, 0.f};
+          R[p] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) {
+            const SliceOps w = slice_ops(w4l, p, cb);
+            const v4f G = project_block<true>(w, H);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) Q[p] = mfma_f32(G[r] * xv[cb][r], gb[cb][r], Q[p]);
+            const v4f Gt = project_block<true>(w, T);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) R[p] = mfma_f32(Gt[r] * xv[cb][r], gb[cb][r], R[p]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        // lane (q, j): edges t0 + 4q + r, component j
+        float dv[4];
+        int32_t eo[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int k = t0 + 4 * q + r;
+          eo[r] = __shfl(ch.e, k);
+          float qv = 0.f, rv = 0.f;
+#pragma unroll
+          for (int p = 0; p < PG; ++p) {
+            qv = degj == p ? Q[p][r] : qv;
+            rv = degj == p ? R[p][r] : rv;
+          }
+          const bool ok = k < count && j < NY;
+          dv[r] = ok ? a.sh[(int64_t)eo[r] * NY + j] * rv : 0.f;
+          if (ok && dsh) {
+            float* d = dsh + (int64_t)eo[r] * NY + j;
+            *d = acc ? *d + qv : qv;
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int off = 8; off > 0; off >>= 1) dv[r] += __shfl_xor(dv[r], off);
+        }
+        if (j == 0) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (t0 + 4 * q + r < count) {
+              float* d = dr + eo[r];
+              *d = acc ? *d + dv[r] : dv[r];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
 int fail(int code, const char* msg) { return set_error(code, msg); }
 
 int launch_status(const char* what) {
@@ -496,6 +775,18 @@ struct Launch {
 template <class TG>
 int launch_group(const Launch& L) {
   const size_t lds = (size_t)TG::PG * kSlice * sizeof(bf16x8);
+  if constexpr (TG::LI == 0) {
+    // degree-0 input: the MFMA contraction kernels (the source-owned adjoint keeps the generic kernel)
+    if (L.pass == Pass::kFwd) {
+      hipLaunchKernelGGL(msg_s0_fwd_kernel<TG>, dim3((unsigned)cus()), dim3(kS0FwdWaves * 64), lds, L.st, L.a, L.out);
+      return launch_status("fused message launch");
+    }
+    if (L.pass == Pass::kBwdRcv) {
+      hipLaunchKernelGGL(msg_s0_bwd_rcv_kernel<TG>, dim3((unsigned)cus()), dim3(kS0BwdWaves * 64), lds, L.st,
+                         L.a, L.grad, L.dsh, L.dr, L.acc);
+      return launch_status("fused message launch");
+    }
+  }
   const dim3 grid((unsigned)cus()), block(fused_waves<TG>() * 64);
   switch (L.pass) {
     case Pass::kFwd:

@@ -59,7 +59,7 @@ def _oracle(x, sh, r, src, dst, m, Ws, li, C, go, keep):
     return out.detach(), xr.grad, shr.grad, rr.grad
 
 
-def _product(x, sh, r, src, dst, m, Ws, li, C, go, device, positions=None, params=False):
+def _product(x, sh, r, src, dst, m, Ws, li, C, go, device, positions=None, params=False, dfeatures=True):
     from ictc_o3.ops import tensor_product as tpo
     fc = _fc(Ws[-1].shape[0], Ws, device)
     for p in fc.parameters():
@@ -67,9 +67,10 @@ def _product(x, sh, r, src, dst, m, Ws, li, C, go, device, positions=None, param
     spec = tpo.make_spec(li, 2, 2, C)
     topo = tpo.Topology(src.to(device), dst.to(device), x.shape[0], positions=positions)
     xd, shd, rd = (t.float().to(device).requires_grad_(True) for t in (x, sh, r))
+    xd.requires_grad_(dfeatures)
     md = None if m is None else m.float().to(device)
     out = tpo.radial_message(xd, shd, rd, fc, spec, topo, md, CFG)
-    wrt = [xd, shd, rd] + ([p for p in fc.parameters()] if params else [])
+    wrt = ([xd] if dfeatures else []) + [shd, rd] + ([p for p in fc.parameters()] if params else [])
     grads = torch.autograd.grad(out, wrt, go.float().to(device))
     return out.detach(), grads, out.grad_fn
 
@@ -97,6 +98,27 @@ def test_fused_message_matches_oracle(device, N, E, C, li, mask):
     # repeatable bit for bit
     out2, (dx2, dsh2, dr2), _ = _product(x, sh, r, src, dst, m, Ws, li, C, go, device)
     assert torch.equal(out, out2) and torch.equal(dx, dx2) and torch.equal(dsh, dsh2) and torch.equal(dr, dr2)
+
+
+@pytest.mark.parametrize("N,E,C,mask", [(50, 1500, 64, True), (40, 1100, 128, True), (33, 29, 64, False)])
+def test_fused_scalar_input_receiver_adjoint(device, N, E, C, mask):
+    """Input degree 0 without a feature gradient (the model's first layer): the receiver-owned adjoint
+    (harmonic and edge-length gradients only) and the forward, against the oracle; partial edge tiles,
+    two channel groups, masks and out-of-range ids."""
+    li = 0
+    x, sh, r, src, dst, m, Ws = _case(N, E, C, li, 300 + N, mask)
+    go = torch.randn(N, 9 * C, generator=torch.Generator().manual_seed(9), dtype=torch.float64)
+    keep = (src >= 0) & (src < N) & (dst >= 0) & (dst < N)
+    ref, _, dsh0, dr0 = _oracle(x, sh, r, src, dst, m, Ws, li, C, go, keep)
+    out, (dsh, dr), fn = _product(x, sh, r, src, dst, m, Ws, li, C, go, device, dfeatures=False)
+    assert type(fn).__name__.startswith("FusedRadialMessage")
+    assert rel_err(out, ref) < TOL
+    assert rel_err(dsh, dsh0) < TOL
+    assert rel_err(dr, dr0) < TOL
+    assert torch.count_nonzero(dr[~keep.to(device)]) == 0
+    assert torch.count_nonzero(dsh[~keep.to(device)]) == 0
+    out2, (dsh2, dr2), _ = _product(x, sh, r, src, dst, m, Ws, li, C, go, device, dfeatures=False)
+    assert torch.equal(out, out2) and torch.equal(dsh, dsh2) and torch.equal(dr, dr2)
 
 
 def test_fused_message_spatial_rows_and_unfused_route(device):
