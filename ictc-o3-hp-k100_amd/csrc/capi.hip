@@ -370,11 +370,11 @@ int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh,
                    "ictc_msg_fwd launch");
 }
 
-int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
-                 const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
-                 const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
-                 const int32_t* dst_rows, const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dg,
-                 void* workspace, int64_t workspace_bytes, void* stream) {
+static int msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                   const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
+                   const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
+                   const int32_t* dst_rows, const int32_t* src_rows, const float* grad, float* dx, float* dsh,
+                   float* dg, void* workspace, int64_t workspace_bytes, void* stream, int dg_acc) {
   if (int rc = check_shape(li, le, lo, C)) return rc;
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "negative size");
   if (E == 0) {
@@ -388,10 +388,31 @@ int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh,
   if (dx && !sptr) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd: dfeatures needs the source CSR");
   if (int rc = check_ws(dsh, (const float*)workspace, workspace_bytes, le, C, E, "ictc_msg_bwd")) return rc;
   const ictc::TpShape s{li, le, lo, C};
-  return check_hip(route_msg_bwd(s, operands(x, sh, g, w, mask, N, E, C), src, dst, ictc::Csr{dptr, dorder, dst_rows},
-                                        ictc::Csr{sptr, sorder, src_rows}, grad, dx, dsh, dg, (float*)workspace,
-                                        (hipStream_t)stream),
+  ictc::Operands a = operands(x, sh, g, w, mask, N, E, C);
+  a.dg_acc = dg_acc;
+  return check_hip(route_msg_bwd(s, a, src, dst, ictc::Csr{dptr, dorder, dst_rows}, ictc::Csr{sptr, sorder, src_rows},
+                                 grad, dx, dsh, dg, (float*)workspace, (hipStream_t)stream),
                    "ictc_msg_bwd launch");
+}
+
+int ictc_msg_bwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,
+                 const float* mask, const int64_t* src, const int64_t* dst, int64_t N, int64_t E,
+                 const int32_t* dptr, const int32_t* dorder, const int32_t* sptr, const int32_t* sorder,
+                 const int32_t* dst_rows, const int32_t* src_rows, const float* grad, float* dx, float* dsh, float* dg,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
+  return msg_bwd(li, le, lo, C, x, sh, g, w, mask, src, dst, N, E, dptr, dorder, sptr, sorder, dst_rows, src_rows,
+                 grad, dx, dsh, dg, workspace, workspace_bytes, stream, 0);
+}
+
+int ictc_msg_bwd_accumulate(int li, int le, int lo, int C, const float* x, const float* sh, const float* g,
+                            const float* w, const float* mask, const int64_t* src, const int64_t* dst, int64_t N,
+                            int64_t E, const int32_t* dptr, const int32_t* dorder, const int32_t* sptr,
+                            const int32_t* sorder, const int32_t* dst_rows, const int32_t* src_rows,
+                            const float* grad, float* dx, float* dsh, float* dg, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  if (!dg) return fail(ICTC_ERR_ARGUMENT, "ictc_msg_bwd_accumulate: dgates is required");
+  return msg_bwd(li, le, lo, C, x, sh, g, w, mask, src, dst, N, E, dptr, dorder, sptr, sorder, dst_rows, src_rows,
+                 grad, dx, dsh, dg, workspace, workspace_bytes, stream, 1);
 }
 
 int64_t ictc_msg_bwd_tangent_workspace_bytes(int edge_lmax, int C, int64_t E) {

@@ -96,6 +96,8 @@ struct Operands {
   // Gate row of each edge ([E], nullptr = the edge itself): the radial gates depend on the edge length
   // only, and an edge and its reverse have bitwise-equal lengths, so one row can serve both.
   const int32_t* grow = nullptr;
+  // Gate-gradient outputs add to the rows already there (ictc_msg_bwd_accumulate) instead of overwriting them.
+  int dg_acc = 0;
 };
 
 // Row of the gate (and gate-tangent) arrays that edge e reads.
@@ -150,6 +152,18 @@ __device__ __forceinline__ void store_row(float* __restrict__ base, int C, int c
     *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + off) = v[i];
     base += C;
   }
+}
+
+// store_row of a gate-gradient row, or with a.dg_acc the sum of the row already there and v.
+template <int N>
+__device__ __forceinline__ void store_dg_row(const Operands& a, float* __restrict__ base, int C, int c, float* v) {
+  if (a.dg_acc) {
+    float o[N];
+    load_row<N>(base, C, c, o);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = o[i] + v[i];
+  }
+  store_row<N>(base, C, c, v);
 }
 
 // Gates of edge e for channel c, times the per-path weight (if any) and `scale`.
@@ -577,7 +591,7 @@ __global__ __launch_bounds__(kBlock, (edge_adjoint_waves<T, TAN>())) void msg_bw
 #pragma unroll
             for (int p = 0; p < T::P; ++p) d[p] *= a.weight[p * C + c];
           }
-          store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, d);
+          store_dg_row<T::P>(a, dgates + e * (int64_t)(T::P * C), C, c, d);
         }
       }
       if (dsh) {
@@ -771,7 +785,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
 #pragma unroll
             for (int p = 0; p < T::P; ++p) dg[p] *= a.weight[p * C + c];
           }
-          store_row<T::P>(dgates + e * (int64_t)(T::P * C), C, c, dg);
+          store_dg_row<T::P>(a, dgates + e * (int64_t)(T::P * C), C, c, dg);
         }
       }
       if (dsh) {

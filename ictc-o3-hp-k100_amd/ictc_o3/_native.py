@@ -38,6 +38,8 @@ _SIGNATURES = {
     "ictc_msg_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_msg_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
                           _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "ictc_msg_bwd_accumulate": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
+                                     _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_msg_bwd_tangent_workspace_bytes": (_i64, [_i, _i, _i64]),
     "ictc_msg_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
                                   _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p]),

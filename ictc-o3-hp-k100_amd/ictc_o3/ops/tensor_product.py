@@ -368,14 +368,16 @@ def _msg_fwd_raw(spec, topo, x, sh, g, mask, gate_rows=None):
     return out
 
 
-def _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need):
+def _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need, dg_into=None):
+    """First adjoint (dx, dsh, dg); dg_into (contiguous, like g): the gate gradient is added to it in place
+    (ictc_msg_bwd_accumulate) and returned as dg."""
     N, E = x.shape[0], sh.shape[0]
     dx = torch.empty_like(x) if need[0] else None
     dsh = torch.empty_like(sh) if need[1] else None
-    dg = torch.empty_like(g) if need[2] else None
+    dg = dg_into if dg_into is not None else torch.empty_like(g) if need[2] else None
     sp = topo.by_src if need[0] else None
     ws, ws_bytes = _group_ws(spec, E, dsh)
-    nat.call("ictc_msg_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
+    nat.call("ictc_msg_bwd_accumulate" if dg_into is not None else "ictc_msg_bwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
              nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
              nat.ptr(sp.ptr) if sp else None, nat.ptr(sp.order) if sp else None, nat.ptr(topo.dst_rows),
@@ -405,24 +407,98 @@ def _msg_second_raw(spec, topo, x, sh, g, mask, go, tx, tsh, tg, need):
     return dx, dsh, dg, dgo
 
 
+def _graph_task():
+    """Id of the running backward pass (graph task); -1 outside one."""
+    return torch._C._current_graph_task_id()
+
+
+class _GateLink:
+    """Hands the gate gradient of a message's mixed second derivative to the first-order adjoint of the
+    same message in the same backward pass.
+
+    In a force-loss backward both passes differentiate the same gates g: the
+    mixed second derivative of the force pass's adjoint (MessageAdjoint.backward,
+    which runs first) and the first-order adjoint of the forward message
+    (Message.backward, later, with the energy term's cotangent and what the
+    second derivatives send into the forward graph).  Autograd would add the two
+    [E, P*C] gradients with a separate tensor add; instead the second-order pass
+    leaves its gradient here and the first-order kernel adds it in its own store
+    (ictc_msg_bwd_accumulate; a + b = b + a in IEEE arithmetic, so the sum is
+    bitwise autograd's).  The gradient is left only when the engine will still
+    run the forward message's node in this pass (torch._C._will_engine_execute_node)
+    and that node has not run yet; a callback at the end of the pass raises if
+    it was not taken, so a gradient is never dropped silently.
+    """
+    __slots__ = ("node", "ran", "pending", "__weakref__")
+
+    def __init__(self, node):
+        self.node = weakref.ref(node)
+        self.ran = None          # graph task in which the forward message's backward last ran
+        self.pending = None      # (graph task, gate gradient)
+
+    def can_hold(self):
+        from torch.fx.experimental.proxy_tensor import get_proxy_mode
+        if (torch.compiler.is_compiling() or get_proxy_mode() is not None
+                or torch._C._are_functorch_transforms_active()
+                or not hasattr(torch._C, "_will_engine_execute_node")):
+            return False
+        task, node = _graph_task(), self.node()
+        if task < 0 or node is None or self.ran == task or self.pending is not None:
+            return False
+        try:
+            return bool(torch._C._will_engine_execute_node(node))
+        except (RuntimeError, AttributeError, AssertionError):
+            return False
+
+    def hold(self, dg):
+        task = _graph_task()
+        self.pending = (task, dg)
+        ref = weakref.ref(self)
+
+        def check():
+            link = ref()
+            if link is not None and link.pending is not None and link.pending[0] == task:
+                link.pending = None
+                raise RuntimeError("message gate gradient of the mixed second derivative was not consumed")
+        torch.autograd.Variable._execution_engine.queue_callback(check)
+
+    def take(self):
+        task = _graph_task()
+        self.ran = task
+        if self.pending is not None and self.pending[0] == task:
+            dg, self.pending = self.pending[1], None
+            return dg
+        return None
+
+
 class Message(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, sh, g, spec, topo, mask):
         ctx.set_materialize_grads(False)
         ctx.spec, ctx.topo, ctx.mask = spec, topo, mask
+        ctx.link = _GateLink(ctx)
         x, sh, g = _c(x), _c(sh), _c(g)
         ctx.save_for_backward(x, sh, g)
         return _msg_fwd_raw(spec, topo, x, sh, g, mask)
 
     @staticmethod
     def backward(ctx, go):
+        dg_in = ctx.link.take()   # gate gradient the mixed second derivative left for this pass
         if go is None:
-            return (None,) * 6
+            return None, None, dg_in, None, None, None
         x, sh, g = ctx.saved_tensors
         need = required_gradients((x, sh, g), ctx.needs_input_grad[:3])
         if not any(need):
-            return (None,) * 6
-        dx, dsh, dg = MessageAdjoint.apply(x, sh, g, _c(go), ctx.spec, ctx.topo, ctx.mask, need)
+            return None, None, dg_in, None, None, None
+        if torch.is_grad_enabled():
+            dx, dsh, dg = MessageAdjoint.apply(x, sh, g, _c(go), ctx.spec, ctx.topo, ctx.mask, need, ctx.link)
+        elif dg_in is not None and need[2]:
+            dx, dsh, dg = _msg_bwd_raw(ctx.spec, ctx.topo, x, sh, g, ctx.mask, _c(go), need, dg_into=dg_in)
+            dg_in = None
+        else:
+            dx, dsh, dg = _msg_bwd_raw(ctx.spec, ctx.topo, x, sh, g, ctx.mask, _c(go), need)
+        if dg_in is not None:
+            dg = dg_in if dg is None else dg + dg_in
         return dx, dsh, dg, None, None, None
 
 
@@ -624,9 +700,9 @@ def message_adjoint(x, sh, g, go, spec, topo, mask, need):
 
 class MessageAdjoint(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, sh, g, go, spec, topo, mask, need):
+    def forward(ctx, x, sh, g, go, spec, topo, mask, need, link=None):
         ctx.set_materialize_grads(False)
-        ctx.spec, ctx.topo, ctx.mask = spec, topo, mask
+        ctx.spec, ctx.topo, ctx.mask, ctx.link = spec, topo, mask, link
         x, sh, g, go = _c(x), _c(sh), _c(g), _c(go)
         ctx.save_for_backward(x, sh, g, go)
         return _msg_bwd_raw(spec, topo, x, sh, g, mask, go, need)
@@ -639,7 +715,10 @@ class MessageAdjoint(torch.autograd.Function):
         if not torch.is_grad_enabled():
             # the mixed second derivative itself is the last order asked for: fused kernels
             dx, dsh, dg, dgo = _msg_second_raw(spec, topo, x, sh, g, mask, go, hx, hsh, hg, (nx, nsh, ng, ngo))
-            return dx, dsh, dg, dgo, None, None, None, None
+            if dg is not None and ctx.link is not None and ctx.link.can_hold():
+                ctx.link.hold(dg)   # added by the forward message's first-order adjoint later in this pass
+                dg = None
+            return dx, dsh, dg, dgo, None, None, None, None, None
         # higher orders: compose differentiable first-order operators (multilinearity)
         dx = dsh = dg = dgo = None
         if ngo:
@@ -664,4 +743,4 @@ class MessageAdjoint(torch.autograd.Function):
                 dg = _add(dg, message_adjoint(hx, sh, g, go, spec, topo, mask, (False, False, True))[2])
             if hsh is not None:
                 dg = _add(dg, message_adjoint(x, hsh, g, go, spec, topo, mask, (False, False, True))[2])
-        return dx, dsh, dg, dgo, None, None, None, None
+        return dx, dsh, dg, dgo, None, None, None, None, None

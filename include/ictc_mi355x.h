@@ -151,6 +151,23 @@ int ictc_msg_bwd(int input_lmax, int edge_lmax, int output_lmax, int channels,
                  float* dfeatures, float* dharmonics, float* dgates, void* workspace,
                  int64_t workspace_bytes, void* stream);
 
+/* ictc_msg_bwd with dgates (required) as an input-output: the gate gradient
+ * is added to the [E, P*C] rows dgates holds (each element read and written
+ * by one lane: dgates <- dgates + gradient), every other output as in
+ * ictc_msg_bwd.  No counterpart in the reference, whose autograd adds the
+ * gate gradients of the first-order and mixed second-order passes with a
+ * separate tensor add; for training callers that hold the mixed second
+ * derivative's gate gradient when the first-order adjoint runs, so that the
+ * sum is formed in the adjoint's own store.                                  */
+int ictc_msg_bwd_accumulate(int input_lmax, int edge_lmax, int output_lmax, int channels,
+                            const float* features, const float* harmonics, const float* gates,
+                            const float* weight, const float* mask, const int64_t* src, const int64_t* dst,
+                            int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                            const int32_t* src_ptr, const int32_t* src_order, const int32_t* dst_rows,
+                            const int32_t* src_rows, const float* grad,
+                            float* dfeatures, float* dharmonics, float* dgates, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* ictc_msg_bwd for a caller that holds gtangent [E, P*C] = d gates / d r
  * (ictc_radial_gates_tangent_fwd) and wants the edge-length gradient rather
  * than the gate gradient: dr [E] (required) = sum over paths and channels of

@@ -140,6 +140,9 @@ def test_fused_and_gemm_entry_points_host_checks():
     with pytest.raises(ValueError, match="multiple of 64"):
         _native.call("ictc_msg_fused_fwd", 2, 2, 2, 96, None, None, None, None, None, None, 10, 10, None, None, None,
                      None, None, None)
+    with pytest.raises(ValueError, match="dgates is required"):
+        _native.call("ictc_msg_bwd_accumulate", 2, 2, 2, 64, None, None, None, None, None, None, None, 10, 10, None,
+                     None, None, None, None, None, None, None, None, None, None, 0, None)
     with pytest.raises(ValueError, match="dr is required"):
         _native.call("ictc_msg_fused_bwd_tangent", 2, 2, 2, 64, None, None, None, None, None, None, None, None, 10,
                      10, None, None, None, None, None, None, None, None, None, None, None, None)

@@ -74,6 +74,45 @@ def test_force_loss_parameter_gradients(device):
         assert rl2 < 3e-5, (k, rl2)
 
 
+def test_force_loss_gate_gradient_handoff(device):
+    """The mixed second derivative's gate gradient, handed to the forward message's first-order adjoint and
+    added in its store (ictc_msg_bwd_accumulate), gives bitwise the gradients of autograd's separate add;
+    it is handed over once per message layer per backward pass."""
+    from ictc_o3.ops import tensor_product as tpo
+    from mace_ictc.hp import energy_and_forces
+    model, pos, Z, batch, cell, src, dst, sh = _setup(device, 4, 64, 2, 3, 4, cells=2)
+    g = torch.Generator().manual_seed(5)
+    E_t = torch.randn(2, generator=g).to(device)
+    F_t = (torch.randn(pos.shape, generator=g) * 0.5).to(device)
+    params = [p for p in model.parameters() if p.requires_grad]
+    args = (pos.float().to(device), Z.to(device), batch.to(device), src.to(device), dst.to(device),
+            sh.float().to(device), cell.float().to(device))
+
+    def grads():
+        out = energy_and_forces(model, *args, training=True)
+        loss = ((out["energy"] - E_t) ** 2).mean() + ((out["forces"] - F_t) ** 2).mean()
+        return torch.autograd.grad(loss, params, allow_unused=True)
+
+    held = []
+    hold = tpo._GateLink.hold
+    tpo._GateLink.hold = lambda self, dg: (held.append(dg.shape), hold(self, dg))[1]
+    try:
+        with_handoff = grads()
+    finally:
+        tpo._GateLink.hold = hold
+    assert len(held) == len(model.interactions)
+    can_hold = tpo._GateLink.can_hold
+    tpo._GateLink.can_hold = lambda self: False
+    try:
+        without = grads()
+    finally:
+        tpo._GateLink.can_hold = can_hold
+    for a, b in zip(with_handoff, without):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
+
+
 def test_configure_model_contract(device):
     from mace_ictc.hp import configure_model, create_model
     model = create_model(channels=8, lmax=2, device=device)
