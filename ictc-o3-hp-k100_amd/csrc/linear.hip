@@ -1,5 +1,7 @@
-// Channel-mixing linears on the packed component-major layout, on FP32 MFMA
-// (v_mfma_f32_16x16x4_f32).  One kernel covers
+// Channel-mixing linears on the packed component-major layout, on split-bf16
+// MFMA (v_mfma_f32_16x16x32_bf16, six products: FP32-level accuracy) where the
+// weight panel fits LDS (K <= 256, every linear of the cfg4 model) and on FP32
+// MFMA (v_mfma_f32_16x16x4_f32) beyond.  One kernel covers
 //   EquivariantChannelLinearSO3 / product o3.Linear (ictd_irreps.py:207-227, products.py:817):
 //       out[n, l, m, :] = s_l W_l x[n, l, m, :]                       (1 path in, 1 path out)
 //   PathPreservingLinearSO3 (layers.py:317-355, common.py:368-374):
@@ -10,8 +12,8 @@
 //
 // A degree block is a GEMM of (N rows per component m) x (paths_in * Cin) by
 // (paths_in * Cin) x (paths_out * Cout).  A wave computes 16 nodes x 64
-// output columns of one component; the block's 4 waves share the weight
-// panel (64 output columns x K) staged in LDS, whole or per k-chunk.  Operand k
+// output columns of one component; the block's waves share the weight
+// panel (64 output columns x K) staged in LDS.  FP32 operand k
 // order (consistent for A and B, which is all the MFMA needs): at k-step j,
 // lane group g = l/16 supplies k = 16 g + j of the chunk, so each lane reads
 // 16 contiguous floats of its row (four 16-byte loads).
@@ -20,6 +22,7 @@
 #include <stdio.h>
 
 #include "../../include/ictc_mi355x.h"
+#include "split_bf16.h"
 
 namespace ictc {
 int set_error(int code, const char* msg);
@@ -45,9 +48,10 @@ __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// WHOLE: the block's whole weight panel (64 output columns x K, K <= kWholeK) is staged in LDS once,
-// and the block loops over 64-node tiles (grid.x persistent blocks); otherwise the panel is staged
-// per 64-wide k-chunk.  MFMA operands: A = weights (M = 16 output columns), B = inputs (N = 16 nodes),
+// FP32 MFMA form for panels too wide for LDS (K > kWholeK; K <= kWholeK runs the split-bf16 kernel
+// below).  WHOLE: the block's whole weight panel (64 output columns x K) is staged in LDS once, and the
+// block loops over 64-node tiles (grid.x persistent blocks); otherwise the panel is staged per 64-wide
+// k-chunk.  MFMA operands: A = weights (M = 16 output columns), B = inputs (N = 16 nodes),
 // so each lane ends with 4 consecutive output columns of one node and stores them as one 16-byte write.
 constexpr int kWholeK = 256;
 
@@ -139,6 +143,99 @@ __global__ __launch_bounds__(256) void packed_linear_kernel(const float* __restr
   }
 }
 
+// Split-bf16 form of the whole-panel path (K <= kWholeK): the weight panel is split once into three bf16
+// parts in LDS (the A operand of v_mfma_f32_16x16x32_bf16, lane l: output column 16 cb + l % 16,
+// k = 32 ks + 8 (l / 16) .. + 7), each 16-node tile's inputs are split once per 32-wide k-step (B
+// operand: node l % 16, the same k), and each 16 x 16 x 32 block keeps the six products whose size is at
+// least 2^-24 of hi*hi (split_bf16.h), smallest first: FP32-level accuracy at a third of the FP32 MFMA
+// time.  kLinWaves waves per block share the panel.
+constexpr int kLinWaves = 16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v4f mfma_bf16(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
+    const float* __restrict__ in, int64_t in_stride, float* __restrict__ out, int64_t out_stride, int Ci, int Co,
+    int64_t N, LinearDesc d, int64_t node_tiles) {
+  extern __shared__ bf16x8 wpanel[];  // [ks][cb][part][lane]
+  int l = 0, m = blockIdx.y;
+  while (m >= 2 * l + 1) {
+    m -= 2 * l + 1;
+    ++l;
+  }
+  const int w = 2 * l + 1;
+  const int K = d.pin[l] * Ci, ncols = d.pout[l] * Co;
+  const int col0 = 64 * blockIdx.z;
+  if (col0 >= ncols) return;
+  const float* __restrict__ W = d.w[l];
+  const int nks = (K + 31) / 32;
+  for (int t = threadIdx.x; t < nks * 4 * 64; t += blockDim.x) {
+    const int lane = t & 63, cb = (t >> 6) & 3, ks = t >> 8;
+    const int col = col0 + 16 * cb + (lane & 15), k = 32 * ks + 8 * (lane >> 4);
+    float v[8];
+    if (col < ncols && k < K) {
+      const float4 a = *reinterpret_cast<const float4*>(W + (int64_t)col * K + k);
+      const float4 b = *reinterpret_cast<const float4*>(W + (int64_t)col * K + k + 4);
+      v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    const Split sp = split8(v);
+    bf16x8* o = wpanel + ((ks * 4 + cb) * 3) * 64 + lane;
+    o[0] = sp.hi;
+    o[64] = sp.mid;
+    o[128] = sp.lo;
+  }
+  __syncthreads();
+  const float sc = d.scale[l];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = lane & 15, g = lane >> 4;
+  for (int64_t tile = (int64_t)blockIdx.x * kLinWaves + wave; tile < node_tiles; tile += (int64_t)gridDim.x * kLinWaves) {
+    const int64_t n = tile * 16 + i;
+    v4f acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int ks = 0; ks < nks; ++ks) {
+      const int k0 = 32 * ks + 8 * g;
+      float a[8];
+      if (n < N && k0 < K) {
+        const int p = k0 / Ci, c = k0 % Ci;
+        const float* src = in + n * in_stride + d.in_off[l] + ((int64_t)p * w + m) * Ci + c;
+        const float4 x0 = *reinterpret_cast<const float4*>(src), x1 = *reinterpret_cast<const float4*>(src + 4);
+        a[0] = x0.x, a[1] = x0.y, a[2] = x0.z, a[3] = x0.w, a[4] = x1.x, a[5] = x1.y, a[6] = x1.z, a[7] = x1.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[e] = 0.f;
+      }
+      const Split B = split8(a);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const bf16x8* pp = wpanel + ((ks * 4 + cb) * 3) * 64 + lane;
+        const bf16x8 wh = pp[0], wm = pp[64], wl = pp[128];
+        // weight part x input part: lo*hi, hi*lo, mid*mid, mid*hi, hi*mid, hi*hi (smallest first)
+        acc[cb] = mfma_bf16(wl, B.hi, acc[cb]);
+        acc[cb] = mfma_bf16(wh, B.lo, acc[cb]);
+        acc[cb] = mfma_bf16(wm, B.mid, acc[cb]);
+        acc[cb] = mfma_bf16(wm, B.hi, acc[cb]);
+        acc[cb] = mfma_bf16(wh, B.mid, acc[cb]);
+        acc[cb] = mfma_bf16(wh, B.hi, acc[cb]);
+      }
+    }
+    // D: lane holds output columns col0 + 16 cb + 4 g .. + 3 of node n0 + i.
+    if (n < N) {
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) {
+        const int col = col0 + 16 * cb + 4 * g;
+        if (col >= ncols) continue;
+        const int p = col / Co, c = col % Co;
+        *reinterpret_cast<v4f*>(out + n * out_stride + d.out_off[l] + ((int64_t)p * w + m) * Co + c) = sc * acc[cb];
+      }
+    }
+  }
+}
+
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
 
 }  // namespace
@@ -183,16 +280,19 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
   const int64_t node_blocks = (nodes + 63) / 64;
   const unsigned gy = (unsigned)((lmax + 1) * (lmax + 1)), gz = (unsigned)((maxcols + 63) / 64);
   if (maxk <= kWholeK) {
-    // persistent blocks: about 8 per CU over all (component, column block) pairs
+    // one 16-wave block per CU over all (component, column block) pairs
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
                                                  hipSuccess || cus <= 0)
       cus = 256;
-    int64_t gx = (int64_t)8 * cus / (gy * gz);
-    gx = gx < 1 ? 1 : (gx > node_blocks ? node_blocks : gx);
-    const size_t lds = (size_t)64 * (maxk + 4) * sizeof(float);
-    hipLaunchKernelGGL(packed_linear_kernel<true>, dim3((unsigned)gx, gy, gz), dim3(256), lds, (hipStream_t)stream, in,
-                       in_stride, out, out_stride, channels_in, channels_out, nodes, d, node_blocks);
+    const int64_t node_tiles = (nodes + 15) / 16;
+    int64_t gx = (int64_t)cus / (gy * gz);
+    const int64_t most = (node_tiles + kLinWaves - 1) / kLinWaves;
+    gx = gx < 1 ? 1 : (gx > most ? most : gx);
+    const size_t lds = (size_t)(maxk / 32) * 4 * 3 * 64 * sizeof(bf16x8);
+    hipLaunchKernelGGL(packed_linear_bf16_kernel, dim3((unsigned)gx, gy, gz), dim3(kLinWaves * 64), lds,
+                       (hipStream_t)stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d,
+                       node_tiles);
   } else {
     hipLaunchKernelGGL(packed_linear_kernel<false>, dim3((unsigned)node_blocks, gy, gz), dim3(256),
                        (size_t)64 * kPanel * sizeof(float), (hipStream_t)stream, in, in_stride, out, out_stride,
