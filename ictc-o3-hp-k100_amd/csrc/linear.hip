@@ -156,9 +156,15 @@ __device__ __forceinline__ v4f mfma_bf16(bf16x8 a, bf16x8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
+// NZ: 64-column blocks per workgroup (all of a narrow linear's output columns, so its inputs are read once).
+template <int NZ>
+constexpr int lin_waves() { return NZ == 1 ? kLinWaves : kLinWaves / 2; }  // 64 accumulator VGPRs at NZ = 4
+
+template <int NZ>
+__global__ __launch_bounds__(lin_waves<NZ>() * 64, 1) void packed_linear_bf16_kernel(
     const float* __restrict__ in, int64_t in_stride, float* __restrict__ out, int64_t out_stride, int Ci, int Co,
     int64_t N, LinearDesc d, int64_t node_tiles) {
+  constexpr int NCB = 4 * NZ;  // 16-column blocks
   extern __shared__ bf16x8 wpanel[];  // [ks][cb][part][lane]
   int l = 0, m = blockIdx.y;
   while (m >= 2 * l + 1) {
@@ -167,12 +173,12 @@ __global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
   }
   const int w = 2 * l + 1;
   const int K = d.pin[l] * Ci, ncols = d.pout[l] * Co;
-  const int col0 = 64 * blockIdx.z;
+  const int col0 = 64 * NZ * blockIdx.z;
   if (col0 >= ncols) return;
   const float* __restrict__ W = d.w[l];
   const int nks = (K + 31) / 32;
-  for (int t = threadIdx.x; t < nks * 4 * 64; t += blockDim.x) {
-    const int lane = t & 63, cb = (t >> 6) & 3, ks = t >> 8;
+  for (int t = threadIdx.x; t < nks * NCB * 64; t += blockDim.x) {
+    const int lane = t & 63, cb = (t >> 6) % NCB, ks = (t >> 6) / NCB;
     const int col = col0 + 16 * cb + (lane & 15), k = 32 * ks + 8 * (lane >> 4);
     float v[8];
     if (col < ncols && k < K) {
@@ -184,7 +190,7 @@ __global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
       for (int e = 0; e < 8; ++e) v[e] = 0.f;
     }
     const Split sp = split8(v);
-    bf16x8* o = wpanel + ((ks * 4 + cb) * 3) * 64 + lane;
+    bf16x8* o = wpanel + ((ks * NCB + cb) * 3) * 64 + lane;
     o[0] = sp.hi;
     o[64] = sp.mid;
     o[128] = sp.lo;
@@ -192,11 +198,12 @@ __global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
   __syncthreads();
   const float sc = d.scale[l];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = lane & 15, g = lane >> 4;
-  for (int64_t tile = (int64_t)blockIdx.x * kLinWaves + wave; tile < node_tiles; tile += (int64_t)gridDim.x * kLinWaves) {
+  constexpr int NW = lin_waves<NZ>();
+  for (int64_t tile = (int64_t)blockIdx.x * NW + wave; tile < node_tiles; tile += (int64_t)gridDim.x * NW) {
     const int64_t n = tile * 16 + i;
-    v4f acc[4];
+    v4f acc[NCB];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < NCB; ++cb) acc[cb] = v4f{0.f, 0.f, 0.f, 0.f};
     for (int ks = 0; ks < nks; ++ks) {
       const int k0 = 32 * ks + 8 * g;
       float a[8];
@@ -211,8 +218,8 @@ __global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
       }
       const Split B = split8(a);
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
-        const bf16x8* pp = wpanel + ((ks * 4 + cb) * 3) * 64 + lane;
+      for (int cb = 0; cb < NCB; ++cb) {
+        const bf16x8* pp = wpanel + ((ks * NCB + cb) * 3) * 64 + lane;
         const bf16x8 wh = pp[0], wm = pp[64], wl = pp[128];
         // weight part x input part: lo*hi, hi*lo, mid*mid, mid*hi, hi*mid, hi*hi (smallest first)
         acc[cb] = mfma_bf16(wl, B.hi, acc[cb]);
@@ -226,7 +233,7 @@ __global__ __launch_bounds__(kLinWaves * 64, 1) void packed_linear_bf16_kernel(
     // D: lane holds output columns col0 + 16 cb + 4 g .. + 3 of node n0 + i.
     if (n < N) {
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) {
+      for (int cb = 0; cb < NCB; ++cb) {
         const int col = col0 + 16 * cb + 4 * g;
         if (col >= ncols) continue;
         const int p = col / Co, c = col % Co;
@@ -286,13 +293,22 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
                                                  hipSuccess || cus <= 0)
       cus = 256;
     const int64_t node_tiles = (nodes + 15) / 16;
-    int64_t gx = (int64_t)cus / (gy * gz);
-    const int64_t most = (node_tiles + kLinWaves - 1) / kLinWaves;
+    // a narrow linear with up to 256 output columns covers them all in one workgroup (inputs read once)
+    const bool wide4 = maxk <= 64 && maxcols > 64 && maxcols <= 256;
+    const unsigned gzw = wide4 ? 1u : gz;
+    int64_t gx = (int64_t)cus / (gy * gzw);
+    const int nw = wide4 ? lin_waves<4>() : lin_waves<1>();
+    const int64_t most = (node_tiles + nw - 1) / nw;
     gx = gx < 1 ? 1 : (gx > most ? most : gx);
-    const size_t lds = (size_t)(maxk / 32) * 4 * 3 * 64 * sizeof(bf16x8);
-    hipLaunchKernelGGL(packed_linear_bf16_kernel, dim3((unsigned)gx, gy, gz), dim3(kLinWaves * 64), lds,
-                       (hipStream_t)stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d,
-                       node_tiles);
+    const size_t lds = (size_t)(maxk / 32) * 4 * (wide4 ? 4 : 1) * 3 * 64 * sizeof(bf16x8);
+    if (wide4)
+      hipLaunchKernelGGL(packed_linear_bf16_kernel<4>, dim3((unsigned)gx, gy, 1), dim3(lin_waves<4>() * 64), lds,
+                         (hipStream_t)stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d,
+                         node_tiles);
+    else
+      hipLaunchKernelGGL(packed_linear_bf16_kernel<1>, dim3((unsigned)gx, gy, gz), dim3(lin_waves<1>() * 64), lds,
+                         (hipStream_t)stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d,
+                         node_tiles);
   } else {
     hipLaunchKernelGGL(packed_linear_kernel<false>, dim3((unsigned)node_blocks, gy, gz), dim3(256),
                        (size_t)64 * kPanel * sizeof(float), (hipStream_t)stream, in, in_stride, out, out_stride,
