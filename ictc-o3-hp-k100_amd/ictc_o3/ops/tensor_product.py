@@ -443,6 +443,8 @@ class _GateLink:
                 or not hasattr(torch._C, "_will_engine_execute_node")):
             return False
         task, node = _graph_task(), self.node()
+        if self.pending is not None and self.pending[0] != task:
+            self.pending = None   # left by a backward pass that stopped early (its callback did not run)
         if task < 0 or node is None or self.ran == task or self.pending is not None:
             return False
         try:
