@@ -484,7 +484,7 @@ __global__ __launch_bounds__(fused_waves<TG>() * 64, 1) void msg_fused_bwd_rcv_k
 // 63 % of two 32-edge tiles against 83 % of three 16-edge tiles, and fewer waves hide less latency.
 constexpr int kS0FwdTiles = 1;
 constexpr int kS0FwdWaves = kS0FwdTiles == 1 ? 16 : 12;
-constexpr int kS0BwdWaves = 12;  // 167 VGPRs: 3 waves per SIMD, one block per CU
+constexpr int kS0BwdWaves = 16;  // 122 VGPRs: 4 waves per SIMD, one block per CU
 
 __device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -667,18 +667,19 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
     for (int32_t pos = beg; pos < end; pos += 64) {
       const int32_t count = min(end - pos, 64);
       const S0Chunk ch = s0_stage(a, pos, count);
-      for (int t0 = 0; t0 < count; t0 += 16) {
-        // projection columns and contraction rows: edge t0 + j
-        const int ci = t0 + j;
+      for (int t0 = 0; t0 < count; t0 += 8) {
+        // 8-edge tiles: projection column / contraction row j holds edge t0 + (j & 7), its h3 in rows 0..7 and
+        // its t3 in rows 8..15, so one projection and one contraction chain give the gates' Q (rows 0..7) and
+        // the tangents' R (rows 8..15) together
+        const int ci = t0 + (j & 7);
         const bool oki = ci < count;
-        const int32_t ei = __shfl(ch.e, ci);
+        const int32_t ei = __shfl(ch.e, ci & 63);
+        const int32_t si = __shfl(ch.s, ci & 63);
+        const float mi = __shfl(ch.m, ci & 63);
         const int64_t hr = oki ? hrow(a, ei) : 0;
-        const int32_t si = __shfl(ch.s, ci);
-        const float mi = __shfl(ch.m, ci);
-        Split H[2], T[2];
-        load_a(a.h, hr, oki, H);
-        load_a(a.t, hr, oki, T);
-        // sender features of edge t0 + j at channels 16 cb + 4 q .. + 3, times the mask
+        Split A[2];
+        load_a((j & 8) ? a.t : a.h, hr, oki, A);
+        // sender features of the row's edge at channels 16 cb + 4 q .. + 3, times the mask
         float xv[4][4];
 #pragma unroll
         for (int cb = 0; cb < 4; ++cb) {
@@ -687,41 +688,35 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
 #pragma unroll
           for (int r = 0; r < 4; ++r) xv[cb][r] = mi * v[r];
         }
-        v4f Q[PG], R[PG];
+        v4f QR[PG];
 #pragma unroll
         for (int p = 0; p < PG; ++p) {
-          Q[p] = v4f{0.f, 0.f, 0.f, 0.f};
-          R[p] = v4f{0.f, 0.f, 0.f, 0.f};
+          QR[p] = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int cb = 0; cb < 4; ++cb) {
             const SliceOps w = slice_ops(w4l, p, cb);
-            const v4f G = project_block<true>(w, H);
+            const v4f G = project_block<true>(w, A);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) Q[p] = mfma_f32(G[r] * xv[cb][r], gb[cb][r], Q[p]);
-            const v4f Gt = project_block<true>(w, T);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) R[p] = mfma_f32(Gt[r] * xv[cb][r], gb[cb][r], R[p]);
+            for (int r = 0; r < 4; ++r) QR[p] = mfma_f32(G[r] * xv[cb][r], gb[cb][r], QR[p]);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-        // lane (q, j): edges t0 + 4q + r, component j
+        // lane (q, j): rows 4q + r (q < 2: dsh of edge t0 + 4q + r; q >= 2: R of edge t0 + 4(q - 2) + r),
+        // component j
         float dv[4];
         int32_t eo[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int k = t0 + 4 * q + r;
-          eo[r] = __shfl(ch.e, k);
-          float qv = 0.f, rv = 0.f;
+          const int k = t0 + 4 * (q & 1) + r;
+          eo[r] = __shfl(ch.e, k & 63);
+          float v = 0.f;
 #pragma unroll
-          for (int p = 0; p < PG; ++p) {
-            qv = degj == p ? Q[p][r] : qv;
-            rv = degj == p ? R[p][r] : rv;
-          }
+          for (int p = 0; p < PG; ++p) v = degj == p ? QR[p][r] : v;
           const bool ok = k < count && j < NY;
-          dv[r] = ok ? a.sh[(int64_t)eo[r] * NY + j] * rv : 0.f;
-          if (ok && dsh) {
+          dv[r] = ok && q >= 2 ? a.sh[(int64_t)eo[r] * NY + j] * v : 0.f;
+          if (ok && q < 2 && dsh) {
             float* d = dsh + (int64_t)eo[r] * NY + j;
-            *d = acc ? *d + qv : qv;
+            *d = acc ? *d + v : v;
           }
         }
 #pragma unroll
@@ -729,10 +724,10 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
 #pragma unroll
           for (int off = 8; off > 0; off >>= 1) dv[r] += __shfl_xor(dv[r], off);
         }
-        if (j == 0) {
+        if (j == 0 && q >= 2) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (t0 + 4 * q + r < count) {
+            if (t0 + 4 * (q & 1) + r < count) {
               float* d = dr + eo[r];
               *d = acc ? *d + dv[r] : dv[r];
             }
