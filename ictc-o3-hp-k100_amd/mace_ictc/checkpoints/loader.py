@@ -109,11 +109,16 @@ def load_checkpoint(checkpoint_path: str, element_types: List[str], max_radius: 
                     generated_layout: str = "packed", *, _potential_class=LoadedPotential) -> LoadedPotential:
     """Rebuild a baseline MACE-ICTC checkpoint (loader.py:87-1211, the pure-cartesian-ictd-fix route).
 
-    Hyperparameters resolve as in the reference: explicit argument, then the
-    checkpoint's top-level entry, then ``model_hyperparameters``, then the
-    reference's historical defaults (max_radius 5.0, polynomial cutoff p = 6,
-    sqrt(num_basis) radial norm on, 2 interactions); channels, radial basis
-    size, species count and correlation are read from the weights' shapes.
+    Hyperparameters resolve in the reference's order for each of them:
+    max_radius from the checkpoint when it holds one, else the argument, else
+    5.0 (loader.py:138-139); num_interaction and avg_num_neighbors from the
+    argument, else the checkpoint (avg_num_neighbors: its top-level entry, then
+    ``model_hyperparameters``; num_interaction: ``model_hyperparameters``),
+    else 2 / see below (loader.py:164-165, 372-394); the radial options from
+    the checkpoint's top level, then ``model_hyperparameters``, then the
+    historical defaults (polynomial cutoff p = 6, sqrt(num_basis) radial norm
+    on); channels, radial basis size, species count and correlation are read
+    from the weights' shapes.
     avg_num_neighbors is required for correct energies: without it the
     reference's 14.38 fallback is used with a RuntimeWarning (loader.py:372-394).
     """
