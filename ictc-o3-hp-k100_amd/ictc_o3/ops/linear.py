@@ -259,6 +259,83 @@ def _fast_ok(x, weights, C):
             and all(w.numel() > 0 and w.dtype == torch.float32 for w in weights))
 
 
+class _PackedLinearAny(torch.autograd.Function):
+    """The packed linear, differentiable to any order (second-order callers: force-loss training).
+
+    layout = (lmax, Ci, Co, pin, in_off, pout, out_off, scales, out_cols): degree l maps pin[l] input paths
+    of Ci channels to pout[l] output paths of Co channels with W_l [pout Co, pin Ci].  The input adjoint
+    is the same map with W_l^T (itself a _PackedLinearAny, so its derivative is this map again); the
+    weight gradient dW_l = scale_l * dout_l^T x_l over the (node, component) rows runs on the
+    split-reduction kernel (_WeightGrad, differentiable in both operands).  One launch per map instead
+    of one GEMM per degree, and no split / concatenation of the packed rows.
+    """
+
+    @staticmethod
+    def forward(ctx, x, layout, *weights):
+        lmax, Ci, Co, pin, in_off, pout, out_off, scales, out_cols = layout
+        ctx.layout = layout
+        x = x if x.is_contiguous() else x.contiguous()
+        ctx.save_for_backward(x, *weights)
+        ws = [w.detach().contiguous() for w in weights]
+        return _packed_call(x, Ci, Co, lmax, pin, in_off, pout, out_off, ws, scales, out_cols)
+
+    @staticmethod
+    def backward(ctx, dout):
+        from ictc_o3.autograd import required_gradients
+        from ictc_o3.ops.radial_mlp import _WeightGrad
+        x, *ws = ctx.saved_tensors
+        lmax, Ci, Co, pin, in_off, pout, out_off, scales, out_cols = ctx.layout
+        needs = required_gradients((x, *ws), ctx.needs_input_grad[:1] + ctx.needs_input_grad[2:])
+        if dout is None or not any(needs):
+            return (None, None) + (None,) * len(ws)
+        dout = dout if dout.is_contiguous() else dout.contiguous()
+        dx = None
+        if needs[0]:
+            layout_t = (lmax, Co, Ci, pout, out_off, pin, in_off, scales, x.shape[1])
+            dx = _PackedLinearAny.apply(dout, layout_t, *[w.t() for w in ws])
+        N, dws = x.shape[0], []
+        for l, need in enumerate(needs[1:]):
+            if not need:
+                dws.append(None)
+                continue
+            m = 2 * l + 1
+            xin = x[:, in_off[l]:in_off[l] + pin[l] * m * Ci].reshape(N, pin[l], m, Ci).transpose(1, 2) \
+                .reshape(N * m, pin[l] * Ci)
+            dl = dout[:, out_off[l]:out_off[l] + pout[l] * m * Co].reshape(N, pout[l], m, Co).transpose(1, 2) \
+                .reshape(N * m, pout[l] * Co)
+            dws.append(scales[l] * _WeightGrad.apply(dl, xin))
+        return (dx, None, *dws)
+
+
+def degree_linear_any(x, weights, C, lmax, scale=1.0):
+    """degree_linear on the packed kernel, differentiable to any order (composable form where it does
+    not apply)."""
+    if not _fast_ok(x, weights, C) or weights[0].shape[0] % 16:
+        return degree_linear(x, weights, C, lmax, scale)
+    Co = weights[0].shape[0]
+    layout = (lmax, C, Co, [1] * (lmax + 1), [l * l * C for l in range(lmax + 1)], [1] * (lmax + 1),
+              [l * l * Co for l in range(lmax + 1)], [float(scale)] * (lmax + 1), (lmax + 1) ** 2 * Co)
+    return _PackedLinearAny.apply(x, layout, *weights[:lmax + 1])
+
+
+def path_linear_any(m, weights, counts, C, lmax, scale=1.0):
+    """path_linear on the packed kernel, differentiable to any order (composable form where it does not
+    apply)."""
+    if not _fast_ok(m, weights, C) or weights[0].shape[0] % 16 or any(counts.get(l, 0) == 0 for l in range(lmax + 1)):
+        return path_linear(m, weights, counts, C, lmax, scale)
+    Co = weights[0].shape[0]
+    pin, in_off, off = [], [], 0
+    for l in range(lmax + 1):
+        pin.append(counts[l])
+        in_off.append(off)
+        off += counts[l] * (2 * l + 1) * C
+    if off != m.shape[1]:
+        return path_linear(m, weights, counts, C, lmax, scale)
+    layout = (lmax, C, Co, pin, in_off, [1] * (lmax + 1), [l * l * Co for l in range(lmax + 1)],
+              [float(scale)] * (lmax + 1), (lmax + 1) ** 2 * Co)
+    return _PackedLinearAny.apply(m, layout, *weights[:lmax + 1])
+
+
 def degree_linear_fast(x, weights, C, lmax, scale=1.0):
     """degree_linear on the MFMA kernel (first derivatives only)."""
     if not _fast_ok(x, weights, C):

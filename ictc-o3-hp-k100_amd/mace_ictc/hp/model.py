@@ -57,9 +57,10 @@ def _mace_linear_init(linear: nn.Linear):
 def degree_linear(x, weights: List[torch.Tensor], C: int, lmax: int, scale: float = 1.0, first_order=False):
     """Per-degree channel map on the packed layout: out[n, l*l+m, :] = scale * W_l @ x[n, l*l+m, :].
 
-    first_order=True runs the MFMA kernel, whose adjoint supports first derivatives only."""
-    from ictc_o3.ops.linear import degree_linear as impl, degree_linear_fast
-    return (degree_linear_fast if first_order else impl)(x, weights, C, lmax, scale)
+    first_order=True runs the MFMA kernel with a first-derivative adjoint; otherwise the same kernel with
+    adjoints differentiable to any order (the composable per-degree form where the kernel does not apply)."""
+    from ictc_o3.ops.linear import degree_linear_any, degree_linear_fast
+    return (degree_linear_fast if first_order else degree_linear_any)(x, weights, C, lmax, scale)
 
 
 class ChannelLinear(nn.Module):
@@ -93,8 +94,8 @@ class PathPreservingLinear(nn.Module):
             self.weights[str(l)] = w
 
     def forward(self, m, scale: float, first_order=False):
-        from ictc_o3.ops.linear import path_linear, path_linear_fast
-        return (path_linear_fast if first_order else path_linear)(
+        from ictc_o3.ops.linear import path_linear_any, path_linear_fast
+        return (path_linear_fast if first_order else path_linear_any)(
             m, [self.weights[str(l)] for l in range(self.lmax + 1)], self.counts, self.channels, self.lmax, scale)
 
 

@@ -100,3 +100,47 @@ def test_graph_sum_exact_and_repeatable(device):
     w = torch.randn(37, generator=g, dtype=torch.float64)
     (gv,) = torch.autograd.grad((out * w.to(device)).sum(), vd)
     assert torch.equal(gv.cpu(), w[batch].float())
+
+
+@pytest.mark.parametrize("kind,C,lmax,N", [("degree", 64, 2, 300), ("path", 128, 2, 129), ("degree", 32, 3, 77)])
+def test_packed_linear_any_order(device, kind, C, lmax, N):
+    """The any-order packed linear (second-order callers): output, first derivatives and the derivative of
+    a first-derivative quantity (double backward through the adjoint and the weight gradients) vs float64
+    autograd of the composable form."""
+    from ictc_o3.ops.linear import degree_linear, degree_linear_any, path_linear, path_linear_any
+    g = torch.Generator().manual_seed(C + lmax + N)
+    counts = {0: 3, 1: 4, 2: 4, 3: 2}
+    if kind == "degree":
+        width_in = (lmax + 1) ** 2 * C
+        Ws = [torch.randn(C, C, generator=g, dtype=torch.float64) / C ** 0.5 for _ in range(lmax + 1)]
+        ref_fn = lambda x, W: degree_linear(x, W, C, lmax, 0.7)
+        fn = lambda x, W: degree_linear_any(x, W, C, lmax, 0.7)
+    else:
+        width_in = sum(counts[l] * (2 * l + 1) for l in range(lmax + 1)) * C
+        Ws = [torch.randn(C, counts[l] * C, generator=g, dtype=torch.float64) / (counts[l] * C) ** 0.5
+              for l in range(lmax + 1)]
+        ref_fn = lambda x, W: path_linear(x, W, counts, C, lmax, 1 / 42.0)
+        fn = lambda x, W: path_linear_any(x, W, counts, C, lmax, 1 / 42.0)
+    x = torch.randn(N, width_in, generator=g, dtype=torch.float64)
+    go = torch.randn(N, (lmax + 1) ** 2 * C, generator=g, dtype=torch.float64)
+    v = torch.randn(N, width_in, generator=g, dtype=torch.float64)
+
+    def run(f, xs, Wl):
+        xs = xs.clone().requires_grad_(True)
+        Wl = [w.clone().requires_grad_(True) for w in Wl]
+        out = f(xs, Wl)
+        dx, *dW = torch.autograd.grad(out, [xs] + Wl, go.to(out), create_graph=True)
+        # a scalar of the first derivatives, differentiated again (the force-loss pattern)
+        s = (dx * v.to(dx)).sum() + sum((d ** 2).sum() for d in dW)
+        gg = torch.autograd.grad(s, [xs] + Wl, allow_unused=True)
+        return out, [dx] + dW, gg
+
+    out0, d0, gg0 = run(ref_fn, x, Ws)
+    out1, d1, gg1 = run(fn, x.float().to(device), [w.float().to(device) for w in Ws])
+    assert rel_err(out1, out0) < 1e-5
+    for a, b in zip(d1, d0):
+        assert rel_err(a, b) < 1e-5
+    for a, b in zip(gg1, gg0):
+        if b is None:
+            continue
+        assert rel_err(a, b) < 1e-5
