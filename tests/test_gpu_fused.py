@@ -100,11 +100,12 @@ def test_fused_message_matches_oracle(device, N, E, C, li, mask):
     assert torch.equal(out, out2) and torch.equal(dx, dx2) and torch.equal(dsh, dsh2) and torch.equal(dr, dr2)
 
 
-@pytest.mark.parametrize("N,E,C,mask", [(50, 1500, 64, True), (40, 1100, 128, True), (33, 29, 64, False)])
+@pytest.mark.parametrize("N,E,C,mask", [(50, 1500, 64, True), (40, 1100, 128, True), (33, 29, 64, False),
+                                         (10, 1500, 64, True)])
 def test_fused_scalar_input_receiver_adjoint(device, N, E, C, mask):
     """Input degree 0 without a feature gradient (the model's first layer): the receiver-owned adjoint
     (harmonic and edge-length gradients only) and the forward, against the oracle; partial edge tiles,
-    two channel groups, masks and out-of-range ids."""
+    two channel groups, masks, out-of-range ids, and receivers with several 64-edge chunks (N = 10)."""
     li = 0
     x, sh, r, src, dst, m, Ws = _case(N, E, C, li, 300 + N, mask)
     go = torch.randn(N, 9 * C, generator=torch.Generator().manual_seed(9), dtype=torch.float64)
