@@ -121,6 +121,32 @@ def test_message_second_raw_abi(device):
     assert torch.count_nonzero(full[1][~k]) == 0 and torch.count_nonzero(full[2][~k]) == 0
 
 
+@pytest.mark.parametrize("li,le,lo,C,need", [(2, 2, 2, 64, (True, True, True)), (2, 3, 3, 128, (True, True, True)),
+                                             (2, 2, 2, 64, (False, True, True)), (0, 3, 3, 128, (False, False, True))])
+def test_message_adjoint_accumulates_gate_gradient(device, li, le, lo, C, need):
+    """ictc_msg_bwd_accumulate: the gate gradient is added to the rows dgates holds (bitwise the stored rows
+    plus ictc_msg_bwd's gate gradient), the other outputs are ictc_msg_bwd's; one-pass source-owned and
+    two-kernel routes, masks and out-of-range ids."""
+    from ictc_o3.ops import tensor_product as tpo
+    N, E = 60, 2400
+    f64, sh64, g64, src, dst, m64 = _graph(N, E, C, li, le, lo, 77, mask=True)
+    src[::11] = N + 1
+    spec = tpo.make_spec(li, le, lo, C)
+    topo = tpo.Topology(src.to(device), dst.to(device), N)
+    x, sh, gt = (t.float().to(device) for t in (f64, sh64, g64))
+    m = m64.float().to(device)
+    go = torch.randn(N, spec.out_components * C, device=device, generator=torch.Generator(device=device).manual_seed(3))
+    dx0, dsh0, dg0 = tpo._msg_bwd_raw(spec, topo, x, sh, gt, m, go, need)
+    held = torch.randn_like(gt)
+    expect = held + dg0
+    dx1, dsh1, dg1 = tpo._msg_bwd_raw(spec, topo, x, sh, gt, m, go, need, dg_into=held)
+    assert dg1 is held and torch.equal(dg1, expect)
+    for a, b in ((dx0, dx1), (dsh0, dsh1)):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
+
+
 def test_message_deterministic_bitwise(device):
     from ictc_o3 import PackedGraphMessage
     op = PackedGraphMessage.create(channels=64, input_lmax=2, edge_lmax=2, device=device)
