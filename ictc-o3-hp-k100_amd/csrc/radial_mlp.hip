@@ -184,10 +184,15 @@ __device__ __forceinline__ void stage_adj(AdjWeights& w, const float* __restrict
 // The weight formats are loop invariant: without this the compiler hoists every
 // LDS operand read out of the tile loop and spills.  Passing the LDS pointer
 // through an empty asm statement each tile keeps the reads next to their MFMAs.
+// What crosses the asm is the 32-bit LDS address: a generic pointer would leave
+// the compiler unable to tell the reads are LDS reads, and it would emit flat
+// loads, which also wait on the vector-memory counter behind the wave's stores.
 template <class T>
 __device__ __forceinline__ const T* opaque(const T* p) {
-  asm volatile("" : "+v"(p));
-  return p;
+  typedef const T __attribute__((address_space(3))) * LdsPtr;
+  LdsPtr q = (LdsPtr)p;
+  asm volatile("" : "+v"(q));
+  return (const T*)q;
 }
 
 // acc[nb] (units 16*nb + 4*(l/16) + r of the lane's edge) = sum_k A[unit][k] B[k],
@@ -510,6 +515,164 @@ __global__ __launch_bounds__(GATE_TILES * 64, 2) void gates_fwd_kernel(
   }
 }
 
+// W4-resident projection (gates <= RES_MAX_GATES): the grouped kernel above
+// streams its 6 KB of split W4 operands per row block from L2 inside the store
+// loop, and every wait for them also waits for the stores issued before them
+// (one vector-memory counter), which keeps its single wave per SIMD well below
+// the write rate.  Here each of a block's 8 waves keeps its share of the split
+// W4 in registers for the whole launch, and the 16-edge tiles reach every wave
+// through a double-buffered LDS ring (4 tiles per group): while all waves
+// project group k, waves 4..7 each run the MLP of one tile of group k + 1 into
+// the other ring slot, radii read through the scalar cache.  Waves 0..3 hold 7
+// row blocks (rb = w + 4j), waves 4..7, which also run the MLP, hold 4
+// (rb = 28 + (w - 4) + 4j): 44 row blocks, 704 gates.  The store loop issues no
+// vector loads at all; one barrier per 64-edge group.
+constexpr int RES_WAVES = 8;
+constexpr int RES_RB_PROJ = 7;                                          // row blocks of waves 0..3
+constexpr int RES_RB_DUTY = 4;                                          // row blocks of waves 4..7
+constexpr int RES_MAX_GATES = 4 * 16 * (RES_RB_PROJ + RES_RB_DUTY);    // 704
+constexpr int RES_TILES = 4;                                            // 16-edge tiles per group
+
+template <int KINDS>
+struct ResRing {
+  bf16x8 b[2][RES_TILES][KINDS][2][3][64];  // [slot][tile][value, tangent][ks][part][lane]
+};
+
+// The lane's radius (edge e0 + l%16) of a tile, through 16 scalar loads (indices
+// clamped to the last edge; lanes past it take `dflt`): no vector load, whose
+// wait would also wait for the wave's pending stores.
+__device__ __forceinline__ float tile_radius(const float* __restrict__ r, int64_t e0, int64_t E, float dflt) {
+  const int i = threadIdx.x & 15;
+  float x = r[e0 < E - 1 ? e0 : E - 1];
+#pragma unroll
+  for (int j = 1; j < 16; ++j) {
+    const float v = r[e0 + j < E - 1 ? e0 + j : E - 1];
+    x = i == j ? v : x;
+  }
+  return e0 + i < E ? x : dflt;
+}
+
+// C row blocks (rb0 + 4j) of one tile: 12 split-bf16 MFMA steps on C independent chains, then the stores.
+template <int C, int CMAX>
+__device__ __forceinline__ void res_project(const bf16x8 (&A)[CMAX][2][3], const Split* B, float* __restrict__ out,
+                                            int64_t e, int64_t E, int M, int rb0) {
+  const int g = (threadIdx.x & 63) >> 4;
+  v4f acc[C];
+#pragma unroll
+  for (int j = 0; j < C; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+#define ICTC_STEP(PA, PB, KS) \
+  _Pragma("unroll") for (int j = 0; j < C; ++j) acc[j] = mfma16(A[j][KS][PA], B[KS].p[PB], acc[j]);
+  ICTC_STEP(2, 0, 0) ICTC_STEP(0, 2, 0) ICTC_STEP(1, 1, 0)
+  ICTC_STEP(2, 0, 1) ICTC_STEP(0, 2, 1) ICTC_STEP(1, 1, 1)
+  ICTC_STEP(1, 0, 0) ICTC_STEP(0, 1, 0) ICTC_STEP(1, 0, 1)
+  ICTC_STEP(0, 1, 1) ICTC_STEP(0, 0, 0) ICTC_STEP(0, 0, 1)
+#undef ICTC_STEP
+  if (e < E) {
+#pragma unroll
+    for (int j = 0; j < C; ++j) *reinterpret_cast<v4f*>(out + e * M + 16 * (rb0 + 4 * j) + 4 * g) = acc[j];
+  }
+}
+
+// Runtime row-block count n <= C to a compile-time chain count.
+template <int C, int CMAX>
+__device__ __forceinline__ void res_project_n(int n, const bf16x8 (&A)[CMAX][2][3], const Split* B,
+                                              float* __restrict__ out, int64_t e, int64_t E, int M, int rb0) {
+  if (n == C) res_project<C>(A, B, out, e, E, M, rb0);
+  else if constexpr (C > 1) res_project_n<C - 1>(n, A, B, out, e, E, M, rb0);
+}
+
+// One wave's whole launch: C row blocks held in registers; DUTY waves also run
+// the MLP of one tile of the next group in every iteration.  The two roles are
+// separate instantiations, so the MLP's registers only meet 4 row blocks.
+template <bool TAN, int C, bool DUTY>
+__device__ __forceinline__ void res_wave(const float* __restrict__ r, int64_t E, float rc, int p, float s,
+                                         const bf16x8* __restrict__ w4s, int M, float* __restrict__ gates,
+                                         float* __restrict__ gdot, const FwdWeights& ws,
+                                         ResRing<TAN ? 2 : 1>& ring, int w) {
+  constexpr int KINDS = TAN ? 2 : 1;
+  const int l = threadIdx.x & 63, i = l & 15;
+  const int nrb = M / 16;
+  const int rb0 = DUTY ? 4 * RES_RB_PROJ + (w - 4) : w;
+  int cnt = nrb > rb0 ? (nrb - rb0 + 3) / 4 : 0;
+  cnt = cnt < C ? cnt : C;
+  bf16x8 A[C][2][3];
+#pragma unroll
+  for (int j = 0; j < C; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int pt = 0; pt < 3; ++pt)
+        A[j][ks][pt] = j < cnt ? w4s[((int64_t)(rb0 + 4 * j) * 6 + ks * 3 + pt) * 64 + l] : bf16x8{};
+  // complete the row-block loads here, not at a first use inside the loop (whose wait would recur every iteration)
+#pragma unroll
+  for (int j = 0; j < C; ++j)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int pt = 0; pt < 3; ++pt) asm volatile("" : "+v"(A[j][ks][pt]));
+  const Radial q = radial_consts(rc, p);
+  const int64_t groups = (E + 16 * RES_TILES - 1) / (16 * RES_TILES);
+  auto mlp = [&](int64_t grp, int buf) {
+    const int t = w - 4;
+    const int64_t e0 = 16 * (RES_TILES * grp + t);
+    const float x = tile_radius(r, e0, E, 2.f * rc);
+    const FwdWeights& wf = *opaque(&ws);
+    v4f a[4];
+    Split B[2];
+    if (TAN) {
+      v4f t3[4];
+      forward_tangent_tile(wf, q, x, s, a, t3);
+      split_units(t3, B);
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 3; ++pt) ring.b[buf][t][KINDS - 1][ks][pt][l] = B[ks].p[pt];
+    } else {
+      float db[2];
+      forward_tile<false>(wf, q, x, s, a, nullptr, nullptr, nullptr, db, nullptr, nullptr, e0 + i, false);
+    }
+    split_units(a, B);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int pt = 0; pt < 3; ++pt) ring.b[buf][t][0][ks][pt][l] = B[ks].p[pt];
+  };
+  // Iteration k runs the MLP of group k + 1 and projects group k; k = -1 only fills
+  // the first slot (one MLP call site, so every tile's gates come from the same code).
+  int k = -1;
+  for (int64_t grp = (int64_t)blockIdx.x - gridDim.x; grp < groups; grp += gridDim.x, ++k) {
+    const int64_t nxt = grp + gridDim.x;
+    if (DUTY && nxt < groups) mlp(nxt, (k + 1) & 1);
+    const ResRing<KINDS>& rg = *opaque(&ring);
+#pragma unroll 1
+    for (int tk = 0; tk < (grp >= 0 ? RES_TILES * KINDS : 0); ++tk) {
+      const int t = tk / KINDS, kind = tk % KINDS;
+      Split B[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int pt = 0; pt < 3; ++pt) B[ks].p[pt] = rg.b[k & 1][t][kind][ks][pt][l];
+      res_project_n<C>(cnt, A, B, kind ? gdot : gates, 16 * (RES_TILES * grp + t) + i, E, M, rb0);
+    }
+    __syncthreads();  // the slot just read is rewritten in the next iteration
+  }
+}
+
+// Block of 8 waves, one block per CU (M <= RES_MAX_GATES).
+template <bool TAN>
+__global__ __launch_bounds__(RES_WAVES * 64, 1) void gates_res_kernel(
+    const float* __restrict__ r, int64_t E, float rc, int p, const float* __restrict__ W1,
+    const float* __restrict__ W2, const float* __restrict__ W3, float s, const bf16x8* __restrict__ w4s, int M,
+    float* __restrict__ gates, float* __restrict__ gdot) {
+  __shared__ FwdWeights ws;
+  __shared__ ResRing<TAN ? 2 : 1> ring;
+  stage_fwd(ws, W1, W2, W3);
+  __syncthreads();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (w < 4) res_wave<TAN, RES_RB_PROJ, false>(r, E, rc, p, s, w4s, M, gates, gdot, ws, ring, w);
+  else res_wave<TAN, RES_RB_DUTY, true>(r, E, rc, p, s, w4s, M, gates, gdot, ws, ring, w);
+}
+
 // Narrow projections with r tangents (M <= 256 gates, e.g. an l = 0 input
 // layer's 3 paths x 64): the split W4 (M * 384 bytes) fits in LDS beside the
 // MLP weights, so every wave projects its own 16-edge tile (values and
@@ -693,6 +856,13 @@ int gates_tangent_launch(const float* r, int64_t edges, float cutoff, int poly_p
                        (const bf16x8*)ws, gates, out, tangent);
     return launch_status("ictc_radial_gates_tangent_fwd launch");
   }
+  if (gates <= RES_MAX_GATES) {
+    const int64_t groups = (edges + 16 * RES_TILES - 1) / (16 * RES_TILES), cap = cu_count();
+    hipLaunchKernelGGL(gates_res_kernel<true>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(RES_WAVES * 64),
+                       0, st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)ws, gates, out,
+                       tangent);
+    return launch_status("ictc_radial_gates_tangent_fwd launch");
+  }
   const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
   const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel<true>, GATE_TILES * 64, 3);
   hipLaunchKernelGGL(gates_fwd_kernel<true>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0,
@@ -785,6 +955,13 @@ int ictc_radial_gates_fwd(const float* r, int64_t edges, int num_basis, int hidd
   hipLaunchKernelGGL(gates_split_kernel, dim3((split_threads + 255) / 256), dim3(256), 0, st, W4, gates,
                      (bf16x8*)workspace);
   if (int rc = launch_status("ictc_radial_gates_fwd split")) return rc;
+  if (gates > SMALL_MAX_GATES && gates <= RES_MAX_GATES) {
+    const int64_t groups = (edges + 16 * RES_TILES - 1) / (16 * RES_TILES), cap = cu_count();
+    hipLaunchKernelGGL(gates_res_kernel<false>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(RES_WAVES * 64),
+                       0, st, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, (const bf16x8*)workspace, gates,
+                       out, nullptr);
+    return launch_status("ictc_radial_gates_fwd launch");
+  }
   const int64_t groups = (edges + 16 * GATE_TILES - 1) / (16 * GATE_TILES);
   const int64_t cap = (int64_t)cu_count() * resident_per_cu(gates_fwd_kernel<false>, GATE_TILES * 64, 3);
   hipLaunchKernelGGL(gates_fwd_kernel<false>, dim3((unsigned)(groups < cap ? groups : cap)), dim3(GATE_TILES * 64), 0,

@@ -35,7 +35,8 @@ def _fc(out, Ws, device):
     return fc
 
 
-@pytest.mark.parametrize("E,out", [(1000, 704), (77, 192), (4099, 64), (33, 2176)])
+@pytest.mark.parametrize("E,out", [(1000, 704), (77, 192), (4099, 64), (33, 2176), (40001, 704), (5, 704), (300, 464),
+                                   (129, 272)])
 def test_radial_gates_tangent(device, E, out):
     from ictc_o3.ops.radial_mlp import radial_gates, radial_gates_tangent
     g = torch.Generator().manual_seed(E + out)

@@ -22,7 +22,7 @@ def _ref_gates(r, Ws, cutoff, p):
     return h
 
 
-@pytest.mark.parametrize("E,out", [(1000, 704), (77, 192), (4099, 64)])
+@pytest.mark.parametrize("E,out", [(1000, 704), (77, 192), (4099, 64), (40001, 704), (17, 272), (300, 464)])
 def test_fused_radial_gates(device, E, out):
     from ictc_o3.ops.radial_mlp import radial_gates
     g = torch.Generator().manual_seed(E)
