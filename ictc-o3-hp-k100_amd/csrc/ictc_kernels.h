@@ -166,13 +166,13 @@ __device__ __forceinline__ void store_dg_row(const Operands& a, float* __restric
   store_row<N>(base, C, c, v);
 }
 
-// Gates of edge e for channel c, times the per-path weight (if any) and `scale`.
+// Gates of gate row `row` for channel c, times the per-path weight (if any) and `scale`.
 // All P gate loads are issued before any use so they are in flight together;
 // the optional weight is a separate uniform branch after them.
 template <class T, bool STREAM = false>
-__device__ __forceinline__ void load_gw(const Operands& a, int64_t e, int c, float scale, float* gw) {
-  if (STREAM) load_row_stream<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * a.channels), a.channels, c, gw);
-  else load_row<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * a.channels), a.channels, c, gw);
+__device__ __forceinline__ void load_gw(const Operands& a, int64_t row, int c, float scale, float* gw) {
+  if (STREAM) load_row_stream<T::P>(a.gates + row * (int64_t)(T::P * a.channels), a.channels, c, gw);
+  else load_row<T::P>(a.gates + row * (int64_t)(T::P * a.channels), a.channels, c, gw);
   if (a.weight) {
     float w[T::P];
 #pragma unroll
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeFwd, T::LI, T::LE, T::LO>::
   float y[T::NY], xv[T::NX], gw[T::P], o[T::NO];
   load_harmonics<T>(a.sh, e, y);
   load_row<T::NX>(a.x + e * (int64_t)(T::NX * C), C, c, xv);
-  load_gw<T>(a, e, c, 1.f, gw);
+  load_gw<T>(a, gate_row(a, e), c, 1.f, gw);
 #pragma unroll
   for (int k = 0; k < T::NO; ++k) o[k] = 0.f;
   T::fwd(xv, y, gw, o);
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
     float xv[T::NX], gw[T::P], go[T::NO];
     load_row<T::NX>(a.x + e * (int64_t)(T::NX * C), C, c, xv);
     load_row<T::NO>(grad + e * (int64_t)(T::NO * C), C, c, go);
-    load_gw<T>(a, e, c, 1.f, gw);
+    load_gw<T>(a, gate_row(a, e), c, 1.f, gw);
     if (dx) {
       float d[T::NX];
 #pragma unroll
@@ -351,6 +351,8 @@ __device__ __forceinline__ bool row_part(const Csr& csr, int64_t n, int part, in
 template <class T>
 struct Chunk {
   int32_t e;        // edge id of this lane's position
+  int32_t row;      // its gate row (staged with the chunk: a per-edge index load inside the edge loop
+                    // would be a vector load whose wait also drains the rows already in flight)
   int32_t peer;     // src (receiver-sorted CSR) or dst (source-sorted CSR); 0 when out of range
   float m;          // mask, 0 when the peer is out of range or the lane is past the chunk
   float y[T::NY];   // harmonics of this lane's edge
@@ -362,6 +364,7 @@ __device__ __forceinline__ void stage_chunk(const Operands& a, const int64_t* __
                                             Chunk<T>& ch) {
   const int l = lane_id();
   ch.e = 0;
+  ch.row = 0;
   ch.peer = 0;
   ch.m = 0.f;
 #pragma unroll
@@ -371,17 +374,32 @@ __device__ __forceinline__ void stage_chunk(const Operands& a, const int64_t* __
     const int64_t p = peer_ids[e];
     const bool ok = p >= 0 && p < a.rows;
     ch.e = e;
+    ch.row = a.grow ? a.grow[e] : e;
     ch.peer = ok ? (int32_t)p : 0;
     ch.m = ok ? (a.mask ? a.mask[e] : 1.f) : 0.f;
 #pragma unroll
     for (int j = 0; j < T::NY; ++j) ch.y[j] = a.sh[(int64_t)e * T::NY + j];
   }
+  // The chunk's loads complete here, once per chunk.  Left to their first use inside the edge loop,
+  // the wait for them would recur at every edge (some paths through the loop body do not use them)
+  // and would also drain the next edge's rows already in flight.
+  asm volatile("" : "+v"(ch.e), "+v"(ch.row), "+v"(ch.peer), "+v"(ch.m));
+#pragma unroll
+  for (int j = 0; j < T::NY; ++j) asm volatile("" : "+v"(ch.y[j]));
 }
 
 __device__ __forceinline__ int32_t lane_i(int32_t v, int i) { return __builtin_amdgcn_readlane(v, i); }
 __device__ __forceinline__ float lane_f(float v, int i) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
 }
+
+// Compile-time flag for generic lambdas: the edge loops below are compiled once with and once without
+// the per-path weight, chosen once per wave.  A weight branch inside the loop loads the weights per
+// edge, and the wait where its paths merge drains the next edge's rows already in flight.
+template <bool B>
+struct Flag {
+  static constexpr bool value = B;
+};
 
 // The forward keeps two edges' feature and gate rows in flight (loads of edge i + 1 issued before
 // edge i's products) where the per-lane state stays small, NX + NY + P + NO <= 64 values with input
@@ -407,15 +425,17 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
   for (int k = 0; k < T::NO; ++k) o[k] = 0.f;
   const int32_t beg = csr.ptr[n], end = csr.ptr[n + 1];
   if constexpr (msg_fwd_pipelined<T>()) {
+    auto run = [&](auto weighted) {
+    constexpr bool W = decltype(weighted)::value;
     for (int32_t pos = beg; pos < end; pos += kWave) {
       const int32_t count = min(end - pos, kWave);
       Chunk<T> ch;
       stage_chunk<T>(a, src, csr.order, pos, count, ch);
       float x0[T::NX], g0[T::P], x1[T::NX], g1[T::P];
       auto fetch = [&](int i, float* xv, float* gr) {
-        const int64_t e = lane_i(ch.e, i), s = lane_i(ch.peer, i);
+        const int64_t s = lane_i(ch.peer, i), row = lane_i(ch.row, i);
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
-        load_row<T::P>(a.gates + gate_row(a, e) * (int64_t)(T::P * C), C, c, gr);
+        load_row<T::P>(a.gates + row * (int64_t)(T::P * C), C, c, gr);
       };
       auto consume = [&](int i, const float* xv, const float* gr) {
         const float m = lane_f(ch.m, i);
@@ -424,7 +444,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
         for (int j = 0; j < T::NY; ++j) y[j] = lane_f(ch.y[j], i);
 #pragma unroll
         for (int p = 0; p < T::P; ++p) gw[p] = gr[p];
-        if (a.weight) {
+        if constexpr (W) {
 #pragma unroll
           for (int p = 0; p < T::P; ++p) gw[p] *= a.weight[p * C + c];
         }
@@ -442,6 +462,9 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
         consume(i + 1, x1, g1);
       }
     }
+    };
+    if (a.weight) run(Flag<true>{});
+    else run(Flag<false>{});
     if (active) store_row<T::NO>(out + n * (int64_t)(T::NO * C), C, c, o);
     return;
   }
@@ -459,7 +482,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgFwd, T::LI, T::LE, T::LO>::v
       if (active) {
         float xv[T::NX], gw[T::P];
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
-        load_gw<T>(a, e, c, m, gw);
+        load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
         T::fwd_b(xv, y, gw, o);
       }
     }
@@ -496,11 +519,12 @@ __device__ __forceinline__ void store_dsh_dr(float* __restrict__ dsh_g, float* _
 }
 
 // This lane's share of the gate-tangent dot: sum_p dg[p] w[p] gdot[p] (dg unweighted, unmasked).
-template <class T>
+// W: 1 / 0 = with / without the per-path weight, known at compile time; -1 = tested at run time.
+template <class T, int W = -1>
 __device__ __forceinline__ float gate_tangent_dot(const Operands& a, const float* __restrict__ gdot, int64_t e, int c,
                                                   const float* gt, const float* dg) {
   float t = 0.f;
-  if (a.weight) {
+  if (W == 1 || (W < 0 && a.weight)) {
 #pragma unroll
     for (int p = 0; p < T::P; ++p) t += dg[p] * a.weight[p * a.channels + c] * gt[p];
   } else {
@@ -566,8 +590,8 @@ __global__ __launch_bounds__(kBlock, (edge_adjoint_waves<T, TAN>())) void msg_bw
       if (TAN && active) {
         float xv[T::NX], gw[T::P], gt[T::P], d[T::P];
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
-        load_gw<T>(a, e, c, m, gw);
-        load_row<T::P>(gdot + gate_row(a, e) * (int64_t)(T::P * C), C, c, gt);
+        load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
+        load_row<T::P>(gdot + lane_i(ch.row, i) * (int64_t)(T::P * C), C, c, gt);
         if (dsh) T::dydg(xv, y, gw, go, dyv, d);
         else T::dg(xv, y, go, d);
         dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, d);
@@ -579,7 +603,7 @@ __global__ __launch_bounds__(kBlock, (edge_adjoint_waves<T, TAN>())) void msg_bw
       if (active) {
         float xv[T::NX], gw[T::P];
         load_row<T::NX>(a.x + s * (int64_t)(T::NX * C), C, c, xv);
-        load_gw<T>(a, e, c, m, gw);
+        load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
         float d[T::P];
         if (dsh && dgates) T::dydg(xv, y, gw, go, dyv, d);
         else if (dsh) T::dy(xv, gw, go, dyv);
@@ -633,7 +657,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::
       if (active) {
         float go[T::NO], gw[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
-        load_gw<T>(a, e, c, m, gw);
+        load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
         T::dx(y, gw, go, d);
       }
     }
@@ -691,13 +715,15 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
     // Two edges in flight: the cotangent, gate and gate-tangent rows of edge i + 1 load while edge i
     // computes (2 waves per SIMD leave room for the second set of rows).  Per-edge arithmetic is that
     // of the unpipelined form, operand for operand.
+    auto run = [&](auto weighted) {
+    constexpr bool W = decltype(weighted)::value;
     for (int32_t pos = beg; pos < end; pos += kWave) {
       const int32_t count = min(end - pos, kWave);
       Chunk<T> ch;
       stage_chunk<T>(a, dst, scsr.order, pos, count, ch);
       float go0[T::NO], gr0[T::P], gt0[T::P], go1[T::NO], gr1[T::P], gt1[T::P];
       auto fetch = [&](int i, float* go, float* gr, float* gt) {
-        const int64_t e = lane_i(ch.e, i), r = lane_i(ch.peer, i), row = gate_row(a, e);
+        const int64_t r = lane_i(ch.peer, i), row = lane_i(ch.row, i);
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
         load_row_stream<T::P>(a.gates + row * (int64_t)(T::P * C), C, c, gr);
         load_row_stream<T::P>(gdot + row * (int64_t)(T::P * C), C, c, gt);
@@ -715,7 +741,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
         if (active) {
 #pragma unroll
           for (int p = 0; p < T::P; ++p) gw[p] = gr[p];
-          if (a.weight) {
+          if constexpr (W) {
 #pragma unroll
             for (int p = 0; p < T::P; ++p) gw[p] *= a.weight[p * C + c];
           }
@@ -724,7 +750,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
           if (!tail) T::dx(y, gw, go, d);
           if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
           else T::dg(xv, y, go, dg);
-          dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, dg);
+          dgt = m * gate_tangent_dot<T, W ? 1 : 0>(a, gdot, e, c, gt, dg);
         }
         store_dsh_dr<T::NY>(dsh_g, dr_g, e, dyv, dgt);
       };
@@ -737,6 +763,9 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
         consume(i + 1, go1, gr1, gt1);
       }
     }
+    };
+    if (a.weight) run(Flag<true>{});
+    else run(Flag<false>{});
     if (active && !tail && dx) store_row<T::NX>(dx + n * (int64_t)(T::NX * C), C, c, d);
     return;
   }
@@ -759,8 +788,8 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
       if (TAN && active) {
         float go[T::NO], gw[T::P], gt[T::P], dg[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
-        load_gw<T, true>(a, e, c, m, gw);
-        load_row_stream<T::P>(gdot + gate_row(a, e) * (int64_t)(T::P * C), C, c, gt);
+        load_gw<T, true>(a, lane_i(ch.row, i), c, m, gw);
+        load_row_stream<T::P>(gdot + lane_i(ch.row, i) * (int64_t)(T::P * C), C, c, gt);
         if (!tail) T::dx(y, gw, go, d);
         if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
         else T::dg(xv, y, go, dg);
@@ -773,7 +802,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
       if (active) {
         float go[T::NO], gw[T::P], dg[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
-        load_gw<T>(a, e, c, m, gw);
+        load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
         if (!tail) T::dx(y, gw, go, d);
         if (dsh && dgates) T::dydg(xv, y, gw, go, dyv, dg);
         else if (dsh) T::dy(xv, gw, go, dyv);
