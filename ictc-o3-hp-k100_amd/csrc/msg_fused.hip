@@ -541,20 +541,24 @@ __device__ __forceinline__ v4f project_block(const SliceOps& w, const Split* A) 
 
 // Edge id, sender and mask of up to 64 consecutive CSR positions, one edge per lane.
 struct S0Chunk {
-  int32_t e, s;
+  int32_t e, s, row;  // edge, sender, its h / t row
   float m;
 };
 __device__ __forceinline__ S0Chunk s0_stage(const FusedArgs& a, int32_t pos, int32_t count) {
   const int l = lane_id();
-  S0Chunk ch{0, 0, 0.f};
+  S0Chunk ch{0, 0, 0, 0.f};
   if (l < count) {
     const int32_t e = a.csr.order ? a.csr.order[pos + l] : pos + l;
     const int64_t p = a.peer[e];
     const bool ok = p >= 0 && p < a.rows;
     ch.e = e;
     ch.s = ok ? (int32_t)p : 0;
+    ch.row = (int32_t)hrow(a, e);
     ch.m = ok ? (a.mask ? a.mask[e] : 1.f) : 0.f;
   }
+  // complete the chunk's loads here, once per chunk: a per-tile index load or a first use inside the
+  // tile loop would wait, with the same counter, for the previous tile's stores
+  asm volatile("" : "+v"(ch.e), "+v"(ch.s), "+v"(ch.row), "+v"(ch.m));
   return ch;
 }
 
@@ -587,8 +591,8 @@ __global__ __launch_bounds__(kS0FwdWaves * 64, 1) void msg_s0_fwd_kernel(FusedAr
 #pragma unroll
         for (int u = 0; u < kS0FwdTiles; ++u) {
           const int ci = t0 + 16 * u + j;
-          const int32_t ei = __shfl(ch.e, ci & 63);
-          load_a(a.h, ci < count ? hrow(a, ei) : 0, ci < count, A[u]);
+          const int32_t ri = __shfl(ch.row, ci & 63);
+          load_a(a.h, ci < count ? ri : 0, ci < count, A[u]);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int k = t0 + 16 * u + 4 * q + r;
@@ -673,10 +677,9 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
         // the tangents' R (rows 8..15) together
         const int ci = t0 + (j & 7);
         const bool oki = ci < count;
-        const int32_t ei = __shfl(ch.e, ci & 63);
         const int32_t si = __shfl(ch.s, ci & 63);
         const float mi = __shfl(ch.m, ci & 63);
-        const int64_t hr = oki ? hrow(a, ei) : 0;
+        const int64_t hr = oki ? __shfl(ch.row, ci & 63) : 0;
         Split A[2];
         load_a((j & 8) ? a.t : a.h, hr, oki, A);
         // sender features of the row's edge at channels 16 cb + 4 q .. + 3, times the mask
@@ -687,6 +690,15 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
           if (oki) v = *reinterpret_cast<const v4f*>(a.x + (int64_t)si * C + c0 + 16 * cb + 4 * q);
 #pragma unroll
           for (int r = 0; r < 4; ++r) xv[cb][r] = mi * v[r];
+        }
+        // harmonics of the rows' edges for dr (lanes q >= 2), loaded with the tile's other operands: a load
+        // after the contraction would wait, with the same counter, for the stores before it
+        float shv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int k = t0 + 4 * (q & 1) + r;
+          const int32_t ek = __shfl(ch.e, k & 63);
+          shv[r] = k < count && j < NY && q >= 2 ? a.sh[(int64_t)ek * NY + j] : 0.f;
         }
         v4f QR[PG];
 #pragma unroll
@@ -713,7 +725,7 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
 #pragma unroll
           for (int p = 0; p < PG; ++p) v = degj == p ? QR[p][r] : v;
           const bool ok = k < count && j < NY;
-          dv[r] = ok && q >= 2 ? a.sh[(int64_t)eo[r] * NY + j] * v : 0.f;
+          dv[r] = ok && q >= 2 ? shv[r] * v : 0.f;
           if (ok && q < 2 && dsh) {
             float* d = dsh + (int64_t)eo[r] * NY + j;
             *d = acc ? *d + v : v;
