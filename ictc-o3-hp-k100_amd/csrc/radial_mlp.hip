@@ -368,7 +368,7 @@ __global__ __launch_bounds__(FWD_WAVES * 64) void mlp_fwd_kernel(const float* __
 
 // Forward with the forward-mode derivative along r: a3 and t3 = d a3 / dr,
 // both [E, 64] (the hidden state the fused radial-gate message projects).
-__global__ __launch_bounds__(FWD_WAVES * 64) void mlp_tan_kernel(const float* __restrict__ r, int64_t E, float rc,
+__global__ __launch_bounds__(FWD_WAVES * 64, 3) void mlp_tan_kernel(const float* __restrict__ r, int64_t E, float rc,
                                                                  int p, const float* __restrict__ W1,
                                                                  const float* __restrict__ W2,
                                                                  const float* __restrict__ W3, float s,
