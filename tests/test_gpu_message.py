@@ -276,3 +276,42 @@ def test_message_backward_without_edges(device, which):
     grads = torch.autograd.grad(out.sum(), [t for t in (x, sh, g) if t.requires_grad], allow_unused=True)
     for t, d in zip([t for t in (x, sh, g) if t.requires_grad], grads):
         assert d is None or (d.shape == t.shape and (d.numel() == 0 or float(d.abs().max()) == 0.0))
+
+
+@pytest.mark.parametrize("N,E,C,li,le,lo", [(64, 2000, 64, 2, 2, 2), (40, 500, 128, 2, 3, 3), (20, 150, 17, 1, 2, 2)])
+def test_message_fixed_path_weight(device, N, E, C, li, le, lo):
+    """Fixed non-unit path coefficients (the TP's weight [P, C]): forward, adjoint and gate-tangent adjoint
+    against the float64 oracle with the weight folded into the gates (the same products).  The
+    pipelined kernels (forward and gate-tangent adjoint at (2, 2, 2)) run a separate weighted loop."""
+    from ictc_o3 import PackedGraphMessage
+    from ictc_o3.ops import tensor_product as tpo
+    op = PackedGraphMessage.create(channels=C, input_lmax=li, edge_lmax=le, output_lmax=lo, device=device)
+    P = len(orc.natural_paths(li, le, lo))
+    gen = torch.Generator().manual_seed(900 + N)
+    w64 = 0.5 + torch.rand(P, C, generator=gen, dtype=torch.float64)
+    with torch.no_grad():
+        op.tp.weight.copy_(w64.float().to(device))
+    spec = op.edge._prepare()
+    assert spec.weight is not None
+    f64, sh64, g64, src, dst, m64 = _graph(N, E, C, li, le, lo, 900 + N, mask=True)
+    ref_in = [t.clone().requires_grad_(True) for t in (f64, sh64, g64)]
+    gw = (ref_in[2].view(E, P, C) * w64).view(E, P * C)
+    ref = orc.message_packed(ref_in[0], ref_in[1], gw, src, dst, m64, li, le, lo, C)
+    x = [t.float().to(device).requires_grad_(True) for t in (f64, sh64, g64)]
+    m = m64.float().to(device)
+    out = op(*x, src.to(device), dst.to(device), m)
+    assert rel_err(out, ref) < TOL
+    go = torch.randn(ref.shape, generator=gen, dtype=torch.float64)
+    torch.autograd.backward(ref, go)
+    torch.autograd.backward(out, go.float().to(device))
+    for a, b in zip(x, ref_in):
+        assert rel_err(a.grad, b.grad) < TOL
+    # gate-tangent adjoint: dr = sum over gates of dL/dgates * gdot (the weight is inside dL/dgates)
+    topo = tpo.Topology(src.to(device), dst.to(device), N)
+    gdot64 = torch.randn(g64.shape, generator=gen, dtype=torch.float64)
+    xs, shs, gs = (t.detach() for t in x)
+    dx, dsh, dr = tpo._msg_bwd_tangent_raw(spec, topo, xs, shs, gs, gdot64.float().to(device), m,
+                                           go.float().to(device), (True, True))
+    assert rel_err(dx, ref_in[0].grad) < TOL
+    assert rel_err(dsh, ref_in[1].grad) < TOL
+    assert rel_err(dr, (ref_in[2].grad * gdot64).sum(1)) < TOL
