@@ -13,11 +13,11 @@
 // each) replace eight v_mfma_f32_16x16x4_f32 (32 cycles each) per 16x16x32
 // block, which makes the projection HBM-bound (it writes E * M floats).
 //
-// Tiling: a block owns 256 edges, staged from HBM into LDS once; its 4 waves
+// Tiling: a block owns 256 edges, split from HBM into LDS once; its 8 waves
 // take 64-row slices of W in turn.  A wave holds its slice pre-split in
-// registers (A operand: 4 row blocks x 2 k-steps x 3 parts) and streams
-// 16-edge tiles of h from LDS (B operand), so every gate is produced by one
-// wave and stored as a 16-byte vector per lane.
+// registers (A operand: 4 row blocks x 2 k-steps x 3 parts) and streams the
+// pre-split 16-edge tiles of h from LDS (B operand), so every gate is produced
+// by one wave and stored as a 16-byte vector per lane.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -49,20 +49,23 @@ __device__ __forceinline__ void load8(const float* __restrict__ p, float* v) {
   v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
 }
 
-constexpr int kRow = kK + 4;  // LDS row pitch (floats): spreads the 16 edge rows of an operand read over the banks
+// The block's 16-edge tiles of h, split once into bf16 parts in the B operand
+// layout ([tile][k-step][hi, mid, lo][lane]); every slice reads them from LDS.
+struct HTiles {
+  bf16x8 b[kTiles][2][3][64];
+};
 
-// The 16-edge tiles of one 64-row slice.  The NRB row blocks are independent
+// The tiles [t0, t1) of one 64-row slice.  The NRB row blocks are independent
 // accumulator chains, interleaved so that no MFMA waits on its predecessor.
 template <int NRB>
-__device__ __forceinline__ void slice_tiles(const Split (&A)[4][2], const float* __restrict__ tile, int64_t e_base,
+__device__ __forceinline__ void slice_tiles(const Split (&A)[4][2], const HTiles& ht, int t0, int t1, int64_t e_base,
                                             int64_t E, int M, int s, float* __restrict__ out) {
   const int l = threadIdx.x & 63, i = l & 15, g = l >> 4;
-  for (int t = 0; t < kTiles; ++t) {
+  for (int t = t0; t < t1; ++t) {
     const int64_t e = e_base + 16 * t + i;
-    float cur[16];
-    load8(tile + (16 * t + i) * kRow + 8 * g, cur);
-    load8(tile + (16 * t + i) * kRow + 32 + 8 * g, cur + 8);
-    const Split B0 = split8(cur), B1 = split8(cur + 8);
+    Split B0, B1;
+    B0.hi = ht.b[t][0][0][l], B0.mid = ht.b[t][0][1][l], B0.lo = ht.b[t][0][2][l];
+    B1.hi = ht.b[t][1][0][l], B1.mid = ht.b[t][1][1][l], B1.lo = ht.b[t][1][2][l];
     v4f acc[NRB];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) acc[rb] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -83,24 +86,42 @@ __device__ __forceinline__ void slice_tiles(const Split (&A)[4][2], const float*
 // MFMA operand layout (both operands use the same k order, which is all the
 // instruction requires): lane l holds row/column l % 16 and k = 32*ks + 8*(l/16) + e.
 // D: lane l holds column l % 16 (an edge) and rows 4*(l/16) + r (gate outputs).
-// The block's 256 hidden rows are staged in LDS once, so the gate stream
-// cannot evict them between the slices that reuse them.
-__global__ __launch_bounds__(256, 2) void gate_gemm_nt_kernel(const float* __restrict__ h, int64_t E,
-                                                              const float* __restrict__ W, int M,
-                                                              float* __restrict__ out) {
-  __shared__ float tile[kEdgesPerBlock * kRow];
+// The block's 256 hidden rows are split into LDS once (each slice used to
+// split them again), so the gate stream cannot evict them between the slices
+// that reuse them.  With fewer slices than waves, the waves of a slice share
+// its tiles (a power-of-two number of waves per slice).
+constexpr int kNtWaves = 8;
+__global__ __launch_bounds__(64 * kNtWaves, 1) void gate_gemm_nt_kernel(const float* __restrict__ h, int64_t E,
+                                                                         const float* __restrict__ W, int M,
+                                                                         float* __restrict__ out) {
+  __shared__ HTiles ht;
   const int l = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = l & 15, g = l >> 4;
   const int64_t e_base = (int64_t)blockIdx.x * kEdgesPerBlock;
-  for (int idx = threadIdx.x; idx < kEdgesPerBlock * (kK / 4); idx += 256) {
-    const int r = idx / (kK / 4), q = idx % (kK / 4);
-    const int64_t e = e_base + r;
-    const float4 v = e < E ? *reinterpret_cast<const float4*>(h + e * kK + 4 * q) : float4{0.f, 0.f, 0.f, 0.f};
-    *reinterpret_cast<float4*>(tile + r * kRow + 4 * q) = v;
+  for (int t = wave; t < kTiles; t += kNtWaves) {
+    const int64_t e = e_base + 16 * t + i;
+    float cur[16];
+    if (e < E) {
+      load8(h + e * kK + 8 * g, cur);
+      load8(h + e * kK + 32 + 8 * g, cur + 8);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) cur[q] = 0.f;
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const Split B = split8(cur + 8 * ks);
+      ht.b[t][ks][0][l] = B.hi;
+      ht.b[t][ks][1][l] = B.mid;
+      ht.b[t][ks][2][l] = B.lo;
+    }
   }
   __syncthreads();
   const int slices = (M + 63) / 64;
-  for (int s = wave; s < slices; s += 4) {
+  int wps = 1;  // waves per slice
+  while (2 * wps * slices <= kNtWaves) wps *= 2;
+  const int per = kTiles / wps, t0 = (wave % wps) * per;
+  for (int s = wave / wps; s < slices; s += kNtWaves / wps) {
     const int nrb = min(4, (M - 64 * s) / 16);
     Split A[4][2];
 #pragma unroll
@@ -113,10 +134,10 @@ __global__ __launch_bounds__(256, 2) void gate_gemm_nt_kernel(const float* __res
       }
     }
     switch (nrb) {
-      case 4: slice_tiles<4>(A, tile, e_base, E, M, s, out); break;
-      case 3: slice_tiles<3>(A, tile, e_base, E, M, s, out); break;
-      case 2: slice_tiles<2>(A, tile, e_base, E, M, s, out); break;
-      default: slice_tiles<1>(A, tile, e_base, E, M, s, out); break;
+      case 4: slice_tiles<4>(A, ht, t0, t0 + per, e_base, E, M, s, out); break;
+      case 3: slice_tiles<3>(A, ht, t0, t0 + per, e_base, E, M, s, out); break;
+      case 2: slice_tiles<2>(A, ht, t0, t0 + per, e_base, E, M, s, out); break;
+      default: slice_tiles<1>(A, ht, t0, t0 + per, e_base, E, M, s, out); break;
     }
   }
 }
@@ -231,7 +252,7 @@ int ictc_gate_gemm_fwd(const float* hidden, int64_t edges, int hidden_width, con
       15)
     return fail(ICTC_ERR_ARGUMENT, "gate projection: operands must be 16-byte aligned");
   const unsigned blocks = (unsigned)((edges + kEdgesPerBlock - 1) / kEdgesPerBlock);
-  hipLaunchKernelGGL(gate_gemm_nt_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, hidden, edges, weight,
+  hipLaunchKernelGGL(gate_gemm_nt_kernel, dim3(blocks), dim3(64 * kNtWaves), 0, (hipStream_t)stream, hidden, edges, weight,
                      gates, out);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
