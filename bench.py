@@ -52,8 +52,8 @@ METRIC = "atom-steps/s (E+F, 1 GPU) C64/lmax2 MACE; TP edges/s & % HBM roofline"
 # WRITE x1.0); see profiles/msg_cfg4_hbm_traffic.md.  msg_fwd, msg_bwd_tan and gates_tan are the step's
 # forms: gates shared by each edge and its reverse (2,631,352 gate rows), measured in the cfg4 step
 # (profiles/step_cfg4_hbm_traffic.md).
-MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 19.65e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.18e9,
-                    ("msg_bwd_x", 131072, 5262704, 64): 32.01e9, ("msg_bwd", 131072, 5262704, 64): 61.45e9,
+MEASURED_TRAFFIC = {("msg_fwd", 131072, 5262704, 64): 19.65e9, ("msg_bwd_edge", 131072, 5262704, 64): 37.16e9,
+                    ("msg_bwd_x", 131072, 5262704, 64): 31.91e9, ("msg_bwd", 131072, 5262704, 64): 61.18e9,
                     ("msg_bwd_tan", 131072, 5262704, 64): 42.93e9, ("gates_tan", 131072, 5262704, 64): 14.87e9}
 
 
