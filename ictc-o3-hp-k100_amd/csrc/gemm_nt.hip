@@ -119,14 +119,37 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ 
 
 constexpr int kSumThreads = 256;
 
+// First index i in [0, n) with batch[i] >= g (batch ascending).
+__device__ int64_t lower_bound_graph(const int64_t* __restrict__ batch, int64_t n, int64_t g) {
+  int64_t lo = 0, hi = n;
+  while (lo < hi) {
+    const int64_t mid = lo + ((hi - lo) >> 1);
+    if (batch[mid] < g) lo = mid + 1;
+    else hi = mid;
+  }
+  return lo;
+}
+
+// One block per graph. Sorted batch: the block sums its own [begin, end) range, O(n + graphs) in all;
+// unsorted batch: the block filters all n atoms, O(graphs * n). Same fixed summation order per thread
+// slot in both (atom index ascending), then a fixed tree.
+template <bool kSorted>
 __global__ __launch_bounds__(kSumThreads) void graph_sum_kernel(const float* __restrict__ values,
                                                                 const int64_t* __restrict__ batch, int64_t n,
                                                                 double* __restrict__ out) {
   __shared__ double part[kSumThreads];
+  __shared__ int64_t range[2];
   const int64_t b = blockIdx.x;
+  int64_t begin = 0, end = n;
+  if (kSorted) {
+    if (threadIdx.x < 2) range[threadIdx.x] = lower_bound_graph(batch, n, b + threadIdx.x);
+    __syncthreads();
+    begin = range[0];
+    end = range[1];
+  }
   double s = 0.0;
-  for (int64_t i = threadIdx.x; i < n; i += kSumThreads)
-    if (batch[i] == b) s += (double)values[i];
+  for (int64_t i = begin + threadIdx.x; i < end; i += kSumThreads)
+    if (kSorted || batch[i] == b) s += (double)values[i];
   part[threadIdx.x] = s;
   __syncthreads();
   for (int h = kSumThreads / 2; h > 0; h >>= 1) {
@@ -167,13 +190,18 @@ int ictc_gemm_nt(const float* a, int64_t m, int64_t k, int64_t lda, const float*
   return launch_status("ictc_gemm_nt launch");
 }
 
-int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, double* out, void* stream) {
+int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, int batch_sorted, double* out,
+                   void* stream) {
   if (n < 0 || graphs < 0) return fail(ICTC_ERR_ARGUMENT, "graph_sum: negative size");
   if (graphs == 0) return ICTC_OK;
   if (!out || (n > 0 && (!values || !batch))) return fail(ICTC_ERR_ARGUMENT, "graph_sum: null operand");
   if (graphs > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "graph_sum: too many graphs");
-  hipLaunchKernelGGL(graph_sum_kernel, dim3((unsigned)graphs), dim3(kSumThreads), 0, (hipStream_t)stream, values,
-                     batch, n, out);
+  if (batch_sorted)
+    hipLaunchKernelGGL(graph_sum_kernel<true>, dim3((unsigned)graphs), dim3(kSumThreads), 0, (hipStream_t)stream,
+                       values, batch, n, out);
+  else
+    hipLaunchKernelGGL(graph_sum_kernel<false>, dim3((unsigned)graphs), dim3(kSumThreads), 0, (hipStream_t)stream,
+                       values, batch, n, out);
   return launch_status("ictc_graph_sum launch");
 }
 

@@ -73,7 +73,7 @@ _SIGNATURES = {
     "ictc_gate_gemm_bwd_strided": (_i, [_p, _i64, _i64, _i, _p, _i, _p, _i, _p]),
     "ictc_gemm_tn_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "ictc_gemm_nt": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i, _p]),
-    "ictc_graph_sum": (_i, [_p, _p, _i64, _i64, _p, _p]),
+    "ictc_graph_sum": (_i, [_p, _p, _i64, _i64, _i, _p, _p]),
     "ictc_gemm_tn": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p]),
     "ictc_edge_geometry_fwd": (_i, [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _p]),
     "ictc_edge_geometry_bwd": (_i, [_p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),

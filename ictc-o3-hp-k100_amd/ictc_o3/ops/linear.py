@@ -85,12 +85,17 @@ class _GraphSum(torch.autograd.Function):
     is the gather grad[batch], differentiable to any order."""
 
     @staticmethod
-    def forward(ctx, values, batch, graphs):
+    def forward(ctx, values, batch, graphs, batch_sorted):
         from ictc_o3 import _native as nat
+        if values.dtype != torch.float32 or batch.dtype != torch.int64:
+            raise TypeError("graph_sum: values must be float32 and batch int64")
+        if values.shape != batch.shape:
+            raise ValueError("graph_sum: values and batch must have the same shape [N]")
         values = values if values.is_contiguous() else values.contiguous()
         batch = batch if batch.is_contiguous() else batch.contiguous()
         out = torch.empty(graphs, dtype=torch.float64, device=values.device)
-        nat.call("ictc_graph_sum", nat.ptr(values), nat.ptr(batch), values.numel(), graphs, nat.ptr(out),
+        nat.call("ictc_graph_sum", nat.ptr(values), nat.ptr(batch), values.numel(), graphs,
+                 1 if batch_sorted else 0, nat.ptr(out),
                  nat.stream_of(values))
         ctx.save_for_backward(batch)
         ctx.dtype = values.dtype
@@ -99,12 +104,13 @@ class _GraphSum(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad):
         (batch,) = ctx.saved_tensors
-        return grad.index_select(0, batch).to(ctx.dtype), None, None
+        return grad.index_select(0, batch).to(ctx.dtype), None, None, None
 
 
-def graph_sum(values: torch.Tensor, batch: torch.Tensor, graphs: int) -> torch.Tensor:
-    """Per-graph FP64 sums of per-atom values (batch int64 graph ids in [0, graphs))."""
-    return _GraphSum.apply(values, batch, int(graphs))
+def graph_sum(values: torch.Tensor, batch: torch.Tensor, graphs: int, batch_sorted: bool = False) -> torch.Tensor:
+    """Per-graph FP64 sums of float32 per-atom values (batch int64 graph ids in [0, graphs)).
+    batch_sorted=True promises ascending ids (each graph's atoms contiguous) and makes the cost O(N + graphs)."""
+    return _GraphSum.apply(values, batch, int(graphs), bool(batch_sorted))
 
 
 def channel_linear(features: torch.Tensor, weight: torch.Tensor, bias=None):

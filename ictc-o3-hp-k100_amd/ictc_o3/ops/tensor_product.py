@@ -412,6 +412,11 @@ def _graph_task():
     return torch._C._current_graph_task_id()
 
 
+# Whether the mixed second derivative hands its gate gradient to the first-order message adjoint of the
+# same backward pass (_GateLink) instead of returning it for autograd to add; False = autograd's own add.
+LINK_GATE_GRADIENTS = True
+
+
 class _GateLink:
     """Hands the gate gradient of a message's mixed second derivative to the first-order adjoint of the
     same message in the same backward pass.
@@ -438,7 +443,7 @@ class _GateLink:
 
     def can_hold(self):
         from torch.fx.experimental.proxy_tensor import get_proxy_mode
-        if (torch.compiler.is_compiling() or get_proxy_mode() is not None
+        if (not LINK_GATE_GRADIENTS or torch.compiler.is_compiling() or get_proxy_mode() is not None
                 or torch._C._are_functorch_transforms_active()
                 or not hasattr(torch._C, "_will_engine_execute_node")):
             return False

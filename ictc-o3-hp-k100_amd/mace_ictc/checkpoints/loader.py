@@ -162,7 +162,9 @@ def load_checkpoint(checkpoint_path: str, element_types: List[str], max_radius: 
     if poly_p is None:
         raise ValueError("a radial basis without polynomial cutoff is not part of the MI355X build")
     sqrt_norm = bool(_meta(ckpt, arch, "radial_sqrt_num_basis", True))
-    function_type = str(arch.get("function_type", "bessel"))
+    # The reference resolves a missing key to a Gaussian basis
+    # (reference mace_ictc/checkpoints/loader.py:156), which is not built here.
+    function_type = str(_meta(ckpt, arch, "function_type", "gaussian"))
     if function_type != "bessel":
         raise ValueError(f"radial function_type {function_type!r} is not built here (Bessel only)")
     lmax = int(arch.get("lmax", 2))

@@ -246,6 +246,24 @@ class MACEStyleReadout(nn.Module):
         return edge_linear(self.activation(edge_linear(h0, self.linear_1.weight)), self.linear_2.weight)
 
 
+def shift_vectors(shifts: torch.Tensor, cell: torch.Tensor, batch: torch.Tensor, edge_src: torch.Tensor):
+    """Cartesian image shifts [E, 3] = shifts [E, 3] (lattice coordinates) . cell of the edge's graph.
+
+    Topology.pair_edges lets an edge and its reverse (shift -S) share one row of
+    radial gates, which is only exact when their lengths are bitwise equal.  They
+    are because this form is odd in the shift bit for bit: each component is a
+    sum of three products s_k * c_kj in a fixed order, and negating every s_k
+    negates every product and every partial sum exactly.  A library GEMM or an
+    FMA-contracted form need not keep that (its order or fusion may differ with
+    the operand's sign pattern), so do not change it without re-running the
+    shared-row bitwise tests.
+    """
+    if cell.shape[0] == 1:   # [E, 3] x [3, 3] as three broadcast products (no library GEMM)
+        return (shifts.unsqueeze(-1) * cell[0].to(shifts.dtype)).sum(1)
+    # per-edge cell rows without a batched 1x3x3 GEMM per edge
+    return (shifts.unsqueeze(-1) * cell[batch[edge_src]].to(shifts.dtype)).sum(1)
+
+
 class PureCartesianICTDFix(nn.Module):
     """The baseline MACE-ICTC backbone restricted to the create_model route."""
 
@@ -332,12 +350,7 @@ class PureCartesianICTDFix(nn.Module):
             # spatial row order for one periodic system; batched graphs keep index order (their
             # atoms are contiguous per graph, and the graphs' coordinates overlap)
             topology = tpo.Topology(edge_src, edge_dst, N, positions=pos if cell.shape[0] == 1 else None)
-        shifts = edge_shifts.to(pos.dtype)
-        if cell.shape[0] == 1:   # [E, 3] x [3, 3] as three broadcast products (no library GEMM)
-            shift_vec = (shifts.unsqueeze(-1) * cell[0].to(shifts.dtype)).sum(1)
-        else:  # per-edge cell rows without a batched 1x3x3 GEMM per edge
-            cells = cell[batch[edge_src]]
-            shift_vec = (shifts.unsqueeze(-1) * cells).sum(1)
+        shift_vec = shift_vectors(edge_shifts.to(pos.dtype), cell, batch, edge_src)
         if second_order or pos.dtype != torch.float32:
             if pos.dtype == torch.float32 and pos.is_cuda:
                 from ictc_o3.ops.geometry import edge_vectors

@@ -79,9 +79,13 @@ def energy_and_forces(model, positions, atomic_numbers, batch, edge_src, edge_ds
         # per-graph sums in FP64 without atomics (deterministic, contention free)
         if cell.shape[0] == 1:
             energy64 = selected.double().sum().reshape(1)
-        elif selected.is_cuda:
+        elif selected.is_cuda and selected.dtype == torch.float32:
             from ictc_o3.ops.linear import graph_sum
-            energy64 = graph_sum(selected, batch, cell.shape[0])
+            graphs = cell.shape[0]
+            # Many small graphs: the contiguous-batch form is O(N + graphs) instead of O(graphs * N); the
+            # one host read deciding it is paid only where the quadratic form would cost more.
+            ordered = graphs > 64 and n > 1 and bool((batch[1:] >= batch[:-1]).all())
+            energy64 = graph_sum(selected, batch, graphs, batch_sorted=ordered)
         else:
             onehot = torch.nn.functional.one_hot(batch, cell.shape[0]).to(torch.float64)
             energy64 = onehot.t() @ selected.double()

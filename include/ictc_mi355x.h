@@ -354,8 +354,12 @@ int ictc_gemm_nt(const float* a, int64_t m, int64_t k, int64_t lda, const float*
                  int64_t ldc, int accumulate, void* stream);
 /* Per-graph energy: out [graphs] (FP64) = sum of values [n] over atoms with
  * batch [n] == graph, a fixed-order reduction (deterministic, no atomics);
- * replaces the per-graph scatter of hp/runtime.py:86-113.                     */
-int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, double* out, void* stream);
+ * replaces the per-graph scatter of hp/runtime.py:86-113.  batch_sorted != 0
+ * promises an ascending batch (each graph's atoms contiguous, as the
+ * reference's collate builds it): each graph then binary-searches its range,
+ * O(n + graphs); batch_sorted == 0 accepts any order at O(graphs * n).        */
+int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, int batch_sorted,
+                   double* out, void* stream);
 
 /* Weight gradient of a per-edge linear (replaces the library GEMM dW = dy^T x
  * that autograd runs for every Linear of the radial MLP fc in the force-loss

@@ -128,3 +128,20 @@ def test_refusals(tmp_path):
     with pytest.warns(RuntimeWarning, match="avg_num_neighbors"):
         got = load_checkpoint(str(path), ["H", "C", "O"]).model
     assert got.avg_num_neighbors == 14.38
+
+
+def test_missing_function_type_resolves_to_gaussian(tmp_path):
+    """Reference mace_ictc/checkpoints/loader.py:156 reads a missing function_type as 'gaussian'; a Gaussian
+    radial basis is not built here, so such a checkpoint must be refused rather than loaded as Bessel."""
+    from mace_ictc.checkpoints import load_checkpoint
+    model = _model()
+    ck = _ckpt(model)
+    del ck["model_hyperparameters"]["function_type"]
+    path = tmp_path / "noft.pth"
+    torch.save(ck, path)
+    with pytest.raises(ValueError, match="gaussian"):
+        load_checkpoint(str(path), ["H", "C", "O"])
+    ck = _ckpt(model, function_type="bessel")
+    del ck["model_hyperparameters"]["function_type"]
+    torch.save(ck, path)
+    assert load_checkpoint(str(path), ["H", "C", "O"]).model.number_of_basis == model.number_of_basis

@@ -9,14 +9,14 @@
   batch equals the one taken on the cell alone, and the whole step is bitwise
   repeatable.
 
-Tolerances (north star): energies 1e-6 relative to sum |e_i| of the cell,
+Tolerances (north star): energies 1e-6 relative to |E| of the cell,
 forces 1e-5 relative (max-norm), parameter gradients relative L2 < 3e-5.
 """
 import pytest
 import torch
 
 import model_oracle as mo
-from helpers import rel_err
+from helpers import assert_energy_close, rel_err
 from model_helpers import build_graph, fcc_cells
 
 pytestmark = pytest.mark.gpu
@@ -57,7 +57,7 @@ def _param_grads(model, loss):
 def _check_cell_against_oracle(model, out, system, b, E0, F0, A0):
     pos, Z, batch, cell, src, dst, sh = system
     rows = torch.nonzero(batch == b).flatten()
-    assert abs(float(out["energy"][b]) - float(E0[0])) <= 1e-6 * float(A0.abs().sum()), b
+    assert_energy_close(out["energy"][b], E0[0], A0, f"cfg5 cell {b}")
     assert rel_err(out["forces"][rows.to(out["forces"].device)], F0) < 1e-5, b
 
 
@@ -94,7 +94,7 @@ def test_cfg5_cell_force_loss_gradients_match_oracle(device):
     ref = torch.autograd.grad(_loss(E, -gpos, E_t, F_t), [sd[k] for k in names], allow_unused=True)
     # product
     out = _run(model, device, system, training=True)
-    assert abs(float(out["energy"][0]) - float(E.detach()[0])) <= 1e-6 * float(atomic.detach().abs().sum())
+    assert_energy_close(out["energy"][0], E.detach()[0], atomic, "cfg5 force-loss cell")
     assert rel_err(out["forces"], -gpos.detach()) < 1e-5
     got_names, got = _param_grads(model, _loss(out["energy"].double(), out["forces"].double(), E_t.to(device),
                                                F_t.to(device)))

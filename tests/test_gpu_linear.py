@@ -100,6 +100,16 @@ def test_graph_sum_exact_and_repeatable(device):
     w = torch.randn(37, generator=g, dtype=torch.float64)
     (gv,) = torch.autograd.grad((out * w.to(device)).sum(), vd)
     assert torch.equal(gv.cpu(), w[batch].float())
+    # contiguous-per-graph batch (the collate order) through the binary-searched form, with empty graphs
+    sb, order = torch.sort(batch[batch % 5 != 3], stable=True)
+    sv = v[batch % 5 != 3][order]
+    ref = torch.zeros(37, dtype=torch.float64).index_add(0, sb, sv.double())
+    got = graph_sum(sv.to(device), sb.to(device), 37, batch_sorted=True)
+    assert float((got.cpu() - ref).abs().max()) < 1e-9
+    assert torch.equal(got, graph_sum(sv.to(device), sb.to(device), 37))
+    assert torch.equal(got[3::5].cpu(), torch.zeros_like(got[3::5].cpu()))
+    with pytest.raises(TypeError):
+        graph_sum(sv.double().to(device), sb.to(device), 37)
 
 
 @pytest.mark.parametrize("kind,C,lmax,N", [("degree", 64, 2, 300), ("path", 128, 2, 129), ("degree", 32, 3, 77)])

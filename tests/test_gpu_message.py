@@ -315,3 +315,46 @@ def test_message_fixed_path_weight(device, N, E, C, li, le, lo):
     assert rel_err(dx, ref_in[0].grad) < TOL
     assert rel_err(dsh, ref_in[1].grad) < TOL
     assert rel_err(dr, (ref_in[2].grad * gdot64).sum(1)) < TOL
+
+
+@pytest.mark.parametrize("inputs", [(0, 1, 2), (2,), (0,), (1, 2)])
+def test_gate_link_partial_inputs_and_retained_graph(device, inputs):
+    """Force-loss objective L = a.E + <dE/dx, v> (both the forward message's first-order adjoint and the
+    mixed second derivative reach the gates): autograd.grad over a subset of the inputs, and two backward
+    passes over one retained graph, give the float64 gradients, and the gate-gradient hand-off between the
+    two passes (LINK_GATE_GRADIENTS) gives bitwise the gradients of autograd's own add."""
+    from ictc_o3 import PackedGraphMessage
+    from ictc_o3.ops import tensor_product as tp
+    N, E, C = 24, 200, 64
+    op = PackedGraphMessage.create(channels=C, input_lmax=2, edge_lmax=2, output_lmax=2, device=device)
+    f64, sh64, g64, src, dst, m64 = _graph(N, E, C, 2, 2, 2, 91, mask=True)
+    gen = torch.Generator().manual_seed(92)
+    a64 = torch.randn(N, op.output_width, generator=gen, dtype=torch.float64)
+    v64 = torch.randn(f64.shape, generator=gen, dtype=torch.float64)
+
+    def objective(xs, fn, a, v):
+        out = fn(*xs)
+        (dx,) = torch.autograd.grad(out, xs[0], a, create_graph=True)
+        return (out * a).sum() + (dx * v).sum()
+
+    ref_x = [t.clone().requires_grad_(True) for t in (f64, sh64, g64)]
+    ref = torch.autograd.grad(objective(ref_x, lambda p, q, r: orc.message_packed(
+        p, q, r, src, dst, m64, 2, 2, 2, C), a64, v64), [ref_x[k] for k in inputs])
+    s, d, m = src.to(device), dst.to(device), m64.float().to(device)
+    a, v = a64.float().to(device), v64.float().to(device)
+    results = {}
+    for link in (True, False):
+        tp.LINK_GATE_GRADIENTS = link
+        try:
+            xs = [t.float().to(device).requires_grad_(True) for t in (f64, sh64, g64)]
+            L = objective(xs, lambda p, q, r: op(p, q, r, s, d, m), a, v)
+            got = torch.autograd.grad(L, [xs[k] for k in inputs], retain_graph=True)
+            again = torch.autograd.grad(L, [xs[k] for k in inputs])
+        finally:
+            tp.LINK_GATE_GRADIENTS = True
+        for g1, g2, r in zip(got, again, ref):
+            assert torch.equal(g1, g2)
+            assert rel_err(g1, r) < TOL
+        results[link] = got
+    for g1, g2 in zip(results[True], results[False]):
+        assert torch.equal(g1, g2)

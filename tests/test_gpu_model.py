@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import model_oracle as mo
-from helpers import rel_err
+from helpers import assert_energy_close, rel_err
 from model_helpers import build_graph, fcc_cells
 
 pytestmark = pytest.mark.gpu
@@ -33,9 +33,8 @@ def test_energy_and_forces_match_oracle(device, C, lmax, edge_lmax, S, cells):
                                       cells)
     out = energy_and_forces(model, pos.float().to(device), Z.to(device), batch.to(device), src.to(device),
                             dst.to(device), sh.float().to(device), cell.float().to(device))
-    # energy: 1e-6 relative to the scale of the summed atomic energies of each graph (sum |e_i|)
-    scale = torch.zeros(cells, dtype=torch.float64).index_add(0, batch, A0.abs())
-    assert bool(((out["energy"].double().cpu() - E0).abs() <= 1e-6 * scale).all())
+    for b in range(cells):
+        assert_energy_close(out["energy"][b], E0[b], A0[batch == b], f"C{C} L{edge_lmax} S{S} graph {b}")
     assert rel_err(out["forces"], F0) < 1e-5
     assert rel_err(out["atomic_energy"], A0) < 1e-5
 
@@ -146,6 +145,6 @@ def test_energy_and_forces_without_edges(device, training):
                                       sh.double(), cell, 1)
     out = energy_and_forces(model, pos.float().to(device), Z.to(device), batch.to(device), src.to(device),
                             dst.to(device), sh.to(device), cell.float().to(device), training=training)
-    assert abs(float(out["energy"][0]) - float(E0[0])) <= 1e-6 * float(A0.abs().sum())
+    assert_energy_close(out["energy"][0], E0[0], A0, "no edges")
     assert float(out["forces"].abs().max()) == 0.0
     assert rel_err(out["atomic_energy"], A0) < 1e-5

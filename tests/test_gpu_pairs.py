@@ -162,3 +162,22 @@ def test_shared_rows_parameter_gradients_bitwise(device):
     assert len(grads[0]) == len(grads[1]) > 5
     for x, y in zip(*grads):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("cells", [1, 3])
+def test_paired_edges_have_bitwise_equal_lengths(device, cells):
+    """The premise of shared rows: with the model's own shift vectors (mace_ictc.hp.model.shift_vectors) and
+    edge geometry, every edge reading its reverse's gate row has bitwise that edge's length."""
+    from ictc_o3.ops.geometry import edge_geometry
+    from mace_ictc.hp.model import shift_vectors
+    pos, Z, batch, cell = fcc_cells(3 if cells == 1 else 2, 0.1, 0.3, 13, 3, cells=cells)
+    src, dst, sh = build_graph(pos, batch, cell, 4.5)
+    topo = _pairs(src, dst, sh, pos.shape[0], device)
+    assert topo.gate_rows is not None
+    shift = shift_vectors(sh.float().to(device), cell.float().to(device), batch.to(device), src.to(device))
+    r, _, _ = edge_geometry(pos.float().to(device), shift, topo, 4.5)
+    rows, reps = topo.gate_rows.long(), topo.gate_reps.long()
+    owner = reps[rows]
+    other = owner != torch.arange(src.numel(), device=device)
+    assert int(other.sum()) * 2 == src.numel()
+    assert torch.equal(r[other], r[owner[other]])
