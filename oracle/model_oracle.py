@@ -16,9 +16,9 @@ create_model route in the reference's own layout (degree dictionaries
 
 Pinning: composes the pinned pieces of ictc_oracle / sc_oracle; whole-model
 checks in tests are rotation invariance of E, force equivariance, finite
-differences of E against F, and translation invariance.  Against the
-reference itself the whole model is "parity unpinned" (e3nn is absent, see
-sc_oracle).
+differences of E against F, and translation invariance.  The SC's U, the one
+piece built from e3nn (absent here), is pinned block by block and path by
+path in tests/test_sc_oracle.py (see sc_oracle).
 """
 from __future__ import annotations
 

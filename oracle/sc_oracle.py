@@ -12,11 +12,14 @@ product's code:
   * the species-selected contraction recursion
     (ictc_o3/ops/_mace_symmetric_contraction.py:298-355).
 
-Pinning: SU(2) CG from sympy; wigner_3j equivariance and e3nn spherical
-harmonics reproduce the fixture Q (tests); U symmetric-part invariance under
-simultaneous rotation of all legs.  "Parity unpinned" against the reference
-itself: e3nn is absent, so U's path order and per-path signs cannot be
-compared with the reference's own tensors (only with this restatement).
+Pinning (tests/test_sc_oracle.py): SU(2) CG from sympy; the real->complex
+basis q_l against scipy's complex SH and the reference's real SH (fixture Q);
+every wigner_3j block up to l = 4 against closed forms ((0,l,l), (l,0,l),
+(l,l,0), (1,1,1)), positive Gaunt integrals (even blocks) and the sympy/scipy
+construction (odd blocks); U at correlations 2 and 3 path by path against
+lists written out by hand from the recursion; U symmetric-part equivariance.
+The one rule taken from e3nn rather than mathematics: rows sort by irrep
+(l, then parity o before e).
 """
 from __future__ import annotations
 
