@@ -17,9 +17,10 @@ One step = radial MLP -> gates -> CSR message forward -> backward to
 resident in HBM before the timed region.
 
 Roofline: the step's layer-1 kernels (radial gates with their r tangents,
-message forward, gate-tangent message adjoint) are timed live with HIP events
-on the stream they run on (torch's current stream), averaged over repeated
-launches; the one with the largest time is the roofline kernel: its
+message forward, gate-tangent message adjoint) are timed inside five real
+steps after the timed ones, with HIP events recorded around each launch on
+the stream it runs on (torch's current stream; ictc_o3._timing), averaged
+over those launches; the one with the largest time is the roofline kernel: its
 algorithmic bytes (compulsory traffic: each operand read once, each output
 written once, index arrays included, gathers not counted; the message kernels
 counted per edge with one gate row each, the gate kernel per computed row) /
@@ -122,6 +123,38 @@ def time_launches(fn, reps, stream):
     return start.elapsed_time(end) / reps * 1e-3
 
 
+def host_cpu():
+    """CPU model of the host (first 'model name' of /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def time_cpu(step, warmup=3, runs=5):
+    """The reference's CPU protocol: `warmup` untimed steps, then the median of `runs` timed steps (s)."""
+    for _ in range(warmup):
+        step()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_record(value, unit, sample):
+    import torch
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "cpu": host_cpu(), "threads": torch.get_num_threads(),
+            "sample": sample + f", {host_cpu()}, {torch.get_num_threads()} torch threads, 3 warm-up steps then "
+                               "the median of 5"}
+
+
 def cpu_baseline(data, budget_s=20.0):
     """Reference-path CPU eager (FP32 torch on host cores) on a bounded sample of receivers."""
     import torch
@@ -142,17 +175,9 @@ def cpu_baseline(data, budget_s=20.0):
         c = gs.clone().requires_grad_(True)
         out = orc.message_packed(a, b, c, ss, ds, None, 2, 2, 2, C)
         out.backward(torch.ones_like(out))
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 and (time.perf_counter() < t_end or len(times) < 1):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": take / med, "unit": "edges/s", "cores": threads, "kind": "port",
-            "sample": f"message fwd+bwd (oracle FP32 torch eager) on the first {take} receiver-sorted edges "
-                      f"of the cfg2 graph, median of {len(times)} runs, {torch.get_num_threads()} threads"}
+    med = time_cpu(step)
+    return cpu_record(take / med, "edges/s", f"message fwd+bwd (oracle FP32 torch eager) on the first {take} "
+                      "receiver-sorted edges of the cfg2 graph")
 
 
 def run_cfg2(args):
@@ -268,18 +293,9 @@ def cpu_baseline_model(model, budget_s=25.0):
     def step():
         s2, d2, sh2 = radius_graph_pbc(pos, cell[0], 4.5)
         mo.energy_and_forces(sd, cfg, pos, Z, batch, s2, d2, sh2, cell, 1, dtype=torch.float32)
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 and (time.perf_counter() < t_end or not times):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": pos.shape[0] / med, "unit": "atom-steps/s", "cores": threads, "kind": "port",
-            "sample": f"cfg4 model (same weights) E+F incl. neighbour list on a 2,048-atom FCC 8^3 sample "
-                      f"(E={src.numel()}), oracle FP32 torch eager, median of {len(times)} steps, "
-                      f"{torch.get_num_threads()} threads"}
+    med = time_cpu(step)
+    return cpu_record(pos.shape[0] / med, "atom-steps/s", f"cfg4 model (same weights) E+F incl. neighbour list "
+                      f"on a 2,048-atom FCC 8^3 sample (E={src.numel()}), oracle FP32 torch eager")
 
 
 def run_cfg4(args):
@@ -311,10 +327,27 @@ def run_cfg4(args):
 
     if args.no_kernel_timing:
         return {"metric": METRIC, "value": N / dt, "unit": "atom-steps/s", "ms_per_step": dt * 1e3}, model
+    # the step's own layer-1 launches, timed inside real steps (HIP events on the launching stream around
+    # each launch: same operands, same cache state as the timed steps above)
+    from ictc_o3 import _timing
+    _timing.enable()
+    for _ in range(5):
+        step()
+    spans = _timing.collect()
     src, dst, sh = radius_graph_pbc(pos, cell[0], 4.5)
     kern, nbytes, G = layer_message_kernels(model, src, dst, N, pos, sh)
-    # the layer-1 radial gates with their r tangents over the step's gate rows, timed the same way
+    # the layer-1 radial gates with their r tangents over the step's gate rows (standalone, for the log)
     kern["gates_tan"], nbytes["gates_tan"] = layer_gate_kernel(model, G)
+    standalone = dict(kern)
+    M = model.interactions[-1].spec().num_paths * 64
+    for k, name in (("msg_fwd", "msg_fwd[222C64]"), ("msg_bwd_tan", "msg_bwd_tan[222C64]"),
+                    ("gates_tan", f"gates_tan[M{M}]")):
+        if spans.get(name):
+            kern[k] = sum(spans[name]) / len(spans[name]) * 1e-3
+            log(f"  in-step {k}: {kern[k] * 1e6:.1f} us over {len(spans[name])} launches "
+                f"(standalone {standalone[k] * 1e6:.1f} us)")
+        else:
+            raise RuntimeError(f"no in-step launches of {name} were recorded")
     # the step's own layer-1 kernels (energy + forces: radial gates with tangents, message forward,
     # gate-tangent adjoint); the other adjoint forms are timed for reference only
     in_step = [k for k in ("gates_tan", "msg_fwd", "msg_bwd_tan") if k in kern]
@@ -338,8 +371,10 @@ def run_cfg4(args):
                    "atoms": N, "edges": E, "gate_rows": G, "channels": 64, "lmax": 2,
                    "tp_edges_per_s": 2 * E / dt,
                    "kernel_us_layer1": {k: round(t * 1e6, 2) for k, t in kern.items()},
+                   "kernel_us_layer1_standalone": {k: round(t * 1e6, 2) for k, t in standalone.items()},
                    "kernel_algorithmic_MB_layer1": {k: round(v / 1e6, 2) for k, v in nbytes.items()}},
-        "roofline": {"bound": "hbm", "kernel": f"{dom} (layer 1, P11 C64)", "achieved": achieved,
+        "roofline": {"bound": "hbm", "kernel": f"{dom} (layer 1, P11 C64)", "timing": "in-step launches",
+                     "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": MEASURED_TRAFFIC.get((dom, N, E, 64)),
                      "algorithmic_GB": round(per_unit[dom] / 1e9, 3),
@@ -519,17 +554,8 @@ def cpu_baseline_tp(data, budget_s=15.0):
         c = gates.clone().requires_grad_(True)
         out = orc.edge_tp_packed(a, b, c, 2, 2, 2, C)
         (out * out).mean().backward()
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 50 and time.perf_counter() < t_end:
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": E / med, "unit": "edges/s", "cores": threads, "kind": "port",
-            "sample": f"cfg1 in full (E=257, C32), oracle FP32 torch eager fwd+bwd, median of {len(times)} runs, "
-                      f"{torch.get_num_threads()} threads"}
+    med = time_cpu(step)
+    return cpu_record(E / med, "edges/s", "cfg1 in full (E=257, C32), oracle FP32 torch eager fwd+bwd")
 
 
 def run_cfg3(args):
@@ -611,17 +637,8 @@ def cpu_baseline_sc(data, budget_s=15.0):
         a = xs.clone().requires_grad_(True)
         out = so.symmetric_contraction(a, sp, W, 2, 1, 3)
         out.backward(gos[:, :out.shape[1]])
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 and (time.perf_counter() < t_end or not times):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": take / med, "unit": "node-steps/s", "cores": threads, "kind": "port",
-            "sample": f"first {take} nodes of cfg3, oracle FP32 torch eager SC fwd + dx, median of {len(times)} "
-                      f"runs, {torch.get_num_threads()} threads"}
+    med = time_cpu(step)
+    return cpu_record(take / med, "node-steps/s", f"first {take} nodes of cfg3, oracle FP32 torch eager SC fwd + dx")
 
 
 def batched_cells(cells, n, density, jitter, seed, species, cutoff, device):
@@ -724,17 +741,9 @@ def cpu_baseline_train(model, budget_s=25.0):
         (gp,) = torch.autograd.grad(En.sum(), p, create_graph=True)
         loss = ((En - E_t) ** 2).mean() + ((-gp - F_t) ** 2).mean()
         torch.autograd.grad(loss, [sd[k] for k in names], allow_unused=True)
-    step()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 5 and (time.perf_counter() < t_end or not times):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
-    return {"value": pos.shape[0] / med, "unit": "atom-steps/s", "cores": threads, "kind": "port",
-            "sample": f"one 256-atom cell of cfg5 (E={src.numel()}), oracle FP32 torch eager E+F+force-loss "
-                      f"parameter gradients, median of {len(times)} steps, {torch.get_num_threads()} threads"}
+    med = time_cpu(step)
+    return cpu_record(pos.shape[0] / med, "atom-steps/s", f"one 256-atom cell of cfg5 (E={src.numel()}), oracle "
+                      "FP32 torch eager E+F+force-loss parameter gradients")
 
 
 
@@ -854,6 +863,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true",
                     help="skip the per-kernel HIP-event timings after the timed steps (clean profiles of the step)")
+    ap.add_argument("--no-cfg5", action="store_true", help="cfg4 only: skip the cfg5 training-step line")
+    ap.add_argument("--cfg5-steps", type=int, default=10)
+    ap.add_argument("--cfg5-warmup", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (one-GPU hot path by design); "
@@ -870,6 +882,16 @@ def main():
         return
     run, cpu = runners[args.workload]
     result, data = run(args)
+    if args.workload == "cfg4" and not args.no_cfg5:
+        # the force-loss training step timed in the same run, beside the headline
+        sub = argparse.Namespace(**{**vars(args), "no_kernel_timing": True, "steps": args.cfg5_steps,
+                                    "warmup": args.cfg5_warmup})
+        r5, _ = run_cfg5(sub)
+        result["cfg5"] = {"workload": "cfg5: force-loss training step (E+F MSE backward through mixed second "
+                                      "derivatives + Adam), C128, edge L3, hidden L2, 10 species, 32 cells x 256 "
+                                      "atoms, rc 5 A",
+                          "metric": "atom-steps/s", "value": r5["value"], "ms_per_step": r5["ms_per_step"],
+                          "steps": sub.steps, "warmup": sub.warmup}
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu(data)
     print(json.dumps(result), flush=True)

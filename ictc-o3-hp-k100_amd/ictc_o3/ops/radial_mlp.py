@@ -21,6 +21,7 @@ import torch
 from torch.autograd.function import once_differentiable
 
 from ictc_o3 import _native as nat
+from ictc_o3 import _timing
 
 
 def _c(t):
@@ -250,9 +251,11 @@ def radial_gates_tangent(r, weights, cutoff, poly_p, scale):
     gates, gdot = r.new_empty(E, M), r.new_empty(E, M)
     ws_bytes = int(nat.lib().ictc_radial_gates_workspace_bytes(M))
     ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=r.device)
+    tok = _timing.begin(f"gates_tan[M{M}]")
     nat.call("ictc_radial_gates_tangent_fwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
              nat.ptr(W2), nat.ptr(W3), nat.ptr(W4), M, float(scale), nat.ptr(gates), nat.ptr(gdot), nat.ptr(ws),
              ws_bytes, nat.stream_of(r))
+    _timing.end(tok)
     return gates, gdot
 
 

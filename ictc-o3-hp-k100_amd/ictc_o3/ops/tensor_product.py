@@ -26,6 +26,7 @@ from typing import Optional
 import torch
 
 from ictc_o3 import _native as nat
+from ictc_o3 import _timing
 from ictc_o3.autograd import required_gradients
 from torch.autograd.function import once_differentiable
 
@@ -361,10 +362,12 @@ def _expand_gates(g, gate_rows):
 def _msg_fwd_raw(spec, topo, x, sh, g, mask, gate_rows=None):
     N, E = x.shape[0], sh.shape[0]
     out = x.new_empty(N, spec.out_components * spec.channels)
+    tok = _timing.begin(f"msg_fwd[{spec.li}{spec.le}{spec.lo}C{spec.channels}]")
     nat.call("ictc_msg_fwd", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), N, E, nat.ptr(topo.by_dst.ptr),
              nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(out), nat.ptr(gate_rows),
              nat.stream_of(x))
+    _timing.end(tok)
     return out
 
 
@@ -518,6 +521,7 @@ def _msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, mask, go, need, gate_rows=N
     sp = topo.by_src if need[0] else None
     nbytes = int(nat.lib().ictc_msg_bwd_tangent_workspace_bytes(spec.le, spec.channels, E))
     ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=x.device) if nbytes > 0 else None
+    tok = _timing.begin(f"msg_bwd_tan[{spec.li}{spec.le}{spec.lo}C{spec.channels}]")
     nat.call("ictc_msg_bwd_tangent", spec.li, spec.le, spec.lo, spec.channels, nat.ptr(x), nat.ptr(sh), nat.ptr(g),
              _w(spec), nat.ptr(mask), nat.ptr(topo.src), nat.ptr(topo.dst), N, E,
              nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order),
@@ -525,6 +529,7 @@ def _msg_bwd_tangent_raw(spec, topo, x, sh, g, gdot, mask, go, need, gate_rows=N
              nat.ptr(topo.src_rows), nat.ptr(go), nat.ptr(gdot),
              nat.ptr(dx), nat.ptr(dsh), nat.ptr(dr), nat.ptr(ws), max(nbytes, 0), nat.ptr(gate_rows),
              nat.stream_of(x))
+    _timing.end(tok)
     return dx, dsh, dr
 
 
