@@ -26,6 +26,7 @@
 #include <stdio.h>
 
 #include "../../include/ictc_mi355x.h"
+#include "split_bf16.h"
 
 namespace ictc {
 int set_error(int code, const char* msg);
@@ -41,10 +42,21 @@ constexpr int kK = 32;    // K per LDS stage
 
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
 
+// Row r of an operand starts at (r / group) * gstride + (r % group) * ld: rows in groups of `group`
+// consecutive rows `ld` apart, groups `gstride` apart (group = 1: plain row pitch gstride).
+struct RowMap {
+  int64_t ld, group, gstride;
+  __device__ __forceinline__ int64_t off(int64_t r) const {
+    if (group == 1) return r * gstride;
+    const uint32_t g = (uint32_t)r / (uint32_t)group;
+    return (int64_t)g * gstride + (int64_t)((uint32_t)r - g * (uint32_t)group) * ld;
+  }
+};
+
 // Stage rows [r0, r0 + R) x k [k0, k0 + kK) of a row-major operand into lds[k][row] (zero outside).
 // Thread t covers (R * kK / 256) entries as float4 runs along k when the pitch and base allow it.
 template <int R, bool VEC>
-__device__ __forceinline__ void stage(const float* __restrict__ X, int64_t rows, int64_t K, int64_t ld, int64_t r0,
+__device__ __forceinline__ void stage(const float* __restrict__ X, int64_t rows, int64_t K, RowMap map, int64_t r0,
                                       int64_t k0, float (*lds)[R + 4]) {
   constexpr int per = R * kK / 256;   // entries per thread (16 for R = 128, 8 for R = 64)
   constexpr int runs = per / 4;
@@ -54,13 +66,14 @@ __device__ __forceinline__ void stage(const float* __restrict__ X, int64_t rows,
     const int row = idx / (kK / 4), kq = 4 * (idx % (kK / 4));
     const int64_t r = r0 + row, k = k0 + kq;
     float v[4];
+    const int64_t base = r < rows ? map.off(r) : 0;
     if (VEC && r < rows && k + 3 < K) {
-      const v4f x = *reinterpret_cast<const v4f*>(X + r * ld + k);
+      const v4f x = *reinterpret_cast<const v4f*>(X + base + k);
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = x[e];
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = (r < rows && k + e < K) ? X[r * ld + k + e] : 0.f;
+      for (int e = 0; e < 4; ++e) v[e] = (r < rows && k + e < K) ? X[base + k + e] : 0.f;
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) lds[kq + e][row] = v[e];
@@ -68,9 +81,9 @@ __device__ __forceinline__ void stage(const float* __restrict__ X, int64_t rows,
 }
 
 template <bool VEC>
-__global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ A, int64_t M, int64_t K, int64_t lda,
+__global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ A, int64_t M, int64_t K, RowMap amap,
                                                       const float* __restrict__ B, int64_t N, int64_t ldb,
-                                                      float* __restrict__ C, int64_t ldc, int accumulate,
+                                                      float* __restrict__ C, RowMap cmap, int accumulate,
                                                       int64_t n_tiles) {
   __shared__ float As[kK][kTM + 4];
   __shared__ float Bs[kK][kTN + 4];
@@ -83,8 +96,8 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ 
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
   for (int64_t k0 = 0; k0 < K; k0 += kK) {
-    stage<kTM, VEC>(A, M, K, lda, m0, k0, As);
-    stage<kTN, VEC>(B, N, K, ldb, n0, k0, Bs);
+    stage<kTM, VEC>(A, M, K, amap, m0, k0, As);
+    stage<kTN, VEC>(B, N, K, RowMap{ldb, 1, ldb}, n0, k0, Bs);
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < kK; kk += 4) {
@@ -110,7 +123,99 @@ __global__ __launch_bounds__(256) void gemm_nt_kernel(const float* __restrict__ 
       for (int r = 0; r < 4; ++r) {
         const int64_t m = m0 + 32 * w + 16 * i + 4 * (l >> 4) + r;
         if (m < M) {
-          float* c = C + m * ldc + n;
+          float* c = C + cmap.off(m) + n;
+          *c = accumulate ? *c + acc[i][j][r] : acc[i][j][r];
+        }
+      }
+  }
+}
+
+
+// Split-bf16 form of the same product (FP32-level accuracy: each operand written as hi + mid + lo bf16
+// parts, six products kept per pair, split_bf16.h) on v_mfma_f32_16x16x32_bf16 for K a multiple of 32:
+// six 16x16x32 bf16 MFMAs replace eight 16x16x4 FP32 ones per 16x16x32 block, about 2.7x fewer MFMA
+// cycles, for the large projections that are MFMA-bound in FP32.  Slabs are staged row-major
+// ([row][k], float4 runs) and split in registers after the LDS read.
+constexpr int kXK = 32;
+
+__device__ __forceinline__ v4f mfma_bf16(bf16x8 a, bf16x8 b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ Split lds_split8(const float* p) {
+  const v4f x0 = *reinterpret_cast<const v4f*>(p), x1 = *reinterpret_cast<const v4f*>(p + 4);
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = x0[e];
+    v[4 + e] = x1[e];
+  }
+  return split8(v);
+}
+
+__global__ __launch_bounds__(256) void gemm_nt_x3_kernel(const float* __restrict__ A, int64_t M, int64_t K, RowMap amap,
+                                                         const float* __restrict__ B, int64_t N, int64_t ldb,
+                                                         float* __restrict__ C, RowMap cmap, int accumulate,
+                                                         int64_t n_tiles) {
+  __shared__ float As[kTM][kXK + 4];
+  __shared__ float Bs[kTN][kXK + 4];
+  const int l = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t bm = blockIdx.x / n_tiles, bn = blockIdx.x % n_tiles;
+  const int64_t m0 = bm * kTM, n0 = bn * kTN;
+  v4f acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int64_t k0 = 0; k0 < K; k0 += kXK) {
+#pragma unroll
+    for (int q = 0; q < kTM * kXK / 4 / 256; ++q) {
+      const int idx = threadIdx.x + 256 * q, row = idx / (kXK / 4), kq = 4 * (idx % (kXK / 4));
+      const int64_t r = m0 + row;
+      v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+      if (r < M) v = *reinterpret_cast<const v4f*>(A + amap.off(r) + k0 + kq);
+      *reinterpret_cast<v4f*>(&As[row][kq]) = v;
+    }
+#pragma unroll
+    for (int q = 0; q < kTN * kXK / 4 / 256; ++q) {
+      const int idx = threadIdx.x + 256 * q, row = idx / (kXK / 4), kq = 4 * (idx % (kXK / 4));
+      const int64_t r = n0 + row;
+      v4f v = v4f{0.f, 0.f, 0.f, 0.f};
+      if (r < N) v = *reinterpret_cast<const v4f*>(B + r * ldb + k0 + kq);
+      *reinterpret_cast<v4f*>(&Bs[row][kq]) = v;
+    }
+    __syncthreads();
+    // operands: lane l holds row / column l % 16 and k = 8 (l / 16) .. + 7 of the slab
+    Split a[2], b[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) a[i] = lds_split8(&As[32 * w + 16 * i + (l & 15)][8 * (l >> 4)]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = lds_split8(&Bs[16 * j + (l & 15)][8 * (l >> 4)]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // smallest products first: lo*hi, hi*lo, mid*mid, mid*hi, hi*mid, hi*hi
+        acc[i][j] = mfma_bf16(a[i].lo, b[j].hi, acc[i][j]);
+        acc[i][j] = mfma_bf16(a[i].hi, b[j].lo, acc[i][j]);
+        acc[i][j] = mfma_bf16(a[i].mid, b[j].mid, acc[i][j]);
+        acc[i][j] = mfma_bf16(a[i].mid, b[j].hi, acc[i][j]);
+        acc[i][j] = mfma_bf16(a[i].hi, b[j].mid, acc[i][j]);
+        acc[i][j] = mfma_bf16(a[i].hi, b[j].hi, acc[i][j]);
+      }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t n = n0 + 16 * j + (l & 15);
+    if (n >= N) continue;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + 32 * w + 16 * i + 4 * (l >> 4) + r;
+        if (m < M) {
+          float* c = C + cmap.off(m) + n;
           *c = accumulate ? *c + acc[i][j][r] : acc[i][j][r];
         }
       }
@@ -169,25 +274,48 @@ int launch_status(const char* what) {
 
 }  // namespace
 
+namespace ictc {
+
+// C (+)= A . B^T with A's and C's rows in groups (RowMap): row r of A at (r / a_group) * a_gstride +
+// (r % a_group) * lda, likewise for C.  split != 0 takes the split-bf16 MFMA form where K is a multiple of
+// 32 and the operands allow 16-byte loads.  Internal to the library (the species message's per-degree GEMMs).
+int gemm_nt_grouped(const float* a, int64_t m, int64_t k, int64_t lda, int64_t a_group, int64_t a_gstride,
+                    const float* b, int64_t n, int64_t ldb, float* c, int64_t ldc, int64_t c_group,
+                    int64_t c_gstride, int accumulate, void* stream, int split) {
+  if (m < 0 || n < 0 || k < 0 || lda < k || ldb < k || ldc < n || a_group < 1 || c_group < 1 || a_gstride < k ||
+      c_gstride < n)
+    return fail(ICTC_ERR_ARGUMENT, "gemm_nt: need m, n, k >= 0, lda >= k, ldb >= k, ldc >= n, groups >= 1");
+  if ((a_group > 1 || c_group > 1) && m > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: too many rows");
+  if (m == 0 || n == 0) return ICTC_OK;
+  if (!c || (k > 0 && (!a || !b))) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: null operand");
+  const int64_t mt = (m + kTM - 1) / kTM, nt = (n + kTN - 1) / kTN;
+  if (mt * nt > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: too many output tiles");
+  const bool vec = lda % 4 == 0 && ldb % 4 == 0 && (a_group == 1 || a_gstride % 4 == 0) &&
+                   ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+  const RowMap am{lda, a_group, a_gstride}, cm{ldc, c_group, c_gstride};
+  if (split && vec && k % kXK == 0) {
+    hipLaunchKernelGGL(gemm_nt_x3_kernel, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k, am, b,
+                       n, ldb, c, cm, accumulate, nt);
+    return launch_status("ictc_gemm_nt launch");
+  }
+  if (vec)
+    hipLaunchKernelGGL(gemm_nt_kernel<true>, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k,
+                       am, b, n, ldb, c, cm, accumulate, nt);
+  else
+    hipLaunchKernelGGL(gemm_nt_kernel<false>, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k,
+                       am, b, n, ldb, c, cm, accumulate, nt);
+  return launch_status("ictc_gemm_nt launch");
+}
+
+}  // namespace ictc
+
 extern "C" {
 
 int ictc_gemm_nt(const float* a, int64_t m, int64_t k, int64_t lda, const float* b, int64_t n, int64_t ldb, float* c,
                  int64_t ldc, int accumulate, void* stream) {
   if (m < 0 || n < 0 || k < 0 || lda < k || ldb < k || ldc < n)
     return fail(ICTC_ERR_ARGUMENT, "gemm_nt: need m, n, k >= 0, lda >= k, ldb >= k, ldc >= n");
-  if (m == 0 || n == 0) return ICTC_OK;
-  if (!c || (k > 0 && (!a || !b))) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: null operand");
-  const int64_t mt = (m + kTM - 1) / kTM, nt = (n + kTN - 1) / kTN;
-  if (mt * nt > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "gemm_nt: too many output tiles");
-  const bool vec = lda % 4 == 0 && ldb % 4 == 0 &&
-                   ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
-  if (vec)
-    hipLaunchKernelGGL(gemm_nt_kernel<true>, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k,
-                       lda, b, n, ldb, c, ldc, accumulate, nt);
-  else
-    hipLaunchKernelGGL(gemm_nt_kernel<false>, dim3((unsigned)(mt * nt)), dim3(256), 0, (hipStream_t)stream, a, m, k,
-                       lda, b, n, ldb, c, ldc, accumulate, nt);
-  return launch_status("ictc_gemm_nt launch");
+  return ictc::gemm_nt_grouped(a, m, k, lda, 1, lda, b, n, ldb, c, ldc, 1, ldc, accumulate, stream, 0);
 }
 
 int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, int batch_sorted, double* out,

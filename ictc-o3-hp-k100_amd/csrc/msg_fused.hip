@@ -31,6 +31,7 @@
 // kernels.  The adjoint's tiles are 8 edges: rows 0..7 carry h3 and rows
 // 8..15 t3 of the same edges, so one MFMA pass yields gates and tangents.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <stdint.h>
 #include <stdio.h>
 
@@ -40,6 +41,9 @@
 
 namespace ictc {
 int set_error(int code, const char* msg);
+int gemm_nt_grouped(const float* a, int64_t m, int64_t k, int64_t lda, int64_t a_group, int64_t a_gstride,
+                    const float* b, int64_t n, int64_t ldb, float* c, int64_t ldc, int64_t c_group,
+                    int64_t c_gstride, int accumulate, void* stream, int split);
 }
 
 namespace ictc {
@@ -750,6 +754,331 @@ __global__ __launch_bounds__(kS0BwdWaves * 64, 1) void msg_s0_bwd_rcv_kernel(Fus
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Species form of the degree-0-input message (the model's first layer).
+//
+// There the features are a function of the species alone, x[s] = X[sp(s)]
+// (embedding, then linear_up), so with the gates g_e[l, c] = sum_k h3_e[k]
+// W4[l C + c, k] the message of path (0, l, l) factorises:
+//   out[d, lm, c] = coef_l sum_{e -> d} m_e Y_lm(e) X[sp(s_e), c] g_e[l, c]
+//                 = sum_{sp, k} Wf_l[c, (sp, k)] H[d, lm, (sp, k)],
+//   H[d, lm, (sp, k)] = sum_{e -> d, sp(s_e) = sp} m_e Y_lm(e) h3_e[k],
+//   Wf_l[c, (sp, k)]  = coef_l X[sp, c] w[l, c] W4[l C + c, k]   (w: TP path weight).
+// The edge loop only accumulates Y h3 outer products in the hidden space
+// (9 FMAs per lane and edge, no per-edge gate projection), and one GEMM per
+// output component (K = S * 64, FP32 MFMA) applies the projection per node.
+// The energy-and-forces adjoint uses the same factorisation:
+//   Z[d, lm, (sp, k)] = sum_c go[d, lm, c] Wf_l[c, (sp, k)]          (GEMM per component)
+//   dsh[e, lm] = m_e sum_k h3_e[k] Z[d, lm, (sp_e, k)]
+//   dr[e]      = m_e sum_lm Y_lm(e) sum_k t3_e[k] Z[d, lm, (sp_e, k)]
+// one wave per receiver row, lane = hidden index k, Z of the row in registers.
+// ---------------------------------------------------------------------------
+constexpr int kSpeciesMax = 4;
+constexpr int kSpWaves = 4;
+
+struct SpeciesArgs {
+  const float* sh;          // [E, NY]
+  const float* h3;          // [G, 64] (rows through grow)
+  const float* t3;          // [G, 64] (adjoint only)
+  const float* mask;        // [E] or nullptr
+  const int64_t* src;       // [E]
+  const int64_t* species;   // [N] species index of each node
+  const int32_t* grow;      // [E] gate row of each edge, nullptr = the edge itself
+  int64_t rows, edges;
+  int S;
+  Csr csr;                  // receiver CSR
+};
+
+struct SpChunk {
+  int32_t e, row, sp;
+  float m;
+};
+
+__device__ __forceinline__ SpChunk sp_stage(const SpeciesArgs& a, int32_t pos, int32_t count) {
+  const int l = lane_id();
+  SpChunk ch{0, 0, 0, 0.f};
+  if (l < count) {
+    const int32_t e = a.csr.order ? a.csr.order[pos + l] : pos + l;
+    const int64_t s = a.src[e];
+    const int64_t sp = (s >= 0 && s < a.rows) ? a.species[s] : -1;
+    const bool ok = sp >= 0 && sp < a.S;
+    ch.e = e;
+    ch.row = a.grow ? a.grow[e] : e;
+    ch.sp = ok ? (int32_t)sp : 0;
+    ch.m = ok ? (a.mask ? a.mask[e] : 1.f) : 0.f;
+  }
+  asm volatile("" : "+v"(ch.e), "+v"(ch.row), "+v"(ch.sp), "+v"(ch.m));
+  return ch;
+}
+
+__device__ __forceinline__ int64_t sp_slot() { return xcd_block(blockIdx.x, gridDim.x) * kSpWaves + wave_id(); }
+
+// Row of H / Z holding (node n, output component lm): the components of degree l
+// are stored together, [N, 2l+1, K] after the blocks of the lower degrees, so
+// that each degree's projection is one GEMM over contiguous rows.
+__device__ __forceinline__ int64_t hz_row(int64_t n, int lm, int64_t N) {
+  const int l = lm < 1 ? 0 : lm < 4 ? 1 : 2;
+  return N * (int64_t)(l * l) + n * (2 * l + 1) + (lm - l * l);
+}
+
+// H[n, lm, (sp, k)] of every receiver row n on FP32 MFMA (v_mfma_f32_16x16x4f32), four edges per step:
+// A[lm][edge] = m Y_lm [species == sp] (lane: row lm = l % 16, edge l / 16), B[edge][k] = h3[edge][k]
+// (lane: edge l / 16, column k = 16 cb + l % 16); one accumulator per (species, 16-column block).
+template <int NY, int S>
+__global__ __launch_bounds__(kSpWaves * 64) void species_fwd_kernel(SpeciesArgs a, float* __restrict__ H) {
+  const int64_t slot = sp_slot();
+  if (slot >= a.rows) return;
+  const int64_t n = visit_row(a.csr, slot, a.rows);
+  if (n < 0) return;
+  const int l = lane_id(), col = l & 15, eg = l >> 4;
+  v4f acc[S][4];
+#pragma unroll
+  for (int b = 0; b < S; ++b)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[b][cb] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+  for (int32_t pos = beg; pos < end; pos += 64) {
+    const int32_t count = min(end - pos, 64);
+    const SpChunk ch = sp_stage(a, pos, count);
+    for (int t0 = 0; t0 < count; t0 += 4) {
+      const int ci = t0 + eg;
+      const bool ok = ci < count;
+      const int src_lane = min(ci, 63);
+      const int32_t e = __shfl(ch.e, src_lane), row = __shfl(ch.row, src_lane), sp = __shfl(ch.sp, src_lane);
+      const float m = __shfl(ch.m, src_lane);
+      const float yv = (ok && col < NY) ? m * a.sh[(int64_t)e * NY + col] : 0.f;
+      float hb[4];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) hb[cb] = ok ? a.h3[(int64_t)row * 64 + 16 * cb + col] : 0.f;
+#pragma unroll
+      for (int b = 0; b < S; ++b) {
+        const float av = sp == b ? yv : 0.f;
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[b][cb] = mfma_f32(av, hb[cb], acc[b][cb]);
+      }
+    }
+  }
+  // D: lane (q, j) holds rows lm = 4 q + r, column k = 16 cb + j
+  const int q = l >> 4;
+  const int64_t K = (int64_t)S * 64;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int lm = 4 * q + r;
+    if (lm < NY) {
+      float* out = H + hz_row(n, lm, a.rows) * K + col;
+#pragma unroll
+      for (int b = 0; b < S; ++b)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) out[b * 64 + 16 * cb] = acc[b][cb][r];
+    }
+  }
+}
+
+// dsh and dr of every edge, eight edges per tile on split-bf16 MFMA: A rows 0..7 are the tile edges' h3,
+// rows 8..15 their t3 (k = 32 ks + 8 (l / 16) + e), B the receiver's Z of one species transposed (column
+// lm = l % 16), so D[row][lm] gives sum_k h3 Z (dsh, before the mask) and sum_k t3 Z (dr's terms).  The
+// tail slot `rows` holds edges whose receiver is out of range: zero Z, zero gradients.
+template <int NY, int S>
+__global__ __launch_bounds__(kSpWaves * 64) void species_bwd_kernel(SpeciesArgs a, const float* __restrict__ Z,
+                                                                     float* __restrict__ dsh, float* __restrict__ dr) {
+  const int64_t slot = sp_slot();
+  if (slot > a.rows) return;
+  const int64_t n = visit_row(a.csr, slot, a.rows);
+  if (n < 0) return;
+  const bool tail = n == a.rows;
+  const int l = lane_id(), j = l & 15, q = l >> 4;
+  const int64_t K = (int64_t)S * 64;
+  SliceOps Bz[S];
+#pragma unroll
+  for (int b = 0; b < S; ++b) {
+    Split part[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      float v[8];
+      if (!tail && j < NY) {
+        const float* zp = Z + hz_row(n, j, a.rows) * K + b * 64 + 32 * ks + 8 * q;
+        const v4f x0 = *reinterpret_cast<const v4f*>(zp), x1 = *reinterpret_cast<const v4f*>(zp + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = x0[e];
+          v[4 + e] = x1[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.f;
+      }
+      part[ks] = split8(v);
+    }
+    Bz[b] = SliceOps{part[0].hi, part[0].mid, part[0].lo, part[1].hi, part[1].mid, part[1].lo};
+  }
+  const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
+  for (int32_t pos = beg; pos < end; pos += 64) {
+    const int32_t count = min(end - pos, 64);
+    const SpChunk ch = sp_stage(a, pos, count);
+    for (int t0 = 0; t0 < count; t0 += 8) {
+      const int ci = t0 + (j & 7);
+      const bool oki = ci < count;
+      const int32_t ri = __shfl(ch.row, min(ci, 63));
+      Split A[2];
+      load_a((j & 8) ? a.t3 : a.h3, oki ? ri : 0, oki, A);
+      // the edges of this lane's D rows: t0 + 4 (q & 1) + r
+      int32_t eo[4], so[4];
+      float mo[4], yo[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int k = t0 + 4 * (q & 1) + r;
+        const int kl = min(k, 63);
+        eo[r] = __shfl(ch.e, kl);
+        so[r] = __shfl(ch.sp, kl);
+        const float mv = __shfl(ch.m, kl);
+        mo[r] = k < count ? mv : 0.f;
+        yo[r] = (k < count && j < NY && q >= 2) ? a.sh[(int64_t)eo[r] * NY + j] : 0.f;
+      }
+      v4f D[S];
+#pragma unroll
+      for (int b = 0; b < S; ++b) D[b] = project_block<false>(Bz[b], A);
+      float w[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float v = D[0][r];
+#pragma unroll
+        for (int b = 1; b < S; ++b) v = so[r] == b ? D[b][r] : v;
+        const int k = t0 + 4 * (q & 1) + r;
+        if (q < 2) {
+          if (k < count && j < NY) dsh[(int64_t)eo[r] * NY + j] = mo[r] * v;
+          w[r] = 0.f;
+        } else {
+          w[r] = yo[r] * v;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        w[r] += dpp_mov<0x128>(w[r]);   // row_ror:8
+        w[r] += dpp_mov<0x124>(w[r]);   // row_ror:4
+        w[r] += dpp_mov<0x122>(w[r]);   // row_ror:2
+        w[r] += dpp_mov<0x121>(w[r]);   // row_ror:1
+      }
+      if (q >= 2 && j == 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (t0 + 4 * (q & 1) + r < count) dr[eo[r]] = mo[r] * w[r];
+      }
+    }
+  }
+}
+
+
+// Projection GEMM of the species form, C = A . B^T with B [NB*16, KS*32] small and constant:
+// B is split once per block into LDS in the MFMA operand layout (NB*KS*3 KB), and each wave streams
+// 16-row tiles of A straight from HBM (lane l: row l % 16, k = 32 ks + 8 (l / 16) .. + 7), splits them
+// and multiplies on split-bf16 MFMA (six products, FP32-level accuracy); no LDS traffic for A and no
+// barriers after the staging.  Rows of A and C map through (group, group stride, pitch): row r at
+// (r / g) * gs + (r % g) * ld.
+struct ProjMap {
+  int64_t ld, group, gstride;
+  __device__ __forceinline__ int64_t off(int64_t r) const {
+    const uint32_t g = (uint32_t)r / (uint32_t)group;
+    return (int64_t)g * gstride + (int64_t)((uint32_t)r - g * (uint32_t)group) * ld;
+  }
+};
+
+constexpr int kProjWaves = 8;
+
+template <int KS, int NB>
+__global__ __launch_bounds__(kProjWaves * 64) void species_proj_kernel(const float* __restrict__ A, int64_t M,
+                                                                        ProjMap am, const float* __restrict__ B,
+                                                                        float* __restrict__ C, ProjMap cm) {
+  extern __shared__ bf16x8 bl[];   // [NB][KS][3][64]
+  constexpr int K = KS * 32;
+  for (int t = threadIdx.x; t < NB * KS * 64; t += blockDim.x) {
+    const int lane = t & 63, ks = (t >> 6) % KS, j = (t >> 6) / KS;
+    const float* p = B + (int64_t)(16 * j + (lane & 15)) * K + 32 * ks + 8 * (lane >> 4);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = p[e];
+    const Split sp = split8(v);
+    bf16x8* o = bl + ((j * KS + ks) * 3) * 64 + lane;
+    o[0] = sp.hi;
+    o[64] = sp.mid;
+    o[128] = sp.lo;
+  }
+  __syncthreads();
+  const int l = lane_id();
+  const int64_t tiles = (M + 15) / 16;
+  const int64_t wstride = (int64_t)gridDim.x * kProjWaves;
+  for (int64_t tile = (int64_t)blockIdx.x * kProjWaves + wave_id(); tile < tiles; tile += wstride) {
+    // B is re-read from LDS per tile: hoisted out of the loop it would take NB * KS * 12 VGPRs
+    asm volatile("" ::: "memory");
+    const int64_t row = tile * 16 + (l & 15);
+    const bool ok = row < M;
+    const float* ap = A + (ok ? am.off(row) : 0) + 8 * (l >> 4);
+    v4f acc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+    float av[KS][8];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ok) {
+        const v4f x0 = *reinterpret_cast<const v4f*>(ap + 32 * ks), x1 = *reinterpret_cast<const v4f*>(ap + 32 * ks + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          av[ks][e] = x0[e];
+          av[ks][4 + e] = x1[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) av[ks][e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const Split a = split8(av[ks]);
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const bf16x8* b = bl + ((j * KS + ks) * 3) * 64 + l;
+        const bf16x8 bh = b[0], bm = b[64], blo = b[128];
+        acc[j] = mfma_bf16(a.lo, bh, acc[j]);
+        acc[j] = mfma_bf16(a.hi, blo, acc[j]);
+        acc[j] = mfma_bf16(a.mid, bm, acc[j]);
+        acc[j] = mfma_bf16(a.mid, bh, acc[j]);
+        acc[j] = mfma_bf16(a.hi, bm, acc[j]);
+        acc[j] = mfma_bf16(a.hi, bh, acc[j]);
+      }
+    }
+    // D: lane (q, j16) holds rows 4 q + r of the tile, column 16 j + j16
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t rr = tile * 16 + 4 * (l >> 4) + r;
+      if (rr < M) {
+        float* c = C + cm.off(rr) + (l & 15);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) c[16 * j] = acc[j][r];
+      }
+    }
+  }
+}
+
+// Wf[p][c][sp*64 + k] = coef_p X[sp, c] w[p, c] W4[p C + c, k] and Wb[p][sp*64 + k][c] = the same value:
+// the B operands of the forward (N = C, K = S*64) and adjoint (N = S*64, K = C) GEMMs of path p.
+template <class TG>
+__global__ void species_weight_kernel(const float* __restrict__ X, int S, int C, const float* __restrict__ W4,
+                                      const float* __restrict__ tpw, float* __restrict__ Wf, float* __restrict__ Wb) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per = (int64_t)C * S * 64;
+  if (t >= TG::PG * per) return;
+  const int p = (int)(t / per), r = (int)(t % per);
+  const int c = r / (S * 64), sk = r % (S * 64), sp = sk / 64, k = sk % 64;
+  // the path's CG constant: the component coefficient of the path's first output slot (one slot per path)
+  int first = 0;
+  for (int q = 0; q < p; ++q) first += 2 * q + 1;
+  const float coef = s0_coef<TG>(first);
+  const float w = tpw ? tpw[(int64_t)p * C + c] : 1.f;
+  const float v = coef * (X[(int64_t)sp * C + c] * w) * W4[((int64_t)p * C + c) * 64 + k];
+  Wf[(int64_t)p * per + (int64_t)c * S * 64 + sk] = v;
+  Wb[(int64_t)p * per + (int64_t)sk * C + c] = v;
+}
+
 int fail(int code, const char* msg) { return set_error(code, msg); }
 
 int launch_status(const char* what) {
@@ -766,6 +1095,129 @@ int cus() {
       hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
     return 256;
   return n;
+}
+
+
+// ---- species form: launch helpers ----
+int64_t align256(int64_t b) { return (b + 255) & ~(int64_t)255; }
+
+struct SpeciesLayout {
+  int64_t hz, wf, wb, total;   // byte offsets of H (or Z), Wf, Wb; total bytes
+};
+SpeciesLayout species_layout(int ny, int paths, int S, int C, int64_t N) {
+  SpeciesLayout L;
+  L.hz = 0;
+  L.wf = align256(N * ny * S * 64 * (int64_t)sizeof(float));
+  L.wb = L.wf + align256((int64_t)paths * C * S * 64 * sizeof(float));
+  L.total = L.wb + align256((int64_t)paths * C * S * 64 * sizeof(float));
+  return L;
+}
+
+template <class TG>
+int species_weights(const float* X, int S, int C, const float* W4, const float* tpw, float* Wf, float* Wb,
+                    hipStream_t st) {
+  const int64_t n = (int64_t)TG::PG * C * S * 64;
+  hipLaunchKernelGGL(species_weight_kernel<TG>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, X, S, C, W4, tpw,
+                     Wf, Wb);
+  return launch_status("species weight launch");
+}
+
+int species_check(int le, int lo, int C, int S, int64_t N, int64_t E) {
+  if (!(le == lo && le >= 0 && le <= 2))
+    return fail(ICTC_ERR_UNSUPPORTED, "species message: edge_lmax == output_lmax <= 2 only");
+  if (S < 1 || S > kSpeciesMax) return fail(ICTC_ERR_UNSUPPORTED, "species message: 1..4 species");
+  if (C <= 0 || C > 64 * kMaxGroups) return fail(ICTC_ERR_UNSUPPORTED, "species message: channels 1..256");
+  if (N < 0 || E < 0 || N > INT32_MAX || E > INT32_MAX) return fail(ICTC_ERR_ARGUMENT, "species message: bad sizes");
+  return ICTC_OK;
+}
+
+template <int LE>
+int species_weights_le(const float* X, int S, int C, const float* W4, const float* tpw, float* Wf, float* Wb,
+                       hipStream_t st) {
+  return species_weights<TpG<0, LE, LE, 0>>(X, S, C, W4, tpw, Wf, Wb, st);
+}
+
+int species_weights_any(int le, const float* X, int S, int C, const float* W4, const float* tpw, float* Wf, float* Wb,
+                        hipStream_t st) {
+  switch (le) {
+    case 0: return species_weights_le<0>(X, S, C, W4, tpw, Wf, Wb, st);
+    case 1: return species_weights_le<1>(X, S, C, W4, tpw, Wf, Wb, st);
+    default: return species_weights_le<2>(X, S, C, W4, tpw, Wf, Wb, st);
+  }
+}
+
+
+template <int NY, int S>
+void species_fwd_launch(const SpeciesArgs& a, float* H, hipStream_t st) {
+  const unsigned blocks = (unsigned)((a.rows + kSpWaves - 1) / kSpWaves);
+  hipLaunchKernelGGL((species_fwd_kernel<NY, S>), dim3(blocks), dim3(kSpWaves * 64), 0, st, a, H);
+}
+template <int NY, int S>
+void species_bwd_launch(const SpeciesArgs& a, const float* Z, float* dsh, float* dr, hipStream_t st) {
+  const unsigned blocks = (unsigned)((a.rows + 1 + kSpWaves - 1) / kSpWaves);
+  hipLaunchKernelGGL((species_bwd_kernel<NY, S>), dim3(blocks), dim3(kSpWaves * 64), 0, st, a, Z, dsh, dr);
+}
+template <int NY>
+void species_fwd_ny(const SpeciesArgs& a, float* H, hipStream_t st) {
+  switch (a.S) {
+    case 1: species_fwd_launch<NY, 1>(a, H, st); break;
+    case 2: species_fwd_launch<NY, 2>(a, H, st); break;
+    case 3: species_fwd_launch<NY, 3>(a, H, st); break;
+    default: species_fwd_launch<NY, 4>(a, H, st); break;
+  }
+}
+template <int NY>
+void species_bwd_ny(const SpeciesArgs& a, const float* Z, float* dsh, float* dr, hipStream_t st) {
+  switch (a.S) {
+    case 1: species_bwd_launch<NY, 1>(a, Z, dsh, dr, st); break;
+    case 2: species_bwd_launch<NY, 2>(a, Z, dsh, dr, st); break;
+    case 3: species_bwd_launch<NY, 3>(a, Z, dsh, dr, st); break;
+    default: species_bwd_launch<NY, 4>(a, Z, dsh, dr, st); break;
+  }
+}
+
+
+int proj_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
+}
+
+// C [M, NB*16] = A [M, KS*32] . B^T through species_proj_kernel (B row-major [NB*16, KS*32]).
+template <int KS, int NB>
+int species_proj(const float* A, int64_t M, ProjMap am, const float* B, float* C, ProjMap cm, hipStream_t st) {
+  if (M <= 0) return ICTC_OK;
+  const int64_t tiles = (M + 15) / 16;
+  const int64_t blocks = std::min<int64_t>((tiles + kProjWaves - 1) / kProjWaves, 2 * (int64_t)proj_cus());
+  const size_t lds = (size_t)NB * KS * 3 * 64 * sizeof(bf16x8);
+  hipLaunchKernelGGL((species_proj_kernel<KS, NB>), dim3((unsigned)blocks), dim3(kProjWaves * 64), lds, st, A, M, am,
+                     B, C, cm);
+  return launch_status("species projection launch");
+}
+
+// Channel counts with compiled projection kernels: the forward's output width and the adjoint's
+// reduction length are C; species widths S*64 with S <= 4.
+template <int CB>
+int species_proj_fwd_c(int S, const float* A, int64_t M, ProjMap am, const float* B, float* C, ProjMap cm,
+                       hipStream_t st) {
+  switch (S) {
+    case 1: return species_proj<2, CB>(A, M, am, B, C, cm, st);
+    case 2: return species_proj<4, CB>(A, M, am, B, C, cm, st);
+    case 3: return species_proj<6, CB>(A, M, am, B, C, cm, st);
+    default: return species_proj<8, CB>(A, M, am, B, C, cm, st);
+  }
+}
+template <int KS>
+int species_proj_bwd_c(int S, const float* A, int64_t M, ProjMap am, const float* B, float* C, ProjMap cm,
+                       hipStream_t st) {
+  switch (S) {
+    case 1: return species_proj<KS, 4>(A, M, am, B, C, cm, st);
+    case 2: return species_proj<KS, 8>(A, M, am, B, C, cm, st);
+    case 3: return species_proj<KS, 12>(A, M, am, B, C, cm, st);
+    default: return species_proj<KS, 16>(A, M, am, B, C, cm, st);
+  }
 }
 
 enum class Pass { kFwd, kBwdSrc, kBwdRcv };
@@ -931,4 +1383,93 @@ int ictc_msg_fused_bwd_tangent(int li, int le, int lo, int C, const float* x, co
   return ICTC_OK;
 }
 
+int64_t ictc_species_message_workspace_bytes(int edge_lmax, int species, int channels, int64_t nodes) {
+  if (edge_lmax < 0 || edge_lmax > 2 || species < 1 || species > kSpeciesMax || channels <= 0 || nodes < 0) return -1;
+  const int ny = (edge_lmax + 1) * (edge_lmax + 1);
+  return species_layout(ny, edge_lmax + 1, species, channels, nodes).total;
+}
+
+int ictc_species_message_fwd(int edge_lmax, int output_lmax, int C, int S, const float* xtab, const int64_t* species,
+                             const float* sh, const float* h3, const float* W4, const float* tp_weight,
+                             const float* mask, const int64_t* src, int64_t N, int64_t E, const int32_t* dptr,
+                             const int32_t* dorder, const int32_t* dst_rows, const int32_t* gate_rows, float* out,
+                             void* ws, int64_t ws_bytes, void* stream) {
+  if (int rc = species_check(edge_lmax, output_lmax, C, S, N, E)) return rc;
+  if (N == 0) return ICTC_OK;
+  const int ny = (edge_lmax + 1) * (edge_lmax + 1), P = edge_lmax + 1;
+  if (!xtab || !species || !W4 || !out || !dptr || !ws || (E > 0 && (!sh || !h3 || !src)))
+    return fail(ICTC_ERR_ARGUMENT, "ictc_species_message_fwd: null operand");
+  const SpeciesLayout L = species_layout(ny, P, S, C, N);
+  if (ws_bytes < L.total) return fail(ICTC_ERR_ARGUMENT, "ictc_species_message_fwd: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  char* base = static_cast<char*>(ws);
+  float *H = (float*)(base + L.hz), *Wf = (float*)(base + L.wf), *Wb = (float*)(base + L.wb);
+  if (int rc = species_weights_any(edge_lmax, xtab, S, C, W4, tp_weight, Wf, Wb, st)) return rc;
+  SpeciesArgs a{sh, h3, nullptr, mask, src, species, gate_rows, N, E, S, Csr{dptr, dorder, dst_rows}};
+  switch (ny) {
+    case 1: species_fwd_ny<1>(a, H, st); break;
+    case 4: species_fwd_ny<4>(a, H, st); break;
+    default: species_fwd_ny<9>(a, H, st); break;
+  }
+  if (int rc = launch_status("ictc_species_message_fwd launch")) return rc;
+  // per degree l: out[n, l^2 + m, :] = H_l[n, m, :] . Wf_l^T, H_l the rows [N (2l+1), S*64] of degree l
+  const int64_t K = (int64_t)S * 64;
+  for (int l = 0; l <= edge_lmax; ++l) {
+    const int64_t g = 2 * l + 1;
+    const float* Al = H + N * (int64_t)(l * l) * K;
+    const float* Bl = Wf + (int64_t)l * C * K;
+    float* Cl = out + (int64_t)(l * l) * C;
+    int rc;
+    if (C == 64)
+      rc = species_proj_fwd_c<4>(S, Al, N * g, ProjMap{K, 1, K}, Bl, Cl, ProjMap{C, g, (int64_t)ny * C}, st);
+    else
+      rc = gemm_nt_grouped(Al, N * g, K, K, 1, K, Bl, C, K, Cl, C, g, (int64_t)ny * C, 0, stream, 0);
+    if (rc) return rc;
+  }
+  return ICTC_OK;
+}
+
+int ictc_species_message_bwd(int edge_lmax, int output_lmax, int C, int S, const float* xtab, const int64_t* species,
+                             const float* sh, const float* h3, const float* t3, const float* W4,
+                             const float* tp_weight, const float* mask, const int64_t* src, int64_t N, int64_t E,
+                             const int32_t* dptr, const int32_t* dorder, const int32_t* dst_rows,
+                             const int32_t* gate_rows, const float* grad, float* dsh, float* dr, void* ws,
+                             int64_t ws_bytes, void* stream) {
+  if (int rc = species_check(edge_lmax, output_lmax, C, S, N, E)) return rc;
+  if (E == 0) return ICTC_OK;
+  const int ny = (edge_lmax + 1) * (edge_lmax + 1), P = edge_lmax + 1;
+  if (!xtab || !species || !W4 || !dptr || !ws || !sh || !h3 || !t3 || !src || !grad || !dsh || !dr)
+    return fail(ICTC_ERR_ARGUMENT, "ictc_species_message_bwd: null operand (dsh and dr are both required)");
+  const SpeciesLayout L = species_layout(ny, P, S, C, N);
+  if (ws_bytes < L.total) return fail(ICTC_ERR_ARGUMENT, "ictc_species_message_bwd: workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  char* base = static_cast<char*>(ws);
+  float *Z = (float*)(base + L.hz), *Wf = (float*)(base + L.wf), *Wb = (float*)(base + L.wb);
+  if (int rc = species_weights_any(edge_lmax, xtab, S, C, W4, tp_weight, Wf, Wb, st)) return rc;
+  const int64_t K = (int64_t)S * 64;
+  if (N > 0) {
+    // per degree l: Z_l[n, m, :] = go[n, l^2 + m, :] . Wb_l^T  (Wb_l = Wf_l^T, [S*64, C])
+    for (int l = 0; l <= edge_lmax; ++l) {
+      const int64_t g = 2 * l + 1;
+      const float* Al = grad + (int64_t)(l * l) * C;
+      const float* Bl = Wb + (int64_t)l * C * K;
+      float* Cl = Z + N * (int64_t)(l * l) * K;
+      int rc;
+      if (C == 64)
+        rc = species_proj_bwd_c<2>(S, Al, N * g, ProjMap{C, g, (int64_t)ny * C}, Bl, Cl, ProjMap{K, 1, K}, st);
+      else
+        rc = gemm_nt_grouped(Al, N * g, C, C, g, (int64_t)ny * C, Bl, K, C, Cl, K, 1, K, 0, stream, 0);
+      if (rc) return rc;
+    }
+  }
+  SpeciesArgs a{sh, h3, t3, mask, src, species, gate_rows, N, E, S, Csr{dptr, dorder, dst_rows}};
+  switch (ny) {
+    case 1: species_bwd_ny<1>(a, Z, dsh, dr, st); break;
+    case 4: species_bwd_ny<4>(a, Z, dsh, dr, st); break;
+    default: species_bwd_ny<9>(a, Z, dsh, dr, st); break;
+  }
+  return launch_status("ictc_species_message_bwd launch");
+}
+
 }  // extern "C"
+

@@ -46,6 +46,11 @@ _SIGNATURES = {
     "ictc_fused_supported": (_i, [_i, _i, _i, _i]),
     "ictc_fused_weight_bytes": (_i64, [_i, _i]),
     "ictc_fused_weight_split": (_i, [_p, _p, _i, _i, _p, _i64, _p]),
+    "ictc_species_message_workspace_bytes": (_i64, [_i, _i, _i, _i64]),
+    "ictc_species_message_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
+                                      _p, _i64, _p]),
+    "ictc_species_message_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
+                                      _p, _p, _p, _p, _i64, _p]),
     "ictc_msg_fused_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_msg_fused_bwd_tangent": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p,
                                         _p, _p, _p, _p, _p, _p, _p, _p]),

@@ -253,18 +253,21 @@ def morton_order(positions: torch.Tensor, spacing: float) -> torch.Tensor:
     return order[:N]
 
 
-def _index_order_scattered(positions: torch.Tensor, rows: torch.Tensor) -> bool:
-    """True when consecutively numbered atoms lie, on average, over twice as far apart as consecutive ``rows``.
+def _receiver_rows(positions: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """The receiver passes' row order: ``rows`` (Morton) when consecutively numbered atoms lie, on average,
+    over twice as far apart as consecutive ``rows``, else index order (0 .. N-1).
 
     A lattice or domain-ordered numbering lands near 1x (both orders step to a
     neighbour, measured within 2 % of each other on the receiver passes); a
-    shuffled numbering lands near (box / neighbour spacing) x.
+    shuffled numbering lands near (box / neighbour spacing) x.  Decided on the
+    device (no host sync): both candidates are row lists the kernels read the same way.
     """
     pos = positions.detach().float()
     step_index = (pos[1:] - pos[:-1]).norm(dim=1).mean()
     spatial = pos[rows.long()]
     step_rows = (spatial[1:] - spatial[:-1]).norm(dim=1).mean()
-    return bool(step_index > 2.0 * step_rows)
+    ident = torch.arange(rows.numel(), dtype=rows.dtype, device=rows.device)
+    return torch.where(step_index > 2.0 * step_rows, rows, ident)
 
 
 def mark_receiver_sorted(dst: torch.Tensor, nodes: int) -> torch.Tensor:
@@ -302,8 +305,8 @@ class Topology:
         self._by_src = None
         self.dst_rows = None
         self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None
-        if self.src_rows is not None and nodes > 1 and _index_order_scattered(positions, self.src_rows):
-            self.dst_rows = self.src_rows
+        if self.src_rows is not None and nodes > 1:
+            self.dst_rows = _receiver_rows(positions, self.src_rows)
         self.gate_rows = None     # int32 [E]: row of the shared radial gates each edge reads (pair_edges)
         self.gate_reps = None     # int64 [rows]: the edge whose length fills each gate row
         self._pairs_of = None
@@ -621,6 +624,98 @@ def _fused_ok(spec, x):
             and bool(nat.lib().ictc_fused_supported(spec.li, spec.le, spec.lo, spec.channels)))
 
 
+# Whether the first layer's message (input degree 0, features a function of the species) runs in the species
+# form (SpeciesRadialMessage) where the caller supplies the species table; False = FusedRadialMessage.
+SPECIES_FORM = True
+SPECIES_MAX = 4
+
+
+def _species_ok(spec, x, xtab):
+    return (SPECIES_FORM and xtab is not None and spec.li == 0 and spec.le == spec.lo and spec.le <= 2
+            and x.is_cuda and x.dtype == torch.float32 and xtab.dtype == torch.float32
+            and 1 <= xtab.shape[0] <= SPECIES_MAX and xtab.shape[1] == spec.channels)
+
+
+class SpeciesRadialMessage(torch.autograd.Function):
+    """message(x, sh, radial_gates(r, fc)) of input degree 0 for energy + forces, with x = xtab[species].
+
+    The first layer's features depend on the species alone, so the message
+    factorises through the radial MLP's hidden space: the edge pass sums
+    m Y_lm h3 per receiver and source species, and one FP32 GEMM per output
+    component projects those sums with W4 folded with the species rows of
+    xtab (ictc_species_message_fwd).  The energy-and-forces adjoint projects
+    the cotangent the same way and forms dharmonics and dr per edge against the
+    hidden state h3 and its r tangent t3 (ictc_species_message_bwd).  h3 and t3
+    have one row per gate row (Topology.pair_edges).  A backward that needs the
+    feature or weight gradients takes the general route (gates rebuilt from
+    h3, ordinary message and radial adjoints) with the full features x.
+    The caller guarantees x[n] == xtab[species[n]] (up to rounding).
+    """
+
+    @staticmethod
+    def forward(ctx, x, sh, r, W1, W2, W3, W4, spec, topo, mask, cfg, xtab, species):
+        ctx.set_materialize_grads(False)
+        ctx.inputs = (x, sh, r, W1, W2, W3, W4)
+        ctx.spec, ctx.topo, ctx.mask, ctx.cfg = spec, topo, mask, cfg
+        x, sh, rc = _c(x), _c(sh), _c(r.detach())
+        Ws = [_c(w.detach()) for w in (W1, W2, W3, W4)]
+        xtab, species = _c(xtab.detach()), _c(species)
+        E, N, S = rc.shape[0], x.shape[0], xtab.shape[0]
+        rg = _c(topo.gate_input(rc))
+        ctx.rows = topo.gate_rows
+        h3, t3 = rc.new_empty(rg.shape[0], 64), rc.new_empty(rg.shape[0], 64)
+        nat.call("ictc_radial_mlp_tangent_fwd", nat.ptr(rg), rg.shape[0], 8, 64, float(cfg[0]), int(cfg[1]),
+                 nat.ptr(Ws[0]), nat.ptr(Ws[1]), nat.ptr(Ws[2]), float(cfg[2]), nat.ptr(h3), nat.ptr(t3),
+                 nat.stream_of(rc))
+        out = x.new_empty(N, spec.out_components * spec.channels)
+        ws, nbytes = _species_ws(spec, S, N, x.device)
+        tok = _timing.begin(f"species_fwd[{spec.le}C{spec.channels}S{S}]")
+        nat.call("ictc_species_message_fwd", spec.le, spec.lo, spec.channels, S, nat.ptr(xtab), nat.ptr(species),
+                 nat.ptr(sh), nat.ptr(h3), nat.ptr(Ws[3]), _w(spec), nat.ptr(mask), nat.ptr(topo.src), N, E,
+                 nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows), nat.ptr(ctx.rows),
+                 nat.ptr(out), nat.ptr(ws), nbytes, nat.stream_of(x))
+        _timing.end(tok)
+        ctx.save_for_backward(x, sh, rc, *Ws, h3, t3, xtab, species)
+        return out
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, go):
+        from ictc_o3.ops.radial_mlp import gate_projection, radial_gates_adjoint
+        if go is None:
+            return (None,) * 13
+        x, sh, r, W1, W2, W3, W4, h3, t3, xtab, species = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:7])
+        ctx.inputs = None
+        spec, topo, mask = ctx.spec, ctx.topo, ctx.mask
+        go = _c(go)
+        rest = (None,) * 6
+        if needs[0] or any(needs[3:7]):
+            gates = _expand_gates(gate_projection(h3, W4), ctx.rows)   # unweighted: the kernels apply the path weight
+            dx, dsh, dg = _msg_bwd_raw(spec, topo, x, sh, gates, mask, go, (needs[0], needs[1], True))
+            dr, dW = radial_gates_adjoint(r, (W1, W2, W3, W4), ctx.cfg, dg, (needs[2], *needs[3:7]))
+            return (dx, dsh, dr, *dW, *rest)
+        if not (needs[1] or needs[2]):
+            return (None,) * 13
+        N, E, S = x.shape[0], sh.shape[0], xtab.shape[0]
+        dsh, dr = torch.empty_like(sh), sh.new_empty(E)
+        ws, nbytes = _species_ws(spec, S, N, x.device)
+        tok = _timing.begin(f"species_bwd[{spec.le}C{spec.channels}S{S}]")
+        nat.call("ictc_species_message_bwd", spec.le, spec.lo, spec.channels, S, nat.ptr(xtab), nat.ptr(species),
+                 nat.ptr(sh), nat.ptr(h3), nat.ptr(t3), nat.ptr(W4), _w(spec), nat.ptr(mask), nat.ptr(topo.src),
+                 N, E, nat.ptr(topo.by_dst.ptr), nat.ptr(topo.by_dst.order), nat.ptr(topo.dst_rows),
+                 nat.ptr(ctx.rows), nat.ptr(go), nat.ptr(dsh), nat.ptr(dr), nat.ptr(ws), nbytes, nat.stream_of(x))
+        _timing.end(tok)
+        return (None, dsh if needs[1] else None, dr if needs[2] else None, None, None, None, None, *rest)
+
+
+def _species_ws(spec, S, N, device):
+    nbytes = int(nat.lib().ictc_species_message_workspace_bytes(spec.le, S, spec.channels, N))
+    if nbytes < 0:
+        raise ValueError("species message: unsupported shape")
+    return torch.empty(max(nbytes, 256) // 4, dtype=torch.float32, device=device), nbytes
+
+
 class FusedRadialMessage(torch.autograd.Function):
     """message(x, sh, radial_gates(r, fc)) for energy + forces without materialised gates.
 
@@ -688,14 +783,17 @@ class FusedRadialMessage(torch.autograd.Function):
         return (dx, dsh, dr if needs[2] else None, None, None, None, None, None, None, None, None, None)
 
 
-def radial_message(x, sh, r, fc, spec, topo, mask, cfg, basis_scale=1.0):
-    """message() with the fused radial gates of `fc` (FusedRadialMessage where the library compiles the
-    shape, else RadialMessage); cfg = (cutoff, poly_p, silu_scale); basis_scale multiplies the radial
-    basis (folded into the first Linear's weight)."""
+def radial_message(x, sh, r, fc, spec, topo, mask, cfg, basis_scale=1.0, species=None):
+    """message() with the fused radial gates of `fc` (SpeciesRadialMessage where the caller passes
+    species = (xtab, node species) with x == xtab[node species] and the shape allows it, else
+    FusedRadialMessage where the library compiles the shape, else RadialMessage); cfg = (cutoff, poly_p,
+    silu_scale); basis_scale multiplies the radial basis (folded into the first Linear's weight)."""
     W = [m.weight for m in fc if isinstance(m, torch.nn.Linear)]
     if basis_scale != 1.0:
         W[0] = W[0] * basis_scale
     cfg = (float(cfg[0]), int(cfg[1]), float(cfg[2]))
+    if species is not None and _species_ok(spec, x, species[0]):
+        return SpeciesRadialMessage.apply(x, sh, r, *W, spec, topo, mask, cfg, species[0], species[1])
     if _fused_ok(spec, x):
         w4s = _fused_weight(fc, W[-1], spec)
         return FusedRadialMessage.apply(x, sh, r, *W, spec, topo, mask, cfg, w4s)

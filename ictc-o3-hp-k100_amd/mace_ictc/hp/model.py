@@ -173,9 +173,11 @@ class Interaction(nn.Module):
         return layer_entry_fast(h, [a.adapters[str(l)].weight for l in range(a.lmax + 1)], self.channels, a.lmax)
 
     def forward(self, h, species, Y, radial, topo, mask, r=None, radial_cfg=None, forces_only=False,
-                basis_scale=1.0, entry=None):
+                basis_scale=1.0, entry=None, species_table=None):
         """radial: [E, K] basis (composable path) or None with r / radial_cfg (fused first-order path;
-        basis_scale multiplies the radial basis there).  entry: (linear_up(h), h[:, :C]) from entry()."""
+        basis_scale multiplies the radial basis there).  entry: (linear_up(h), h[:, :C]) from entry().
+        species_table: [S, C] with linear_up(h)[n] == species_table[species[n]] (the first layer, whose
+        input is the species embedding), which lets the message run in its species form."""
         C = self.channels
         first_order = radial is None
         if entry is not None:
@@ -183,7 +185,8 @@ class Interaction(nn.Module):
         else:
             x, h0 = self.linear_up(h, first_order), h[:, :C]
         if radial is None and forces_only:
-            m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg, basis_scale)
+            m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg, basis_scale,
+                                   species=None if species_table is None else (species_table, species))
         else:
             if radial is None:
                 from ictc_o3.ops.radial_mlp import radial_gates
@@ -383,8 +386,13 @@ class PureCartesianICTDFix(nn.Module):
             if i > 0:
                 e = self.layer_energy_readouts[i - 1](entry[1] if entry is not None else h[:, :self.channels])
                 energy = e if energy is None else energy + e
+            table = None
+            if i == 0 and radial is None and forces_only and inter.input_lmax == 0:
+                # the first layer's input is the species embedding: its linear_up rows per species
+                with torch.no_grad():
+                    table = inter.linear_up(self.node_embedding.weight.t().contiguous(), True)
             message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only,
-                                self.radial_basis_scale, entry=entry)
+                                self.radial_basis_scale, entry=entry, species_table=table)
             h = prod(message, sc, species, first_order=radial is None)
         e = self.last_layer_energy_readout(h if h.shape[1] == self.channels else h[:, :self.channels])
         return e if energy is None else energy + e

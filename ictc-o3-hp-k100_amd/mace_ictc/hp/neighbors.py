@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import itertools
 import math
+import weakref
 
 import torch
 
@@ -53,9 +54,27 @@ def _cell_list_hip(pos, cell_cpu, cutoff, ncell):
     return src, dst, shifts
 
 
+_cell_seen = None   # (weakref to the live cell tensor, its version, its host copy)
+
+
+def _host_cell(cell: torch.Tensor) -> torch.Tensor:
+    """The cell on the host in float64.  A device cell costs a host sync per copy, which stalls the launch
+    queue at every step of an MD loop; the same live tensor with an unchanged version counter (an
+    in-place update bumps it) reuses the copy made for it."""
+    global _cell_seen
+    if not cell.is_cuda:
+        return cell.detach().to(torch.float64)
+    seen = _cell_seen
+    if seen is not None and seen[0]() is cell and seen[1] == cell._version:
+        return seen[2]
+    host = cell.detach().to("cpu", torch.float64)
+    _cell_seen = (weakref.ref(cell), cell._version, host)
+    return host
+
+
 def radius_graph_pbc(pos: torch.Tensor, cell: torch.Tensor, cutoff: float):
     """pos [N,3], cell [3,3] (rows = lattice vectors) -> (src, dst, shifts[E,3] float)."""
-    cell_cpu = cell.detach().to("cpu", torch.float64)
+    cell_cpu = _host_cell(cell)
     ncell, widths = _ncell(cell_cpu, cutoff)
     if pos.is_cuda and pos.dtype == torch.float32 and all(n >= 3 for n in ncell):
         return _cell_list_hip(pos.detach(), cell_cpu, cutoff, ncell)

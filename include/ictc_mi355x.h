@@ -224,6 +224,42 @@ int ictc_msg_fused_bwd_tangent(int input_lmax, int edge_lmax, int output_lmax, i
                                const int32_t* src_rows, const float* grad, float* dfeatures, float* dharmonics,
                                float* dr, const int32_t* gate_rows, void* stream);
 
+/* ---- Species form of the degree-0-input radial message ----------------------
+ * No direct counterpart in the reference: it evaluates the first layer's
+ * message like every other (streamed_gate_message.py:87-223 over the gates
+ * of layers.py:826-835, scatter-sum of the TP, layers.py:1042-1368).  In the
+ * first layer the features are a function of the species alone
+ * (x[s] = xtab[species[s]], xtab [S, C] = linear_up of the embedding table),
+ * so for the paths (0, l, l) the message factorises through the hidden
+ * space of the radial MLP:
+ *   out[d, lm, c] = sum_{sp,k} Wf_l[c, (sp,k)] H[d, lm, (sp,k)],
+ *   H[d, lm, (sp,k)] = sum_{e -> d, species[src e] = sp} m_e Y_lm(e) h3_e[k],
+ *   Wf_l[c, (sp,k)] = coef_l xtab[sp, c] w[l, c] W4[l C + c, k],
+ * with coef_l the path's CG constant and w the TP path weight [P, C]
+ * (NULL = ones).  ictc_species_message_fwd writes out [N, (L+1)^2 * C]
+ * exactly as ictc_msg_fused_fwd with input degree 0 and features
+ * xtab[species]; ictc_species_message_bwd writes dharmonics [E, NY] and
+ * dr [E] exactly as ictc_msg_fused_bwd_tangent without dfeatures (the
+ * features do not depend on positions).  Edges whose source or its species
+ * is out of range contribute nothing; edges whose receiver is out of range
+ * get zero gradients.  edge_lmax == output_lmax <= 2, 1 <= S <= 4, any
+ * channel count up to 256.  Workspace: ictc_species_message_workspace_bytes
+ * (H or Z: N * NY * S * 64 floats, plus the two [P, C, S*64] projection operands); the
+ * caller allocates it, the entry points do not.                              */
+int64_t ictc_species_message_workspace_bytes(int edge_lmax, int species, int channels, int64_t nodes);
+int ictc_species_message_fwd(int edge_lmax, int output_lmax, int channels, int species, const float* xtab,
+                             const int64_t* node_species, const float* harmonics, const float* h3, const float* W4,
+                             const float* tp_weight, const float* mask, const int64_t* src, int64_t nodes,
+                             int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                             const int32_t* dst_rows, const int32_t* gate_rows, float* out, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+int ictc_species_message_bwd(int edge_lmax, int output_lmax, int channels, int species, const float* xtab,
+                             const int64_t* node_species, const float* harmonics, const float* h3, const float* t3,
+                             const float* W4, const float* tp_weight, const float* mask, const int64_t* src,
+                             int64_t nodes, int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order,
+                             const int32_t* dst_rows, const int32_t* gate_rows, const float* grad,
+                             float* dharmonics, float* dr, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---- Edge pairs for shared radial gates ------------------------------------
  * No direct counterpart in the reference, which evaluates the radial MLP
  * `fc` on every directed edge (layers.py:826-835); the gates depend on the

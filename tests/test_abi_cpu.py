@@ -104,8 +104,9 @@ def test_tp_module_path_enumeration():
 
 
 def test_receiver_row_order_choice():
-    """A spatial atom numbering keeps index order for the receiver passes; a shuffled one takes the Morton rows."""
-    from ictc_o3.ops.tensor_product import _index_order_scattered
+    """A spatial atom numbering keeps index order for the receiver passes; a shuffled one takes the Morton rows
+    (chosen without a host read: both are row lists)."""
+    from ictc_o3.ops.tensor_product import _receiver_rows
     g = torch.Generator().manual_seed(3)
     n = 12
     grid = torch.stack(torch.meshgrid(*[torch.arange(n)] * 3, indexing="ij"), -1).reshape(-1, 3).float() * 3.0
@@ -116,12 +117,14 @@ def test_receiver_row_order_choice():
         for d in range(3):
             key |= ((cell[:, d] >> b) & 1) << (3 * b + d)
     rows = torch.sort(key, stable=True).indices.int()
-    assert not _index_order_scattered(pos, rows)
+    got = _receiver_rows(pos, rows)
+    assert got.dtype == rows.dtype and torch.equal(got, torch.arange(rows.numel(), dtype=rows.dtype))
     perm = torch.randperm(pos.shape[0], generator=g)
     shuffled = pos[perm]
     inv = torch.empty_like(perm)
     inv[perm] = torch.arange(perm.numel())
-    assert _index_order_scattered(shuffled, inv[rows.long()].int())
+    srows = inv[rows.long()].int()
+    assert torch.equal(_receiver_rows(shuffled, srows), srows)
 
 
 def test_fused_and_gemm_entry_points_host_checks():
