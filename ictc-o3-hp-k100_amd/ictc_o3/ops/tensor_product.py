@@ -307,16 +307,51 @@ class Topology:
         self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None
         if self.src_rows is not None and nodes > 1:
             self.dst_rows = _receiver_rows(positions, self.src_rows)
-        self.gate_rows = None     # int32 [E]: row of the shared radial gates each edge reads (pair_edges)
-        self.gate_reps = None     # int64 [rows]: the edge whose length fills each gate row
+        self._gate_rows = None    # int32 [E]: row of the shared radial gates each edge reads (pair_edges)
+        self._gate_reps = None    # int64 [rows]: the edge whose length fills each gate row
+        self._pending = None      # pairing launched, row count on its way to the host
         self._pairs_of = None
+
+    def _resolve(self):
+        """Finish pair_edges: wait for the row count's copy (only that copy, not the whole stream) and keep
+        the shared rows when some edge found its reverse."""
+        pending, self._pending = self._pending, None
+        if pending is None:
+            return
+        host, event, rows, reps, E = pending
+        event.synchronize()
+        n = int(host[0])
+        if n < E:
+            self._gate_rows, self._gate_reps = rows, reps[:n].long()
+
+    @property
+    def gate_rows(self):
+        self._resolve()
+        return self._gate_rows
+
+    @gate_rows.setter
+    def gate_rows(self, value):
+        self._pending = None
+        self._gate_rows = value
+
+    @property
+    def gate_reps(self):
+        self._resolve()
+        return self._gate_reps
+
+    @gate_reps.setter
+    def gate_reps(self, value):
+        self._pending = None
+        self._gate_reps = value
 
     def pair_edges(self, shifts: torch.Tensor | None):
         """Share one radial-gate row between every edge and its reverse (same length, bitwise).
 
         The reverse of (s -> d, shift S) is an edge (d -> s, shift -S); shifts
         [E, 3] are compared exactly (None = no periodic images).  Computed once
-        per live shifts tensor and version (one host sync for the row count).
+        per live shifts tensor and version.  The row count comes to the host by an asynchronous copy and
+        is waited for (that copy only) at the first use of gate_rows / gate_reps, so the launches issued in
+        between keep the GPU busy.
         Where no edge has a reverse, or the graph is past the pairing's index range (2^30 edges), the rows
         stay per edge (gate_rows None).
         """
@@ -326,7 +361,8 @@ class Topology:
                 and seen[1] == key:
             return
         E = self.src.numel()
-        self.gate_rows = self.gate_reps = None
+        self._pending = None
+        self._gate_rows = self._gate_reps = None
         ws_bytes = int(nat.lib().ictc_edge_pairs_workspace_bytes(E))
         # pairing is an optimisation: graphs past its index range keep one gate row per edge
         if E > 0 and ws_bytes >= 0 and self.nodes < (1 << 31) - 2:
@@ -341,9 +377,11 @@ class Topology:
             nat.call("ictc_edge_pairs", nat.ptr(self.src), nat.ptr(self.dst), nat.ptr(sh), self.nodes, E,
                      nat.ptr(self.by_dst.ptr), nat.ptr(self.by_dst.order), nat.ptr(rows), nat.ptr(reps),
                      nat.ptr(count), nat.ptr(ws), ws_bytes, nat.stream_of(self.src))
-            n = int(count.item())
-            if n < E:
-                self.gate_rows, self.gate_reps = rows, reps[:n].long()
+            host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            host.copy_(count, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record(torch.cuda.current_stream(dev))
+            self._pending = (host, event, rows, reps, E)
         self._pairs_of = (None if shifts is None else weakref.ref(shifts), key)
 
     def gate_input(self, r: torch.Tensor) -> torch.Tensor:

@@ -54,21 +54,24 @@ def _cell_list_hip(pos, cell_cpu, cutoff, ncell):
     return src, dst, shifts
 
 
-_cell_seen = None   # (weakref to the live cell tensor, its version, its host copy)
+_cell_seen = None   # (weakref to the cell's base tensor, view geometry + version, host copy)
 
 
 def _host_cell(cell: torch.Tensor) -> torch.Tensor:
     """The cell on the host in float64.  A device cell costs a host sync per copy, which stalls the launch
-    queue at every step of an MD loop; the same live tensor with an unchanged version counter (an
-    in-place update bumps it) reuses the copy made for it."""
+    queue at every step of an MD loop; the same live storage owner, seen through the same view (offset,
+    shape, strides) with an unchanged version counter (an in-place update bumps it, views share it),
+    reuses the copy made for it.  Keyed on the base tensor, so `cell[0]` taken anew each step still hits."""
     global _cell_seen
     if not cell.is_cuda:
         return cell.detach().to(torch.float64)
+    base = cell._base if cell._base is not None else cell
+    key = (cell.storage_offset(), tuple(cell.shape), tuple(cell.stride()), cell.dtype, cell._version)
     seen = _cell_seen
-    if seen is not None and seen[0]() is cell and seen[1] == cell._version:
+    if seen is not None and seen[0]() is base and seen[1] == key:
         return seen[2]
     host = cell.detach().to("cpu", torch.float64)
-    _cell_seen = (weakref.ref(cell), cell._version, host)
+    _cell_seen = (weakref.ref(base), key, host)
     return host
 
 

@@ -77,3 +77,17 @@ def test_receiver_sorted_mark_skips_sort(device):
     d.add_(0)
     assert not tpo.receiver_sorted(d, N)
     assert tpo.Topology(s, d, N).by_dst.order is not None
+
+
+def test_host_cell_copy_follows_views_and_versions(device):
+    """The cached host copy of a device cell (no host sync per step) is reused only for the same base
+    tensor, view and version: a fresh `cell[0]` view hits, an in-place update misses."""
+    import mace_ictc.hp.neighbors as nb
+    cell = torch.eye(3, device=device)[None] * 4.0
+    a = nb._host_cell(cell[0])
+    assert nb._host_cell(cell[0]) is a
+    cell[0, 0, 0] = 5.0
+    b = nb._host_cell(cell[0])
+    assert b is not a and float(b[0, 0]) == 5.0
+    other = torch.eye(3, device=device) * 6.0
+    assert float(nb._host_cell(other)[1, 1]) == 6.0

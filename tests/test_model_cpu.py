@@ -109,3 +109,4 @@ def test_unknown_atomic_number_raises_before_any_kernel(bad_z):
     Z[3] = bad_z
     with pytest.raises(ValueError, match="atomic number"):
         model(pos.float(), Z, batch, src, dst, sh, cell.float())
+
