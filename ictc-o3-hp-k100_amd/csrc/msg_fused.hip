@@ -841,22 +841,30 @@ __global__ __launch_bounds__(kSpWaves * 64) void species_fwd_kernel(SpeciesArgs 
   for (int32_t pos = beg; pos < end; pos += 64) {
     const int32_t count = min(end - pos, 64);
     const SpChunk ch = sp_stage(a, pos, count);
-    for (int t0 = 0; t0 < count; t0 += 4) {
-      const int ci = t0 + eg;
-      const bool ok = ci < count;
-      const int src_lane = min(ci, 63);
-      const int32_t e = __shfl(ch.e, src_lane), row = __shfl(ch.row, src_lane), sp = __shfl(ch.sp, src_lane);
-      const float m = __shfl(ch.m, src_lane);
-      const float yv = (ok && col < NY) ? m * a.sh[(int64_t)e * NY + col] : 0.f;
-      float hb[4];
+    // two 4-edge steps per iteration: both steps' loads are in flight before the first MFMA
+    for (int t0 = 0; t0 < count; t0 += 8) {
+      float yv[2], hb[2][4];
+      int32_t spv[2];
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) hb[cb] = ok ? a.h3[(int64_t)row * 64 + 16 * cb + col] : 0.f;
+      for (int u = 0; u < 2; ++u) {
+        const int ci = t0 + 4 * u + eg;
+        const bool ok = ci < count;
+        const int src_lane = min(ci, 63);
+        const int32_t e = __shfl(ch.e, src_lane), row = __shfl(ch.row, src_lane);
+        spv[u] = __shfl(ch.sp, src_lane);
+        const float m = __shfl(ch.m, src_lane);
+        yv[u] = (ok && col < NY) ? m * a.sh[(int64_t)e * NY + col] : 0.f;
 #pragma unroll
-      for (int b = 0; b < S; ++b) {
-        const float av = sp == b ? yv : 0.f;
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[b][cb] = mfma_f32(av, hb[cb], acc[b][cb]);
+        for (int cb = 0; cb < 4; ++cb) hb[u][cb] = ok ? a.h3[(int64_t)row * 64 + 16 * cb + col] : 0.f;
       }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int b = 0; b < S; ++b) {
+          const float av = spv[u] == b ? yv[u] : 0.f;
+#pragma unroll
+          for (int cb = 0; cb < 4; ++cb) acc[b][cb] = mfma_f32(av, hb[u][cb], acc[b][cb]);
+        }
     }
   }
   // D: lane (q, j) holds rows lm = 4 q + r, column k = 16 cb + j
