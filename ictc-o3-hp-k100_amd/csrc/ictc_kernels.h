@@ -692,7 +692,10 @@ constexpr bool src_adjoint_pipelined() {
 }
 
 // TAN: as in msg_bwd_edge_kernel, dr from gdot in place of the gate gradient.
-template <class T, bool TAN>
+// W: the per-path weight a.weight is set (chosen at launch).  One loop per kernel: with both forms in one
+// kernel they share one register allocation, and the gate-tangent form of Tp<2,2,2> spilled 15 VGPRs
+// (226 without a spill for the unweighted form alone).
+template <class T, bool TAN, bool W = false>
 __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd_src_kernel(
     Operands a, const int64_t* __restrict__ dst, Csr scsr, const float* __restrict__ grad, float* __restrict__ dx,
     float* __restrict__ dsh, float* __restrict__ dsh_part, float* __restrict__ dgates, const float* __restrict__ gdot,
@@ -764,8 +767,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
       }
     }
     };
-    if (a.weight) run(Flag<true>{});
-    else run(Flag<false>{});
+    run(Flag<W>{});
     if (active && !tail && dx) store_row<T::NX>(dx + n * (int64_t)(T::NX * C), C, c, d);
     return;
   }

@@ -20,8 +20,12 @@ struct MsgBwdTan {
     float* ws_dr = ws ? ws + (int64_t)(G - 1) * a.edges * T::NY : nullptr;
     hipError_t err;
     if (Occupancy<kMsgBwdSrc, T::LI, T::LE, T::LO>::value >= 2 && dx) {
-      hipLaunchKernelGGL((msg_bwd_src_kernel<T, true>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock), 0, st, a, dst,
-                         scsr, grad, dx, dsh, ws, nullptr, gdot, dr, ws_dr);
+      if (a.weight)
+        hipLaunchKernelGGL((msg_bwd_src_kernel<T, true, true>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock), 0, st,
+                           a, dst, scsr, grad, dx, dsh, ws, nullptr, gdot, dr, ws_dr);
+      else
+        hipLaunchKernelGGL((msg_bwd_src_kernel<T, true, false>), dim3(blocks_for(a.rows + 1), G), dim3(kBlock), 0, st,
+                           a, dst, scsr, grad, dx, dsh, ws, nullptr, gdot, dr, ws_dr);
       if ((err = hipGetLastError()) != hipSuccess) return err;
     } else {
       const int parts = row_parts(a.rows + 1, G);
