@@ -719,7 +719,6 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
     // computes (2 waves per SIMD leave room for the second set of rows).  Per-edge arithmetic is that
     // of the unpipelined form, operand for operand.
     auto run = [&](auto weighted) {
-    constexpr bool W = decltype(weighted)::value;
     for (int32_t pos = beg; pos < end; pos += kWave) {
       const int32_t count = min(end - pos, kWave);
       Chunk<T> ch;
