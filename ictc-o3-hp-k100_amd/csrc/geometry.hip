@@ -140,6 +140,32 @@ int launch_status(const char* what) {
   return fail(ICTC_ERR_RUNTIME, buf);
 }
 
+// out[e, j] = (s0 c0j + s1 c1j) + s2 c2j with each product and sum rounded on its own (no contraction): the
+// same operations for an edge and its reverse (shift -S), so their image shifts are exact negations.
+__global__ __launch_bounds__(kBlock) void shift_vectors_kernel(const float* __restrict__ shifts, int64_t E,
+                                                               const float* __restrict__ cell, int64_t cells,
+                                                               const int64_t* __restrict__ batch,
+                                                               const int64_t* __restrict__ src, int64_t N,
+                                                               float* __restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  int64_t g = 0;
+  if (batch) {
+    const int64_t s = src[e];
+    g = (s >= 0 && s < N) ? batch[s] : -1;
+  }
+  const float s0 = shifts[3 * e], s1 = shifts[3 * e + 1], s2 = shifts[3 * e + 2];
+  if (g < 0 || g >= cells) {
+    const float nan = __int_as_float(0x7fc00000);
+    out[3 * e] = nan; out[3 * e + 1] = nan; out[3 * e + 2] = nan;
+    return;
+  }
+  const float* c = cell + 9 * g;
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    out[3 * e + j] = __fadd_rn(__fadd_rn(__fmul_rn(s0, c[j]), __fmul_rn(s1, c[3 + j])), __fmul_rn(s2, c[6 + j]));
+}
+
 }  // namespace
 
 extern "C" {
@@ -153,6 +179,17 @@ int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* 
   hipLaunchKernelGGL(geometry_fwd_kernel, dim3((unsigned)((edges + kBlock - 1) / kBlock)), dim3(kBlock), 0,
                      (hipStream_t)stream, pos, shift, src, dst, edges, cutoff, r, n, mask);
   return launch_status("ictc_edge_geometry_fwd launch");
+}
+
+int ictc_shift_vectors(const float* shifts, int64_t edges, const float* cell, int64_t cells, const int64_t* batch,
+                       const int64_t* src, int64_t nodes, float* out, void* stream) {
+  if (edges < 0 || cells < 1 || nodes < 0) return fail(ICTC_ERR_ARGUMENT, "shift vectors: invalid size");
+  if (edges == 0) return ICTC_OK;
+  if (!shifts || !cell || !out || (cells > 1 && (!batch || !src)))
+    return fail(ICTC_ERR_ARGUMENT, "shift vectors: null operand");
+  hipLaunchKernelGGL(shift_vectors_kernel, dim3((unsigned)((edges + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                     (hipStream_t)stream, shifts, edges, cell, cells, cells > 1 ? batch : nullptr, src, nodes, out);
+  return launch_status("ictc_shift_vectors launch");
 }
 
 int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, const float* dn, int64_t nodes,

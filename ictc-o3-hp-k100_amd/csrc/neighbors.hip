@@ -8,8 +8,8 @@
 //
 // Steps: (1) per atom, fractional coordinates in FP64, image k = floor(frac),
 // wrapped position, cell index; (2) atoms grouped by cell with the stable CSR
-// build (ictc_csr_build); (3) one thread per receiver counts its neighbours
-// over the 27 surrounding cells; (4) exclusive scan of the counts; (5) the same
+// build (ictc_csr_build); (3) each receiver counts its neighbours
+// over the 27 surrounding cells (one wave per receiver); (4) exclusive scan of the counts; (5) the same
 // walk writes src / dst / shift at the receiver's offset.  Candidates are
 // visited in a fixed order (cell offsets, then atoms in index order within a
 // cell), so the edge list is receiver-sorted and identical run to run.
@@ -59,7 +59,14 @@ __global__ __launch_bounds__(kBlock) void nl_prepare_kernel(const float* __restr
   cell_key[a] = ((int64_t)ci[0] * g.nc[1] + ci[1]) * g.nc[2] + ci[2];
 }
 
-// Walk the candidates of receiver i; FILL = false counts, FILL = true writes.
+// Walk the candidates of receiver i; FILL = false counts, FILL = true writes.  One wave per receiver: the
+// candidates of its 27 cells (cell offsets in a fixed order, atoms in index order within a cell) are numbered
+// 0 .. total-1 in that order and tested 64 at a time, one per lane; the hits of a chunk are compacted in lane
+// order (ballot + prefix count), so the edges come out in the same order as a sequential walk.  Lanes 0..26
+// hold one cell each (its first candidate and the inclusive prefix of the candidate counts), and a lane finds
+// the cell of its candidate against those prefixes, read as wave-uniform scalars.
+constexpr int kWalkWaves = kBlock / 64;
+
 template <bool FILL>
 __global__ __launch_bounds__(kBlock) void nl_walk_kernel(int64_t N, Geometry g, const double* __restrict__ posw,
                                                         const int32_t* __restrict__ kimg,
@@ -69,48 +76,83 @@ __global__ __launch_bounds__(kBlock) void nl_walk_kernel(int64_t N, Geometry g, 
                                                         int32_t* __restrict__ count, const int64_t* __restrict__ row,
                                                         int64_t* __restrict__ src, int64_t* __restrict__ dst,
                                                         float* __restrict__ shift) {
-  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (i >= N) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t i = (int64_t)blockIdx.x * kWalkWaves + (threadIdx.x >> 6);
+  if (i >= N) return;   // whole waves leave together
   const double pi[3] = {posw[3 * i], posw[3 * i + 1], posw[3 * i + 2]};
   const int ci[3] = {cidx[3 * i], cidx[3 * i + 1], cidx[3 * i + 2]};
-  int64_t out = FILL ? row[i] : 0;
-  int32_t n = 0;
-  for (int o = 0; o < 27; ++o) {
-    const int off[3] = {o / 9 - 1, (o / 3) % 3 - 1, o % 3 - 1};
-    int nb[3], wrap[3];
+  // lane o < 27: cell offset o, its first candidate and candidate count
+  int32_t first = 0, cnt = 0;
+  if (lane < 27) {
+    const int off[3] = {lane / 9 - 1, (lane / 3) % 3 - 1, lane % 3 - 1};
+    int nb[3];
 #pragma unroll
     for (int d = 0; d < 3; ++d) {
       const int c = ci[d] + off[d];
-      wrap[d] = c < 0 ? -1 : (c >= g.nc[d] ? 1 : 0);
-      nb[d] = c - wrap[d] * g.nc[d];
+      nb[d] = c - (c < 0 ? -1 : (c >= g.nc[d] ? 1 : 0)) * g.nc[d];
     }
-    double img[3];
-#pragma unroll
-    for (int d = 0; d < 3; ++d)
-      img[d] = wrap[0] * g.cell[0 * 3 + d] + wrap[1] * g.cell[1 * 3 + d] + wrap[2] * g.cell[2 * 3 + d];
     const int64_t cell = ((int64_t)nb[0] * g.nc[1] + nb[1]) * g.nc[2] + nb[2];
-    for (int32_t q = cptr[cell]; q < cptr[cell + 1]; ++q) {
-      const int32_t j = corder[q];
+    first = cptr[cell];
+    cnt = cptr[cell + 1] - first;
+  }
+  int32_t incl = cnt;   // inclusive prefix over lanes
+#pragma unroll
+  for (int k = 1; k < 32; k <<= 1) {
+    const int32_t v = __shfl_up(incl, k, 64);
+    if (lane >= k) incl += v;
+  }
+  int32_t bound[27];
+#pragma unroll
+  for (int k = 0; k < 27; ++k) bound[k] = __builtin_amdgcn_readlane(incl, k);
+  const int32_t total = bound[26];
+  int64_t out = FILL ? row[i] : 0;
+  int32_t n = 0;
+  for (int32_t t0 = 0; t0 < total; t0 += 64) {
+    const int32_t t = t0 + lane;
+    int o = 0;
+#pragma unroll
+    for (int k = 0; k < 26; ++k) o += t >= bound[k];
+    const int32_t excl = __shfl(incl - cnt, o, 64);
+    const int32_t q = __shfl(first, o, 64) + (t - excl);
+    bool hit = false;
+    int32_t j = 0;
+    int wrap[3] = {0, 0, 0};
+    if (t < total) {
+      const int off[3] = {o / 9 - 1, (o / 3) % 3 - 1, o % 3 - 1};
+#pragma unroll
+      for (int d = 0; d < 3; ++d) {
+        const int c = ci[d] + off[d];
+        wrap[d] = c < 0 ? -1 : (c >= g.nc[d] ? 1 : 0);
+      }
+      double img[3];
+#pragma unroll
+      for (int d = 0; d < 3; ++d)
+        img[d] = wrap[0] * g.cell[0 * 3 + d] + wrap[1] * g.cell[1 * 3 + d] + wrap[2] * g.cell[2 * 3 + d];
+      j = corder[q];
       double r2 = 0.0;
 #pragma unroll
       for (int d = 0; d < 3; ++d) {
         const double v = pi[d] - (posw[3 * j + d] + img[d]);
         r2 += v * v;
       }
-      if (r2 < g.cut2 && r2 > 1e-20) {
-        if (FILL) {
-          src[out] = j;
-          dst[out] = i;
+      hit = r2 < g.cut2 && r2 > 1e-20;
+    }
+    const uint64_t mask = __ballot(hit);
+    if (FILL) {
+      if (hit) {
+        const int64_t at = out + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+        src[at] = j;
+        dst[at] = i;
 #pragma unroll
-          for (int d = 0; d < 3; ++d) shift[3 * out + d] = (float)(kimg[3 * j + d] - kimg[3 * i + d] - wrap[d]);
-          ++out;
-        } else {
-          ++n;
-        }
+        for (int d = 0; d < 3; ++d) shift[3 * at + d] = (float)(kimg[3 * j + d] - kimg[3 * i + d] - wrap[d]);
       }
+      out += __popcll(mask);
+    } else {
+      n += __popcll(mask);
     }
   }
-  if (!FILL) count[i] = n;
+  if (!FILL && lane == 0) count[i] = n;
 }
 
 // count != nullptr: count[atoms] = 0 (scan tail); else edges[0] = row[atoms].
@@ -220,7 +262,8 @@ int ictc_neighbors_count(const float* pos, int64_t atoms, const double* cell, do
     return rc;
   int32_t* count = (int32_t*)(w + L.count);
   if (atoms > 0) {
-    hipLaunchKernelGGL((nl_walk_kernel<false>), dim3(blocks), dim3(kBlock), 0, st, atoms, g, (const double*)(w + L.posw),
+    const unsigned walk_blocks = (unsigned)((atoms + kWalkWaves - 1) / kWalkWaves);
+    hipLaunchKernelGGL((nl_walk_kernel<false>), dim3(walk_blocks), dim3(kBlock), 0, st, atoms, g, (const double*)(w + L.posw),
                        (const int32_t*)(w + L.kimg), (const int32_t*)(w + L.cidx), (const int32_t*)(w + L.cptr),
                        (const int32_t*)(w + L.corder), count, nullptr, nullptr, nullptr, nullptr);
     if (int rc = check_launch("neighbours count")) return rc;
@@ -250,7 +293,7 @@ int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, dou
   if (atoms == 0) return ICTC_OK;
   if (!src || !dst || !shifts) return fail(ICTC_ERR_ARGUMENT, "neighbours: null output");
   const char* w = (const char*)workspace;
-  const unsigned blocks = (unsigned)((atoms + kBlock - 1) / kBlock);
+  const unsigned blocks = (unsigned)((atoms + kWalkWaves - 1) / kWalkWaves);
   hipLaunchKernelGGL((nl_walk_kernel<true>), dim3(blocks), dim3(kBlock), 0, (hipStream_t)stream, atoms, g,
                      (const double*)(w + L.posw), (const int32_t*)(w + L.kimg), (const int32_t*)(w + L.cidx),
                      (const int32_t*)(w + L.cptr), (const int32_t*)(w + L.corder), (int32_t*)nullptr,

@@ -20,6 +20,12 @@
 // are bitwise equal too, and no kernel accumulates into gate rows.  Owners
 // are numbered by a prefix sum in edge order (deterministic), so half of a
 // symmetric list searches and half owns.
+//
+// Source CSR (ictc_edge_pairs_src_csr): when the lookup pairs every edge
+// with its reverse one-to-one, the edges leaving node n are exactly the
+// reverses of the edges entering it, so the source CSR has the receiver CSR's
+// ptr and its order is those reverses ranked into edge order per node: the
+// stable sort over src without sorting.
 #include <hipcub/hipcub.hpp>
 #include <stdint.h>
 #include <stdio.h>
@@ -62,7 +68,7 @@ __global__ __launch_bounds__(256) void partner_kernel(const int64_t* __restrict_
                                                       const int32_t* __restrict__ ptr,
                                                       const int32_t* __restrict__ order,
                                                       const int32_t* __restrict__ sorted_src,
-                                                      int32_t* __restrict__ partner) {
+                                                      int32_t* __restrict__ partner, int32_t* __restrict__ rev) {
   const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kLanes;
   const int sub = threadIdx.x % kLanes;
   if (e >= E) return;   // whole groups leave together (E * kLanes lanes, groups aligned)
@@ -71,23 +77,34 @@ __global__ __launch_bounds__(256) void partner_kernel(const int64_t* __restrict_
   const float sx = shifts ? shifts[3 * e] : 0.f, sy = shifts ? shifts[3 * e + 1] : 0.f,
               sz = shifts ? shifts[3 * e + 2] : 0.f;
   if (s >= 0 && s < N && d >= 0 && d < N && reader(s, d, sx, sy, sz)) {
-    const int32_t end = ptr[s + 1];
+    const int32_t beg = ptr[s], end = ptr[s + 1];
     // every lane runs its whole strided scan (no early exit before the cross-lane reduction) and keeps
-    // its first match
-#pragma unroll 16
-    for (int32_t q = ptr[s] + sub; q < end; q += kLanes) {
-      bool hit = sorted_src[q] == (int32_t)d && best == INT32_MAX;
-      if (hit) {
-        const int32_t e2 = order ? order[q] : q;
-        hit = e2 != e && (!shifts || (shifts[3 * (int64_t)e2] == -sx && shifts[3 * (int64_t)e2 + 1] == -sy &&
-                                      shifts[3 * (int64_t)e2 + 2] == -sz));
+    // its first match; 16-byte loads of 4-aligned quads (the sorted_src slab is padded to 256 bytes, so a
+    // quad past the last edge stays inside it), entries outside [beg, end) ignored
+#pragma unroll 4
+    for (int32_t q4 = (beg & ~3) + 4 * sub; q4 < end; q4 += 4 * kLanes) {
+      const int4 v = *reinterpret_cast<const int4*>(sorted_src + q4);
+      const int32_t cand[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int32_t q = q4 + k;
+        bool hit = cand[k] == (int32_t)d && q >= beg && q < end && best == INT32_MAX;
+        if (hit) {
+          const int32_t e2 = order ? order[q] : q;
+          hit = e2 != e && (!shifts || (shifts[3 * (int64_t)e2] == -sx && shifts[3 * (int64_t)e2 + 1] == -sy &&
+                                        shifts[3 * (int64_t)e2 + 2] == -sz));
+        }
+        if (hit) best = q;
       }
-      if (hit) best = q;
     }
   }
 #pragma unroll
   for (int m = kLanes / 2; m > 0; m >>= 1) best = min(best, __shfl_xor(best, m, kLanes));
-  if (sub == 0) partner[e] = best == INT32_MAX ? -1 : (order ? order[best] : best);
+  if (sub == 0) {
+    const int32_t p = best == INT32_MAX ? -1 : (order ? order[best] : best);
+    partner[e] = p;
+    if (rev && p >= 0) rev[p] = (int32_t)e;   // the reverse of p, for the source CSR (a second claimant races)
+  }
 }
 
 __global__ void canonical_kernel(const int32_t* __restrict__ partner, int64_t E, int32_t* __restrict__ flag) {
@@ -109,6 +126,61 @@ __global__ void rows_kernel(const int32_t* __restrict__ partner, const int32_t* 
 
 __global__ void zero_count_kernel(int32_t* count) { count[0] = 0; }
 
+// The reverse map for the source CSR: reverse(e) = partner[e] for a reader, rev[e] (written by the reader
+// that found e, -1 before) for a row owner.  It is one-to-one when every reader's reverse names it back and
+// every owner was found: two readers finding one owner (duplicated edges) leave one of them unnamed.
+__global__ void fill_kernel(int32_t* __restrict__ a, int64_t n, int32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) a[i] = v;
+}
+
+__device__ __forceinline__ int32_t reverse_of(const int32_t* __restrict__ partner, const int32_t* __restrict__ rev,
+                                              int32_t e) {
+  const int32_t p = partner[e];
+  return p >= 0 ? p : rev[e];
+}
+
+__global__ void check_kernel(const int32_t* __restrict__ partner, const int32_t* __restrict__ rev, int64_t E,
+                             int32_t* __restrict__ bad) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int32_t p = partner[e];
+  const bool ok = p >= 0 ? rev[p] == (int32_t)e : rev[e] >= 0;
+  if (!ok) atomicOr(bad, 1);
+}
+
+__global__ void ok_kernel(const int32_t* __restrict__ bad, int32_t* __restrict__ src_ok) {
+  src_ok[0] = bad[0] == 0 ? 1 : 0;
+}
+
+// One wave per node s: the edges leaving s are the reverses of the edges entering s (segment s of the
+// receiver CSR), and they are written in edge order (a stable sort by source) by ranking each value against
+// the whole segment.  Ranks stay in [0, segment length), so a map that is not one-to-one still writes
+// inside the segment (the host then does not use the result).
+__global__ __launch_bounds__(256) void src_order_kernel(const int32_t* __restrict__ ptr,
+                                                        const int32_t* __restrict__ order,
+                                                        const int32_t* __restrict__ partner,
+                                                        const int32_t* __restrict__ rev, int64_t N,
+                                                        int32_t* __restrict__ src_order) {
+  const int lane = threadIdx.x & 63;
+  const int64_t s = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (s >= N) return;   // whole waves leave together
+  const int32_t beg = ptr[s], k = ptr[s + 1] - beg;
+  for (int32_t t0 = 0; t0 < k; t0 += 64) {
+    const bool mine = t0 + lane < k;
+    const int32_t v = mine ? reverse_of(partner, rev, order ? order[beg + t0 + lane] : beg + t0 + lane) : 0;
+    int32_t rank = 0;
+    for (int32_t u0 = 0; u0 < k; u0 += 64) {
+      const int32_t x = u0 == t0 ? v
+                        : u0 + lane < k ? reverse_of(partner, rev, order ? order[beg + u0 + lane] : beg + u0 + lane)
+                                        : 0;
+      const int32_t n = min(64, k - u0);
+      for (int32_t u = 0; u < n; ++u) rank += __builtin_amdgcn_readlane(x, u) < v;
+    }
+    if (mine) src_order[beg + rank] = v;
+  }
+}
+
 size_t scan_temp_bytes(int64_t E) {
   size_t bytes = 0;
   hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr, (int)(E > 0 ? E : 1));
@@ -121,12 +193,17 @@ extern "C" {
 
 int64_t ictc_edge_pairs_workspace_bytes(int64_t E) {
   if (E < 0 || E >= (int64_t(1) << 30)) return -1;   // E * kLanes threads under 2^31
-  return (int64_t)(4 * align256(sizeof(int32_t) * (size_t)(E > 0 ? E : 1)) + align256(scan_temp_bytes(E)));
+  return (int64_t)(5 * align256(sizeof(int32_t) * (size_t)(E > 0 ? E : 1)) + align256(sizeof(int32_t)) +
+                   align256(scan_temp_bytes(E)));
 }
 
-int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts, int64_t N, int64_t E,
-                    const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps,
-                    int32_t* count, void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts, int64_t N, int64_t E,
+               const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps, int32_t* count,
+               int32_t* src_order, int32_t* src_ok, void* workspace, int64_t workspace_bytes, void* stream) {
   if (N < 0 || E < 0) return fail(ICTC_ERR_ARGUMENT, "edge pairs: negative size");
   if (E >= (int64_t(1) << 30) || N >= (int64_t(1) << 31) - 2)
     return fail(ICTC_ERR_UNSUPPORTED, "edge pairs: 2^30 edges or more, or more than 2^31 nodes");
@@ -134,6 +211,7 @@ int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts,
   hipStream_t st = (hipStream_t)stream;
   if (E == 0) {   // no pairs: count = 0 (a fill kernel, so the call stays graph-capturable)
     hipLaunchKernelGGL(zero_count_kernel, dim3(1), dim3(1), 0, st, count);
+    if (src_ok) hipLaunchKernelGGL(zero_count_kernel, dim3(1), dim3(1), 0, st, src_ok);
     const hipError_t z = hipGetLastError();
     return z == hipSuccess ? ICTC_OK : fail(ICTC_ERR_RUNTIME, "ictc_edge_pairs launch");
   }
@@ -147,17 +225,28 @@ int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts,
   int32_t* flag = (int32_t*)(ws + slab);
   int32_t* idx = (int32_t*)(ws + 2 * slab);
   int32_t* sorted_src = (int32_t*)(ws + 3 * slab);
-  void* temp = ws + 4 * slab;
+  int32_t* rev = (int32_t*)(ws + 4 * slab);
+  int32_t* bad = (int32_t*)(ws + 5 * slab);
+  void* temp = ws + 5 * slab + align256(sizeof(int32_t));
   size_t temp_bytes = scan_temp_bytes(E);
   const unsigned blocks = (unsigned)((E + 255) / 256);
   const unsigned partner_blocks = (unsigned)((E * kLanes + 255) / 256);
   hipLaunchKernelGGL(sorted_src_kernel, dim3(blocks), dim3(256), 0, st, src, N, E, dst_order, sorted_src);
+  if (src_order) hipLaunchKernelGGL(fill_kernel, dim3(blocks), dim3(256), 0, st, rev, E, -1);
   hipLaunchKernelGGL(partner_kernel, dim3(partner_blocks), dim3(256), 0, st, src, dst, shifts, N, E, dst_ptr,
-                     dst_order, sorted_src, partner);
+                     dst_order, sorted_src, partner, src_order ? rev : nullptr);
   hipLaunchKernelGGL(canonical_kernel, dim3(blocks), dim3(256), 0, st, partner, E, flag);
   if (hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, flag, idx, (int)E, st) != hipSuccess)
     return fail(ICTC_ERR_RUNTIME, "edge pairs: scan");
   hipLaunchKernelGGL(rows_kernel, dim3(blocks), dim3(256), 0, st, partner, flag, idx, E, gate_rows, reps, count);
+  if (src_order) {
+    hipLaunchKernelGGL(fill_kernel, dim3(1), dim3(64), 0, st, bad, (int64_t)1, 0);
+    hipLaunchKernelGGL(check_kernel, dim3(blocks), dim3(256), 0, st, partner, rev, E, bad);
+    hipLaunchKernelGGL(ok_kernel, dim3(1), dim3(1), 0, st, bad, src_ok);
+    if (N > 0)
+      hipLaunchKernelGGL(src_order_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, dst_ptr, dst_order,
+                         partner, rev, N, src_order);
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char buf[256];
@@ -165,6 +254,26 @@ int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts,
     return fail(ICTC_ERR_RUNTIME, buf);
   }
   return ICTC_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts, int64_t N, int64_t E,
+                    const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps,
+                    int32_t* count, void* workspace, int64_t workspace_bytes, void* stream) {
+  return edge_pairs(src, dst, shifts, N, E, dst_ptr, dst_order, gate_rows, reps, count, nullptr, nullptr,
+                    workspace, workspace_bytes, stream);
+}
+
+int ictc_edge_pairs_src_csr(const int64_t* src, const int64_t* dst, const float* shifts, int64_t N, int64_t E,
+                            const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps,
+                            int32_t* count, int32_t* src_order, int32_t* src_ok, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  if (!src_order || !src_ok) return fail(ICTC_ERR_ARGUMENT, "edge pairs: null source order");
+  return edge_pairs(src, dst, shifts, N, E, dst_ptr, dst_order, gate_rows, reps, count, src_order, src_ok,
+                    workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -56,6 +56,7 @@ _SIGNATURES = {
                                         _p, _p, _p, _p, _p, _p, _p, _p]),
     "ictc_edge_pairs_workspace_bytes": (_i64, [_i64]),
     "ictc_edge_pairs": (_i, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _i64, _p]),
+    "ictc_edge_pairs_src_csr": (_i, [_p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p]),
     "ictc_sh_fwd": (_i, [_p, _i64, _i, _p, _p]),
     "ictc_sh_bwd": (_i, [_p, _p, _i64, _i, _p, _p]),
     "ictc_sh_jvp": (_i, [_p, _p, _i64, _i, _p, _p]),
@@ -83,6 +84,7 @@ _SIGNATURES = {
     "ictc_edge_geometry_fwd": (_i, [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _p]),
     "ictc_edge_geometry_bwd": (_i, [_p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _p]),
     "ictc_edge_vector_bwd": (_i, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
+    "ictc_shift_vectors": (_i, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
     "ictc_radial_mlp_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p]),
     "ictc_radial_mlp_tangent_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p,
                                          _p]),

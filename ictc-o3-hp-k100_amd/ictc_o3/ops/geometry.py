@@ -110,3 +110,25 @@ def edge_vectors(pos: torch.Tensor, shift: torch.Tensor | None, topo) -> torch.T
     if not pos.is_cuda or pos.dtype != torch.float32:
         raise TypeError("edge_vectors runs on float32 device tensors")
     return _EdgeVectors.apply(pos, shift, topo)
+
+
+def shift_vectors(shifts: torch.Tensor, cell: torch.Tensor, batch: torch.Tensor | None,
+                  src: torch.Tensor | None) -> torch.Tensor:
+    """Cartesian image shifts [E, 3] = shifts [E, 3] (lattice coordinates) . cell of the edge's graph
+    (cell [3, 3] or [G, 3, 3]; graph batch[src[e]] when G > 1), as (s0 c0j + s1 c1j) + s2 c2j with every
+    operation rounded on its own, so an edge and its reverse get exactly negated shifts.  FP32 device
+    tensors; not differentiable (the cell carries no gradient here)."""
+    shifts = _c(shifts.detach())
+    if shifts.dtype != torch.float32 or shifts.dim() != 2 or shifts.shape[1] != 3:
+        raise ValueError("shift_vectors: shifts must be float32 [E, 3]")
+    cells = _c(cell.detach().to(torch.float32).reshape(-1, 3, 3))
+    E, G = shifts.shape[0], cells.shape[0]
+    out = shifts.new_empty(E, 3)
+    if G > 1:
+        if batch is None or src is None:
+            raise ValueError("shift_vectors: batch and src are needed with several cells")
+        batch, src = _c(batch.long()), _c(src.long())
+    nodes = batch.numel() if G > 1 else 0
+    nat.call("ictc_shift_vectors", nat.ptr(shifts), E, nat.ptr(cells), G, nat.ptr(batch) if G > 1 else None,
+             nat.ptr(src) if G > 1 else None, nodes, nat.ptr(out), nat.stream_of(shifts))
+    return out

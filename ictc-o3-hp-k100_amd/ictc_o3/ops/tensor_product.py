@@ -239,6 +239,14 @@ class Csr:
                  nat.ptr(ws), ws_bytes, nat.stream_of(keys))
 
 
+    @classmethod
+    def prebuilt(cls, ptr: torch.Tensor, order: torch.Tensor | None, nodes: int) -> "Csr":
+        """A CSR whose ptr / order were built elsewhere (ictc_edge_pairs_src_csr's source order)."""
+        csr = cls.__new__(cls)
+        csr.nodes, csr.ptr, csr.order = nodes, ptr, order
+        return csr
+
+
 def morton_order(positions: torch.Tensor, spacing: float) -> torch.Tensor:
     """int32 [N] rows sorted (stably) by the Morton key of their grid cell floor(pos / spacing)."""
     pos = _c(positions.detach().float())
@@ -318,11 +326,14 @@ class Topology:
         pending, self._pending = self._pending, None
         if pending is None:
             return
-        host, event, rows, reps, E = pending
+        host, event, rows, reps, E, src_order = pending
         event.synchronize()
         n = int(host[0])
         if n < E:
             self._gate_rows, self._gate_reps = rows, reps[:n].long()
+        if src_order is not None and int(host[1]) == 1 and self._by_src is None:
+            # every edge paired one-to-one with its reverse: the source CSR shares the receiver CSR's ptr
+            self._by_src = Csr.prebuilt(self.by_dst.ptr, src_order, self.nodes)
 
     @property
     def gate_rows(self):
@@ -372,16 +383,25 @@ class Topology:
             dev = self.src.device
             rows = torch.empty(E, dtype=torch.int32, device=dev)
             reps = torch.empty(E, dtype=torch.int32, device=dev)
-            count = torch.empty(1, dtype=torch.int32, device=dev)
+            count = torch.zeros(2, dtype=torch.int32, device=dev)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
-            nat.call("ictc_edge_pairs", nat.ptr(self.src), nat.ptr(self.dst), nat.ptr(sh), self.nodes, E,
-                     nat.ptr(self.by_dst.ptr), nat.ptr(self.by_dst.order), nat.ptr(rows), nat.ptr(reps),
-                     nat.ptr(count), nat.ptr(ws), ws_bytes, nat.stream_of(self.src))
-            host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+            src_order = None
+            if self._by_src is None and SOURCE_CSR_FROM_PAIRS:
+                # the same reverse lookup also yields the source CSR of a symmetric list (no sort)
+                src_order = torch.empty(E, dtype=torch.int32, device=dev)
+                nat.call("ictc_edge_pairs_src_csr", nat.ptr(self.src), nat.ptr(self.dst), nat.ptr(sh), self.nodes,
+                         E, nat.ptr(self.by_dst.ptr), nat.ptr(self.by_dst.order), nat.ptr(rows), nat.ptr(reps),
+                         nat.ptr(count), nat.ptr(src_order), nat.ptr(count[1:]), nat.ptr(ws), ws_bytes,
+                         nat.stream_of(self.src))
+            else:
+                nat.call("ictc_edge_pairs", nat.ptr(self.src), nat.ptr(self.dst), nat.ptr(sh), self.nodes, E,
+                         nat.ptr(self.by_dst.ptr), nat.ptr(self.by_dst.order), nat.ptr(rows), nat.ptr(reps),
+                         nat.ptr(count), nat.ptr(ws), ws_bytes, nat.stream_of(self.src))
+            host = torch.empty(2, dtype=torch.int32, pin_memory=True)
             host.copy_(count, non_blocking=True)
             event = torch.cuda.Event()
             event.record(torch.cuda.current_stream(dev))
-            self._pending = (host, event, rows, reps, E)
+            self._pending = (host, event, rows, reps, E, src_order)
         self._pairs_of = (None if shifts is None else weakref.ref(shifts), key)
 
     def gate_input(self, r: torch.Tensor) -> torch.Tensor:
@@ -390,6 +410,7 @@ class Topology:
 
     @property
     def by_src(self):
+        self._resolve()
         if self._by_src is None:
             self._by_src = Csr(self.src, self.nodes)
         return self._by_src
@@ -635,6 +656,8 @@ FUSED_GATES = "auto"
 # Whether callers of radial_message pair edges with their reverses (Topology.pair_edges) so that the
 # radial gates are evaluated once per undirected edge; False keeps one gate row per directed edge.
 PAIR_GATES = True
+# pair_edges also builds the source CSR from the reverse lookup when the list is symmetric (no sort over src)
+SOURCE_CSR_FROM_PAIRS = True
 
 
 def _fused_weight(fc, W4, spec):

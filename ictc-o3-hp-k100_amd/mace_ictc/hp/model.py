@@ -256,11 +256,18 @@ def shift_vectors(shifts: torch.Tensor, cell: torch.Tensor, batch: torch.Tensor,
     radial gates, which is only exact when their lengths are bitwise equal.  They
     are because this form is odd in the shift bit for bit: each component is a
     sum of three products s_k * c_kj in a fixed order, and negating every s_k
-    negates every product and every partial sum exactly.  A library GEMM or an
+    negates every product and every partial sum exactly (on the device: the
+    kernel ictc_shift_vectors, every operation rounded on its own).  A library GEMM or an
     FMA-contracted form need not keep that (its order or fusion may differ with
     the operand's sign pattern), so do not change it without re-running the
     shared-row bitwise tests.
     """
+    # the kernel carries no gradient: a caller differentiating in the shifts or the cell (the LAMMPS core
+    # passes its edge vectors as shifts) takes the torch form
+    if (shifts.is_cuda and shifts.dtype == torch.float32
+            and not (torch.is_grad_enabled() and (cell.requires_grad or shifts.requires_grad))):
+        from ictc_o3.ops.geometry import shift_vectors as native_shift_vectors
+        return native_shift_vectors(shifts, cell, batch, edge_src)
     if cell.shape[0] == 1:   # [E, 3] x [3, 3] as three broadcast products (no library GEMM)
         return (shifts.unsqueeze(-1) * cell[0].to(shifts.dtype)).sum(1)
     # per-edge cell rows without a batched 1x3x3 GEMM per edge

@@ -280,6 +280,19 @@ int ictc_edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts,
                     const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps,
                     int32_t* count, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ictc_edge_pairs plus the source-sorted CSR from the same reverse lookup (it
+ * replaces the stable sort of ictc_csr_build over src for a symmetric list).
+ * When every edge has a reverse and the map edge -> reverse is one-to-one,
+ * the edges leaving node n are the reverses of the edges entering it, so the
+ * source CSR's ptr equals dst_ptr; src_order [E] int32 then receives those
+ * edges in edge order per node (exactly ictc_csr_build's stable order over
+ * src) and src_ok [1] int32 = 1.  Otherwise src_ok = 0 and src_order holds no
+ * meaning (build the source CSR with ictc_csr_build).  The same workspace.   */
+int ictc_edge_pairs_src_csr(const int64_t* src, const int64_t* dst, const float* shifts, int64_t nodes, int64_t edges,
+                            const int32_t* dst_ptr, const int32_t* dst_order, int32_t* gate_rows, int32_t* reps,
+                            int32_t* count, int32_t* src_order, int32_t* src_ok, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* Mixed second derivative of ictc_msg_bwd along tangents of its outputs
  * (tfeatures [nodes, C*(LI+1)^2], tharmonics [E, NY], tgates [E, P*C]; NULL =
  * zero tangent); replaces generated_second (graph mode,
@@ -439,6 +452,17 @@ int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, dou
 int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* src, const int64_t* dst,
                            int64_t nodes, int64_t edges, float cutoff, float* r, float* n, float* mask,
                            void* stream);
+/* Cartesian image shifts of the edges, replacing `edge_shifts @ cell[batch[src]]`
+ * (backbone.py:940-944, the shift term of vec): out [E,3] = shifts [E,3] (lattice
+ * coordinates) times the 3x3 cell (rows = lattice vectors) of the edge's graph,
+ * cell [cells,3,3]; with cells == 1 every edge uses cell 0 (batch/src may be NULL),
+ * else graph batch[src[e]] (batch [nodes], src [E]).  Each component is
+ * (s0 c0j + s1 c1j) + s2 c2j, every operation rounded on its own, so an edge and
+ * its reverse (shift -S) get exactly negated shifts (the premise of
+ * ictc_edge_pairs' shared rows).  An edge whose source or graph id is out of
+ * range gets NaN.                                                             */
+int ictc_shift_vectors(const float* shifts, int64_t edges, const float* cell, int64_t cells, const int64_t* batch,
+                       const int64_t* src, int64_t nodes, float* out, void* stream);
 int ictc_edge_geometry_bwd(const float* r, const float* n, const float* dr, const float* dn, int64_t nodes,
                            int64_t edges, const int32_t* dst_ptr, const int32_t* dst_order, const int32_t* src_ptr,
                            const int32_t* src_order, float* dshift, float* dpos, void* stream);

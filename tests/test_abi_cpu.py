@@ -157,6 +157,9 @@ def test_fused_and_gemm_entry_points_host_checks():
         _native.call("ictc_edge_pairs", None, None, None, 4, 10, None, None, None, None, None, None, 0, None)
     with pytest.raises(ValueError, match="null operand"):
         _native.call("ictc_edge_pairs", None, None, None, 4, 10, None, None, None, None, 1, None, 0, None)
+    with pytest.raises(ValueError, match="null source order"):
+        _native.call("ictc_edge_pairs_src_csr", None, None, None, 4, 10, None, None, None, None, 1, None, None, None,
+                     0, None)
     with pytest.raises(ValueError, match="lda >= k"):
         _native.call("ictc_gemm_nt", None, 4, 8, 4, None, 4, 8, None, 4, 0, None)
     with pytest.raises(ValueError, match="pitch"):

@@ -99,3 +99,28 @@ def test_edge_vectors_second_order(device, N, E, seed):
             assert rel_err(o, r) < 1e-5
     for a, b in zip(outs[0], outs[1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("cells,E,seed", [(1, 5000, 7), (3, 4000, 8), (1, 0, 9)])
+def test_shift_vectors(device, cells, E, seed):
+    """ictc_shift_vectors against the same three products and two sums rounded one by one on the host
+    (bitwise), exact oddness in the shift (an edge and its reverse), graph selection through batch[src],
+    and NaN rows for an out-of-range source."""
+    from ictc_o3.ops.geometry import shift_vectors
+    g = torch.Generator().manual_seed(seed)
+    N = 50
+    sh = torch.randint(-2, 3, (E, 3), generator=g).float()
+    cell = (torch.randn(cells, 3, 3, generator=g) * 4.0).float()
+    batch = torch.randint(0, cells, (N,), generator=g)
+    src = torch.randint(0, N, (E,), generator=g)
+    c = cell[batch[src]] if cells > 1 else cell[0].expand(E, 3, 3)
+    want = (sh[:, 0:1] * c[:, 0, :] + sh[:, 1:2] * c[:, 1, :]) + sh[:, 2:3] * c[:, 2, :]
+    got = shift_vectors(sh.to(device), cell.to(device), batch.to(device), src.to(device)).cpu()
+    assert torch.equal(got, want)
+    neg = shift_vectors((-sh).to(device), cell.to(device), batch.to(device), src.to(device)).cpu()
+    assert torch.equal(neg, -got)
+    if cells > 1 and E:
+        bad = src.clone()
+        bad[3] = N + 5
+        out = shift_vectors(sh.to(device), cell.to(device), batch.to(device), bad.to(device)).cpu()
+        assert torch.isnan(out[3]).all() and torch.equal(out[torch.arange(E) != 3], got[torch.arange(E) != 3])

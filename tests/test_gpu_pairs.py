@@ -7,6 +7,9 @@
   there is none; owners are numbered in edge order.  Symmetric periodic
   lists halve the rows; edges without a reverse and out-of-range ids own
   rows; every edge that reads another edge's row reads its reverse's.
+* For a symmetric list the same lookup yields the source CSR (the reverses
+  of each node's incoming edges, ranked into edge order): bitwise the stable
+  sort over src; asymmetric lists, duplicates and bad ids fall back to the sort.
 * Shared rows change no result bit: energies, forces and per-atom energies of
   the first-order (forces only) model route are bitwise those with one row
   per edge, on the fused and the materialised-gate message, for one periodic
@@ -55,6 +58,19 @@ def _brute_pairs(src, dst, sh, N):
     return torch.tensor(rows), torch.tensor(reps)
 
 
+def _check_source_csr(topo, src, N, device, symmetric):
+    """The source CSR pair_edges derives from the reverse lookup (symmetric lists) equals the stable sort over
+    src bit for bit; other lists fall back to that sort."""
+    from ictc_o3.ops import tensor_product as tpo
+    topo._resolve()
+    assert (topo._by_src is not None) == symmetric
+    got = topo.by_src
+    want = tpo.Csr(src.to(device), N)
+    E = src.numel()
+    assert torch.equal(got.ptr.cpu(), want.ptr.cpu())
+    assert torch.equal(got.order[:E].cpu(), want.order[:E].cpu())
+
+
 def _pairs(src, dst, sh, N, device):
     from ictc_o3.ops import tensor_product as tpo
     topo = tpo.Topology(src.to(device), dst.to(device), N)
@@ -91,6 +107,7 @@ def test_pairing_matches_brute_force(device, case):
         sh = None
     topo = _pairs(src, dst, sh, N, device)
     rows, reps = _brute_pairs(src, dst, sh, N)
+    _check_source_csr(topo, src, N, device, symmetric=case in ("periodic", "self_images", "no_shifts"))
     if case in ("periodic", "self_images", "no_shifts"):
         assert reps.numel() * 2 == src.numel()
     if reps.numel() == src.numel():
