@@ -1,6 +1,7 @@
 // extern "C" entry points of libictc_mi355x.so (declared in include/ictc_mi355x.h).
 #include <hipcub/hipcub.hpp>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -164,6 +165,67 @@ size_t morton_temp_bytes(int64_t N) {
   (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
                                      (const int32_t*)nullptr, (int32_t*)nullptr, (int)N, 0, 30);
   return bytes;
+}
+
+// Receiver row order: partial sums of |pos[i+1] - pos[i]| (index order) and |pos[rows[i+1]] - pos[rows[i]]|
+// (the candidate order) per block, in a fixed order (deterministic), then every block of the second kernel
+// forms both means from the partials and writes rows or the identity.
+constexpr int kStepBlocks = 256;
+
+__global__ __launch_bounds__(256) void step_partial_kernel(const float* __restrict__ pos, int64_t N,
+                                                           const int32_t* __restrict__ rows,
+                                                           double* __restrict__ part) {
+  double a = 0.0, b = 0.0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i + 1 < N; i += (int64_t)gridDim.x * 256) {
+    const int64_t r0 = rows[i], r1 = rows[i + 1];
+    float da = 0.f, db = 0.f;
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+      const float u = pos[3 * (i + 1) + d] - pos[3 * i + d];
+      const float v = pos[3 * r1 + d] - pos[3 * r0 + d];
+      da += u * u;
+      db += v * v;
+    }
+    a += sqrtf(da);
+    b += sqrtf(db);
+  }
+  __shared__ double sa[256], sb[256];
+  sa[threadIdx.x] = a;
+  sb[threadIdx.x] = b;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) {
+      sa[threadIdx.x] += sa[threadIdx.x + w];
+      sb[threadIdx.x] += sb[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    part[2 * blockIdx.x] = sa[0];
+    part[2 * blockIdx.x + 1] = sb[0];
+  }
+}
+
+__global__ __launch_bounds__(256) void step_choose_kernel(const double* __restrict__ part, int parts,
+                                                          const int32_t* __restrict__ rows, int64_t N,
+                                                          int32_t* __restrict__ out) {
+  __shared__ int use_rows;
+  if (threadIdx.x < 64) {   // one wave: strided partial sums, then a butterfly (a fixed order)
+    double a = 0.0, b = 0.0;
+    for (int k = threadIdx.x; k < parts; k += 64) {
+      a += part[2 * k];
+      b += part[2 * k + 1];
+    }
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+      a += __shfl_xor(a, m, 64);
+      b += __shfl_xor(b, m, 64);
+    }
+    if (threadIdx.x == 0) use_rows = a > 2.0 * b;   // the mean steps share the divisor N - 1
+  }
+  __syncthreads();
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < N) out[i] = use_rows ? rows[i] : (int32_t)i;
 }
 
 // Zero fill as a kernel (not hipMemsetAsync) so the call stays valid under
@@ -354,6 +416,29 @@ int ictc_morton_order(const float* pos, int64_t N, float spacing, int32_t* order
   if (int rc = check_hip(hipGetLastError(), "morton keys")) return rc;
   return check_hip(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys, sorted_keys, ids, order, (int)N, 0, 30, st),
                    "morton sort");
+}
+
+int64_t ictc_receiver_rows_workspace_bytes(int64_t N) {
+  if (N < 0 || N >= (int64_t(1) << 31)) return -1;
+  return (int64_t)(2 * kStepBlocks * sizeof(double));
+}
+
+int ictc_receiver_rows(const float* pos, int64_t N, const int32_t* rows, int32_t* out, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  if (N < 0) return fail(ICTC_ERR_ARGUMENT, "receiver rows: negative size");
+  if (N >= (int64_t(1) << 31)) return fail(ICTC_ERR_UNSUPPORTED, "receiver rows: more than 2^31 rows");
+  if (N == 0) return ICTC_OK;
+  if (!pos || !rows || !out || !workspace) return fail(ICTC_ERR_ARGUMENT, "receiver rows: null operand");
+  if (workspace_bytes < ictc_receiver_rows_workspace_bytes(N))
+    return fail(ICTC_ERR_ARGUMENT, "receiver rows: workspace smaller than ictc_receiver_rows_workspace_bytes");
+  hipStream_t st = (hipStream_t)stream;
+  double* part = (double*)workspace;
+  const int parts = (int)std::min<int64_t>(kStepBlocks, (N + 255) / 256);
+  hipLaunchKernelGGL(step_partial_kernel, dim3(parts), dim3(256), 0, st, pos, N, rows, part);
+  if (int rc = check_hip(hipGetLastError(), "receiver rows partial")) return rc;
+  hipLaunchKernelGGL(step_choose_kernel, dim3((unsigned)((N + 255) / 256)), dim3(256), 0, st, part, parts, rows, N,
+                     out);
+  return check_hip(hipGetLastError(), "receiver rows");
 }
 
 int ictc_msg_fwd(int li, int le, int lo, int C, const float* x, const float* sh, const float* g, const float* w,

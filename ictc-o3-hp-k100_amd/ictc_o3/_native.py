@@ -35,6 +35,8 @@ _SIGNATURES = {
     "ictc_csr_build": (_i, [_p, _i64, _i64, _p, _p, _p, _i64, _p]),
     "ictc_morton_workspace_bytes": (_i64, [_i64]),
     "ictc_morton_order": (_i, [_p, _i64, ctypes.c_float, _p, _p, _i64, _p]),
+    "ictc_receiver_rows_workspace_bytes": (_i64, [_i64]),
+    "ictc_receiver_rows": (_i, [_p, _i64, _p, _p, _p, _i64, _p]),
     "ictc_msg_fwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_msg_bwd": (_i, [_i, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _p, _p, _p, _p,
                           _p, _p, _p, _p, _p, _p, _i64, _p]),

@@ -270,12 +270,16 @@ def _receiver_rows(positions: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
     shuffled numbering lands near (box / neighbour spacing) x.  Decided on the
     device (no host sync): both candidates are row lists the kernels read the same way.
     """
-    pos = positions.detach().float()
-    step_index = (pos[1:] - pos[:-1]).norm(dim=1).mean()
-    spatial = pos[rows.long()]
-    step_rows = (spatial[1:] - spatial[:-1]).norm(dim=1).mean()
-    ident = torch.arange(rows.numel(), dtype=rows.dtype, device=rows.device)
-    return torch.where(step_index > 2.0 * step_rows, rows, ident)
+    pos = _c(positions.detach().float())
+    N = pos.shape[0]
+    out = torch.empty(max(N, 1), dtype=torch.int32, device=pos.device)
+    ws_bytes = int(nat.lib().ictc_receiver_rows_workspace_bytes(N))
+    if ws_bytes < 0:
+        raise ValueError("too many rows for an int32 row order")
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=pos.device)
+    nat.call("ictc_receiver_rows", nat.ptr(pos), N, nat.ptr(_c(rows)), nat.ptr(out), nat.ptr(ws), ws_bytes,
+             nat.stream_of(pos))
+    return out[:N]
 
 
 def mark_receiver_sorted(dst: torch.Tensor, nodes: int) -> torch.Tensor:

@@ -109,6 +109,19 @@ int64_t ictc_morton_workspace_bytes(int64_t rows);
 int ictc_morton_order(const float* pos, int64_t rows, float spacing, int32_t* order, void* workspace,
                       int64_t workspace_bytes, void* stream);
 
+/* Row order of the receiver-owned passes (no counterpart in the reference):
+ * out [N] int32 = rows (a spatial order, e.g. ictc_morton_order's) when the
+ * mean distance between consecutively numbered atoms, pos [N,3] FP32, exceeds
+ * twice the mean distance between consecutive entries of rows, else the
+ * identity 0 .. N-1.  A lattice or domain-ordered numbering keeps index order
+ * (it streams receiver-sorted gate rows sequentially); a scattered one gets
+ * the spatial order.  Decided on the device (no host copy), deterministically;
+ * either order gives the same message results bit for bit.  workspace:
+ * ictc_receiver_rows_workspace_bytes(N) bytes.                               */
+int64_t ictc_receiver_rows_workspace_bytes(int64_t rows);
+int ictc_receiver_rows(const float* pos, int64_t rows, const int32_t* order, int32_t* out, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
 /* ---- Graph message (gather -> TP -> gate -> mask -> receiver sum) --------
  * Replaces PackedGraphMessage.forward's native launches
  * (operators.py:382-409 -> ops/rematerialized_message.py:166-205 ->

@@ -91,3 +91,27 @@ def test_host_cell_copy_follows_views_and_versions(device):
     assert b is not a and float(b[0, 0]) == 5.0
     other = torch.eye(3, device=device) * 6.0
     assert float(nb._host_cell(other)[1, 1]) == 6.0
+
+
+@pytest.mark.parametrize("n", [12, 60])
+def test_receiver_row_order_choice(device, n):
+    """A spatial atom numbering keeps index order for the receiver passes; a shuffled one takes the Morton rows
+    (chosen on the device by ictc_receiver_rows, without a host read: both are row lists)."""
+    from ictc_o3.ops.tensor_product import _receiver_rows
+    g = torch.Generator().manual_seed(3)
+    grid = torch.stack(torch.meshgrid(*[torch.arange(n)] * 3, indexing="ij"), -1).reshape(-1, 3).float() * 3.0
+    pos = grid + (torch.rand(grid.shape, generator=g) - 0.5) * 0.6
+    cell = torch.floor((pos - pos.min(0).values) / 2.0).long()
+    key = torch.zeros(pos.shape[0], dtype=torch.long)
+    for b in range(10):
+        for d in range(3):
+            key |= ((cell[:, d] >> b) & 1) << (3 * b + d)
+    rows = torch.sort(key, stable=True).indices.int()
+    got = _receiver_rows(pos.to(device), rows.to(device)).cpu()
+    assert got.dtype == rows.dtype and torch.equal(got, torch.arange(rows.numel(), dtype=rows.dtype))
+    perm = torch.randperm(pos.shape[0], generator=g)
+    shuffled = pos[perm]
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    srows = inv[rows.long()].int()
+    assert torch.equal(_receiver_rows(shuffled.to(device), srows.to(device)).cpu(), srows)
