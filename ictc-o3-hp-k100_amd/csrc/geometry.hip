@@ -12,6 +12,7 @@
 #include <stdio.h>
 
 #include "../../include/ictc_mi355x.h"
+#include "generated/ictc_tables.h"
 
 namespace ictc {
 int set_error(int code, const char* msg);
@@ -45,18 +46,8 @@ __global__ __launch_bounds__(kBlock) void geometry_fwd_kernel(const float* __res
 // d vec of one edge from dr and dn:
 //   dr * vec / r + dn / max(r, eps) - [r > eps] (dn . vec) vec / (max(r, eps)^2 r)
 // which for r > eps is dr n + (dn - (dn . n) n) / r.
-__device__ __forceinline__ void edge_adjoint(const float* __restrict__ r, const float* __restrict__ n,
-                                             const float* __restrict__ dr, const float* __restrict__ dn, int64_t e,
-                                             float* out) {
-  const float len = r[e];
-  const float nx = n[3 * e], ny = n[3 * e + 1], nz = n[3 * e + 2];
-  const float g = dr ? dr[e] : 0.f;
-  float a[3] = {0.f, 0.f, 0.f};
-  if (dn) {
-    a[0] = dn[3 * e];
-    a[1] = dn[3 * e + 1];
-    a[2] = dn[3 * e + 2];
-  }
+__device__ __forceinline__ void edge_adjoint_values(float len, float nx, float ny, float nz, float g,
+                                                    const float* a, float* out) {
   if (len > kClamp) {
     const float inv = 1.f / len, dot = a[0] * nx + a[1] * ny + a[2] * nz;
     out[0] = g * nx + (a[0] - dot * nx) * inv;
@@ -69,6 +60,18 @@ __device__ __forceinline__ void edge_adjoint(const float* __restrict__ r, const 
     out[1] = gr * ny + a[1] * inv;
     out[2] = gr * nz + a[2] * inv;
   }
+}
+
+__device__ __forceinline__ void edge_adjoint(const float* __restrict__ r, const float* __restrict__ n,
+                                             const float* __restrict__ dr, const float* __restrict__ dn, int64_t e,
+                                             float* out) {
+  float a[3] = {0.f, 0.f, 0.f};
+  if (dn) {
+    a[0] = dn[3 * e];
+    a[1] = dn[3 * e + 1];
+    a[2] = dn[3 * e + 2];
+  }
+  edge_adjoint_values(r[e], n[3 * e], n[3 * e + 1], n[3 * e + 2], dr ? dr[e] : 0.f, a, out);
 }
 
 template <bool VEC>
@@ -130,6 +133,61 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
   if (lane < 3) dpos[3 * i + lane] = lane == 0 ? acc[0] : (lane == 1 ? acc[1] : acc[2]);
 }
 
+// Edge geometry and direction harmonics in one pass (first-order E+F route): r, n (kept for the adjoint),
+// mask and Y = Sh<L>(n), with n and Y computed exactly as geometry_fwd_kernel and sh_fwd_kernel do.
+template <int L>
+__global__ __launch_bounds__(kBlock) void geometry_sh_fwd_kernel(const float* __restrict__ pos,
+                                                                 const float* __restrict__ shift,
+                                                                 const int64_t* __restrict__ src,
+                                                                 const int64_t* __restrict__ dst, int64_t E,
+                                                                 float rc, float* __restrict__ r,
+                                                                 float* __restrict__ n, float* __restrict__ mask,
+                                                                 float* __restrict__ Y) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  const int64_t s = src[e], d = dst[e];
+  float v[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) v[c] = pos[3 * d + c] - pos[3 * s + c] + (shift ? shift[3 * e + c] : 0.f);
+  const float len = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+  const float den = fmaxf(len, kClamp);
+  r[e] = len;
+  float u[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    u[c] = v[c] / den;
+    n[3 * e + c] = u[c];
+  }
+  if (mask) mask[e] = len <= rc ? 1.f : 0.f;
+  float y[ictc::Sh<L>::N];
+  ictc::Sh<L>::fwd(u[0], u[1], u[2], y);
+#pragma unroll
+  for (int k = 0; k < ictc::Sh<L>::N; ++k) Y[e * ictc::Sh<L>::N + k] = y[k];
+}
+
+// Its adjoint per edge: dn = Sh<L> adjoint of dY (as sh_bwd_kernel), then d vec from dr and dn (as
+// edge_adjoint), written per edge for the CSR gather geometry_bwd_kernel<true>.
+template <int L>
+__global__ __launch_bounds__(kBlock) void geometry_sh_bwd_kernel(const float* __restrict__ r,
+                                                                 const float* __restrict__ n,
+                                                                 const float* __restrict__ dr,
+                                                                 const float* __restrict__ dY, int64_t E,
+                                                                 float* __restrict__ dvec) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  float dn[3] = {0.f, 0.f, 0.f};
+  if (dY) {
+    float g[ictc::Sh<L>::N];
+#pragma unroll
+    for (int k = 0; k < ictc::Sh<L>::N; ++k) g[k] = dY[e * ictc::Sh<L>::N + k];
+    ictc::Sh<L>::bwd(n[3 * e], n[3 * e + 1], n[3 * e + 2], g, dn[0], dn[1], dn[2]);
+  }
+  float t[3];
+  edge_adjoint_values(r[e], n[3 * e], n[3 * e + 1], n[3 * e + 2], dr ? dr[e] : 0.f, dn, t);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) dvec[3 * e + c] = t[c];
+}
+
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
 
 int launch_status(const char* what) {
@@ -179,6 +237,41 @@ int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* 
   hipLaunchKernelGGL(geometry_fwd_kernel, dim3((unsigned)((edges + kBlock - 1) / kBlock)), dim3(kBlock), 0,
                      (hipStream_t)stream, pos, shift, src, dst, edges, cutoff, r, n, mask);
   return launch_status("ictc_edge_geometry_fwd launch");
+}
+
+int ictc_edge_harmonics_fwd(const float* pos, const float* shift, const int64_t* src, const int64_t* dst,
+                            int64_t nodes, int64_t edges, float cutoff, int lmax, float* r, float* n, float* mask,
+                            float* Y, void* stream) {
+  if (nodes < 0 || edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge harmonics: negative size");
+  if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "edge harmonics: lmax outside 0..3");
+  if (edges == 0) return ICTC_OK;
+  if (!pos || !src || !dst || !r || !n || !Y) return fail(ICTC_ERR_ARGUMENT, "edge harmonics: null operand");
+  const dim3 grid((unsigned)((edges + kBlock - 1) / kBlock));
+  hipStream_t st = (hipStream_t)stream;
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL(geometry_sh_fwd_kernel<0>, grid, dim3(kBlock), 0, st, pos, shift, src, dst, edges, cutoff, r, n, mask, Y); break;
+    case 1: hipLaunchKernelGGL(geometry_sh_fwd_kernel<1>, grid, dim3(kBlock), 0, st, pos, shift, src, dst, edges, cutoff, r, n, mask, Y); break;
+    case 2: hipLaunchKernelGGL(geometry_sh_fwd_kernel<2>, grid, dim3(kBlock), 0, st, pos, shift, src, dst, edges, cutoff, r, n, mask, Y); break;
+    default: hipLaunchKernelGGL(geometry_sh_fwd_kernel<3>, grid, dim3(kBlock), 0, st, pos, shift, src, dst, edges, cutoff, r, n, mask, Y); break;
+  }
+  return launch_status("ictc_edge_harmonics_fwd launch");
+}
+
+int ictc_edge_harmonics_bwd(const float* r, const float* n, const float* dr, const float* dY, int64_t edges, int lmax,
+                            float* dvec, void* stream) {
+  if (edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge harmonics adjoint: negative size");
+  if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "edge harmonics adjoint: lmax outside 0..3");
+  if (edges == 0) return ICTC_OK;
+  if (!r || !n || !dvec) return fail(ICTC_ERR_ARGUMENT, "edge harmonics adjoint: null operand");
+  const dim3 grid((unsigned)((edges + kBlock - 1) / kBlock));
+  hipStream_t st = (hipStream_t)stream;
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL(geometry_sh_bwd_kernel<0>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
+    case 1: hipLaunchKernelGGL(geometry_sh_bwd_kernel<1>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
+    case 2: hipLaunchKernelGGL(geometry_sh_bwd_kernel<2>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
+    default: hipLaunchKernelGGL(geometry_sh_bwd_kernel<3>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
+  }
+  return launch_status("ictc_edge_harmonics_bwd launch");
 }
 
 int ictc_shift_vectors(const float* shifts, int64_t edges, const float* cell, int64_t cells, const int64_t* batch,

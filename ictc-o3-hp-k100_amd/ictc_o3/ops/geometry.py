@@ -65,6 +65,52 @@ def edge_geometry(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: f
     return _EdgeGeometry.apply(pos, shift, topo, float(cutoff))
 
 
+class _EdgeHarmonics(torch.autograd.Function):
+    """(r, Y, mask) of the edges in one kernel; the adjoint forms d vec per edge (harmonics adjoint folded with
+    dr) and gathers it into dpos, bitwise the result of _EdgeGeometry followed by the harmonics op."""
+
+    @staticmethod
+    def forward(ctx, pos, shift, topo, cutoff, lmax):
+        pos = _c(pos.detach())
+        shift = None if shift is None else _c(shift.detach())
+        E, N = topo.src.numel(), pos.shape[0]
+        r = pos.new_empty(E)
+        n = pos.new_empty(E, 3)
+        mask = pos.new_empty(E)
+        Y = pos.new_empty(E, (lmax + 1) ** 2)
+        nat.call("ictc_edge_harmonics_fwd", nat.ptr(pos), nat.ptr(shift), nat.ptr(topo.src), nat.ptr(topo.dst), N,
+                 E, float(cutoff), lmax, nat.ptr(r), nat.ptr(n), nat.ptr(mask), nat.ptr(Y), nat.stream_of(pos))
+        ctx.topo, ctx.nodes, ctx.lmax = topo, N, lmax
+        ctx.mark_non_differentiable(mask)
+        ctx.save_for_backward(r, n)
+        return r, Y, mask
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dr, dY, _dmask):
+        r, n = ctx.saved_tensors
+        E = r.numel()
+        dvec = r.new_empty(E, 3)
+        nat.call("ictc_edge_harmonics_bwd", nat.ptr(r), nat.ptr(n), nat.ptr(None if dr is None else _c(dr)),
+                 nat.ptr(None if dY is None else _c(dY)), E, ctx.lmax, nat.ptr(dvec), nat.stream_of(r))
+        dpos = _vector_adjoint(dvec, ctx.topo, ctx.nodes) if ctx.needs_input_grad[0] else None
+        return dpos, (dvec if ctx.needs_input_grad[1] else None), None, None, None
+
+
+def edge_harmonics(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: float, lmax: int):
+    """(r [E], Y [E, (lmax+1)^2], mask [E]): edge_geometry followed by the packed direction harmonics of n, in one
+    kernel, float32, first derivatives only (positions and shifts)."""
+    if pos.dtype != torch.float32 or (shift is not None and shift.dtype != torch.float32):
+        raise TypeError("edge_harmonics runs in float32")
+    if pos.dim() != 2 or pos.shape[1] != 3:
+        raise ValueError("pos must be [N, 3]")
+    if shift is not None and tuple(shift.shape) != (topo.src.numel(), 3):
+        raise ValueError("shift must be [E, 3]")
+    if not 0 <= int(lmax) <= 3:
+        raise ValueError("edge_harmonics: lmax outside 0..3")
+    return _EdgeHarmonics.apply(pos, shift, topo, float(cutoff), int(lmax))
+
+
 def _vector_adjoint(dvec: torch.Tensor, topo, N: int) -> torch.Tensor:
     dvec = _c(dvec.detach())
     dpos = dvec.new_empty(N, 3)

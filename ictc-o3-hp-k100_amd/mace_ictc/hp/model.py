@@ -370,10 +370,11 @@ class PureCartesianICTDFix(nn.Module):
             r = vec.norm(dim=1)
             n = vec / r.clamp(min=1e-8).unsqueeze(-1)
             mask = (r <= self.max_radius).to(pos.dtype)
+            Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
         else:
-            from ictc_o3.ops.geometry import edge_geometry
-            r, n, mask = edge_geometry(pos, shift_vec, topology, self.max_radius)
-        Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
+            # first order: edge geometry and harmonics in one kernel, one per-edge adjoint
+            from ictc_o3.ops.geometry import edge_harmonics
+            r, Y, mask = edge_harmonics(pos, shift_vec, topology, self.max_radius, self.ictd_fix_edge_lmax)
         from ictc_o3.ops.radial_mlp import fused_supported
         fused = (not second_order and self.number_of_basis == 8
                  and all(fused_supported(inter.fc) for inter in self.interactions))

@@ -124,3 +124,41 @@ def test_shift_vectors(device, cells, E, seed):
         bad[3] = N + 5
         out = shift_vectors(sh.to(device), cell.to(device), batch.to(device), bad.to(device)).cpu()
         assert torch.isnan(out[3]).all() and torch.equal(out[torch.arange(E) != 3], got[torch.arange(E) != 3])
+
+
+@pytest.mark.parametrize("lmax", [0, 1, 2, 3])
+@pytest.mark.parametrize("N,E,seed,sort,with_shift,cot", [(200, 4000, 21, True, True, "both"),
+                                                         (57, 900, 22, False, True, "dY"),
+                                                         (300, 5000, 23, True, False, "dr"),
+                                                         (7, 0, 24, True, True, "both")])
+def test_edge_harmonics_matches_geometry_then_harmonics(device, lmax, N, E, seed, sort, with_shift, cot):
+    """The one-pass geometry + harmonics op gives bitwise the values and the position / shift adjoints of
+    edge_geometry followed by harmonics_packed (whose parity the tests above and the harmonics tests hold)."""
+    from ictc_o3.ops.geometry import edge_geometry, edge_harmonics
+    from ictc_o3.ops.harmonics import harmonics_packed
+    from ictc_o3.ops.tensor_product import Topology
+    pos, src, dst, shift = _case(N, E, seed, sort)
+    E = src.numel()
+    topo = Topology(src.to(device), dst.to(device), N)
+    g = torch.Generator().manual_seed(seed + 7)
+    gr = torch.randn(E, generator=g).to(device)
+    gY = torch.randn(E, (lmax + 1) ** 2, generator=g).to(device)
+    outs = []
+    for fused in (True, False):
+        pd = pos.float().to(device).requires_grad_(True)
+        sd = shift.float().to(device).requires_grad_(True) if with_shift else None
+        if fused:
+            r, Y, m = edge_harmonics(pd, sd, topo, 4.5, lmax)
+        else:
+            r, n, m = edge_geometry(pd, sd, topo, 4.5)
+            Y = harmonics_packed(n, lmax)
+        if E:
+            ts, gs = ([r] if cot != "dY" else []) + ([Y] if cot != "dr" else []), \
+                ([gr] if cot != "dY" else []) + ([gY] if cot != "dr" else [])
+            torch.autograd.backward(ts, gs)
+        outs.append((r.detach(), Y.detach(), m, None if pd.grad is None else pd.grad.clone(),
+                     None if sd is None or sd.grad is None else sd.grad.clone()))
+    for a, b in zip(*outs):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
