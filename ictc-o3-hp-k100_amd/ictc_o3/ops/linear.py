@@ -129,6 +129,37 @@ import ctypes
 from ictc_o3 import _native as nat
 
 
+_operand_cache = {}   # id(base) -> (weakref to base, {view key: contiguous operand})
+
+
+def _weight_operand(w, transpose=False):
+    """w (or w.t()) detached and contiguous, as the packed kernel reads it.  A non-contiguous view (the
+    product linear's transposed blocks) or a transpose (the input adjoint) costs a copy launch; the copy is
+    kept per live base tensor, view geometry and version counter (an optimizer step bumps the version), so
+    a model whose weights do not change between steps makes it once."""
+    import weakref
+    v = w.detach().t() if transpose else w.detach()
+    if v.is_contiguous():
+        return v
+    base = w._base if w._base is not None else w
+    key = (v.storage_offset(), tuple(v.shape), tuple(v.stride()), w._version, v.dtype, v.device)
+    entry = _operand_cache.get(id(base))
+    if entry is None or entry[0]() is not base:
+        if len(_operand_cache) > 256:
+            for k in [k for k, (ref, _) in _operand_cache.items() if ref() is None]:
+                del _operand_cache[k]
+        entry = (weakref.ref(base), {})
+        _operand_cache[id(base)] = entry
+    views = entry[1]
+    out = views.get(key)
+    if out is None:
+        if len(views) > 64:
+            views.clear()
+        out = v.contiguous()
+        views[key] = out
+    return out
+
+
 def _packed_call(x, Ci, Co, lmax, pin, in_off, pout, out_off, weights, scales, out_cols):
     N = x.shape[0]
     out = x.new_empty(N, out_cols)
@@ -151,7 +182,7 @@ class _PackedLinear(torch.autograd.Function):
         ctx.layout = layout
         ctx.inputs = (x, *weights)
         x = x if x.is_contiguous() else x.contiguous()
-        ws = [w.detach().contiguous() for w in weights]
+        ws = [_weight_operand(w) for w in weights]
         ctx.save_for_backward(x, *ws)
         return _packed_call(x, Ci, Co, lmax, pin, in_off, [1] * (lmax + 1), out_off, ws, scales,
                             (lmax + 1) ** 2 * Co)
@@ -174,7 +205,7 @@ def _packed_adjoint(x, ws, layout, dout, needs):
     dout = dout if dout.is_contiguous() else dout.contiguous()
     dx = None
     if needs[0]:
-        wt = [w.t().contiguous() for w in ws]
+        wt = [_weight_operand(w, transpose=True) for w in ws]
         dx = _packed_call(dout, Co, Ci, lmax, [1] * (lmax + 1), out_off, pin, in_off, wt, scales, in_cols)
     dws = []
     N = x.shape[0]
@@ -207,7 +238,7 @@ class _LayerEntry(torch.autograd.Function):
         ctx.layout, ctx.C = layout, C
         ctx.inputs = (h, *weights)
         x = h if h.is_contiguous() else h.contiguous()
-        ws = [w.detach().contiguous() for w in weights]
+        ws = [_weight_operand(w) for w in weights]
         ctx.save_for_backward(x, *ws)
         y = _packed_call(x, Ci, Co, lmax, pin, in_off, [1] * (lmax + 1), out_off, ws, scales, (lmax + 1) ** 2 * Co)
         return y, x[:, :C].contiguous()
@@ -282,7 +313,7 @@ class _PackedLinearAny(torch.autograd.Function):
         ctx.layout = layout
         x = x if x.is_contiguous() else x.contiguous()
         ctx.save_for_backward(x, *weights)
-        ws = [w.detach().contiguous() for w in weights]
+        ws = [_weight_operand(w) for w in weights]
         return _packed_call(x, Ci, Co, lmax, pin, in_off, pout, out_off, ws, scales, out_cols)
 
     @staticmethod
