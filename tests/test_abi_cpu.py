@@ -156,3 +156,22 @@ def test_fused_and_gemm_entry_points_host_checks():
     with pytest.raises(ValueError, match="static scratch"):
         _native.call("ictc_radial_gates_tangent_fwd_noalloc", None, 10, 8, 64, 4.5, 5, None, None, None, None,
                      4096 + 16, 1.0, None, None, None)
+
+
+def test_weight_operand_cache_follows_versions():
+    """The packed linears' weight operands: contiguous weights pass through; a view or transpose is copied
+    once per live base, view and version, and an in-place update (new version) gives a fresh copy."""
+    from ictc_o3.ops.linear import _weight_operand
+    w = torch.randn(3 * 16 * 16)
+    blk = w[256:512].view(16, 16).t()
+    a = _weight_operand(blk)
+    assert a.is_contiguous() and torch.equal(a, blk) and _weight_operand(blk) is a
+    assert _weight_operand(w[256:512].view(16, 16).t()) is a          # the same view taken anew
+    t = _weight_operand(a, transpose=True)
+    assert torch.equal(t, a.t()) and _weight_operand(a, transpose=True) is t
+    with torch.no_grad():
+        w.mul_(2.0)
+    b = _weight_operand(blk)
+    assert b is not a and torch.equal(b, blk)
+    c = torch.randn(16, 16)
+    assert _weight_operand(c) is not None and _weight_operand(c).data_ptr() == c.data_ptr()
