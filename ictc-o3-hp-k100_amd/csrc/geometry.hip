@@ -135,6 +135,27 @@ __global__ __launch_bounds__(kBlock) void geometry_bwd_kernel(const float* __res
 
 // Edge geometry and direction harmonics in one pass (first-order E+F route): r, n (kept for the adjoint),
 // mask and Y = Sh<L>(n), with n and Y computed exactly as geometry_fwd_kernel and sh_fwd_kernel do.
+// Rows of NV floats per edge, for the kBlock edges of a block, move between global memory and LDS as one
+// contiguous span (16-byte vectors over the block's rows, then the tail), so each thread's row of the
+// harmonics (9 floats at lmax 2) costs no strided 4-byte accesses.
+template <int NV>
+__device__ __forceinline__ void rows_to_lds(const float* __restrict__ g, int64_t base, int cnt, float* sm) {
+  const float* src = g + base * NV;   // base is a multiple of kBlock: 16-byte aligned
+  const int total = cnt * NV, n4 = total / 4;
+  for (int i = threadIdx.x; i < n4; i += kBlock) reinterpret_cast<float4*>(sm)[i] = reinterpret_cast<const float4*>(src)[i];
+  for (int i = 4 * n4 + threadIdx.x; i < total; i += kBlock) sm[i] = src[i];
+}
+
+template <int NV>
+__device__ __forceinline__ void rows_from_lds(float* __restrict__ g, int64_t base, int cnt, const float* sm) {
+  float* dst = g + base * NV;
+  const int total = cnt * NV, n4 = total / 4;
+  for (int i = threadIdx.x; i < n4; i += kBlock) reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(sm)[i];
+  for (int i = 4 * n4 + threadIdx.x; i < total; i += kBlock) dst[i] = sm[i];
+}
+
+// Edge geometry and direction harmonics in one pass (first-order E+F route): r, n (kept for the adjoint),
+// mask and Y = Sh<L>(n), with n and Y computed exactly as geometry_fwd_kernel and sh_fwd_kernel do.
 template <int L>
 __global__ __launch_bounds__(kBlock) void geometry_sh_fwd_kernel(const float* __restrict__ pos,
                                                                  const float* __restrict__ shift,
@@ -143,47 +164,67 @@ __global__ __launch_bounds__(kBlock) void geometry_sh_fwd_kernel(const float* __
                                                                  float rc, float* __restrict__ r,
                                                                  float* __restrict__ n, float* __restrict__ mask,
                                                                  float* __restrict__ Y) {
-  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (e >= E) return;
-  const int64_t s = src[e], d = dst[e];
-  float v[3];
+  constexpr int NY = ictc::Sh<L>::N;
+  __shared__ __align__(16) float sy[kBlock * NY];
+  const int64_t base = (int64_t)blockIdx.x * kBlock, e = base + threadIdx.x;
+  const int cnt = (int)(E - base < kBlock ? E - base : kBlock);
+  if (e < E) {
+    const int64_t s = src[e], d = dst[e];
+    float v[3];
 #pragma unroll
-  for (int c = 0; c < 3; ++c) v[c] = pos[3 * d + c] - pos[3 * s + c] + (shift ? shift[3 * e + c] : 0.f);
-  const float len = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
-  const float den = fmaxf(len, kClamp);
-  r[e] = len;
-  float u[3];
+    for (int c = 0; c < 3; ++c) v[c] = pos[3 * d + c] - pos[3 * s + c] + (shift ? shift[3 * e + c] : 0.f);
+    const float len = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+    const float den = fmaxf(len, kClamp);
+    r[e] = len;
+    float u[3];
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
-    u[c] = v[c] / den;
-    n[3 * e + c] = u[c];
+    for (int c = 0; c < 3; ++c) {
+      u[c] = v[c] / den;
+      n[3 * e + c] = u[c];
+    }
+    if (mask) mask[e] = len <= rc ? 1.f : 0.f;
+    float y[NY];
+    ictc::Sh<L>::fwd(u[0], u[1], u[2], y);
+#pragma unroll
+    for (int k = 0; k < NY; ++k) sy[threadIdx.x * NY + k] = y[k];
   }
-  if (mask) mask[e] = len <= rc ? 1.f : 0.f;
-  float y[ictc::Sh<L>::N];
-  ictc::Sh<L>::fwd(u[0], u[1], u[2], y);
-#pragma unroll
-  for (int k = 0; k < ictc::Sh<L>::N; ++k) Y[e * ictc::Sh<L>::N + k] = y[k];
+  __syncthreads();
+  rows_from_lds<NY>(Y, base, cnt, sy);
 }
 
 // Its adjoint per edge: dn = Sh<L> adjoint of dY (as sh_bwd_kernel), then d vec from dr and dn (as
-// edge_adjoint), written per edge for the CSR gather geometry_bwd_kernel<true>.
+// edge_adjoint), written per edge for the CSR gather geometry_bwd_kernel<true>.  dY2 / dr2 (optional): a
+// second consumer's cotangents, added to dY / dr first (the sum autograd would form, in the same rounding).
 template <int L>
 __global__ __launch_bounds__(kBlock) void geometry_sh_bwd_kernel(const float* __restrict__ r,
                                                                  const float* __restrict__ n,
                                                                  const float* __restrict__ dr,
-                                                                 const float* __restrict__ dY, int64_t E,
+                                                                 const float* __restrict__ dY,
+                                                                 const float* __restrict__ dr2,
+                                                                 const float* __restrict__ dY2, int64_t E,
                                                                  float* __restrict__ dvec) {
-  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  constexpr int NY = ictc::Sh<L>::N;
+  __shared__ __align__(16) float sa[kBlock * NY];
+  __shared__ __align__(16) float sb[kBlock * NY];
+  const int64_t base = (int64_t)blockIdx.x * kBlock, e = base + threadIdx.x;
+  const int cnt = (int)(E - base < kBlock ? E - base : kBlock);
+  if (dY) rows_to_lds<NY>(dY, base, cnt, sa);
+  if (dY2) rows_to_lds<NY>(dY2, base, cnt, sb);
+  __syncthreads();
   if (e >= E) return;
   float dn[3] = {0.f, 0.f, 0.f};
-  if (dY) {
-    float g[ictc::Sh<L>::N];
+  if (dY || dY2) {
+    float g[NY];
 #pragma unroll
-    for (int k = 0; k < ictc::Sh<L>::N; ++k) g[k] = dY[e * ictc::Sh<L>::N + k];
+    for (int k = 0; k < NY; ++k) {
+      const int i = threadIdx.x * NY + k;
+      g[k] = dY ? (dY2 ? sa[i] + sb[i] : sa[i]) : sb[i];
+    }
     ictc::Sh<L>::bwd(n[3 * e], n[3 * e + 1], n[3 * e + 2], g, dn[0], dn[1], dn[2]);
   }
+  const float gr = dr ? (dr2 ? dr[e] + dr2[e] : dr[e]) : (dr2 ? dr2[e] : 0.f);
   float t[3];
-  edge_adjoint_values(r[e], n[3 * e], n[3 * e + 1], n[3 * e + 2], dr ? dr[e] : 0.f, dn, t);
+  edge_adjoint_values(r[e], n[3 * e], n[3 * e + 1], n[3 * e + 2], gr, dn, t);
 #pragma unroll
   for (int c = 0; c < 3; ++c) dvec[3 * e + c] = t[c];
 }
@@ -246,6 +287,7 @@ int ictc_edge_harmonics_fwd(const float* pos, const float* shift, const int64_t*
   if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "edge harmonics: lmax outside 0..3");
   if (edges == 0) return ICTC_OK;
   if (!pos || !src || !dst || !r || !n || !Y) return fail(ICTC_ERR_ARGUMENT, "edge harmonics: null operand");
+  if (reinterpret_cast<uintptr_t>(Y) % 16) return fail(ICTC_ERR_ARGUMENT, "edge harmonics: Y must be 16-byte aligned");
   const dim3 grid((unsigned)((edges + kBlock - 1) / kBlock));
   hipStream_t st = (hipStream_t)stream;
   switch (lmax) {
@@ -257,19 +299,21 @@ int ictc_edge_harmonics_fwd(const float* pos, const float* shift, const int64_t*
   return launch_status("ictc_edge_harmonics_fwd launch");
 }
 
-int ictc_edge_harmonics_bwd(const float* r, const float* n, const float* dr, const float* dY, int64_t edges, int lmax,
-                            float* dvec, void* stream) {
+int ictc_edge_harmonics_bwd(const float* r, const float* n, const float* dr, const float* dY, const float* dr2,
+                            const float* dY2, int64_t edges, int lmax, float* dvec, void* stream) {
   if (edges < 0) return fail(ICTC_ERR_ARGUMENT, "edge harmonics adjoint: negative size");
   if (lmax < 0 || lmax > 3) return fail(ICTC_ERR_UNSUPPORTED, "edge harmonics adjoint: lmax outside 0..3");
   if (edges == 0) return ICTC_OK;
   if (!r || !n || !dvec) return fail(ICTC_ERR_ARGUMENT, "edge harmonics adjoint: null operand");
+  if (reinterpret_cast<uintptr_t>(dY) % 16 || reinterpret_cast<uintptr_t>(dY2) % 16)
+    return fail(ICTC_ERR_ARGUMENT, "edge harmonics adjoint: dY and dY2 must be 16-byte aligned");
   const dim3 grid((unsigned)((edges + kBlock - 1) / kBlock));
   hipStream_t st = (hipStream_t)stream;
   switch (lmax) {
-    case 0: hipLaunchKernelGGL(geometry_sh_bwd_kernel<0>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
-    case 1: hipLaunchKernelGGL(geometry_sh_bwd_kernel<1>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
-    case 2: hipLaunchKernelGGL(geometry_sh_bwd_kernel<2>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
-    default: hipLaunchKernelGGL(geometry_sh_bwd_kernel<3>, grid, dim3(kBlock), 0, st, r, n, dr, dY, edges, dvec); break;
+    case 0: hipLaunchKernelGGL(geometry_sh_bwd_kernel<0>, grid, dim3(kBlock), 0, st, r, n, dr, dY, dr2, dY2, edges, dvec); break;
+    case 1: hipLaunchKernelGGL(geometry_sh_bwd_kernel<1>, grid, dim3(kBlock), 0, st, r, n, dr, dY, dr2, dY2, edges, dvec); break;
+    case 2: hipLaunchKernelGGL(geometry_sh_bwd_kernel<2>, grid, dim3(kBlock), 0, st, r, n, dr, dY, dr2, dY2, edges, dvec); break;
+    default: hipLaunchKernelGGL(geometry_sh_bwd_kernel<3>, grid, dim3(kBlock), 0, st, r, n, dr, dY, dr2, dY2, edges, dvec); break;
   }
   return launch_status("ictc_edge_harmonics_bwd launch");
 }

@@ -88,7 +88,7 @@ _SIGNATURES = {
     "ictc_edge_vector_bwd": (_i, [_p, _i64, _i64, _p, _p, _p, _p, _p, _p]),
     "ictc_shift_vectors": (_i, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p]),
     "ictc_edge_harmonics_fwd": (_i, [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _i, _p, _p, _p, _p, _p]),
-    "ictc_edge_harmonics_bwd": (_i, [_p, _p, _p, _p, _i64, _i, _p, _p]),
+    "ictc_edge_harmonics_bwd": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i, _p, _p]),
     "ictc_radial_mlp_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p]),
     "ictc_radial_mlp_tangent_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p,
                                          _p]),

@@ -67,10 +67,13 @@ def edge_geometry(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: f
 
 class _EdgeHarmonics(torch.autograd.Function):
     """(r, Y, mask) of the edges in one kernel; the adjoint forms d vec per edge (harmonics adjoint folded with
-    dr) and gathers it into dpos, bitwise the result of _EdgeGeometry followed by the harmonics op."""
+    dr) and gathers it into dpos: the values of _EdgeGeometry followed by the harmonics op (bitwise), and their
+    adjoint to FP32 rounding.  With
+    uses = 2 the forward also returns r and Y a second time (views) for a second consumer: their cotangents
+    reach the backward apart and the kernel adds them, where autograd would have launched the additions."""
 
     @staticmethod
-    def forward(ctx, pos, shift, topo, cutoff, lmax):
+    def forward(ctx, pos, shift, topo, cutoff, lmax, uses):
         pos = _c(pos.detach())
         shift = None if shift is None else _c(shift.detach())
         E, N = topo.src.numel(), pos.shape[0]
@@ -80,26 +83,36 @@ class _EdgeHarmonics(torch.autograd.Function):
         Y = pos.new_empty(E, (lmax + 1) ** 2)
         nat.call("ictc_edge_harmonics_fwd", nat.ptr(pos), nat.ptr(shift), nat.ptr(topo.src), nat.ptr(topo.dst), N,
                  E, float(cutoff), lmax, nat.ptr(r), nat.ptr(n), nat.ptr(mask), nat.ptr(Y), nat.stream_of(pos))
-        ctx.topo, ctx.nodes, ctx.lmax = topo, N, lmax
+        ctx.topo, ctx.nodes, ctx.lmax, ctx.uses = topo, N, lmax, uses
         ctx.mark_non_differentiable(mask)
         ctx.save_for_backward(r, n)
+        if uses == 2:
+            return r, r.view_as(r), Y, Y.view_as(Y), mask
         return r, Y, mask
 
     @staticmethod
     @once_differentiable
-    def backward(ctx, dr, dY, _dmask):
+    def backward(ctx, *grads):
+        if ctx.uses == 2:
+            dr, dr2, dY, dY2, _dmask = grads
+        else:
+            (dr, dY, _dmask), dr2, dY2 = grads, None, None
         r, n = ctx.saved_tensors
         E = r.numel()
         dvec = r.new_empty(E, 3)
-        nat.call("ictc_edge_harmonics_bwd", nat.ptr(r), nat.ptr(n), nat.ptr(None if dr is None else _c(dr)),
-                 nat.ptr(None if dY is None else _c(dY)), E, ctx.lmax, nat.ptr(dvec), nat.stream_of(r))
+        cot = [None if g is None else _c(g) for g in (dr, dY, dr2, dY2)]
+        # the kernel reads dY / dY2 as 16-byte vectors
+        cot = [g if g is None or k in (0, 2) or g.data_ptr() % 16 == 0 else g.clone() for k, g in enumerate(cot)]
+        nat.call("ictc_edge_harmonics_bwd", nat.ptr(r), nat.ptr(n), *[nat.ptr(g) for g in cot], E, ctx.lmax,
+                 nat.ptr(dvec), nat.stream_of(r))
         dpos = _vector_adjoint(dvec, ctx.topo, ctx.nodes) if ctx.needs_input_grad[0] else None
-        return dpos, (dvec if ctx.needs_input_grad[1] else None), None, None, None
+        return dpos, (dvec if ctx.needs_input_grad[1] else None), None, None, None, None
 
 
-def edge_harmonics(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: float, lmax: int):
+def edge_harmonics(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: float, lmax: int, uses: int = 1):
     """(r [E], Y [E, (lmax+1)^2], mask [E]): edge_geometry followed by the packed direction harmonics of n, in one
-    kernel, float32, first derivatives only (positions and shifts)."""
+    kernel, float32, first derivatives only (positions and shifts).  uses = 2 returns (r, r', Y, Y', mask) with
+    r' and Y' the same values for a second consumer, whose cotangents the adjoint adds in its kernel."""
     if pos.dtype != torch.float32 or (shift is not None and shift.dtype != torch.float32):
         raise TypeError("edge_harmonics runs in float32")
     if pos.dim() != 2 or pos.shape[1] != 3:
@@ -108,7 +121,9 @@ def edge_harmonics(pos: torch.Tensor, shift: torch.Tensor | None, topo, cutoff: 
         raise ValueError("shift must be [E, 3]")
     if not 0 <= int(lmax) <= 3:
         raise ValueError("edge_harmonics: lmax outside 0..3")
-    return _EdgeHarmonics.apply(pos, shift, topo, float(cutoff), int(lmax))
+    if uses not in (1, 2):
+        raise ValueError("edge_harmonics: uses is 1 or 2")
+    return _EdgeHarmonics.apply(pos, shift, topo, float(cutoff), int(lmax), int(uses))
 
 
 def _vector_adjoint(dvec: torch.Tensor, topo, N: int) -> torch.Tensor:

@@ -361,6 +361,7 @@ class PureCartesianICTDFix(nn.Module):
             # atoms are contiguous per graph, and the graphs' coordinates overlap)
             topology = tpo.Topology(edge_src, edge_dst, N, positions=pos if cell.shape[0] == 1 else None)
         shift_vec = shift_vectors(edge_shifts.to(pos.dtype), cell, batch, edge_src)
+        r_first = Y_first = None
         if second_order or pos.dtype != torch.float32:
             if pos.dtype == torch.float32 and pos.is_cuda:
                 from ictc_o3.ops.geometry import edge_vectors
@@ -372,9 +373,15 @@ class PureCartesianICTDFix(nn.Module):
             mask = (r <= self.max_radius).to(pos.dtype)
             Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
         else:
-            # first order: edge geometry and harmonics in one kernel, one per-edge adjoint
+            # first order: edge geometry and harmonics in one kernel, one per-edge adjoint; with two or more
+            # layers, the first layer takes its own r and Y outputs so that the adjoint adds the two layers'
+            # cotangents in its kernel
             from ictc_o3.ops.geometry import edge_harmonics
-            r, Y, mask = edge_harmonics(pos, shift_vec, topology, self.max_radius, self.ictd_fix_edge_lmax)
+            if self.num_interaction >= 2:
+                r, r_first, Y, Y_first, mask = edge_harmonics(pos, shift_vec, topology, self.max_radius,
+                                                              self.ictd_fix_edge_lmax, uses=2)
+            else:
+                r, Y, mask = edge_harmonics(pos, shift_vec, topology, self.max_radius, self.ictd_fix_edge_lmax)
         from ictc_o3.ops.radial_mlp import fused_supported
         fused = (not second_order and self.number_of_basis == 8
                  and all(fused_supported(inter.fc) for inter in self.interactions))
@@ -399,7 +406,9 @@ class PureCartesianICTDFix(nn.Module):
                 # the first layer's input is the species embedding: its linear_up rows per species
                 with torch.no_grad():
                     table = inter.linear_up(self.node_embedding.weight.t().contiguous(), True)
-            message, sc = inter(h, species, Y, radial, topology, mask, r, radial_cfg, forces_only,
+            first = i == 0 and r_first is not None
+            message, sc = inter(h, species, Y_first if first else Y, radial, topology, mask,
+                                r_first if first else r, radial_cfg, forces_only,
                                 self.radial_basis_scale, entry=entry, species_table=table)
             h = prod(message, sc, species, first_order=radial is None)
         e = self.last_layer_energy_readout(h if h.shape[1] == self.channels else h[:, :self.channels])

@@ -469,17 +469,18 @@ int ictc_edge_geometry_fwd(const float* pos, const float* shift, const int64_t* 
  * (energy + forces) route: the edge-vector block above (r, n, mask) and
  * Y [E,(lmax+1)^2] = ictc_sh_fwd(n) (the harmonics of the model forward,
  * pure_cartesian_ictd_layers.py:1298), lmax 0..3, each value exactly as the
- * two separate calls compute it.  n [E,3] is kept for the adjoint.  The
+ * two separate calls compute it (bitwise).  n [E,3] is kept for the adjoint.  The
  * adjoint ictc_edge_harmonics_bwd takes dr [E] and dY (either may be NULL =
- * zero) and writes dvec [E,3] per edge (ictc_sh_bwd's dn folded with dr as
+ * zero), plus dr2 / dY2 of a second consumer of r and Y (NULL = none; added
+ * to dr / dY first, as autograd would sum them), and writes dvec [E,3] per edge (ictc_sh_bwd's dn folded with dr as
  * ictc_edge_geometry_bwd does); ictc_edge_vector_bwd then gathers dvec into
- * dpos, in the same order, so dpos is bitwise that of ictc_sh_bwd followed by
- * ictc_edge_geometry_bwd.                                                     */
+ * dpos, in the same order, so dpos is that of ictc_sh_bwd followed by
+ * ictc_edge_geometry_bwd to FP32 rounding.  Y, dY and dY2 are 16-byte aligned. */
 int ictc_edge_harmonics_fwd(const float* pos, const float* shift, const int64_t* src, const int64_t* dst,
                             int64_t nodes, int64_t edges, float cutoff, int lmax, float* r, float* n, float* mask,
                             float* Y, void* stream);
-int ictc_edge_harmonics_bwd(const float* r, const float* n, const float* dr, const float* dY, int64_t edges, int lmax,
-                            float* dvec, void* stream);
+int ictc_edge_harmonics_bwd(const float* r, const float* n, const float* dr, const float* dY, const float* dr2,
+                            const float* dY2, int64_t edges, int lmax, float* dvec, void* stream);
 
 /* Cartesian image shifts of the edges, replacing `edge_shifts @ cell[batch[src]]`
  * (backbone.py:940-944, the shift term of vec): out [E,3] = shifts [E,3] (lattice

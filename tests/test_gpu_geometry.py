@@ -132,8 +132,10 @@ def test_shift_vectors(device, cells, E, seed):
                                                          (300, 5000, 23, True, False, "dr"),
                                                          (7, 0, 24, True, True, "both")])
 def test_edge_harmonics_matches_geometry_then_harmonics(device, lmax, N, E, seed, sort, with_shift, cot):
-    """The one-pass geometry + harmonics op gives bitwise the values and the position / shift adjoints of
-    edge_geometry followed by harmonics_packed (whose parity the tests above and the harmonics tests hold)."""
+    """The one-pass geometry + harmonics op gives bitwise the values (r, Y, mask) of edge_geometry followed by
+    harmonics_packed (whose parity the tests above and the harmonics tests hold), and their position / shift
+    adjoints to FP32 rounding (1e-6 of the largest entry: the compiler may fuse a product into a
+    multiply-add differently in the one-pass adjoint kernel and in the two separate ones)."""
     from ictc_o3.ops.geometry import edge_geometry, edge_harmonics
     from ictc_o3.ops.harmonics import harmonics_packed
     from ictc_o3.ops.tensor_product import Topology
@@ -158,7 +160,53 @@ def test_edge_harmonics_matches_geometry_then_harmonics(device, lmax, N, E, seed
             torch.autograd.backward(ts, gs)
         outs.append((r.detach(), Y.detach(), m, None if pd.grad is None else pd.grad.clone(),
                      None if sd is None or sd.grad is None else sd.grad.clone()))
-    for a, b in zip(*outs):
+    for k, (a, b) in enumerate(zip(*outs)):
         assert (a is None) == (b is None)
-        if a is not None:
+        if a is None:
+            continue
+        if k < 3:
             assert torch.equal(a, b)
+        elif a.numel():
+            assert (a - b).abs().max().item() <= 1e-6 * b.abs().max().item()
+
+
+@pytest.mark.parametrize("lmax", [1, 2])
+@pytest.mark.parametrize("cot", ["both", "first_only", "second_only", "mixed"])
+def test_edge_harmonics_two_consumers(device, lmax, cot):
+    """uses = 2: the second (r, Y) outputs' cotangents are added in the adjoint kernel; dpos and dshift are
+    bitwise those of one consumer fed with the fp32 sums (what autograd's addition would form)."""
+    from ictc_o3.ops.geometry import edge_harmonics
+    from ictc_o3.ops.tensor_product import Topology
+    N, E, seed = 300, 6000, 31
+    pos, src, dst, shift = _case(N, E, seed, True)
+    E = src.numel()
+    topo = Topology(src.to(device), dst.to(device), N)
+    g = torch.Generator().manual_seed(seed)
+    ga, gb = torch.randn(E, generator=g).to(device), torch.randn(E, generator=g).to(device)
+    Ya, Yb = (torch.randn(E, (lmax + 1) ** 2, generator=g).to(device) for _ in range(2))
+    # one cotangent as a view 4 bytes into a buffer (not 16-byte aligned): the op realigns it
+    buf = torch.zeros(E * (lmax + 1) ** 2 + 1, device=device)
+    buf[1:] = Yb.reshape(-1)
+    Yb = buf[1:].view(E, (lmax + 1) ** 2)
+    assert Yb.data_ptr() % 16 != 0
+    use = {"both": (True, True, True, True), "first_only": (True, False, True, False),
+           "second_only": (False, True, False, True), "mixed": (True, False, False, True)}[cot]
+
+    def run(two):
+        pd = pos.float().to(device).requires_grad_(True)
+        sd = shift.float().to(device).requires_grad_(True)
+        if two:
+            r, r2, Y, Y2, _ = edge_harmonics(pd, sd, topo, 4.5, lmax, uses=2)
+            ts = [t for t, u in zip((r, r2, Y, Y2), use) if u]
+            gs = [t for t, u in zip((ga, gb, Ya, Yb), use) if u]
+        else:
+            r, Y, _ = edge_harmonics(pd, sd, topo, 4.5, lmax)
+            sr = ga + gb if use[0] and use[1] else (ga if use[0] else gb if use[1] else None)
+            sY = Ya + Yb if use[2] and use[3] else (Ya if use[2] else Yb if use[3] else None)
+            ts = [t for t, gg in ((r, sr), (Y, sY)) if gg is not None]
+            gs = [gg for gg in (sr, sY) if gg is not None]
+        torch.autograd.backward(ts, gs)
+        return pd.grad.clone(), sd.grad.clone()
+
+    a, b = run(True), run(False)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
