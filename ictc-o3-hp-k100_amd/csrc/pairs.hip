@@ -42,10 +42,11 @@ int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-// kLanes lanes per edge scan the receiver segment of src[e] in strides of kLanes and keep the smallest CSR
-// position that matches (the first match in CSR order), reduced across the group (2 lanes measured
-// fastest against 4, 8 and 16 on the cfg4 graph: more edges in flight per wave, loads unrolled).
-constexpr int kLanes = 2;
+// Each wave takes kPerWave consecutive edges (two per lane), finds which of them are readers and hands the
+// readers out to its lanes in edge order (ballot + prefix count through LDS), so every lane scans for one
+// reader's reverse: owners cost no lane time in the scans.
+constexpr int kPerWave = 128;
+constexpr int kPartnerWaves = 4;
 
 // true when the edge (s -> d, shift (x, y, z)) reads the row of its reverse rather than owning one
 __device__ __forceinline__ bool reader(int64_t s, int64_t d, float x, float y, float z) {
@@ -63,47 +64,70 @@ __global__ void sorted_src_kernel(const int64_t* __restrict__ src, int64_t N, in
   sorted_src[q] = (s >= 0 && s < N) ? (int32_t)s : -1;
 }
 
-__global__ __launch_bounds__(256) void partner_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
-                                                      const float* __restrict__ shifts, int64_t N, int64_t E,
-                                                      const int32_t* __restrict__ ptr,
-                                                      const int32_t* __restrict__ order,
-                                                      const int32_t* __restrict__ sorted_src,
-                                                      int32_t* __restrict__ partner, int32_t* __restrict__ rev) {
-  const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kLanes;
-  const int sub = threadIdx.x % kLanes;
-  if (e >= E) return;   // whole groups leave together (E * kLanes lanes, groups aligned)
-  const int64_t s = src[e], d = dst[e];
-  int32_t best = INT32_MAX;
-  const float sx = shifts ? shifts[3 * e] : 0.f, sy = shifts ? shifts[3 * e + 1] : 0.f,
-              sz = shifts ? shifts[3 * e + 2] : 0.f;
-  if (s >= 0 && s < N && d >= 0 && d < N && reader(s, d, sx, sy, sz)) {
-    const int32_t beg = ptr[s], end = ptr[s + 1];
-    // every lane runs its whole strided scan (no early exit before the cross-lane reduction) and keeps
-    // its first match; 16-byte loads of 4-aligned quads (the sorted_src slab is padded to 256 bytes, so a
-    // quad past the last edge stays inside it), entries outside [beg, end) ignored
+struct ReaderSlot {
+  int32_t e, s, d;
+  float x, y, z;
+};
+
+__global__ __launch_bounds__(kPartnerWaves * 64) void partner_kernel(
+    const int64_t* __restrict__ src, const int64_t* __restrict__ dst, const float* __restrict__ shifts, int64_t N,
+    int64_t E, const int32_t* __restrict__ ptr, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ sorted_src, int32_t* __restrict__ partner, int32_t* __restrict__ rev) {
+  __shared__ ReaderSlot slots[kPartnerWaves][kPerWave];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t base = ((int64_t)blockIdx.x * kPartnerWaves + w) * kPerWave;
+  ReaderSlot* sl = slots[w];
+  int total = 0;
+#pragma unroll
+  for (int h = 0; h < kPerWave / 64; ++h) {
+    const int64_t e = base + 64 * h + lane;
+    bool rd = false;
+    int64_t s = -1, d = -1;
+    float x = 0.f, y = 0.f, z = 0.f;
+    if (e < E) {
+      s = src[e];
+      d = dst[e];
+      if (shifts) {
+        x = shifts[3 * e];
+        y = shifts[3 * e + 1];
+        z = shifts[3 * e + 2];
+      }
+      rd = s >= 0 && s < N && d >= 0 && d < N && reader(s, d, x, y, z);
+      if (!rd) partner[e] = -1;   // owners and edges with ids out of range
+    }
+    const uint64_t m = __ballot(rd);
+    if (rd) {
+      const int k = total + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+      sl[k] = ReaderSlot{(int32_t)e, (int32_t)s, (int32_t)d, x, y, z};
+    }
+    total += __popcll(m);
+  }
+  __syncthreads();
+  for (int k = lane; k < total; k += 64) {
+    const ReaderSlot r = sl[k];
+    const int32_t beg = ptr[r.s], end = ptr[r.s + 1];
+    int32_t best = INT32_MAX;
+    // the first reverse in CSR order: sources d among the edges into s, read as 16-byte quads of 4-aligned
+    // positions (the sorted_src slab is padded to 256 bytes, so a quad past the last edge stays inside it)
 #pragma unroll 4
-    for (int32_t q4 = (beg & ~3) + 4 * sub; q4 < end; q4 += 4 * kLanes) {
+    for (int32_t q4 = beg & ~3; q4 < end && best == INT32_MAX; q4 += 4) {
       const int4 v = *reinterpret_cast<const int4*>(sorted_src + q4);
       const int32_t cand[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int32_t q = q4 + k;
-        bool hit = cand[k] == (int32_t)d && q >= beg && q < end && best == INT32_MAX;
+      for (int c = 0; c < 4; ++c) {
+        const int32_t q = q4 + c;
+        bool hit = cand[c] == r.d && q >= beg && q < end && best == INT32_MAX;
         if (hit) {
           const int32_t e2 = order ? order[q] : q;
-          hit = e2 != e && (!shifts || (shifts[3 * (int64_t)e2] == -sx && shifts[3 * (int64_t)e2 + 1] == -sy &&
-                                        shifts[3 * (int64_t)e2 + 2] == -sz));
+          hit = e2 != r.e && (!shifts || (shifts[3 * (int64_t)e2] == -r.x && shifts[3 * (int64_t)e2 + 1] == -r.y &&
+                                          shifts[3 * (int64_t)e2 + 2] == -r.z));
         }
         if (hit) best = q;
       }
     }
-  }
-#pragma unroll
-  for (int m = kLanes / 2; m > 0; m >>= 1) best = min(best, __shfl_xor(best, m, kLanes));
-  if (sub == 0) {
     const int32_t p = best == INT32_MAX ? -1 : (order ? order[best] : best);
-    partner[e] = p;
-    if (rev && p >= 0) rev[p] = (int32_t)e;   // the reverse of p, for the source CSR (a second claimant races)
+    partner[r.e] = p;
+    if (rev && p >= 0) rev[p] = r.e;   // the reverse of p, for the source CSR (a second claimant races)
   }
 }
 
@@ -192,7 +216,7 @@ size_t scan_temp_bytes(int64_t E) {
 extern "C" {
 
 int64_t ictc_edge_pairs_workspace_bytes(int64_t E) {
-  if (E < 0 || E >= (int64_t(1) << 30)) return -1;   // E * kLanes threads under 2^31
+  if (E < 0 || E >= (int64_t(1) << 30)) return -1;   // int32 edge ids
   return (int64_t)(5 * align256(sizeof(int32_t) * (size_t)(E > 0 ? E : 1)) + align256(sizeof(int32_t)) +
                    align256(scan_temp_bytes(E)));
 }
@@ -230,10 +254,10 @@ int edge_pairs(const int64_t* src, const int64_t* dst, const float* shifts, int6
   void* temp = ws + 5 * slab + align256(sizeof(int32_t));
   size_t temp_bytes = scan_temp_bytes(E);
   const unsigned blocks = (unsigned)((E + 255) / 256);
-  const unsigned partner_blocks = (unsigned)((E * kLanes + 255) / 256);
+  const unsigned partner_blocks = (unsigned)((E + kPerWave * kPartnerWaves - 1) / (kPerWave * kPartnerWaves));
   hipLaunchKernelGGL(sorted_src_kernel, dim3(blocks), dim3(256), 0, st, src, N, E, dst_order, sorted_src);
   if (src_order) hipLaunchKernelGGL(fill_kernel, dim3(blocks), dim3(256), 0, st, rev, E, -1);
-  hipLaunchKernelGGL(partner_kernel, dim3(partner_blocks), dim3(256), 0, st, src, dst, shifts, N, E, dst_ptr,
+  hipLaunchKernelGGL(partner_kernel, dim3(partner_blocks), dim3(kPartnerWaves * 64), 0, st, src, dst, shifts, N, E, dst_ptr,
                      dst_order, sorted_src, partner, src_order ? rev : nullptr);
   hipLaunchKernelGGL(canonical_kernel, dim3(blocks), dim3(256), 0, st, partner, E, flag);
   if (hipcub::DeviceScan::ExclusiveSum(temp, temp_bytes, flag, idx, (int)E, st) != hipSuccess)
