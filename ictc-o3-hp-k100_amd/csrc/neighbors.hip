@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kBlock) void nl_walk_kernel(int64_t N, Geometry g, 
                                                         const int32_t* __restrict__ corder,
                                                         int32_t* __restrict__ count, const int64_t* __restrict__ row,
                                                         int64_t* __restrict__ src, int64_t* __restrict__ dst,
-                                                        float* __restrict__ shift) {
+                                                        float* __restrict__ shift, int64_t capacity) {
   const int lane = threadIdx.x & 63;
   const int64_t i = (int64_t)blockIdx.x * kWalkWaves + (threadIdx.x >> 6);
   if (i >= N) return;   // whole waves leave together
@@ -139,9 +139,9 @@ __global__ __launch_bounds__(kBlock) void nl_walk_kernel(int64_t N, Geometry g, 
     }
     const uint64_t mask = __ballot(hit);
     if (FILL) {
-      if (hit) {
-        const int64_t at = out + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
-                                                           __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+      const int64_t at = out + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+      if (hit && at < capacity) {   // edges past the caller's capacity are counted, not written
         src[at] = j;
         dst[at] = i;
 #pragma unroll
@@ -265,7 +265,7 @@ int ictc_neighbors_count(const float* pos, int64_t atoms, const double* cell, do
     const unsigned walk_blocks = (unsigned)((atoms + kWalkWaves - 1) / kWalkWaves);
     hipLaunchKernelGGL((nl_walk_kernel<false>), dim3(walk_blocks), dim3(kBlock), 0, st, atoms, g, (const double*)(w + L.posw),
                        (const int32_t*)(w + L.kimg), (const int32_t*)(w + L.cidx), (const int32_t*)(w + L.cptr),
-                       (const int32_t*)(w + L.corder), count, nullptr, nullptr, nullptr, nullptr);
+                       (const int32_t*)(w + L.corder), count, nullptr, nullptr, nullptr, nullptr, (int64_t)0);
     if (int rc = check_launch("neighbours count")) return rc;
   }
   // count[atoms] = 0, so the exclusive scan's last entry row[atoms] is the edge count.
@@ -280,9 +280,9 @@ int ictc_neighbors_count(const float* pos, int64_t atoms, const double* cell, do
   return check_launch("neighbours total");
 }
 
-int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, double cutoff, const int* ncell,
-                        const void* workspace, int64_t workspace_bytes, int64_t* src, int64_t* dst, float* shifts,
-                        void* stream) {
+int ictc_neighbors_fill_capacity(const float* pos, int64_t atoms, const double* cell, double cutoff,
+                                 const int* ncell, const void* workspace, int64_t workspace_bytes, int64_t* src,
+                                 int64_t* dst, float* shifts, int64_t capacity, void* stream) {
   Geometry g;
   if (int rc = make_geometry(cell, cutoff, ncell, &g)) return rc;
   (void)pos;
@@ -290,15 +290,23 @@ int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, dou
   Layout L;
   if (atoms < 0 || !workspace || !layout_for(atoms, ncells, &L) || workspace_bytes < (int64_t)L.total)
     return fail(ICTC_ERR_ARGUMENT, "neighbours: workspace too small");
-  if (atoms == 0) return ICTC_OK;
+  if (capacity < 0) return fail(ICTC_ERR_ARGUMENT, "neighbours: negative capacity");
+  if (atoms == 0 || capacity == 0) return ICTC_OK;
   if (!src || !dst || !shifts) return fail(ICTC_ERR_ARGUMENT, "neighbours: null output");
   const char* w = (const char*)workspace;
   const unsigned blocks = (unsigned)((atoms + kWalkWaves - 1) / kWalkWaves);
   hipLaunchKernelGGL((nl_walk_kernel<true>), dim3(blocks), dim3(kBlock), 0, (hipStream_t)stream, atoms, g,
                      (const double*)(w + L.posw), (const int32_t*)(w + L.kimg), (const int32_t*)(w + L.cidx),
                      (const int32_t*)(w + L.cptr), (const int32_t*)(w + L.corder), (int32_t*)nullptr,
-                     (const int64_t*)(w + L.row), src, dst, shifts);
+                     (const int64_t*)(w + L.row), src, dst, shifts, capacity);
   return check_launch("neighbours fill");
+}
+
+int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, double cutoff, const int* ncell,
+                        const void* workspace, int64_t workspace_bytes, int64_t* src, int64_t* dst, float* shifts,
+                        void* stream) {
+  return ictc_neighbors_fill_capacity(pos, atoms, cell, cutoff, ncell, workspace, workspace_bytes, src, dst, shifts,
+                                      INT64_MAX, stream);
 }
 
 }  // extern "C"

@@ -69,6 +69,7 @@ _SIGNATURES = {
     "ictc_neighbors_workspace_bytes": (_i64, [_i64, _p]),
     "ictc_neighbors_count": (_i, [_p, _i64, _p, ctypes.c_double, _p, _p, _i64, _p, _p]),
     "ictc_neighbors_fill": (_i, [_p, _i64, _p, ctypes.c_double, _p, _p, _i64, _p, _p, _p, _p]),
+    "ictc_neighbors_fill_capacity": (_i, [_p, _i64, _p, ctypes.c_double, _p, _p, _i64, _p, _p, _p, _i64, _p]),
     "ictc_gate_gemm_fwd": (_i, [_p, _i64, _i, _p, _i, _p, _p]),
     "ictc_radial_gates_workspace_bytes": (_i64, [_i]),
     "ictc_radial_gates_fwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, _p, _i, ctypes.c_float, _p, _p,

@@ -27,7 +27,14 @@ def _ncell(cell_cpu: torch.Tensor, cutoff: float):
     return [max(1, int(math.floor(w / cutoff))) for w in widths], widths
 
 
+_fill_capacity = {}   # (atoms, cells, cutoff, device) -> edge capacity for the next fill (from the last count)
+
+
 def _cell_list_hip(pos, cell_cpu, cutoff, ncell):
+    """The HIP cell list.  The edge count must reach the host to size the edge arrays; where an earlier call
+    on the same kind of system left a capacity estimate, the fill is launched into arrays of that capacity
+    before the count is read (only the count's copy is waited for, the fill runs meanwhile), and the arrays
+    are trimmed to the count; a count above the capacity refills arrays of the exact size."""
     import ctypes
     from ictc_o3 import _native as nat
     pos = pos.contiguous()
@@ -42,13 +49,35 @@ def _cell_list_hip(pos, cell_cpu, cutoff, ncell):
     stream = nat.stream_of(pos)
     nat.call("ictc_neighbors_count", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
              nat.ptr(count), stream)
-    E = int(count.item())
-    src = torch.empty(E, dtype=torch.int64, device=dev)
-    dst = torch.empty(E, dtype=torch.int64, device=dev)
-    shifts = torch.empty(E, 3, dtype=torch.float32, device=dev)
-    if E:
-        nat.call("ictc_neighbors_fill", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
-                 nat.ptr(src), nat.ptr(dst), nat.ptr(shifts), stream)
+    key = (N, tuple(ncell), float(cutoff), str(dev))
+    cap = _fill_capacity.get(key, 0)
+    E = -1
+    if cap > 0:
+        host = torch.empty(1, dtype=torch.int64, pin_memory=True)
+        host.copy_(count, non_blocking=True)
+        ready = torch.cuda.Event()
+        ready.record(torch.cuda.current_stream(dev))
+        src = torch.empty(cap, dtype=torch.int64, device=dev)
+        dst = torch.empty(cap, dtype=torch.int64, device=dev)
+        shifts = torch.empty(cap, 3, dtype=torch.float32, device=dev)
+        nat.call("ictc_neighbors_fill_capacity", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
+                 nat.ptr(src), nat.ptr(dst), nat.ptr(shifts), cap, stream)
+        ready.synchronize()
+        E = int(host[0])
+        if E <= cap:
+            src, dst, shifts = src[:E], dst[:E], shifts[:E]
+    if not 0 <= E <= cap:
+        if E < 0:
+            E = int(count.item())
+        src = torch.empty(E, dtype=torch.int64, device=dev)
+        dst = torch.empty(E, dtype=torch.int64, device=dev)
+        shifts = torch.empty(E, 3, dtype=torch.float32, device=dev)
+        if E:
+            nat.call("ictc_neighbors_fill", nat.ptr(pos), N, cellh, float(cutoff), nc, nat.ptr(ws), ws_bytes,
+                     nat.ptr(src), nat.ptr(dst), nat.ptr(shifts), stream)
+    if len(_fill_capacity) > 64:
+        _fill_capacity.clear()
+    _fill_capacity[key] = E + E // 32 + 1024   # room for the next step's fluctuation in the count
     from ictc_o3.ops.tensor_product import mark_receiver_sorted
     mark_receiver_sorted(dst, N)    # emitted receiver by receiver, ids in [0, N): Topology skips the sort
     return src, dst, shifts

@@ -451,6 +451,14 @@ int ictc_neighbors_count(const float* pos, int64_t atoms, const double* cell, do
 int ictc_neighbors_fill(const float* pos, int64_t atoms, const double* cell, double cutoff, const int* ncell,
                         const void* workspace, int64_t workspace_bytes, int64_t* src, int64_t* dst, float* shifts,
                         void* stream);
+/* _fill into arrays of `capacity` edges: the walk writes the first `capacity`
+ * edges (those at list positions below it) and skips the rest, so it can be
+ * launched before the edge count reaches the host, into arrays sized by an
+ * estimate; when the count exceeds the capacity, call _fill again into arrays
+ * of the exact size.  ictc_neighbors_fill is this with no limit.             */
+int ictc_neighbors_fill_capacity(const float* pos, int64_t atoms, const double* cell, double cutoff,
+                                 const int* ncell, const void* workspace, int64_t workspace_bytes, int64_t* src,
+                                 int64_t* dst, float* shifts, int64_t capacity, void* stream);
 
 /* ---- Edge geometry ---------------------------------------------------------
  * Replaces the edge-vector block of the model forward

@@ -30,6 +30,25 @@ def test_cell_list_matches_torch(device, n, cutoff, seed):
     assert bool((d1[1:] >= d1[:-1]).all())
 
 
+def test_fill_capacity_from_earlier_counts(device):
+    """Repeated calls on one kind of system fill arrays sized by the previous count before reading the new one:
+    the same edges as the torch formulation when the count fits, when it shrinks, and when it grows past the
+    estimate (the atoms gathered into a smaller region, about twice the pairs: the exact-size refill)."""
+    from mace_ictc.hp import neighbors as nb
+    pos, cell = _fcc(8, 3.42, 0.3, 4)
+    nb._fill_capacity.clear()
+    cases = [pos, pos + 0.01, pos * 0.98, pos * 0.6]
+    counts = []
+    for p in cases:
+        s1, d1, h1 = nb.radius_graph_pbc(p.to(device), cell.to(device), 4.5)
+        s0, d0, h0 = nb._radius_graph_torch(p.to(device), cell.to(device), 4.5)
+        assert torch.equal(s1, s0) and torch.equal(d1, d0) and torch.equal(h1, h0)
+        assert s1.is_contiguous() and h1.is_contiguous()
+        counts.append(s1.numel())
+    assert counts[3] > counts[0] + counts[0] // 32 + 1024     # the last case ran the refill
+    assert len(nb._fill_capacity) == 1
+
+
 def test_triclinic_against_brute_force(device):
     from mace_ictc.hp.neighbors import radius_graph_pbc
     g = torch.Generator().manual_seed(5)
