@@ -749,9 +749,12 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
           }
 #pragma unroll
           for (int p = 0; p < T::P; ++p) gw[p] *= m;
-          if (!tail) T::dx(y, gw, go, d);
-          if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
-          else T::dg(xv, y, go, dg);
+          if (dsh) {
+            T::dxdydg(xv, y, gw, go, d, dyv, dg);   // (the tail row's d is never stored)
+          } else {
+            if (!tail) T::dx(y, gw, go, d);
+            T::dg(xv, y, go, dg);
+          }
           dgt = m * gate_tangent_dot<T, W ? 1 : 0>(a, gdot, e, c, gt, dg);
         }
         store_dsh_dr<T::NY>(dsh_g, dr_g, e, dyv, dgt);
