@@ -17,6 +17,7 @@ component order (component k of degree l sits at l*l + m):
   dg    dg[p]  = sum_k go[k] sum C_p x[m1] y[m2]
   dydg  dy and dg of the same x in one pass
   dxdydg dx, dy and dg in one pass, factorised through V_p[i][j] = sum_k C go[k]
+  dydg_v, dx_v  the same factorisation for dy + dg alone and for dx alone
 
 The sums are grouped so that the lane-varying operand meets the CG literal
 first: B_jk = sum_i C x[i] costs one VALU op per nonzero, and the per-edge
@@ -141,32 +142,44 @@ def tp_struct(li, le, lo):
     #   dyv[j] += gw[p] sum_i V_p[i][j] x[i]
     #   dg[p]   = sum_j y[j] sum_i V_p[i][j] x[i]
     # path by path (V_p, its row sums and its column sums live only inside the path's block)
-    lines.append("  __device__ __forceinline__ static void dxdydg(const float* __restrict__ x, const float* __restrict__ y,"
-                 " const float* __restrict__ gw, const float* __restrict__ go, float* __restrict__ d,"
-                 " float* __restrict__ dyv, float* __restrict__ dg) {")
     by_pij = {}
     for p, i, j, k, v in ent:
         by_pij.setdefault(p, {}).setdefault((i, j), []).append((k, v))
-    for p in range(P):
-        pairs = by_pij.get(p, {})
-        lines.append("    {")
-        for (i, j), ks in sorted(pairs.items()):
-            lines.append(f"      const float v{i}_{j} = {' + '.join(f'{f(v)} * go[{k}]' for k, v in ks)};")
-        rows = {}
-        cols = {}
-        for (i, j) in sorted(pairs):
-            rows.setdefault(i, []).append(j)
-            cols.setdefault(j, []).append(i)
-        for i, js in sorted(rows.items()):
-            lines.append(f"      d[{i}] = fmaf(gw[{p}], {' + '.join(f'v{i}_{j} * y[{j}]' for j in js)}, d[{i}]);")
-        tl = []
-        for j, is_ in sorted(cols.items()):
-            lines.append(f"      const float t{j} = {' + '.join(f'v{i}_{j} * x[{i}]' for i in is_)};")
-            lines.append(f"      dyv[{j}] = fmaf(gw[{p}], t{j}, dyv[{j}]);")
-            tl.append(f"y[{j}] * t{j}")
-        lines.append(f"      dg[{p}] = {' + '.join(tl) if tl else '0.f'};")
-        lines.append(f"    }}{SB}")
-    lines.append("  }")
+
+    def factored(name, args, want_dx, want_dydg):
+        lines.append(f"  __device__ __forceinline__ static void {name}({args}) {{")
+        for p in range(P):
+            pairs = by_pij.get(p, {})
+            lines.append("    {")
+            for (i, j), ks in sorted(pairs.items()):
+                lines.append(f"      const float v{i}_{j} = {' + '.join(f'{f(v)} * go[{k}]' for k, v in ks)};")
+            rows = {}
+            cols = {}
+            for (i, j) in sorted(pairs):
+                rows.setdefault(i, []).append(j)
+                cols.setdefault(j, []).append(i)
+            if want_dx:
+                for i, js in sorted(rows.items()):
+                    lines.append(f"      d[{i}] = fmaf(gw[{p}], {' + '.join(f'v{i}_{j} * y[{j}]' for j in js)}, d[{i}]);")
+            if want_dydg:
+                tl = []
+                for j, is_ in sorted(cols.items()):
+                    lines.append(f"      const float t{j} = {' + '.join(f'v{i}_{j} * x[{i}]' for i in is_)};")
+                    lines.append(f"      dyv[{j}] = fmaf(gw[{p}], t{j}, dyv[{j}]);")
+                    tl.append(f"y[{j}] * t{j}")
+                lines.append(f"      dg[{p}] = {' + '.join(tl) if tl else '0.f'};")
+            lines.append(f"    }}{SB}")
+        lines.append("  }")
+
+    factored("dxdydg", "const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ gw, "
+             "const float* __restrict__ go, float* __restrict__ d, float* __restrict__ dyv, float* __restrict__ dg",
+             True, True)
+    # dy and dg alone (x varies per edge, so nothing of dydg's B_jk(x) survives between edges)
+    factored("dydg_v", "const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ gw, "
+             "const float* __restrict__ go, float* __restrict__ dyv, float* __restrict__ dg", False, True)
+    # dx alone
+    factored("dx_v", "const float* __restrict__ y, const float* __restrict__ gw, const float* __restrict__ go, "
+             "float* __restrict__ d", True, False)
     lines.append("};")
     return "\n".join(lines)
 

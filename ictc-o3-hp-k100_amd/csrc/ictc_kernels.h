@@ -290,7 +290,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeBwd, T::LI, T::LE, T::LO>::
       float d[T::NX];
 #pragma unroll
       for (int i = 0; i < T::NX; ++i) d[i] = 0.f;
-      T::dx(y, gw, go, d);
+      T::dx_v(y, gw, go, d);
       store_row<T::NX>(dx + e * (int64_t)(T::NX * C), C, c, d);
     }
     float d[T::P];
@@ -658,7 +658,7 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX, T::LI, T::LE, T::LO>::
         float go[T::NO], gw[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
         load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
-        T::dx(y, gw, go, d);
+        T::dx_v(y, gw, go, d);
       }
     }
   }
@@ -752,7 +752,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
           if (dsh) {
             T::dxdydg(xv, y, gw, go, d, dyv, dg);   // (the tail row's d is never stored)
           } else {
-            if (!tail) T::dx(y, gw, go, d);
+            if (!tail) T::dx_v(y, gw, go, d);
             T::dg(xv, y, go, dg);
           }
           dgt = m * gate_tangent_dot<T, W ? 1 : 0>(a, gdot, e, c, gt, dg);
@@ -794,7 +794,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
         load_gw<T, true>(a, lane_i(ch.row, i), c, m, gw);
         load_row_stream<T::P>(gdot + lane_i(ch.row, i) * (int64_t)(T::P * C), C, c, gt);
-        if (!tail) T::dx(y, gw, go, d);
+        if (!tail) T::dx_v(y, gw, go, d);
         if (dsh) T::dydg(xv, y, gw, go, dyv, dg);
         else T::dg(xv, y, go, dg);
         dgt = m * gate_tangent_dot<T>(a, gdot, e, c, gt, dg);
@@ -807,7 +807,7 @@ __global__ __launch_bounds__(kBlock, (src_adjoint_waves<T, TAN>())) void msg_bwd
         float go[T::NO], gw[T::P], dg[T::P];
         load_row<T::NO>(grad + r * (int64_t)(T::NO * C), C, c, go);
         load_gw<T>(a, lane_i(ch.row, i), c, m, gw);
-        if (!tail) T::dx(y, gw, go, d);
+        if (!tail) T::dx_v(y, gw, go, d);
         if (dsh && dgates) T::dydg(xv, y, gw, go, dyv, dg);
         else if (dsh) T::dy(xv, gw, go, dyv);
         else if (dgates) T::dg(xv, y, go, dg);

@@ -111,8 +111,8 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kEdgeSecond, T::LI, T::LE, T::LO
       if (dx) {
         float d[T::NX];
         zero<T::NX>(d);
-        if (t.sh) T::dx(ty, gw, go, d);
-        if (t.gates) T::dx(y, tg, go, d);
+        if (t.sh) T::dx_v(ty, gw, go, d);
+        if (t.gates) T::dx_v(y, tg, go, d);
         store_row<T::NX>(dx + xo, C, c, d);
       }
       float d[T::P];
@@ -313,12 +313,12 @@ __global__ __launch_bounds__(kBlock, (Occupancy<kMsgBwdX2, T::LI, T::LE, T::LO>:
         if (t.sh) {
           float gw[T::P];
           load_gates<T>(a.gates, a, e, c, m, gw);
-          T::dx(ty, gw, go, d);
+          T::dx_v(ty, gw, go, d);
         }
         if (t.gates) {
           float tg[T::P];
           load_gates<T>(t.gates, a, e, c, m, tg);
-          T::dx(y, tg, go, d);
+          T::dx_v(y, tg, go, d);
         }
       }
     }
