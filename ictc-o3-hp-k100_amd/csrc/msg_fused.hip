@@ -825,25 +825,30 @@ __device__ __forceinline__ int64_t hz_row(int64_t n, int lm, int64_t N) {
 // H[n, lm, (sp, k)] of every receiver row n on FP32 MFMA (v_mfma_f32_16x16x4f32), four edges per step:
 // A[lm][edge] = m Y_lm [species == sp] (lane: row lm = l % 16, edge l / 16), B[edge][k] = h3[edge][k]
 // (lane: edge l / 16, column k = 16 cb + l % 16); one accumulator per (species, 16-column block).
-template <int NY, int S>
+// PARTS waves share a row, each taking 4 / PARTS of the 16-column blocks of k: fewer accumulators per
+// wave, so more waves (and more edges' loads) in flight on this latency-bound pass.
+template <int NY, int S, int PARTS>
 __global__ __launch_bounds__(kSpWaves * 64) void species_fwd_kernel(SpeciesArgs a, float* __restrict__ H) {
-  const int64_t slot = sp_slot();
+  constexpr int CBW = 4 / PARTS;
+  const int64_t wslot = sp_slot();
+  const int64_t slot = wslot / PARTS;
+  const int cb0 = (int)(wslot % PARTS) * CBW;
   if (slot >= a.rows) return;
   const int64_t n = visit_row(a.csr, slot, a.rows);
   if (n < 0) return;
   const int l = lane_id(), col = l & 15, eg = l >> 4;
-  v4f acc[S][4];
+  v4f acc[S][CBW];
 #pragma unroll
   for (int b = 0; b < S; ++b)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[b][cb] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < CBW; ++cb) acc[b][cb] = v4f{0.f, 0.f, 0.f, 0.f};
   const int32_t beg = a.csr.ptr[n], end = a.csr.ptr[n + 1];
   for (int32_t pos = beg; pos < end; pos += 64) {
     const int32_t count = min(end - pos, 64);
     const SpChunk ch = sp_stage(a, pos, count);
     // two 4-edge steps per iteration: both steps' loads are in flight before the first MFMA
     for (int t0 = 0; t0 < count; t0 += 8) {
-      float yv[2], hb[2][4];
+      float yv[2], hb[2][CBW];
       int32_t spv[2];
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
@@ -855,7 +860,7 @@ __global__ __launch_bounds__(kSpWaves * 64) void species_fwd_kernel(SpeciesArgs 
         const float m = __shfl(ch.m, src_lane);
         yv[u] = (ok && col < NY) ? m * a.sh[(int64_t)e * NY + col] : 0.f;
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) hb[u][cb] = ok ? a.h3[(int64_t)row * 64 + 16 * cb + col] : 0.f;
+        for (int cb = 0; cb < CBW; ++cb) hb[u][cb] = ok ? a.h3[(int64_t)row * 64 + 16 * (cb0 + cb) + col] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -863,7 +868,7 @@ __global__ __launch_bounds__(kSpWaves * 64) void species_fwd_kernel(SpeciesArgs 
         for (int b = 0; b < S; ++b) {
           const float av = spv[u] == b ? yv[u] : 0.f;
 #pragma unroll
-          for (int cb = 0; cb < 4; ++cb) acc[b][cb] = mfma_f32(av, hb[u][cb], acc[b][cb]);
+          for (int cb = 0; cb < CBW; ++cb) acc[b][cb] = mfma_f32(av, hb[u][cb], acc[b][cb]);
         }
     }
   }
@@ -878,7 +883,7 @@ __global__ __launch_bounds__(kSpWaves * 64) void species_fwd_kernel(SpeciesArgs 
 #pragma unroll
       for (int b = 0; b < S; ++b)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) out[b * 64 + 16 * cb] = acc[b][cb][r];
+        for (int cb = 0; cb < CBW; ++cb) out[b * 64 + 16 * (cb0 + cb)] = acc[b][cb][r];
     }
   }
 }
@@ -1157,8 +1162,9 @@ int species_weights_any(int le, const float* X, int S, int C, const float* W4, c
 
 template <int NY, int S>
 void species_fwd_launch(const SpeciesArgs& a, float* H, hipStream_t st) {
-  const unsigned blocks = (unsigned)((a.rows + kSpWaves - 1) / kSpWaves);
-  hipLaunchKernelGGL((species_fwd_kernel<NY, S>), dim3(blocks), dim3(kSpWaves * 64), 0, st, a, H);
+  constexpr int PARTS = 2;   // 766 -> 703 us at cfg4 (one wave per row); 4 parts: 1016 us
+  const unsigned blocks = (unsigned)((a.rows * PARTS + kSpWaves - 1) / kSpWaves);
+  hipLaunchKernelGGL((species_fwd_kernel<NY, S, PARTS>), dim3(blocks), dim3(kSpWaves * 64), 0, st, a, H);
 }
 template <int NY, int S>
 void species_bwd_launch(const SpeciesArgs& a, const float* Z, float* dsh, float* dr, hipStream_t st) {
