@@ -315,14 +315,43 @@ class Topology:
         self.src, self.dst, self.nodes = _c(src), _c(dst), nodes
         self.by_dst = Csr(self.dst, nodes, presorted=receiver_sorted(self.dst, nodes))
         self._by_src = None
-        self.dst_rows = None
-        self.src_rows = morton_order(positions, spacing) if positions is not None and nodes > 0 else None
-        if self.src_rows is not None and nodes > 1:
-            self.dst_rows = _receiver_rows(positions, self.src_rows)
+        # the row orders are made at their first use (the message kernels), so that work enqueued right
+        # after the topology (the edge pairing) reaches the GPU before their launches; they change no
+        # result bit, only the visiting order
+        self._rows_from = (positions.detach(), spacing) if positions is not None and nodes > 0 else None
+        self._src_rows = self._dst_rows = None
         self._gate_rows = None    # int32 [E]: row of the shared radial gates each edge reads (pair_edges)
         self._gate_reps = None    # int64 [rows]: the edge whose length fills each gate row
         self._pending = None      # pairing launched, row count on its way to the host
         self._pairs_of = None
+
+    def _make_rows(self):
+        made, self._rows_from = self._rows_from, None
+        if made is not None:
+            positions, spacing = made
+            self._src_rows = morton_order(positions, spacing)
+            if self.nodes > 1:
+                self._dst_rows = _receiver_rows(positions, self._src_rows)
+
+    @property
+    def src_rows(self):
+        self._make_rows()
+        return self._src_rows
+
+    @src_rows.setter
+    def src_rows(self, value):
+        self._rows_from = None
+        self._src_rows = value
+
+    @property
+    def dst_rows(self):
+        self._make_rows()
+        return self._dst_rows
+
+    @dst_rows.setter
+    def dst_rows(self, value):
+        self._make_rows()
+        self._dst_rows = value
 
     def _resolve(self):
         """Finish pair_edges: wait for the row count's copy (only that copy, not the whole stream) and keep

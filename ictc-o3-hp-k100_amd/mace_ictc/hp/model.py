@@ -360,6 +360,13 @@ class PureCartesianICTDFix(nn.Module):
             # spatial row order for one periodic system; batched graphs keep index order (their
             # atoms are contiguous per graph, and the graphs' coordinates overlap)
             topology = tpo.Topology(edge_src, edge_dst, N, positions=pos if cell.shape[0] == 1 else None)
+        from ictc_o3.ops.radial_mlp import fused_supported
+        fused = (not second_order and self.number_of_basis == 8
+                 and all(fused_supported(inter.fc) for inter in self.interactions))
+        if fused and forces_only and tpo.PAIR_GATES:
+            # an edge and its reverse share one row of radial gates (equal lengths, bitwise); enqueued first,
+            # so the GPU runs the pairing while the host prepares the geometry launches
+            topology.pair_edges(edge_shifts)
         shift_vec = shift_vectors(edge_shifts.to(pos.dtype), cell, batch, edge_src)
         r_first = Y_first = None
         if second_order or pos.dtype != torch.float32:
@@ -382,13 +389,7 @@ class PureCartesianICTDFix(nn.Module):
                                                               self.ictd_fix_edge_lmax, uses=2)
             else:
                 r, Y, mask = edge_harmonics(pos, shift_vec, topology, self.max_radius, self.ictd_fix_edge_lmax)
-        from ictc_o3.ops.radial_mlp import fused_supported
-        fused = (not second_order and self.number_of_basis == 8
-                 and all(fused_supported(inter.fc) for inter in self.interactions))
         radial = None if fused else self.radial_embedding(r)
-        if fused and forces_only and tpo.PAIR_GATES:
-            # an edge and its reverse share one row of radial gates (equal lengths, bitwise)
-            topology.pair_edges(edge_shifts)
         if radial is not None and self.radial_basis_scale != 1.0:
             radial = radial * self.radial_basis_scale
         radial_cfg = (self.max_radius, self.polynomial_cutoff_p, SILU_SCALE)
