@@ -122,11 +122,31 @@ int key_bits(int64_t N) {
   return bits;
 }
 
+// Temporary-storage queries of the library sorts and scans ask the runtime for device properties on
+// every call (tens of microseconds of host time per step); the answer is kept per thread for the last
+// (device, size) asked.
+struct TempMemo {
+  int dev = -1;
+  int64_t a = -1, b = -1;
+  size_t bytes = 0;
+  bool hit(int64_t x, int64_t y, int* d) {
+    if (hipGetDevice(d) != hipSuccess) *d = -1;
+    return *d == dev && x == a && y == b;
+  }
+  size_t keep(int d, int64_t x, int64_t y, size_t v) {
+    dev = d, a = x, b = y, bytes = v;
+    return v;
+  }
+};
+
 size_t sort_temp_bytes(int64_t E, int64_t N) {
+  thread_local TempMemo memo;
+  int dev;
+  if (memo.hit(E, key_bits(N), &dev)) return memo.bytes;
   size_t bytes = 0;
   (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
                                      (const int32_t*)nullptr, (int32_t*)nullptr, (int)E, 0, key_bits(N));
-  return bytes;
+  return memo.keep(dev, E, key_bits(N), bytes);
 }
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -161,10 +181,13 @@ __global__ void morton_keys_kernel(const float* __restrict__ pos, int64_t N, flo
 }
 
 size_t morton_temp_bytes(int64_t N) {
+  thread_local TempMemo memo;
+  int dev;
+  if (memo.hit(N, 30, &dev)) return memo.bytes;
   size_t bytes = 0;
   (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr,
                                      (const int32_t*)nullptr, (int32_t*)nullptr, (int)N, 0, 30);
-  return bytes;
+  return memo.keep(dev, N, 30, bytes);
 }
 
 // Receiver row order: partial sums of |pos[i+1] - pos[i]| (index order) and |pos[rows[i+1]] - pos[rows[i]]|

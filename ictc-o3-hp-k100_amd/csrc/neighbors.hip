@@ -174,8 +174,20 @@ size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 bool layout_for(int64_t N, int64_t ncells, Layout* L) {
   const int64_t csr = ictc_csr_workspace_bytes(N, ncells);
   if (csr < 0) return false;
+  // the scan's temporary-storage query asks the runtime for device properties: kept per thread for the
+  // last (device, size)
+  thread_local int memo_dev = -1;
+  thread_local int64_t memo_n = -1;
+  thread_local size_t memo_scan = 0;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
   size_t scan = 0;
-  (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan, (const int32_t*)nullptr, (int64_t*)nullptr, (int)(N + 1));
+  if (dev == memo_dev && N == memo_n) {
+    scan = memo_scan;
+  } else {
+    (void)hipcub::DeviceScan::ExclusiveSum(nullptr, scan, (const int32_t*)nullptr, (int64_t*)nullptr, (int)(N + 1));
+    memo_dev = dev, memo_n = N, memo_scan = scan;
+  }
   size_t o = 0;
   L->key = o;    o += align256(sizeof(int64_t) * N);
   L->posw = o;   o += align256(sizeof(double) * 3 * N);

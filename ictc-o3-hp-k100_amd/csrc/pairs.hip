@@ -205,9 +205,18 @@ __global__ __launch_bounds__(256) void src_order_kernel(const int32_t* __restric
   }
 }
 
+// The scan's temporary-storage query asks the runtime for device properties; its answer is kept per
+// thread for the last (device, size).
 size_t scan_temp_bytes(int64_t E) {
+  thread_local int memo_dev = -1;
+  thread_local int64_t memo_e = -1;
+  thread_local size_t memo_bytes = 0;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  if (dev == memo_dev && E == memo_e) return memo_bytes;
   size_t bytes = 0;
   hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, (const int32_t*)nullptr, (int32_t*)nullptr, (int)(E > 0 ? E : 1));
+  memo_dev = dev, memo_e = E, memo_bytes = bytes;
   return bytes;
 }
 
