@@ -46,6 +46,7 @@ constexpr int H = 64;          // hidden width (compiled for 64)
 constexpr int KB = 8;          // radial basis size (compiled for 8)
 constexpr int FWD_WAVES = 4;   // waves per forward block (three blocks per CU: 51 KB of LDS each)
 constexpr int BWD_WAVES = 8;   // waves per adjoint block (one block per CU: 102 KB of LDS)
+constexpr int BWD2_WAVES = 4;  // waves per second-derivative block (one block per CU: 102 KB of LDS)
 
 // ---- split-bf16 helpers ------------------------------------------------------
 
@@ -122,6 +123,30 @@ __device__ __forceinline__ void radial_one(const Radial& q, float x, int k, floa
   const float f = q.pre * sn * inv;
   b = f * env;
   db = q.pre * (w * cs * inv - sn * inv * inv) * env + f * denv;
+}
+
+// b_k(r), db_k/dr and d2b_k/dr2 for one basis index k (1-based).
+__device__ __forceinline__ void radial_two(const Radial& q, float x, int k, float& b, float& db, float& d2b) {
+  const bool inside = x < q.rc;
+  const float u = x / q.rc;
+  const float upm2 = ipow(u, q.p - 2);
+  const float upm1 = upm2 * u;
+  const float up = upm1 * u;
+  const float env = inside ? 1.f - q.c1 * up + q.c2 * up * u - q.c3 * up * u * u : 0.f;
+  const float denv = inside ? (-q.c1 * q.p * upm1 + q.c2 * (q.p + 1) * up - q.c3 * (q.p + 2) * up * u) / q.rc : 0.f;
+  const float d2env = inside ? (-q.c1 * q.p * (q.p - 1) * upm2 + q.c2 * (q.p + 1) * q.p * upm1 -
+                                q.c3 * (q.p + 2) * (q.p + 1) * up) / (q.rc * q.rc)
+                             : 0.f;
+  const float xr = fmaxf(x, 1e-12f), inv = 1.f / xr;
+  const float w = k * 3.14159265358979323846f / q.rc;
+  float sn, cs;
+  sincosf(w * x, &sn, &cs);
+  const float f = q.pre * sn * inv;
+  const float df = q.pre * (w * cs * inv - sn * inv * inv);
+  const float d2f = q.pre * (-w * w * sn * inv - 2.f * w * cs * inv * inv + 2.f * sn * inv * inv * inv);
+  b = f * env;
+  db = df * env + f * denv;
+  d2b = d2f * env + 2.f * df * denv + f * d2env;
 }
 
 // ---- weights in LDS ----------------------------------------------------------
@@ -784,6 +809,152 @@ __global__ __launch_bounds__(BWD_WAVES * 64) void mlp_bwd_kernel(
   }
 }
 
+// ---- second derivative of the hidden MLP ------------------------------------
+// With u = da3 the cotangent of the last activation, the first adjoint's d/dr is
+// dr = u . t3, t3 = d a3 / dr (the forward-mode tangent).  Its derivative for a
+// cotangent rho on dr is the reverse pass through the tangent network, seeded
+// with rho u on t3: per layer k (z_k = W_k a_{k-1}, a_k = s silu(z_k), primes
+// = d/dr)
+//   zb3' = rho u . sl3,   zb3 = rho u . cv3
+//   zbk' = (W_{k+1}^T zb_{k+1}') . slk
+//   zbk  = (W_{k+1}^T zb_{k+1}) . slk + (W_{k+1}^T zb_{k+1}') . cvk
+// with slk = s silu'(z_k) and cvk = s silu''(z_k) z_k'; then
+//   d W_k += zbk'^T a_{k-1}' + zbk^T a_{k-1}     (a_0 = R(r), a_0' = R'(r))
+//   d r    = (W1^T zb1') . R''(r) + (W1^T zb1) . R'(r)
+//   d u    = rho t3.
+// s silu''(z) = s sig (1 - sig) (2 + z (1 - 2 sig)).
+// The weight-gradient rows go to [2E, 64] arrays (primed rows 0..E-1, unprimed
+// rows E..2E-1; the radial rows [2E, 8]), so that each d W_k is one product
+// zrows^T arows over 2E rows.
+__device__ __forceinline__ void act_dual(const v4f* z, const v4f* tz, float s, v4f* a, v4f* t, v4f* sl, v4f* cv) {
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float x = z[nb][k], g = sigm(x), h = 1.f - g;
+      a[nb][k] = s * x * g;
+      sl[nb][k] = s * g * (1.f + x * h);
+      t[nb][k] = sl[nb][k] * tz[nb][k];
+      cv[nb][k] = s * g * h * (2.f + x * (h - g)) * tz[nb][k];
+    }
+}
+
+__global__ __launch_bounds__(BWD2_WAVES * 64, 1) void mlp_bwd2_kernel(
+    const float* __restrict__ r, int64_t E, float rc, int p, const float* __restrict__ W1,
+    const float* __restrict__ W2, const float* __restrict__ W3, float s, const float* __restrict__ u,
+    const float* __restrict__ rho, float* __restrict__ dr, float* __restrict__ du, float* __restrict__ z3rows,
+    float* __restrict__ a2rows, float* __restrict__ z2rows, float* __restrict__ a1rows, float* __restrict__ z1rows,
+    float* __restrict__ brows) {
+  __shared__ FwdWeights wfs;
+  __shared__ AdjWeights was;
+  stage_fwd(wfs, W1, W2, W3);
+  stage_adj(was, W1, W2, W3);
+  __syncthreads();
+  const Radial q = radial_consts(rc, p);
+  const int l = threadIdx.x & 63, g = l >> 4;
+  const int waves = blockDim.x >> 6;
+  const int64_t tiles = (E + 15) / 16, stride = (int64_t)gridDim.x * waves;
+  const bool rows = z3rows != nullptr;
+  for (int64_t t = (int64_t)blockIdx.x * waves + (threadIdx.x >> 6); t < tiles; t += stride) {
+    const int64_t e = 16 * t + (l & 15);
+    const bool ok = e < E;
+    const float x = ok ? r[e] : 2.f * rc;
+    const float rh = ok ? rho[e] : 0.f;
+    const FwdWeights& wf = *opaque(&wfs);
+    const AdjWeights& wa = *opaque(&was);
+    float b[2], db[2], d2b[2];
+    radial_two(q, x, 2 * g + 1, b[0], db[0], d2b[0]);
+    radial_two(q, x, 2 * g + 2, b[1], db[1], d2b[1]);
+    if (rows && ok) {
+      *reinterpret_cast<float2*>(brows + e * KB + 2 * g) = make_float2(db[0], db[1]);
+      *reinterpret_cast<float2*>(brows + (E + e) * KB + 2 * g) = make_float2(b[0], b[1]);
+    }
+    // forward with the tangent: slopes and curvatures kept per layer
+    v4f sl1[4], cv1[4], sl2[4], cv2[4], sl3[4], cv3[4];
+    v4f z[4], tz[4], a[4], ta[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      z[jb] = tz[jb] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        z[jb] = mfma32(wf.w1f[jb][ks][l], b[ks], z[jb]);
+        tz[jb] = mfma32(wf.w1f[jb][ks][l], db[ks], tz[jb]);
+      }
+    }
+    act_dual(z, tz, s, a, ta, sl1, cv1);
+    if (rows) {
+      store_units(a1rows, e, ok, ta);
+      store_units(a1rows + E * H, e, ok, a);
+    }
+    Split B[2], Bt[2];
+    split_units(a, B);
+    split_units(ta, Bt);
+    gemm6_pair(wf.wf[0], B, Bt, z, tz);
+    act_dual(z, tz, s, a, ta, sl2, cv2);
+    if (rows) {
+      store_units(a2rows, e, ok, ta);
+      store_units(a2rows + E * H, e, ok, a);
+    }
+    split_units(a, B);
+    split_units(ta, Bt);
+    gemm6_pair(wf.wf[1], B, Bt, z, tz);
+    act_dual(z, tz, s, a, ta, sl3, cv3);   // a = a3 (unused), ta = t3
+    if (du) {
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) a[nb] = rh * ta[nb];
+      store_units(du, e, ok, a);
+    }
+    // reverse through the tangent network
+    load_units(u, e, ok, a);
+    v4f zp[4], zu[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const v4f seed = rh * a[nb];
+      zp[nb] = seed * sl3[nb];
+      zu[nb] = seed * cv3[nb];
+    }
+    if (rows) {
+      store_units(z3rows, e, ok, zp);
+      store_units(z3rows + E * H, e, ok, zu);
+    }
+    split_units(zp, B);
+    split_units(zu, Bt);
+    gemm6_pair(wa.wa[1], B, Bt, zp, zu);   // W3^T zb3', W3^T zb3
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      zu[nb] = zu[nb] * sl2[nb] + zp[nb] * cv2[nb];
+      zp[nb] = zp[nb] * sl2[nb];
+    }
+    if (rows) {
+      store_units(z2rows, e, ok, zp);
+      store_units(z2rows + E * H, e, ok, zu);
+    }
+    split_units(zp, B);
+    split_units(zu, Bt);
+    gemm6_pair(wa.wa[0], B, Bt, zp, zu);   // W2^T zb2', W2^T zb2
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      zu[nb] = zu[nb] * sl1[nb] + zp[nb] * cv1[nb];
+      zp[nb] = zp[nb] * sl1[nb];
+    }
+    if (rows) {
+      store_units(z1rows, e, ok, zp);
+      store_units(z1rows + E * H, e, ok, zu);
+    }
+    // W1^T zb1' and W1^T zb1 on FP32 MFMA (rows of the lane's two basis functions)
+    v4f dRp = v4f{0.f, 0.f, 0.f, 0.f}, dRu = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 16; ++ks) {
+      dRp = mfma32(wa.w1a[ks][l], zp[ks >> 2][ks & 3], dRp);
+      dRu = mfma32(wa.w1a[ks][l], zu[ks >> 2][ks & 3], dRu);
+    }
+    float v = dRp[0] * d2b[0] + dRp[1] * d2b[1] + dRu[0] * db[0] + dRu[1] * db[1];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if (l < 16 && ok) dr[e] = v;
+  }
+}
+
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
 
 int launch_status(const char* what) {
@@ -1013,6 +1184,30 @@ int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden
                      (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, dr, dz1, dz2, dz3,
                      a1, a2);
   return launch_status("ictc_radial_mlp_bwd launch");
+}
+
+int ictc_radial_mlp_bwd2(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
+                         const float* rho, float* dr, float* dda3, float* z3rows, float* a2rows, float* z2rows,
+                         float* a1rows, float* z1rows, float* brows, void* stream) {
+  if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
+  if (edges < 0 || !(cutoff > 0.f) || poly_p < 2) return fail(ICTC_ERR_ARGUMENT, "radial MLP: invalid arguments");
+  if (edges == 0) return ICTC_OK;
+  if (!r || !W1 || !W2 || !W3 || !da3 || !rho || !dr) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
+  const float* rows[] = {z3rows, a2rows, z2rows, a1rows, z1rows, brows};
+  const bool any = z3rows || a2rows || z2rows || a1rows || z1rows || brows;
+  for (const float* q : rows)
+    if (any && !q) return fail(ICTC_ERR_ARGUMENT, "radial MLP: weight-gradient rows are all given or all null");
+  for (const float* q : {da3, (const float*)dda3, (const float*)z3rows, (const float*)a2rows, (const float*)z2rows,
+                         (const float*)a1rows, (const float*)z1rows})
+    if (q && !aligned16(q)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: [E, 64] operands must be 16-byte aligned");
+  if (brows && (reinterpret_cast<uintptr_t>(brows) & 7))
+    return fail(ICTC_ERR_ARGUMENT, "radial MLP: radial rows must be 8-byte aligned");
+  const int per_cu = resident_per_cu(mlp_bwd2_kernel, BWD2_WAVES * 64, 1);
+  hipLaunchKernelGGL(mlp_bwd2_kernel, dim3(grid_for(edges, BWD2_WAVES, per_cu)), dim3(BWD2_WAVES * 64), 0,
+                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, rho, dr, dda3,
+                     z3rows, a2rows, z2rows, a1rows, z1rows, brows);
+  return launch_status("ictc_radial_mlp_bwd2 launch");
 }
 
 }  // extern "C"

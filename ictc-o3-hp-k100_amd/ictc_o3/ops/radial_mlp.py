@@ -16,6 +16,7 @@ tiles only the small output.
 from __future__ import annotations
 
 import ctypes
+import math
 
 import torch
 from torch.autograd.function import once_differentiable
@@ -279,3 +280,161 @@ def radial_gates(r: torch.Tensor, fc: torch.nn.Sequential, cutoff: float, poly_p
     W1 = lin[0].weight if basis_scale == 1.0 else lin[0].weight * basis_scale
     return _RadialGates.apply(r, W1, lin[1].weight, lin[2].weight, lin[3].weight, float(cutoff),
                               int(poly_p), float(scale))
+
+
+# ---- hidden layers with first and second derivatives on the fused kernels ----------------------------------
+
+class EdgeLengths:
+    """Radial input of an interaction block that runs fc's hidden layers on the fused kernels to second order
+    (radial_hidden) instead of taking a materialised radial basis; the lengths themselves are the block's r."""
+    __slots__ = ()
+
+
+def hidden_supported(fc: torch.nn.Sequential, r: torch.Tensor) -> bool:
+    return fused_supported(fc) and r.is_cuda and r.dtype == torch.float32
+
+
+def radial_mlp_lengths(r: torch.Tensor, fc: torch.nn.Sequential, cutoff: float, poly_p: int, scale: float,
+                       basis_scale: float = 1.0) -> torch.Tensor:
+    """fc(radial_embedding(r) * basis_scale) with the hidden layers on the fused kernels (radial_hidden) and
+    the gate projection as edge_linear; differentiable to any order (second order on the fused kernels)."""
+    lin = [m for m in fc if isinstance(m, torch.nn.Linear)]
+    W1 = lin[0].weight if basis_scale == 1.0 else lin[0].weight * basis_scale
+    h3 = radial_hidden(r, W1, lin[1].weight, lin[2].weight, cutoff, poly_p, scale)
+    return edge_linear(h3, lin[3].weight)
+
+
+def radial_hidden(r, W1, W2, W3, cutoff: float, poly_p: int, scale: float) -> torch.Tensor:
+    """h3 [E, 64] = s silu(W3 s silu(W2 s silu(W1 R(r)))) with R the Bessel x polynomial-cutoff basis
+    (8 functions, radial_basis.py:11-92): the forward, the first adjoint and its derivative (the force-loss
+    second derivative) on the fused kernels; third and higher orders on composed torch operations."""
+    if r.dim() != 1 or tuple(W1.shape) != (64, 8) or tuple(W2.shape) != (64, 64) or tuple(W3.shape) != (64, 64):
+        raise ValueError("radial_hidden needs r [E] and weights [64, 8], [64, 64], [64, 64]")
+    return _Hidden.apply(r, W1, W2, W3, float(cutoff), int(poly_p), float(scale))
+
+
+def _hidden_torch(r, W1, W2, W3, cutoff, poly_p, scale):
+    """The same function on plain torch operations (any derivative order)."""
+    rr = r.unsqueeze(-1)
+    k = torch.arange(1, 9, device=r.device, dtype=r.dtype)
+    u = rr / cutoff
+    p = poly_p
+    env = (1.0 - 0.5 * (p + 1) * (p + 2) * u ** p + p * (p + 2) * u ** (p + 1) - 0.5 * p * (p + 1) * u ** (p + 2))
+    env = env * (rr < cutoff).to(r.dtype)
+    h = math.sqrt(2.0 / cutoff) * torch.sin(k * math.pi * rr / cutoff) / rr.clamp(min=1e-12) * env
+    for W in (W1, W2, W3):
+        h = torch.nn.functional.silu(h @ W.t()) * scale
+    return h
+
+
+def _hidden_weight_grads(rows, needs):
+    """d W1..W3 from the kernel's weight-gradient rows: (z1, b), (z2, a1), (z3, a2) pairs over the same rows."""
+    z1, b, z2, a1, z3, a2 = rows
+    return [weight_grad(z1, b) if needs[0] else None, weight_grad(z2, a1) if needs[1] else None,
+            weight_grad(z3, a2) if needs[2] else None]
+
+
+def _hidden_adjoint(r, Ws, cfg, u, needs):
+    """First adjoint for cotangent u [E, 64]: (dr or None, [dW1, dW2, dW3] or None entries)."""
+    cutoff, poly_p, scale = cfg
+    r, u = _c(r.detach()), _c(u.detach())
+    W1, W2, W3 = (_c(w.detach()) for w in Ws)
+    E = r.shape[0]
+    need_w = any(needs[1:4])
+    dr = r.new_empty(E)
+    extra = [r.new_empty(E, 64) for _ in range(5)] if need_w else [None] * 5   # dz1, dz2, dz3, a1, a2
+    nat.call("ictc_radial_mlp_bwd", nat.ptr(r), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
+             nat.ptr(W3), float(scale), nat.ptr(u), nat.ptr(dr), *[nat.ptr(t) for t in extra], nat.stream_of(r))
+    dW = [None] * 3
+    if need_w:
+        from ictc_o3.ops.activation import _radial
+        dz1, dz2, dz3, a1, a2 = extra
+        R = _radial(0, r, None, None, 8, cutoff, poly_p)
+        dW = _hidden_weight_grads((dz1, R, dz2, a1, dz3, a2), needs[1:4])
+    return (dr if needs[0] else None), dW
+
+
+class _Hidden(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, r, W1, W2, W3, cutoff, poly_p, scale):
+        ctx.cfg = (cutoff, poly_p, scale)
+        ctx.inputs = (r, W1, W2, W3)
+        rc = _c(r.detach())
+        Ws = [_c(w.detach()) for w in (W1, W2, W3)]
+        h3 = rc.new_empty(rc.shape[0], 64)
+        nat.call("ictc_radial_mlp_fwd", nat.ptr(rc), rc.shape[0], 8, 64, float(cutoff), int(poly_p),
+                 nat.ptr(Ws[0]), nat.ptr(Ws[1]), nat.ptr(Ws[2]), float(scale), nat.ptr(h3), nat.stream_of(rc))
+        ctx.save_for_backward(r, W1, W2, W3)
+        return h3
+
+    @staticmethod
+    def backward(ctx, u):
+        from ictc_o3.autograd import required_gradients
+        r, W1, W2, W3 = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:4]) if ctx.inputs else ctx.needs_input_grad[:4]
+        ctx.inputs = None
+        if u is None or not any(needs):
+            return (None,) * 7
+        if torch.is_grad_enabled():
+            # differentiable adjoint (the force pass of a force-loss step)
+            out = _HiddenAdjoint.apply(r, W1, W2, W3, u, ctx.cfg, tuple(needs))
+            return (*out, None, None, None)
+        dr, dW = _hidden_adjoint(r, (W1, W2, W3), ctx.cfg, u, needs)
+        return (dr, *dW, None, None, None)
+
+
+class _HiddenAdjoint(torch.autograd.Function):
+    """(dr, dW1, dW2, dW3) of radial_hidden for cotangent u, differentiable once more on the fused kernel
+    (ictc_radial_mlp_bwd2: cotangents on dr only); cotangents on the weight gradients, or a backward that
+    itself builds a graph, go through _hidden_torch."""
+
+    @staticmethod
+    def forward(ctx, r, W1, W2, W3, u, cfg, needs):
+        ctx.cfg = cfg
+        ctx.inputs = (r, W1, W2, W3, u)
+        ctx.save_for_backward(r, W1, W2, W3, u)
+        dr, dW = _hidden_adjoint(r, (W1, W2, W3), cfg, u, needs)
+        return dr, *dW
+
+    @staticmethod
+    def backward(ctx, hr, h1, h2, h3):
+        from ictc_o3.autograd import required_gradients
+        r, W1, W2, W3, u = ctx.saved_tensors
+        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:5]) if ctx.inputs else ctx.needs_input_grad[:5]
+        ctx.inputs = None
+        none = (None,) * 7
+        if not any(needs) or (hr is None and h1 is None and h2 is None and h3 is None):
+            return none
+        if torch.is_grad_enabled() or h1 is not None or h2 is not None or h3 is not None:
+            return (*_hidden_adjoint_torch(ctx.cfg, (r, W1, W2, W3, u), (hr, h1, h2, h3), needs), None, None)
+        cutoff, poly_p, scale = ctx.cfg
+        rc, uc, hrc = _c(r.detach()), _c(u.detach()), _c(hr.detach())
+        Ws = [_c(w.detach()) for w in (W1, W2, W3)]
+        E = rc.shape[0]
+        need_w = any(needs[1:4])
+        d_r = rc.new_empty(E)
+        d_u = rc.new_empty(E, 64) if needs[4] else None
+        rows = [rc.new_empty(2 * E, 64) for _ in range(5)] + [rc.new_empty(2 * E, 8)] if need_w else [None] * 6
+        z3, a2, z2, a1, z1, b = rows
+        nat.call("ictc_radial_mlp_bwd2", nat.ptr(rc), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(Ws[0]),
+                 nat.ptr(Ws[1]), nat.ptr(Ws[2]), float(scale), nat.ptr(uc), nat.ptr(hrc), nat.ptr(d_r),
+                 nat.ptr(d_u), *[nat.ptr(t) for t in rows], nat.stream_of(rc))
+        dW = _hidden_weight_grads((z1, b, z2, a1, z3, a2), needs[1:4]) if need_w else [None] * 3
+        return (d_r if needs[0] else None, *dW, d_u, None, None)
+
+
+def _hidden_adjoint_torch(cfg, saved, cotangents, needs):
+    """Derivative of the first adjoint on composed torch operations (any order)."""
+    create = torch.is_grad_enabled()
+    # building a graph: differentiate the saved tensors themselves, so the result stays connected to theirs
+    inputs = [t if create and t.requires_grad else t.detach().requires_grad_(True) for t in saved]
+    r, W1, W2, W3, u = inputs
+    with torch.enable_grad():
+        h = _hidden_torch(r, W1, W2, W3, *cfg)
+        first = torch.autograd.grad(h, (r, W1, W2, W3), u, create_graph=True, allow_unused=True)
+        outs = [(f, c) for f, c in zip(first, cotangents) if f is not None and c is not None]
+        wanted = [t for t, n in zip(inputs, needs) if n]
+        got = torch.autograd.grad([f for f, _ in outs], wanted, [c for _, c in outs], create_graph=create,
+                                  allow_unused=True)
+    it = iter(got)
+    return tuple(next(it) if n else None for n in needs)

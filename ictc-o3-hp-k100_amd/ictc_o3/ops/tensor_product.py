@@ -686,6 +686,11 @@ class RadialMessage(torch.autograd.Function):
 # "always" = every compiled shape; "never" = nowhere.
 FUSED_GATES = "auto"
 
+# Whether models that need second derivatives run the radial MLP's hidden layers on the fused kernels
+# (ictc_o3.ops.radial_mlp.radial_hidden: forward, first adjoint and its derivative in one launch each)
+# instead of composing them from per-layer Linear and SiLU operations.
+FUSED_HIDDEN = True
+
 # Whether callers of radial_message pair edges with their reverses (Topology.pair_edges) so that the
 # radial gates are evaluated once per undirected edge; False keeps one gate row per directed edge.
 PAIR_GATES = True

@@ -34,7 +34,7 @@ from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops import tensor_product as tpo
 from ictc_o3.ops.harmonics import harmonics_packed
 from ictc_o3.ops.linear import species_rows
-from ictc_o3.ops.radial_mlp import edge_linear
+from ictc_o3.ops.radial_mlp import EdgeLengths, edge_linear, hidden_supported, radial_mlp_lengths
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
 SILU_SCALE = 1.6791767923989418   # _Normalize2MomSiLU (layers.py:307-314)
@@ -191,6 +191,8 @@ class Interaction(nn.Module):
             if radial is None:
                 from ictc_o3.ops.radial_mlp import radial_gates
                 gates = radial_gates(r, self.fc, *radial_cfg, basis_scale=basis_scale)
+            elif isinstance(radial, EdgeLengths):
+                gates = radial_mlp_lengths(r, self.fc, *radial_cfg, basis_scale=basis_scale)
             else:
                 from ictc_o3.ops.radial_mlp import radial_mlp
                 gates = radial_mlp(radial, self.fc)
@@ -389,8 +391,15 @@ class PureCartesianICTDFix(nn.Module):
                                                               self.ictd_fix_edge_lmax, uses=2)
             else:
                 r, Y, mask = edge_harmonics(pos, shift_vec, topology, self.max_radius, self.ictd_fix_edge_lmax)
-        radial = None if fused else self.radial_embedding(r)
-        if radial is not None and self.radial_basis_scale != 1.0:
+        if fused:
+            radial = None
+        elif (tpo.FUSED_HIDDEN and self.number_of_basis == 8
+              and all(hidden_supported(inter.fc, r) for inter in self.interactions)):
+            # second derivatives: the radial MLP's hidden layers on the fused kernels (lengths in, not the basis)
+            radial = EdgeLengths()
+        else:
+            radial = self.radial_embedding(r)
+        if isinstance(radial, torch.Tensor) and self.radial_basis_scale != 1.0:
             radial = radial * self.radial_basis_scale
         radial_cfg = (self.max_radius, self.polynomial_cutoff_p, SILU_SCALE)
         h = species_rows(self.node_embedding.weight.t(), species)

@@ -571,6 +571,18 @@ int ictc_radial_mlp_tangent_fwd(const float* r, int64_t edges, int num_basis, in
 int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
                         float* dr, float* dz1, float* dz2, float* dz3, float* a1, float* a2, void* stream);
+/* Derivative of ictc_radial_mlp_bwd's dr for a cotangent rho [E] on it: what
+ * torch's double backward through `fc` (layers.py:826-835, without its last
+ * Linear) computes in a force-loss training step.  With dr = da3 . t3
+ * (t3 = d a3 / dr), writes dr_out [E] = d (rho dr) / dr, dda3 [E, 64] =
+ * rho t3 (nullable), and, when the six row arrays are given (all or none),
+ * the rows whose products are the weight gradients over 2E rows:
+ * d W3 = z3rows^T a2rows, d W2 = z2rows^T a1rows, d W1 = z1rows^T brows
+ * (z/a rows [2E, 64] 16-byte aligned, brows [2E, 8] 8-byte aligned).       */
+int ictc_radial_mlp_bwd2(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
+                         const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
+                         const float* rho, float* dr_out, float* dda3, float* z3rows, float* a2rows, float* z2rows,
+                         float* a1rows, float* z1rows, float* brows, void* stream);
 
 /* ---- Symmetric contraction (bridge-U, correlation 1..3) -------------------
  * Replaces the SC circuits of ICTDBridgeUSymmetricContractionSO3.forward

@@ -72,3 +72,68 @@ def test_normalized_silu_derivatives(device, n, offset):
     got = run(xd, v64.float().to(device), w64.float().to(device), lambda t: normalized_silu(t, mo.SILU))
     for a, b in zip(got, ref):
         assert rel_err(a, b) < 1e-5
+
+
+def _ref_hidden(r, Ws, cutoff, p):
+    h = mo.radial(r, cutoff, 8, p)
+    for W in Ws:
+        h = torch.nn.functional.silu(h @ W.t()) * mo.SILU
+    return h
+
+
+def _hidden_case(E, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    r = torch.rand(E, generator=g, dtype=torch.float64) * 4.6 + 0.4        # some beyond the 4.5 cutoff
+    sizes = [8, 64, 64, 64]
+    Ws = [torch.randn(o, i, generator=g, dtype=torch.float64) / math.sqrt(i) for i, o in zip(sizes, sizes[1:])]
+    u = torch.randn(E, 64, generator=g, dtype=torch.float64)
+    v = torch.randn(E, 64, generator=g, dtype=torch.float64)
+    rho = torch.randn(E, generator=g, dtype=torch.float64)
+    ref = [t.clone() for t in (r, *Ws, u, v, rho)]
+    got = [t.float().to(device) for t in (r, *Ws, u, v, rho)]
+    return ref, got
+
+
+def _force_loss_grads(hidden, r, W1, W2, W3, u, v, rho):
+    """grad of <v, h> + <rho, d<u, h>/dr> w.r.t. (r, W1, W2, W3, u): the shape of a force-loss step."""
+    leaves = [t.clone().requires_grad_(True) for t in (r, W1, W2, W3, u)]
+    r, W1, W2, W3, u = leaves
+    h = hidden(r, W1, W2, W3)
+    (dr,) = torch.autograd.grad(h, r, u, create_graph=True)
+    loss = (v * h).sum() + (rho * dr).sum()
+    return [h, dr, *torch.autograd.grad(loss, leaves)]
+
+
+@pytest.mark.parametrize("E", [1, 77, 4099, 40001])
+def test_radial_hidden_second_derivatives(device, E):
+    """radial_hidden: h3, the force-pass d/dr and the gradients of a force-loss-shaped objective (the
+    second-derivative kernel ictc_radial_mlp_bwd2 and the first adjoint) vs float64 autograd, 1e-5 relative."""
+    from ictc_o3.ops.radial_mlp import radial_hidden
+    (r, W1, W2, W3, u, v, rho), got = _hidden_case(E, 100 + E, device)
+    ref = _force_loss_grads(lambda *a: _ref_hidden(a[0], a[1:], 4.5, 5), r, W1, W2, W3, u, v, rho)
+    out = _force_loss_grads(lambda *a: radial_hidden(a[0], *a[1:], 4.5, 5, mo.SILU), *got)
+    names = ["h3", "dr", "d/dr", "d/dW1", "d/dW2", "d/dW3", "d/du"]
+    for name, a, b in zip(names, out, ref):
+        assert rel_err(a, b) < 1e-5, name
+
+
+def test_radial_hidden_other_orders(device):
+    """Cotangents on the first adjoint's weight gradients and a third derivative take the composed torch
+    route (_hidden_torch); both against float64 autograd."""
+    from ictc_o3.ops.radial_mlp import radial_hidden
+    (r, W1, W2, W3, u, v, rho), got = _hidden_case(300, 7, device)
+
+    def run(hidden, r, W1, W2, W3, u, rho):
+        leaves = [t.clone().requires_grad_(True) for t in (r, W1, W2, W3, u)]
+        r, W1, W2, W3, u = leaves
+        h = hidden(r, W1, W2, W3)
+        dr, dW2 = torch.autograd.grad(h, (r, W2), u, create_graph=True)
+        s = (rho * dr).sum() + (dW2 * W2).sum()
+        (sr,) = torch.autograd.grad(s, r, create_graph=True)          # a third derivative follows
+        (t,) = torch.autograd.grad((sr * rho).sum(), r)
+        return [dr, dW2, sr, t]
+
+    ref = run(lambda *a: _ref_hidden(a[0], a[1:], 4.5, 5), r, W1, W2, W3, u, rho)
+    out = run(lambda *a: radial_hidden(a[0], *a[1:], 4.5, 5, mo.SILU), *got[:5], got[6])
+    for a, b in zip(out, ref):
+        assert rel_err(a, b) < 1e-5
