@@ -823,6 +823,9 @@ __global__ __launch_bounds__(BWD_WAVES * 64) void mlp_bwd_kernel(
 //   d r    = (W1^T zb1') . R''(r) + (W1^T zb1) . R'(r)
 //   d u    = rho t3.
 // s silu''(z) = s sig (1 - sig) (2 + z (1 - 2 sig)).
+// With v (nullable), the cotangent of a3 itself, zb3 also takes v . sl3: the
+// first adjoint's chain runs along the unprimed one, so one pass returns the sum
+// of both derivatives.  Without dr only d u is written.
 // The weight-gradient rows go to [2E, 64] arrays (primed rows 0..E-1, unprimed
 // rows E..2E-1; the radial rows [2E, 8]), so that each d W_k is one product
 // zrows^T arows over 2E rows.
@@ -842,7 +845,8 @@ __device__ __forceinline__ void act_dual(const v4f* z, const v4f* tz, float s, v
 __global__ __launch_bounds__(BWD2_WAVES * 64, 1) void mlp_bwd2_kernel(
     const float* __restrict__ r, int64_t E, float rc, int p, const float* __restrict__ W1,
     const float* __restrict__ W2, const float* __restrict__ W3, float s, const float* __restrict__ u,
-    const float* __restrict__ rho, float* __restrict__ dr, float* __restrict__ du, float* __restrict__ z3rows,
+    const float* __restrict__ rho, const float* __restrict__ v, float* __restrict__ dr, float* __restrict__ du,
+    float* __restrict__ z3rows,
     float* __restrict__ a2rows, float* __restrict__ z2rows, float* __restrict__ a1rows, float* __restrict__ z1rows,
     float* __restrict__ brows) {
   __shared__ FwdWeights wfs;
@@ -904,7 +908,8 @@ __global__ __launch_bounds__(BWD2_WAVES * 64, 1) void mlp_bwd2_kernel(
       for (int nb = 0; nb < 4; ++nb) a[nb] = rh * ta[nb];
       store_units(du, e, ok, a);
     }
-    // reverse through the tangent network
+    if (!dr) continue;   // d u only
+    // reverse through the tangent network (and, with v, the first adjoint for cotangent v on a3)
     load_units(u, e, ok, a);
     v4f zp[4], zu[4];
 #pragma unroll
@@ -912,6 +917,11 @@ __global__ __launch_bounds__(BWD2_WAVES * 64, 1) void mlp_bwd2_kernel(
       const v4f seed = rh * a[nb];
       zp[nb] = seed * sl3[nb];
       zu[nb] = seed * cv3[nb];
+    }
+    if (v) {
+      load_units(v, e, ok, a);
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) zu[nb] += a[nb] * sl3[nb];
     }
     if (rows) {
       store_units(z3rows, e, ok, zp);
@@ -1188,24 +1198,26 @@ int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden
 
 int ictc_radial_mlp_bwd2(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                          const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
-                         const float* rho, float* dr, float* dda3, float* z3rows, float* a2rows, float* z2rows,
-                         float* a1rows, float* z1rows, float* brows, void* stream) {
+                         const float* rho, const float* v, float* dr, float* dda3, float* z3rows, float* a2rows,
+                         float* z2rows, float* a1rows, float* z1rows, float* brows, void* stream) {
   if (num_basis != KB || hidden != H) return fail(ICTC_ERR_UNSUPPORTED, "fused radial MLP is compiled for 8 -> 64");
   if (edges < 0 || !(cutoff > 0.f) || poly_p < 2) return fail(ICTC_ERR_ARGUMENT, "radial MLP: invalid arguments");
   if (edges == 0) return ICTC_OK;
-  if (!r || !W1 || !W2 || !W3 || !da3 || !rho || !dr) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
+  if (!r || !W1 || !W2 || !W3 || !da3 || !rho) return fail(ICTC_ERR_ARGUMENT, "radial MLP: null operand");
+  if (!dr && (!dda3 || v || z3rows || a2rows || z2rows || a1rows || z1rows || brows))
+    return fail(ICTC_ERR_ARGUMENT, "radial MLP: without dr only dda3 is written");
   const float* rows[] = {z3rows, a2rows, z2rows, a1rows, z1rows, brows};
   const bool any = z3rows || a2rows || z2rows || a1rows || z1rows || brows;
   for (const float* q : rows)
     if (any && !q) return fail(ICTC_ERR_ARGUMENT, "radial MLP: weight-gradient rows are all given or all null");
-  for (const float* q : {da3, (const float*)dda3, (const float*)z3rows, (const float*)a2rows, (const float*)z2rows,
+  for (const float* q : {da3, v, (const float*)dda3, (const float*)z3rows, (const float*)a2rows, (const float*)z2rows,
                          (const float*)a1rows, (const float*)z1rows})
     if (q && !aligned16(q)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: [E, 64] operands must be 16-byte aligned");
   if (brows && (reinterpret_cast<uintptr_t>(brows) & 7))
     return fail(ICTC_ERR_ARGUMENT, "radial MLP: radial rows must be 8-byte aligned");
   const int per_cu = resident_per_cu(mlp_bwd2_kernel, BWD2_WAVES * 64, 1);
   hipLaunchKernelGGL(mlp_bwd2_kernel, dim3(grid_for(edges, BWD2_WAVES, per_cu)), dim3(BWD2_WAVES * 64), 0,
-                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, rho, dr, dda3,
+                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, rho, v, dr, dda3,
                      z3rows, a2rows, z2rows, a1rows, z1rows, brows);
   return launch_status("ictc_radial_mlp_bwd2 launch");
 }

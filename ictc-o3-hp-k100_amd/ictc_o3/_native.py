@@ -96,7 +96,7 @@ _SIGNATURES = {
     "ictc_radial_mlp_bwd": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p,
                                  _p, _p, _p, _p]),
     "ictc_radial_mlp_bwd2": (_i, [_p, _i64, _i, _i, ctypes.c_float, _i, _p, _p, _p, ctypes.c_float, _p, _p, _p, _p,
-                                  _p, _p, _p, _p, _p, _p, _p]),
+                                  _p, _p, _p, _p, _p, _p, _p, _p]),
     "ictc_sc_terms": (_i, [_i, _i, _i]),
     "ictc_sc_shape": (_i, [_i, _i, _i, _p, _p]),
     "ictc_sc_workspace_bytes": (_i64, [_i, _i, _i, _i, _i64, _i]),

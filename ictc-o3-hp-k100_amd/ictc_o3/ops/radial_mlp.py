@@ -354,11 +354,53 @@ def _hidden_adjoint(r, Ws, cfg, u, needs):
     return (dr if needs[0] else None), dW
 
 
+# Whether the derivative of the hidden layers' first adjoint (the force pass) hands its cotangent to the
+# forward node's first adjoint in the same backward pass, so that one kernel launch returns the sum of both
+# (ictc_radial_mlp_bwd2 with v); False = two launches added by autograd.
+LINK_HIDDEN = True
+
+
+def _hidden_second(r, Ws, cfg, u, rho, v, needs, want_du=False):
+    """ictc_radial_mlp_bwd2 for inputs (r, W1, W2, W3): (dr, [dW1, dW2, dW3]) of rho . d<u, a3>/dr, plus the
+    first adjoint for cotangent v (nullable) on a3; with want_du also d u = rho t3 (a third result)."""
+    cutoff, poly_p, scale = cfg
+    rc, uc, rh = _c(r.detach()), _c(u.detach()), _c(rho.detach())
+    vc = None if v is None else _c(v.detach())
+    W1, W2, W3 = (_c(w.detach()) for w in Ws)
+    E = rc.shape[0]
+    need_w = any(needs[1:4])
+    d_r = rc.new_empty(E)
+    rows = [rc.new_empty(2 * E, 64) for _ in range(5)] + [rc.new_empty(2 * E, 8)] if need_w else [None] * 6
+    z3, a2, z2, a1, z1, b = rows
+    d_u = rc.new_empty(E, 64) if want_du else None
+    nat.call("ictc_radial_mlp_bwd2", nat.ptr(rc), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(W1), nat.ptr(W2),
+             nat.ptr(W3), float(scale), nat.ptr(uc), nat.ptr(rh), nat.ptr(vc), nat.ptr(d_r), nat.ptr(d_u),
+             *[nat.ptr(t) for t in rows], nat.stream_of(rc))
+    dW = _hidden_weight_grads((z1, b, z2, a1, z3, a2), needs[1:4]) if need_w else [None] * 3
+    if want_du:
+        return (d_r if needs[0] else None), dW, d_u
+    return (d_r if needs[0] else None), dW
+
+
+def _hidden_tangent_cotangent(r, Ws, cfg, u, rho):
+    """d u = rho t3 alone (ictc_radial_mlp_bwd2 without dr)."""
+    cutoff, poly_p, scale = cfg
+    rc, uc, rh = _c(r.detach()), _c(u.detach()), _c(rho.detach())
+    W1, W2, W3 = (_c(w.detach()) for w in Ws)
+    d_u = rc.new_empty(rc.shape[0], 64)
+    nat.call("ictc_radial_mlp_bwd2", nat.ptr(rc), rc.shape[0], 8, 64, float(cutoff), int(poly_p), nat.ptr(W1),
+             nat.ptr(W2), nat.ptr(W3), float(scale), nat.ptr(uc), nat.ptr(rh), None, None, nat.ptr(d_u),
+             *([None] * 6), nat.stream_of(rc))
+    return d_u
+
+
 class _Hidden(torch.autograd.Function):
     @staticmethod
     def forward(ctx, r, W1, W2, W3, cutoff, poly_p, scale):
+        from ictc_o3.ops.tensor_product import _GateLink
         ctx.cfg = (cutoff, poly_p, scale)
         ctx.inputs = (r, W1, W2, W3)
+        ctx.link = _GateLink(ctx, "cotangent of the radial MLP's second derivative", lambda: LINK_HIDDEN)
         rc = _c(r.detach())
         Ws = [_c(w.detach()) for w in (W1, W2, W3)]
         h3 = rc.new_empty(rc.shape[0], 64)
@@ -370,14 +412,20 @@ class _Hidden(torch.autograd.Function):
     @staticmethod
     def backward(ctx, u):
         from ictc_o3.autograd import required_gradients
+        held = ctx.link.take()   # (u of the force pass, rho) the second derivative left for this pass
         r, W1, W2, W3 = ctx.saved_tensors
         needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:4]) if ctx.inputs else ctx.needs_input_grad[:4]
         ctx.inputs = None
-        if u is None or not any(needs):
+        if not any(needs):
+            return (None,) * 7
+        if held is not None:
+            dr, dW = _hidden_second(r, (W1, W2, W3), ctx.cfg, held[0], held[1], u, needs)
+            return (dr, *dW, None, None, None)
+        if u is None:
             return (None,) * 7
         if torch.is_grad_enabled():
             # differentiable adjoint (the force pass of a force-loss step)
-            out = _HiddenAdjoint.apply(r, W1, W2, W3, u, ctx.cfg, tuple(needs))
+            out = _HiddenAdjoint.apply(r, W1, W2, W3, u, ctx.cfg, tuple(needs), ctx.link)
             return (*out, None, None, None)
         dr, dW = _hidden_adjoint(r, (W1, W2, W3), ctx.cfg, u, needs)
         return (dr, *dW, None, None, None)
@@ -386,11 +434,12 @@ class _Hidden(torch.autograd.Function):
 class _HiddenAdjoint(torch.autograd.Function):
     """(dr, dW1, dW2, dW3) of radial_hidden for cotangent u, differentiable once more on the fused kernel
     (ictc_radial_mlp_bwd2: cotangents on dr only); cotangents on the weight gradients, or a backward that
-    itself builds a graph, go through _hidden_torch."""
+    itself builds a graph, go through _hidden_torch.  When the forward node's first adjoint runs later in
+    the same pass, the r and weight parts are left to it (one launch for both derivatives)."""
 
     @staticmethod
-    def forward(ctx, r, W1, W2, W3, u, cfg, needs):
-        ctx.cfg = cfg
+    def forward(ctx, r, W1, W2, W3, u, cfg, needs, link):
+        ctx.cfg, ctx.link = cfg, link
         ctx.inputs = (r, W1, W2, W3, u)
         ctx.save_for_backward(r, W1, W2, W3, u)
         dr, dW = _hidden_adjoint(r, (W1, W2, W3), cfg, u, needs)
@@ -402,25 +451,20 @@ class _HiddenAdjoint(torch.autograd.Function):
         r, W1, W2, W3, u = ctx.saved_tensors
         needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:5]) if ctx.inputs else ctx.needs_input_grad[:5]
         ctx.inputs = None
-        none = (None,) * 7
+        none = (None,) * 8
         if not any(needs) or (hr is None and h1 is None and h2 is None and h3 is None):
             return none
         if torch.is_grad_enabled() or h1 is not None or h2 is not None or h3 is not None:
-            return (*_hidden_adjoint_torch(ctx.cfg, (r, W1, W2, W3, u), (hr, h1, h2, h3), needs), None, None)
-        cutoff, poly_p, scale = ctx.cfg
-        rc, uc, hrc = _c(r.detach()), _c(u.detach()), _c(hr.detach())
-        Ws = [_c(w.detach()) for w in (W1, W2, W3)]
-        E = rc.shape[0]
-        need_w = any(needs[1:4])
-        d_r = rc.new_empty(E)
-        d_u = rc.new_empty(E, 64) if needs[4] else None
-        rows = [rc.new_empty(2 * E, 64) for _ in range(5)] + [rc.new_empty(2 * E, 8)] if need_w else [None] * 6
-        z3, a2, z2, a1, z1, b = rows
-        nat.call("ictc_radial_mlp_bwd2", nat.ptr(rc), E, 8, 64, float(cutoff), int(poly_p), nat.ptr(Ws[0]),
-                 nat.ptr(Ws[1]), nat.ptr(Ws[2]), float(scale), nat.ptr(uc), nat.ptr(hrc), nat.ptr(d_r),
-                 nat.ptr(d_u), *[nat.ptr(t) for t in rows], nat.stream_of(rc))
-        dW = _hidden_weight_grads((z1, b, z2, a1, z3, a2), needs[1:4]) if need_w else [None] * 3
-        return (d_r if needs[0] else None, *dW, d_u, None, None)
+            return (*_hidden_adjoint_torch(ctx.cfg, (r, W1, W2, W3, u), (hr, h1, h2, h3), needs), None, None, None)
+        Ws = (W1, W2, W3)
+        if any(needs[:4]) and ctx.link.can_hold():
+            ctx.link.hold((u, hr))
+            d_u = _hidden_tangent_cotangent(r, Ws, ctx.cfg, u, hr) if needs[4] else None
+            return (None, None, None, None, d_u, None, None, None)
+        if not any(needs[:4]):
+            return (None, None, None, None, _hidden_tangent_cotangent(r, Ws, ctx.cfg, u, hr), None, None, None)
+        dr, dW, d_u = _hidden_second(r, Ws, ctx.cfg, u, hr, None, needs, want_du=needs[4])
+        return (dr, *dW, d_u, None, None, None)
 
 
 def _hidden_adjoint_torch(cfg, saved, cotangents, needs):

@@ -532,16 +532,19 @@ class _GateLink:
     and that node has not run yet; a callback at the end of the pass raises if
     it was not taken, so a gradient is never dropped silently.
     """
-    __slots__ = ("node", "ran", "pending", "__weakref__")
+    __slots__ = ("node", "ran", "pending", "what", "enabled", "__weakref__")
 
-    def __init__(self, node):
+    def __init__(self, node, what="message gate gradient of the mixed second derivative",
+                 enabled=lambda: LINK_GATE_GRADIENTS):
         self.node = weakref.ref(node)
-        self.ran = None          # graph task in which the forward message's backward last ran
-        self.pending = None      # (graph task, gate gradient)
+        self.ran = None          # graph task in which the forward node's backward last ran
+        self.pending = None      # (graph task, held value)
+        self.what = what
+        self.enabled = enabled
 
     def can_hold(self):
         from torch.fx.experimental.proxy_tensor import get_proxy_mode
-        if (not LINK_GATE_GRADIENTS or torch.compiler.is_compiling() or get_proxy_mode() is not None
+        if (not self.enabled() or torch.compiler.is_compiling() or get_proxy_mode() is not None
                 or torch._C._are_functorch_transforms_active()
                 or not hasattr(torch._C, "_will_engine_execute_node")):
             return False
@@ -564,7 +567,7 @@ class _GateLink:
             link = ref()
             if link is not None and link.pending is not None and link.pending[0] == task:
                 link.pending = None
-                raise RuntimeError("message gate gradient of the mixed second derivative was not consumed")
+                raise RuntimeError(f"{link.what} was not consumed")
         torch.autograd.Variable._execution_engine.queue_callback(check)
 
     def take(self):

@@ -578,11 +578,14 @@ int ictc_radial_mlp_bwd(const float* r, int64_t edges, int num_basis, int hidden
  * rho t3 (nullable), and, when the six row arrays are given (all or none),
  * the rows whose products are the weight gradients over 2E rows:
  * d W3 = z3rows^T a2rows, d W2 = z2rows^T a1rows, d W1 = z1rows^T brows
- * (z/a rows [2E, 64] 16-byte aligned, brows [2E, 8] 8-byte aligned).       */
+ * (z/a rows [2E, 64] 16-byte aligned, brows [2E, 8] 8-byte aligned).  v
+ * [E, 64] (nullable) is a cotangent of a3 itself: dr_out and the rows then
+ * also carry ictc_radial_mlp_bwd's adjoint for da3 = v (the sum of both
+ * derivatives in one pass).  dr_out null: only dda3 is written.            */
 int ictc_radial_mlp_bwd2(const float* r, int64_t edges, int num_basis, int hidden, float cutoff, int poly_p,
                          const float* W1, const float* W2, const float* W3, float silu_scale, const float* da3,
-                         const float* rho, float* dr_out, float* dda3, float* z3rows, float* a2rows, float* z2rows,
-                         float* a1rows, float* z1rows, float* brows, void* stream);
+                         const float* rho, const float* v, float* dr_out, float* dda3, float* z3rows,
+                         float* a2rows, float* z2rows, float* a1rows, float* z1rows, float* brows, void* stream);
 
 /* ---- Symmetric contraction (bridge-U, correlation 1..3) -------------------
  * Replaces the SC circuits of ICTDBridgeUSymmetricContractionSO3.forward

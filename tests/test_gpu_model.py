@@ -94,14 +94,18 @@ def test_force_loss_gate_gradient_handoff(device):
 
     held = []
     hold = tpo._GateLink.hold
-    tpo._GateLink.hold = lambda self, dg: (held.append(dg.shape), hold(self, dg))[1]
+    tpo._GateLink.hold = lambda self, dg: (held.append(self.what), hold(self, dg))[1]
     try:
         with_handoff = grads()
     finally:
         tpo._GateLink.hold = hold
-    assert len(held) == len(model.interactions)
+    # one gate-gradient hand-off per message, one radial-MLP hand-off per interaction's hidden layers
+    # (the latter changes the summation order, so its parity is tested against float64 in
+    # test_gpu_radial_mlp; here only the message hand-off is switched off, which must be bitwise neutral)
+    assert sum(w.startswith("message") for w in held) == len(model.interactions)
+    assert sum(w.startswith("cotangent of the radial") for w in held) == len(model.interactions)
     can_hold = tpo._GateLink.can_hold
-    tpo._GateLink.can_hold = lambda self: False
+    tpo._GateLink.can_hold = lambda self: False if self.what.startswith("message") else can_hold(self)
     try:
         without = grads()
     finally:

@@ -104,11 +104,14 @@ def _force_loss_grads(hidden, r, W1, W2, W3, u, v, rho):
     return [h, dr, *torch.autograd.grad(loss, leaves)]
 
 
-@pytest.mark.parametrize("E", [1, 77, 4099, 40001])
-def test_radial_hidden_second_derivatives(device, E):
+@pytest.mark.parametrize("E,link", [(1, True), (77, True), (4099, True), (40001, True), (4099, False)])
+def test_radial_hidden_second_derivatives(device, monkeypatch, E, link):
     """radial_hidden: h3, the force-pass d/dr and the gradients of a force-loss-shaped objective (the
-    second-derivative kernel ictc_radial_mlp_bwd2 and the first adjoint) vs float64 autograd, 1e-5 relative."""
+    second-derivative kernel ictc_radial_mlp_bwd2 and the first adjoint; with link, both in one launch)
+    vs float64 autograd, 1e-5 relative."""
+    from ictc_o3.ops import radial_mlp
     from ictc_o3.ops.radial_mlp import radial_hidden
+    monkeypatch.setattr(radial_mlp, "LINK_HIDDEN", link)
     (r, W1, W2, W3, u, v, rho), got = _hidden_case(E, 100 + E, device)
     ref = _force_loss_grads(lambda *a: _ref_hidden(a[0], a[1:], 4.5, 5), r, W1, W2, W3, u, v, rho)
     out = _force_loss_grads(lambda *a: radial_hidden(a[0], *a[1:], 4.5, 5, mo.SILU), *got)
