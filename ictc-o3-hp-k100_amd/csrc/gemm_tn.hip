@@ -92,13 +92,34 @@ Plan plan_for(int64_t K, int M, int N) {
   return p;
 }
 
+// Operand addressing.  Dense row-major: element (r, c) at r * ldg + c.  With
+// STRIDED, rows are (group, member) pairs and columns (block, offset) pairs:
+// element (r, c) at (r / rg) * ldg + (r % rg) * ldr + (c / cg) * ldc + c % cg,
+// e.g. the (node, component) rows and (path, channel) columns of one degree of
+// a packed feature array.
+struct Layout {
+  int64_t ldg, ldr, ldc;
+  int rg, cg;
+};
+
+template <bool STRIDED>
+__device__ __forceinline__ int64_t col_offset(const Layout& L, int c) {
+  return STRIDED ? (int64_t)(c / L.cg) * L.ldc + c % L.cg : c;
+}
+template <bool STRIDED>
+__device__ __forceinline__ int64_t row_offset(const Layout& L, int64_t r) {
+  if (!STRIDED) return r * L.ldg;
+  const uint32_t u = (uint32_t)r, g = u / (uint32_t)L.rg;
+  return (int64_t)g * L.ldg + (int64_t)(u - g * (uint32_t)L.rg) * L.ldr;
+}
+
 __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+template <bool STRIDED>
 __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __restrict__ A, int64_t K, int M,
-                                                              int64_t lda, const float* __restrict__ B, int N,
-                                                              int64_t ldb, float* __restrict__ part, int mt,
+    Layout la, const float* __restrict__ B, int N, Layout lb, float* __restrict__ part, int mt,
                                                               int nt, int chunks, int64_t rows, int64_t blocks) {
   // Physical block p runs on XCD p % 8; give XCD x the logical range [x * per, (x + 1) * per).
   const int64_t per = blocks / kXcds;
@@ -117,8 +138,8 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __res
   const int lane = t & 63, wave = t >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const bool a_col = m0 + col < M, b_col = n0 + col < N;
-  const float* __restrict__ Ap = A + m0 + col;
-  const float* __restrict__ Bp = B + n0 + col;
+  const float* __restrict__ Ap = A + (a_col ? col_offset<STRIDED>(la, m0 + col) : 0);
+  const float* __restrict__ Bp = B + (b_col ? col_offset<STRIDED>(lb, n0 + col) : 0);
 
   float ra[4], rb[4];
   auto load = [&](int64_t k) {
@@ -126,8 +147,8 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __res
     for (int j = 0; j < 4; ++j) {
       const int64_t kr = k + r0 + 4 * j;
       const bool in = kr < k1;
-      ra[j] = (in && a_col) ? Ap[kr * lda] : 0.f;
-      rb[j] = (in && b_col) ? Bp[kr * ldb] : 0.f;
+      ra[j] = (in && a_col) ? Ap[row_offset<STRIDED>(la, kr)] : 0.f;
+      rb[j] = (in && b_col) ? Bp[row_offset<STRIDED>(lb, kr)] : 0.f;
     }
   };
 
@@ -172,9 +193,9 @@ __device__ __forceinline__ v4f mfma16(bf16x8 a, bf16x8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+template <bool STRIDED>
 __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* __restrict__ A, int64_t K, int M,
-                                                                   int64_t lda, const float* __restrict__ B, int N,
-                                                                   int64_t ldb, float* __restrict__ part, int mt,
+    Layout la, const float* __restrict__ B, int N, Layout lb, float* __restrict__ part, int mt,
                                                                    int nt, int chunks, int64_t rows, int64_t blocks) {
   const int64_t per = blocks / kXcds;
   const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
@@ -192,8 +213,8 @@ __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* 
   const int lane = t & 63, wave = t >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const bool a_col = m0 + col < M, b_col = n0 + col < N;
-  const float* __restrict__ Ap = A + m0 + col;
-  const float* __restrict__ Bp = B + n0 + col;
+  const float* __restrict__ Ap = A + (a_col ? col_offset<STRIDED>(la, m0 + col) : 0);
+  const float* __restrict__ Bp = B + (b_col ? col_offset<STRIDED>(lb, n0 + col) : 0);
 
   float ra[8], rb[8];
   auto load = [&](int64_t k) {
@@ -201,8 +222,8 @@ __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* 
     for (int e = 0; e < 8; ++e) {
       const int64_t kr = k + 8 * r0 + e;
       const bool in = kr < k1;
-      ra[e] = (in && a_col) ? Ap[kr * lda] : 0.f;
-      rb[e] = (in && b_col) ? Bp[kr * ldb] : 0.f;
+      ra[e] = (in && a_col) ? Ap[row_offset<STRIDED>(la, kr)] : 0.f;
+      rb[e] = (in && b_col) ? Bp[row_offset<STRIDED>(lb, kr)] : 0.f;
     }
   };
 
@@ -274,6 +295,41 @@ __global__ __launch_bounds__(64 * kSumWaves) void gemm_tn_sum_kernel(const float
   }
 }
 
+int gemm_tn_launch(const float* a, const Layout& la, int64_t k, int64_t m, const float* b, const Layout& lb,
+                   int64_t n, bool strided, float* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!out || (k > 0 && (!a || !b))) return fail(ICTC_ERR_ARGUMENT, "gemm_tn: null operand");
+  const Plan p = plan_for(k, (int)m, (int)n);
+  const int64_t need = (int64_t)p.chunks * m * n * (int64_t)sizeof(float);
+  if (!workspace || workspace_bytes < need)
+    return fail(ICTC_ERR_ARGUMENT, "gemm_tn: workspace smaller than ictc_gemm_tn_workspace_bytes");
+  float* part = static_cast<float*>(workspace);
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)p.blocks), block(256);
+  const bool wide = (int64_t)p.mt * p.nt > 16;
+  if (wide && strided)
+    hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel<true>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part,
+                       p.mt, p.nt, p.chunks, p.rows, p.blocks);
+  else if (wide)
+    hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel<false>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part,
+                       p.mt, p.nt, p.chunks, p.rows, p.blocks);
+  else if (strided)
+    hipLaunchKernelGGL(gemm_tn_partial_kernel<true>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part, p.mt,
+                       p.nt, p.chunks, p.rows, p.blocks);
+  else
+    hipLaunchKernelGGL(gemm_tn_partial_kernel<false>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part, p.mt,
+                       p.nt, p.chunks, p.rows, p.blocks);
+  const int64_t total = m * n;
+  hipLaunchKernelGGL(gemm_tn_sum_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64 * kSumWaves), 0, st, part,
+                     total, p.chunks, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "ictc_gemm_tn launch: %s", hipGetErrorString(e));
+    return fail(ICTC_ERR_RUNTIME, buf);
+  }
+  return ICTC_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -288,29 +344,19 @@ int ictc_gemm_tn(const float* a, int64_t k, int64_t m, int64_t lda, const float*
                  float* out, void* workspace, int64_t workspace_bytes, void* stream) {
   if (k < 0 || m <= 0 || n <= 0 || m > (1 << 20) || n > (1 << 20) || lda < m || ldb < n)
     return fail(ICTC_ERR_ARGUMENT, "gemm_tn: need k >= 0, 0 < m, n <= 2^20, lda >= m, ldb >= n");
-  if (!out || (k > 0 && (!a || !b))) return fail(ICTC_ERR_ARGUMENT, "gemm_tn: null operand");
-  const Plan p = plan_for(k, (int)m, (int)n);
-  const int64_t need = (int64_t)p.chunks * m * n * (int64_t)sizeof(float);
-  if (!workspace || workspace_bytes < need)
-    return fail(ICTC_ERR_ARGUMENT, "gemm_tn: workspace smaller than ictc_gemm_tn_workspace_bytes");
-  float* part = static_cast<float*>(workspace);
-  hipStream_t st = (hipStream_t)stream;
-  if ((int64_t)p.mt * p.nt > 16)
-    hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel, dim3((unsigned)p.blocks), dim3(256), 0, st, a, k, (int)m, lda, b,
-                       (int)n, ldb, part, p.mt, p.nt, p.chunks, p.rows, p.blocks);
-  else
-    hipLaunchKernelGGL(gemm_tn_partial_kernel, dim3((unsigned)p.blocks), dim3(256), 0, st, a, k, (int)m, lda, b,
-                       (int)n, ldb, part, p.mt, p.nt, p.chunks, p.rows, p.blocks);
-  const int64_t total = m * n;
-  hipLaunchKernelGGL(gemm_tn_sum_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64 * kSumWaves), 0, st, part,
-                     total, p.chunks, out);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    char buf[256];
-    snprintf(buf, sizeof(buf), "ictc_gemm_tn launch: %s", hipGetErrorString(e));
-    return fail(ICTC_ERR_RUNTIME, buf);
-  }
-  return ICTC_OK;
+  const Layout la{lda, 0, 0, 1, 1 << 30}, lb{ldb, 0, 0, 1, 1 << 30};
+  return gemm_tn_launch(a, la, k, m, b, lb, n, false, out, workspace, workspace_bytes, stream);
+}
+
+int ictc_gemm_tn_grouped(const float* a, int64_t a_ldg, int64_t a_ldr, int a_cg, int64_t a_ldc, const float* b,
+                         int64_t b_ldg, int64_t b_ldr, int b_cg, int64_t b_ldc, int64_t groups, int rows_per_group,
+                         int64_t m, int64_t n, float* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int64_t k = groups * (int64_t)rows_per_group;
+  if (groups < 0 || rows_per_group <= 0 || m <= 0 || n <= 0 || m > (1 << 20) || n > (1 << 20) || a_cg <= 0 ||
+      b_cg <= 0 || k >= ((int64_t)1 << 31))
+    return fail(ICTC_ERR_ARGUMENT, "gemm_tn_grouped: invalid sizes (rows below 2^31, 0 < m, n <= 2^20)");
+  const Layout la{a_ldg, a_ldr, a_ldc, rows_per_group, a_cg}, lb{b_ldg, b_ldr, b_ldc, rows_per_group, b_cg};
+  return gemm_tn_launch(a, la, k, m, b, lb, n, true, out, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

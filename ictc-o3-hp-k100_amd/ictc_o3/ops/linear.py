@@ -331,17 +331,39 @@ class _PackedLinearAny(torch.autograd.Function):
             layout_t = (lmax, Co, Ci, pout, out_off, pin, in_off, scales, x.shape[1])
             dx = _PackedLinearAny.apply(dout, layout_t, *[w.t() for w in ws])
         N, dws = x.shape[0], []
+        direct = not torch.is_grad_enabled() and x.is_cuda and x.dtype == dout.dtype == torch.float32
         for l, need in enumerate(needs[1:]):
             if not need:
                 dws.append(None)
                 continue
             m = 2 * l + 1
+            if direct:
+                # no graph to build: the kernel reads the (node, component) rows of both blocks in place
+                dws.append(scales[l] * _degree_weight_grad(dout, out_off[l], pout[l], Co, x, in_off[l], pin[l],
+                                                           Ci, m))
+                continue
             xin = x[:, in_off[l]:in_off[l] + pin[l] * m * Ci].reshape(N, pin[l], m, Ci).transpose(1, 2) \
                 .reshape(N * m, pin[l] * Ci)
             dl = dout[:, out_off[l]:out_off[l] + pout[l] * m * Co].reshape(N, pout[l], m, Co).transpose(1, 2) \
                 .reshape(N * m, pout[l] * Co)
             dws.append(scales[l] * _WeightGrad.apply(dl, xin))
         return (dx, None, *dws)
+
+
+def _degree_weight_grad(dout, out_off, pout, Co, x, in_off, pin, Ci, m):
+    """dout_l^T x_l [pout Co, pin Ci] over the (node, component) rows of one degree's packed blocks
+    (ictc_gemm_tn_grouped), without rearranging them into [N m, paths C] copies."""
+    N = x.shape[0]
+    M, K = pout * Co, pin * Ci
+    out = x.new_empty(M, K)
+    ws_bytes = int(nat.lib().ictc_gemm_tn_workspace_bytes(N * m, M, K))
+    if ws_bytes < 0:
+        raise ValueError("degree weight gradient: unsupported shape")
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=x.device)
+    nat.call("ictc_gemm_tn_grouped", ctypes.c_void_p(dout.data_ptr() + 4 * out_off), dout.stride(0), Co, Co, m * Co,
+             ctypes.c_void_p(x.data_ptr() + 4 * in_off), x.stride(0), Ci, Ci, m * Ci, N, m, M, K, nat.ptr(out),
+             nat.ptr(ws), ws_bytes, nat.stream_of(x))
+    return out
 
 
 def degree_linear_any(x, weights, C, lmax, scale=1.0):

@@ -434,6 +434,20 @@ int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t
 int64_t ictc_gemm_tn_workspace_bytes(int64_t k, int64_t m, int64_t n);
 int ictc_gemm_tn(const float* a, int64_t k, int64_t m, int64_t lda, const float* b, int64_t n, int64_t ldb,
                  float* out, void* workspace, int64_t workspace_bytes, void* stream);
+/* ictc_gemm_tn over grouped rows and blocked columns, for the weight
+ * gradient of one degree of a packed channel linear (the per-degree
+ * dW_l = dout_l^T x_l of EquivariantChannelLinearSO3 / the path-preserving
+ * linear, ictd_irreps.py:207-227, in the force-loss training step): the k =
+ * groups * rows_per_group rows are (group g, member i) pairs and an operand's
+ * element (row (g, i), column c) is at
+ *   p[g * ldg + i * ldr + (c / cg) * ldc + c % cg]
+ * (for a packed [N, paths, 2l+1, C] block: g the node, i the component, c =
+ * (path, channel), ldr = C, cg = C, ldc = (2l+1) C).  Same arithmetic and
+ * workspace (ictc_gemm_tn_workspace_bytes(groups * rows_per_group, m, n)) as
+ * ictc_gemm_tn; k below 2^31.                                                 */
+int ictc_gemm_tn_grouped(const float* a, int64_t a_ldg, int64_t a_ldr, int a_cg, int64_t a_ldc, const float* b,
+                         int64_t b_ldg, int64_t b_ldr, int b_cg, int64_t b_ldc, int64_t groups, int rows_per_group,
+                         int64_t m, int64_t n, float* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- Periodic radius graph ---------------------------------------------------
  * Replaces the host neighbour search the reference delegates to ASE / matscipy
