@@ -106,13 +106,6 @@ template <bool STRIDED>
 __device__ __forceinline__ int64_t col_offset(const Layout& L, int c) {
   return STRIDED ? (int64_t)(c / L.cg) * L.ldc + c % L.cg : c;
 }
-template <bool STRIDED>
-__device__ __forceinline__ int64_t row_offset(const Layout& L, int64_t r) {
-  if (!STRIDED) return r * L.ldg;
-  const uint32_t u = (uint32_t)r, g = u / (uint32_t)L.rg;
-  return (int64_t)g * L.ldg + (int64_t)(u - g * (uint32_t)L.rg) * L.ldr;
-}
-
 __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -143,12 +136,28 @@ __global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __res
 
   float ra[4], rb[4];
   auto load = [&](int64_t k) {
+    // grouped rows: one division for the first row, then (group, member) steps (both operands share rg)
+    uint32_t g = 0, i = 0;
+    if (STRIDED) {
+      const uint32_t u = (uint32_t)(k + r0);
+      g = u / (uint32_t)la.rg;
+      i = u - g * (uint32_t)la.rg;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int64_t kr = k + r0 + 4 * j;
       const bool in = kr < k1;
-      ra[j] = (in && a_col) ? Ap[row_offset<STRIDED>(la, kr)] : 0.f;
-      rb[j] = (in && b_col) ? Bp[row_offset<STRIDED>(lb, kr)] : 0.f;
+      const int64_t oa = STRIDED ? (int64_t)g * la.ldg + (int64_t)i * la.ldr : kr * la.ldg;
+      const int64_t ob = STRIDED ? (int64_t)g * lb.ldg + (int64_t)i * lb.ldr : kr * lb.ldg;
+      ra[j] = (in && a_col) ? Ap[oa] : 0.f;
+      rb[j] = (in && b_col) ? Bp[ob] : 0.f;
+      if (STRIDED) {
+        i += 4;
+        while (i >= (uint32_t)la.rg) {
+          i -= (uint32_t)la.rg;
+          ++g;
+        }
+      }
     }
   };
 
@@ -218,12 +227,25 @@ __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* 
 
   float ra[8], rb[8];
   auto load = [&](int64_t k) {
+    // grouped rows: one division for the first row, then (group, member) steps (both operands share rg)
+    uint32_t g = 0, i = 0;
+    if (STRIDED) {
+      const uint32_t u = (uint32_t)(k + 8 * r0);
+      g = u / (uint32_t)la.rg;
+      i = u - g * (uint32_t)la.rg;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int64_t kr = k + 8 * r0 + e;
       const bool in = kr < k1;
-      ra[e] = (in && a_col) ? Ap[row_offset<STRIDED>(la, kr)] : 0.f;
-      rb[e] = (in && b_col) ? Bp[row_offset<STRIDED>(lb, kr)] : 0.f;
+      const int64_t oa = STRIDED ? (int64_t)g * la.ldg + (int64_t)i * la.ldr : kr * la.ldg;
+      const int64_t ob = STRIDED ? (int64_t)g * lb.ldg + (int64_t)i * lb.ldr : kr * lb.ldg;
+      ra[e] = (in && a_col) ? Ap[oa] : 0.f;
+      rb[e] = (in && b_col) ? Bp[ob] : 0.f;
+      if (STRIDED && ++i == (uint32_t)la.rg) {
+        i = 0;
+        ++g;
+      }
     }
   };
 
