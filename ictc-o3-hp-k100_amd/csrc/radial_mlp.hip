@@ -393,10 +393,13 @@ __global__ __launch_bounds__(FWD_WAVES * 64) void mlp_fwd_kernel(const float* __
 
 // Forward with the forward-mode derivative along r: a3 and t3 = d a3 / dr,
 // both [E, 64] (the hidden state the fused radial-gate message projects).
+// With rho: t3 = rho[e] * d a3 / dr and no a3 (the d da3 of the second
+// derivative, ictc_radial_mlp_bwd2 without dr).
 __global__ __launch_bounds__(FWD_WAVES * 64, 3) void mlp_tan_kernel(const float* __restrict__ r, int64_t E, float rc,
                                                                  int p, const float* __restrict__ W1,
                                                                  const float* __restrict__ W2,
                                                                  const float* __restrict__ W3, float s,
+                                                                 const float* __restrict__ rho,
                                                                  float* __restrict__ a3, float* __restrict__ t3) {
   __shared__ FwdWeights ws;
   stage_fwd(ws, W1, W2, W3);
@@ -411,7 +414,13 @@ __global__ __launch_bounds__(FWD_WAVES * 64, 3) void mlp_tan_kernel(const float*
     const FwdWeights& w = *opaque(&ws);
     v4f a[4], tg[4];
     forward_tangent_tile(w, q, x, s, a, tg);
-    store_units(a3, e, ok, a);
+    if (rho) {
+      const float rh = ok ? rho[e] : 0.f;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) tg[nb] *= rh;
+    } else {
+      store_units(a3, e, ok, a);
+    }
     store_units(t3, e, ok, tg);
   }
 }
@@ -1111,7 +1120,7 @@ int ictc_radial_mlp_tangent_fwd(const float* r, int64_t edges, int num_basis, in
   if (!aligned16(a3) || !aligned16(t3)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: a3 and t3 must be 16-byte aligned");
   const int per_cu = resident_per_cu(mlp_tan_kernel, FWD_WAVES * 64, 3);
   hipLaunchKernelGGL(mlp_tan_kernel, dim3(grid_for(edges, FWD_WAVES, per_cu)), dim3(FWD_WAVES * 64), 0,
-                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, a3, t3);
+                     (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, nullptr, a3, t3);
   return launch_status("ictc_radial_mlp_tangent_fwd launch");
 }
 
@@ -1215,6 +1224,12 @@ int ictc_radial_mlp_bwd2(const float* r, int64_t edges, int num_basis, int hidde
     if (q && !aligned16(q)) return fail(ICTC_ERR_ARGUMENT, "radial MLP: [E, 64] operands must be 16-byte aligned");
   if (brows && (reinterpret_cast<uintptr_t>(brows) & 7))
     return fail(ICTC_ERR_ARGUMENT, "radial MLP: radial rows must be 8-byte aligned");
+  if (!dr) {   // d da3 = rho t3 alone: the forward-tangent kernel (3 blocks per CU)
+    const int tan_per_cu = resident_per_cu(mlp_tan_kernel, FWD_WAVES * 64, 3);
+    hipLaunchKernelGGL(mlp_tan_kernel, dim3(grid_for(edges, FWD_WAVES, tan_per_cu)), dim3(FWD_WAVES * 64), 0,
+                       (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, rho, nullptr, dda3);
+    return launch_status("ictc_radial_mlp_bwd2 launch");
+  }
   const int per_cu = resident_per_cu(mlp_bwd2_kernel, BWD2_WAVES * 64, 1);
   hipLaunchKernelGGL(mlp_bwd2_kernel, dim3(grid_for(edges, BWD2_WAVES, per_cu)), dim3(BWD2_WAVES * 64), 0,
                      (hipStream_t)stream, r, edges, cutoff, poly_p, W1, W2, W3, silu_scale, da3, rho, v, dr, dda3,
