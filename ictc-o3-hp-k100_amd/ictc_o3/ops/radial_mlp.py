@@ -7,9 +7,12 @@ hidden layers and the 64 -> P*C gate projection in one MFMA kernel (the hidden
 activations stay on chip); its adjoint runs the
 projection's hidden-layer adjoint on a second split-bf16 kernel and fuses the
 hidden-layer backward down to d/dr.  It supports first derivatives (forces,
-first-order parameter gradients); callers that need second derivatives
-(force-loss training) use the composable path ``radial_mlp``, whose Linears
-(``edge_linear``) take their weight gradients dW = dy^T x from a
+first-order parameter gradients).  Callers that need second derivatives
+(force-loss training) use ``radial_mlp_lengths``: the hidden layers through
+``radial_hidden`` (forward, first adjoint and its derivative on fused kernels,
+higher orders composed from torch operations) and the gate projection as an
+``edge_linear``.  ``radial_mlp`` is the fully composable form on a given radial
+basis.  The Linears take their weight gradients dW = dy^T x from a
 split-reduction MFMA kernel (``ictc_gemm_tn``) instead of a library GEMM that
 tiles only the small output.
 """

@@ -104,7 +104,7 @@ def _force_loss_grads(hidden, r, W1, W2, W3, u, v, rho):
     return [h, dr, *torch.autograd.grad(loss, leaves)]
 
 
-@pytest.mark.parametrize("E,link", [(1, True), (77, True), (4099, True), (40001, True), (4099, False)])
+@pytest.mark.parametrize("E,link", [(0, True), (1, True), (77, True), (4099, True), (40001, True), (4099, False)])
 def test_radial_hidden_second_derivatives(device, monkeypatch, E, link):
     """radial_hidden: h3, the force-pass d/dr and the gradients of a force-loss-shaped objective (the
     second-derivative kernel ictc_radial_mlp_bwd2 and the first adjoint; with link, both in one launch)
@@ -117,7 +117,11 @@ def test_radial_hidden_second_derivatives(device, monkeypatch, E, link):
     out = _force_loss_grads(lambda *a: radial_hidden(a[0], *a[1:], 4.5, 5, mo.SILU), *got)
     names = ["h3", "dr", "d/dr", "d/dW1", "d/dW2", "d/dW3", "d/du"]
     for name, a, b in zip(names, out, ref):
-        assert rel_err(a, b) < 1e-5, name
+        assert a.shape == b.shape, name
+        if b.numel() and b.abs().max() > 0:
+            assert rel_err(a, b) < 1e-5, name
+        else:   # no edges: empty per-edge outputs, zero weight gradients
+            assert a.numel() == 0 or bool((a == 0).all()), name
 
 
 def test_radial_hidden_other_orders(device):
