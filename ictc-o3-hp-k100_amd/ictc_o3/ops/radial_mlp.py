@@ -365,7 +365,7 @@ LINK_HIDDEN = True
 
 def _hidden_second(r, Ws, cfg, u, rho, v, needs, want_du=False):
     """ictc_radial_mlp_bwd2 for inputs (r, W1, W2, W3): (dr, [dW1, dW2, dW3]) of rho . d<u, a3>/dr, plus the
-    first adjoint for cotangent v (nullable) on a3; with want_du also d u = rho t3 (a third result)."""
+    first adjoint for cotangent v (nullable) on a3, and d u = rho t3 when want_du (else None)."""
     cutoff, poly_p, scale = cfg
     rc, uc, rh = _c(r.detach()), _c(u.detach()), _c(rho.detach())
     vc = None if v is None else _c(v.detach())
@@ -380,9 +380,7 @@ def _hidden_second(r, Ws, cfg, u, rho, v, needs, want_du=False):
              nat.ptr(W3), float(scale), nat.ptr(uc), nat.ptr(rh), nat.ptr(vc), nat.ptr(d_r), nat.ptr(d_u),
              *[nat.ptr(t) for t in rows], nat.stream_of(rc))
     dW = _hidden_weight_grads((z1, b, z2, a1, z3, a2), needs[1:4]) if need_w else [None] * 3
-    if want_du:
-        return (d_r if needs[0] else None), dW, d_u
-    return (d_r if needs[0] else None), dW
+    return (d_r if needs[0] else None), dW, d_u
 
 
 def _hidden_tangent_cotangent(r, Ws, cfg, u, rho):
@@ -402,7 +400,6 @@ class _Hidden(torch.autograd.Function):
     def forward(ctx, r, W1, W2, W3, cutoff, poly_p, scale):
         from ictc_o3.ops.tensor_product import _GateLink
         ctx.cfg = (cutoff, poly_p, scale)
-        ctx.inputs = (r, W1, W2, W3)
         ctx.link = _GateLink(ctx, "cotangent of the radial MLP's second derivative", lambda: LINK_HIDDEN)
         rc = _c(r.detach())
         Ws = [_c(w.detach()) for w in (W1, W2, W3)]
@@ -417,12 +414,12 @@ class _Hidden(torch.autograd.Function):
         from ictc_o3.autograd import required_gradients
         held = ctx.link.take()   # (u of the force pass, rho) the second derivative left for this pass
         r, W1, W2, W3 = ctx.saved_tensors
-        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:4]) if ctx.inputs else ctx.needs_input_grad[:4]
-        ctx.inputs = None
+        # asked of the engine for every pass (a retained graph runs the same route each time)
+        needs = required_gradients((r, W1, W2, W3), ctx.needs_input_grad[:4])
         if not any(needs):
             return (None,) * 7
         if held is not None:
-            dr, dW = _hidden_second(r, (W1, W2, W3), ctx.cfg, held[0], held[1], u, needs)
+            dr, dW, _ = _hidden_second(r, (W1, W2, W3), ctx.cfg, held[0], held[1], u, needs)
             return (dr, *dW, None, None, None)
         if u is None:
             return (None,) * 7
@@ -443,7 +440,6 @@ class _HiddenAdjoint(torch.autograd.Function):
     @staticmethod
     def forward(ctx, r, W1, W2, W3, u, cfg, needs, link):
         ctx.cfg, ctx.link = cfg, link
-        ctx.inputs = (r, W1, W2, W3, u)
         ctx.save_for_backward(r, W1, W2, W3, u)
         dr, dW = _hidden_adjoint(r, (W1, W2, W3), cfg, u, needs)
         return dr, *dW
@@ -452,8 +448,7 @@ class _HiddenAdjoint(torch.autograd.Function):
     def backward(ctx, hr, h1, h2, h3):
         from ictc_o3.autograd import required_gradients
         r, W1, W2, W3, u = ctx.saved_tensors
-        needs = required_gradients(ctx.inputs, ctx.needs_input_grad[:5]) if ctx.inputs else ctx.needs_input_grad[:5]
-        ctx.inputs = None
+        needs = required_gradients((r, W1, W2, W3, u), ctx.needs_input_grad[:5])
         none = (None,) * 8
         if not any(needs) or (hr is None and h1 is None and h2 is None and h3 is None):
             return none

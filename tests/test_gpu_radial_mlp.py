@@ -144,3 +144,32 @@ def test_radial_hidden_other_orders(device):
     out = run(lambda *a: radial_hidden(a[0], *a[1:], 4.5, 5, mo.SILU), *got[:5], got[6])
     for a, b in zip(out, ref):
         assert rel_err(a, b) < 1e-5
+
+
+@pytest.mark.parametrize("inputs", [(0, 1, 2, 3, 4), (0,), (2,), (4,), (1, 4)])
+def test_radial_hidden_link_partial_inputs_and_retained_graph(device, monkeypatch, inputs):
+    """The force-loss-shaped objective of radial_hidden differentiated for a subset of (r, W1, W2, W3, u) and
+    twice over one retained graph: float64 gradients (1e-5), the two passes bitwise equal, with the
+    second-derivative hand-off (LINK_HIDDEN) on and off."""
+    from ictc_o3.ops import radial_mlp
+    from ictc_o3.ops.radial_mlp import radial_hidden
+    (r, W1, W2, W3, u, v, rho), got_in = _hidden_case(2000, 8, device)
+
+    def objective(hidden, leaves, v, rho):
+        r, W1, W2, W3, u = leaves
+        h = hidden(r, W1, W2, W3)
+        (dr,) = torch.autograd.grad(h, r, u, create_graph=True)
+        return (v * h).sum() + (rho * dr).sum()
+
+    ref_leaves = [t.clone().requires_grad_(True) for t in (r, W1, W2, W3, u)]
+    L = objective(lambda *a: _ref_hidden(a[0], a[1:], 4.5, 5), ref_leaves, v, rho)
+    ref = torch.autograd.grad(L, [ref_leaves[k] for k in inputs])
+    for link in (True, False):
+        monkeypatch.setattr(radial_mlp, "LINK_HIDDEN", link)
+        leaves = [t.clone().requires_grad_(True) for t in got_in[:5]]
+        L = objective(lambda *a: radial_hidden(a[0], *a[1:], 4.5, 5, mo.SILU), leaves, got_in[5], got_in[6])
+        got = torch.autograd.grad(L, [leaves[k] for k in inputs], retain_graph=True)
+        again = torch.autograd.grad(L, [leaves[k] for k in inputs])
+        for g1, g2, want in zip(got, again, ref):
+            assert torch.equal(g1, g2)
+            assert rel_err(g1, want) < 1e-5
