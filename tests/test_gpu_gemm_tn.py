@@ -94,3 +94,58 @@ def test_edge_linear_derivatives(device):
     for o, r in zip(ours, ref):
         rel = float((o - r).norm() / r.norm())
         assert rel < 1e-5, rel
+
+
+def _grouped(device, a, b, groups, rg, a_cg, a_ldc, b_cg, b_ldc, M, N, a_off=0, b_off=0):
+    """ictc_gemm_tn_grouped on row-major a, b with (group, member) rows: element (g, i, c) at
+    g * stride(0) + i * (cg) + (c // cg) * ldc + c % cg, after an offset."""
+    import ctypes
+    from ictc_o3 import _native as nat
+    a, b = a.to(device), b.to(device)
+    out = torch.empty(M, N, device=device)
+    ws_bytes = int(nat.lib().ictc_gemm_tn_workspace_bytes(groups * rg, M, N))
+    ws = torch.empty(max(ws_bytes, 16) // 4, device=device)
+    nat.call("ictc_gemm_tn_grouped", ctypes.c_void_p(a.data_ptr() + 4 * a_off), a.stride(0), a_cg, a_cg, a_ldc,
+             ctypes.c_void_p(b.data_ptr() + 4 * b_off), b.stride(0), b_cg, b_cg, b_ldc, groups, rg, M, N,
+             nat.ptr(out), nat.ptr(ws), ws_bytes, nat.stream_of(a))
+    return out.double().cpu()
+
+
+def _blocks(x, groups, rg, cg, blocks, off):
+    """The [groups * rg, blocks * cg] operand a grouped call reads from x (rows (g, i), columns (block, c))."""
+    v = x[:, off:off + blocks * rg * cg].reshape(groups, blocks, rg, cg).transpose(1, 2)
+    return v.reshape(groups * rg, blocks * cg).double()
+
+
+@pytest.mark.parametrize("groups,rg,pa,pb,C", [(5000, 3, 1, 1, 64), (777, 5, 3, 1, 48), (3001, 1, 2, 5, 32),
+                                               (1200, 7, 1, 3, 128), (0, 3, 2, 2, 16)])
+def test_gemm_tn_grouped(device, groups, rg, pa, pb, C):
+    """ictc_gemm_tn_grouped against a float64 product of the rearranged blocks (the per-degree weight
+    gradient of a packed linear), elementwise bound 1e-5 * (|a|^T |b|); no groups writes zeros."""
+    g = torch.Generator().manual_seed(groups + rg + C)
+    a = torch.randn(groups, pa * rg * C + 13, generator=g)
+    b = torch.randn(groups, pb * rg * C + 7, generator=g)
+    A, B = _blocks(a, groups, rg, C, pa, 13), _blocks(b, groups, rg, C, pb, 7)
+    got = _grouped(device, a, b, groups, rg, C, rg * C, C, rg * C, pa * C, pb * C, a_off=13, b_off=7)
+    ref = A.t() @ B
+    bound = A.abs().t() @ B.abs()
+    assert got.shape == ref.shape
+    if groups == 0:
+        assert bool((got == 0).all())
+    else:
+        assert float(((got - ref).abs() / bound.clamp(min=1e-30)).max()) < 1e-5
+    # bitwise repeatable
+    assert torch.equal(got, _grouped(device, a, b, groups, rg, C, rg * C, C, rg * C, pa * C, pb * C, a_off=13,
+                                     b_off=7))
+
+
+def test_gemm_tn_grouped_rejects_bad_sizes(device):
+    import ctypes
+    from ictc_o3 import _native as nat
+    x = torch.zeros(4, 64, device=device)
+    with pytest.raises(ValueError):
+        nat.call("ictc_gemm_tn_grouped", nat.ptr(x), 64, 16, 0, 16, nat.ptr(x), 64, 16, 16, 16, 4, 1, 16, 16,
+                 nat.ptr(x), nat.ptr(x), 256, nat.stream_of(x))
+    with pytest.raises(ValueError):
+        nat.call("ictc_gemm_tn_grouped", nat.ptr(x), 64, 16, 16, 16, nat.ptr(x), 64, 16, 16, 16, 1 << 30, 4, 16, 16,
+                 nat.ptr(x), nat.ptr(x), 256, nat.stream_of(x))
