@@ -116,6 +116,33 @@ def test_force_loss_gate_gradient_handoff(device):
             assert torch.equal(a, b)
 
 
+def test_fused_hidden_matches_composed_radial_mlp(device, monkeypatch):
+    """Force-loss training gradients (every parameter, energies and forces) with the radial MLP's hidden layers
+    on the fused second-order kernels (radial_hidden) against the composed Linear / SiLU route, 1e-5."""
+    from ictc_o3.ops import tensor_product as tpo
+    from mace_ictc.hp import energy_and_forces
+    model, pos, Z, batch, cell, src, dst, sh = _setup(device, 6, 32, 2, 3, 4, cells=2)
+    g = torch.Generator().manual_seed(7)
+    E_t = torch.randn(2, generator=g).to(device)
+    F_t = (torch.randn(pos.shape, generator=g) * 0.5).to(device)
+    params = [p for p in model.parameters() if p.requires_grad]
+    args = (pos.float().to(device), Z.to(device), batch.to(device), src.to(device), dst.to(device),
+            sh.float().to(device), cell.float().to(device))
+
+    def run(fused):
+        monkeypatch.setattr(tpo, "FUSED_HIDDEN", fused)
+        out = energy_and_forces(model, *args, training=True)
+        loss = ((out["energy"] - E_t) ** 2).mean() + ((out["forces"] - F_t) ** 2).mean()
+        grads = torch.autograd.grad(loss, params, allow_unused=True)
+        return [out["energy"].detach(), out["forces"].detach()] + [gr for gr in grads]
+
+    fused, composed = run(True), run(False)
+    for a, b in zip(fused, composed):
+        assert (a is None) == (b is None)
+        if a is not None and b.abs().max() > 0:
+            assert rel_err(a, b) < 1e-5
+
+
 def test_configure_model_contract(device):
     from mace_ictc.hp import configure_model, create_model
     model = create_model(channels=8, lmax=2, device=device)
