@@ -164,3 +164,29 @@ def test_packed_linear_any_order(device, kind, C, lmax, N):
         assert rel_err(a, b) < 1e-5
     for a, b in zip(plain(fn, x.float().to(device), [w.float().to(device) for w in Ws]), d0):
         assert rel_err(a, b) < 1e-5
+
+
+@pytest.mark.parametrize("C,S,N", [(64, 3, 1000), (128, 10, 517), (16, 1, 33), (32, 4, 4096)])
+def test_species_linear(device, C, S, N):
+    """ictc_species_linear (out[n] = W[species[n]] x[n]): values, first derivatives (input and weights) and the
+    derivative of a first-derivative quantity against float64 autograd of the indexed product, 1e-5."""
+    from ictc_o3.ops.linear import species_linear
+    g = torch.Generator().manual_seed(C + S + N)
+    x64 = torch.randn(N, C, generator=g, dtype=torch.float64)
+    W64 = torch.randn(S, C, C, generator=g, dtype=torch.float64) / C ** 0.5
+    sp = torch.randint(0, S, (N,), generator=g)
+    go = torch.randn(N, C, generator=g, dtype=torch.float64)
+    v = torch.randn(N, C, generator=g, dtype=torch.float64)
+
+    def run(f, x, W, s):
+        x = x.clone().requires_grad_(True)
+        W = W.clone().requires_grad_(True)
+        out = f(x, W, s)
+        dx, dW = torch.autograd.grad(out, (x, W), go.to(out), create_graph=True)
+        gg = torch.autograd.grad((dx * v.to(dx)).sum() + (dW ** 2).sum(), (x, W))
+        return [out, dx, dW, *gg]
+
+    ref = run(lambda x, W, s: torch.einsum("noi,ni->no", W[s], x), x64, W64, sp)
+    got = run(species_linear, x64.float().to(device), W64.float().to(device), sp.to(device))
+    for a, b in zip(got, ref):
+        assert rel_err(a, b) < 1e-5
