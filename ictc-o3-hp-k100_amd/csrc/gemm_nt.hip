@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kSumThreads) void graph_sum_kernel(const float* __r
 // every species and their gather are never formed.  Reduction index b = (l / 16) * C / 4 + ks: each lane
 // reads one contiguous run of its node's row and of its weight row.  Species outside [0, S) give zero rows.
 template <int C, bool TRANS>
-__global__ __launch_bounds__(256) void species_linear_kernel(const float* __restrict__ x, int64_t N,
+__global__ __launch_bounds__(256) void species_linear_kernel(const float* __restrict__ x, int64_t ldx, int64_t N,
                                                              const float* __restrict__ W, int S,
                                                              const int64_t* __restrict__ species,
                                                              float* __restrict__ out) {
@@ -285,7 +285,7 @@ __global__ __launch_bounds__(256) void species_linear_kernel(const float* __rest
   const int64_t spv = ok ? species[n] : -1;
   const int sp = (spv >= 0 && spv < S) ? (int)spv : -1;
   float xa[KR];
-  const float* xp = x + (ok ? n : 0) * C + g * KR;
+  const float* xp = x + (ok ? n : 0) * ldx + g * KR;
 #pragma unroll
   for (int q = 0; q < KR / 4; ++q) {
     const float4 v = ok ? *reinterpret_cast<const float4*>(xp + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -337,13 +337,14 @@ __global__ __launch_bounds__(256) void species_linear_kernel(const float* __rest
 }
 
 template <int C>
-void species_linear_launch(const float* x, int64_t N, const float* W, int S, const int64_t* species, int trans,
-                           float* out, hipStream_t st) {
+void species_linear_launch(const float* x, int64_t ldx, int64_t N, const float* W, int S, const int64_t* species,
+                           int trans, float* out, hipStream_t st) {
   const unsigned grid = (unsigned)((N + 63) / 64);
   if (trans)
-    hipLaunchKernelGGL((species_linear_kernel<C, true>), dim3(grid), dim3(256), 0, st, x, N, W, S, species, out);
+    hipLaunchKernelGGL((species_linear_kernel<C, true>), dim3(grid), dim3(256), 0, st, x, ldx, N, W, S, species, out);
   else
-    hipLaunchKernelGGL((species_linear_kernel<C, false>), dim3(grid), dim3(256), 0, st, x, N, W, S, species, out);
+    hipLaunchKernelGGL((species_linear_kernel<C, false>), dim3(grid), dim3(256), 0, st, x, ldx, N, W, S, species,
+                       out);
 }
 
 int launch_status(const char* what) {
@@ -415,9 +416,10 @@ int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t
   return launch_status("ictc_graph_sum launch");
 }
 
-int ictc_species_linear(const float* x, int64_t nodes, int channels, const float* W, int species_count,
+int ictc_species_linear(const float* x, int64_t ldx, int64_t nodes, int channels, const float* W, int species_count,
                         const int64_t* species, int transpose, float* out, void* stream) {
-  if (nodes < 0 || species_count <= 0) return fail(ICTC_ERR_ARGUMENT, "species_linear: invalid sizes");
+  if (nodes < 0 || species_count <= 0 || ldx < channels || ldx % 4)
+    return fail(ICTC_ERR_ARGUMENT, "species_linear: invalid sizes (row pitch >= channels, a multiple of 4)");
   if (channels != 16 && channels != 32 && channels != 64 && channels != 128)
     return fail(ICTC_ERR_UNSUPPORTED, "species_linear: compiled for 16, 32, 64 and 128 channels");
   if (nodes == 0) return ICTC_OK;
@@ -426,10 +428,10 @@ int ictc_species_linear(const float* x, int64_t nodes, int channels, const float
     return fail(ICTC_ERR_ARGUMENT, "species_linear: x and W must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   switch (channels) {
-    case 16: species_linear_launch<16>(x, nodes, W, species_count, species, transpose, out, st); break;
-    case 32: species_linear_launch<32>(x, nodes, W, species_count, species, transpose, out, st); break;
-    case 64: species_linear_launch<64>(x, nodes, W, species_count, species, transpose, out, st); break;
-    default: species_linear_launch<128>(x, nodes, W, species_count, species, transpose, out, st); break;
+    case 16: species_linear_launch<16>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
+    case 32: species_linear_launch<32>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
+    case 64: species_linear_launch<64>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
+    default: species_linear_launch<128>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
   }
   return launch_status("ictc_species_linear launch");
 }

@@ -77,12 +77,14 @@ class _SpeciesLinear(torch.autograd.Function):
     def forward(ctx, x, W, species, trans):
         ctx.trans = trans
         ctx.save_for_backward(x, W, species)
-        xc = x.detach().contiguous()
+        xc = x.detach()
+        if xc.stride(1) != 1 or xc.stride(0) % 4 or xc.data_ptr() % 16:
+            xc = xc.contiguous()   # the kernel reads rows with a pitch (a column slice stays in place)
         Wc = W.detach().contiguous()
         sp = species.contiguous()
-        out = torch.empty_like(xc)
-        nat.call("ictc_species_linear", nat.ptr(xc), xc.shape[0], xc.shape[1], nat.ptr(Wc), Wc.shape[0],
-                 nat.ptr(sp), 1 if trans else 0, nat.ptr(out), nat.stream_of(xc))
+        out = xc.new_empty(xc.shape[0], xc.shape[1])
+        nat.call("ictc_species_linear", nat.ptr(xc), xc.stride(0), xc.shape[0], xc.shape[1], nat.ptr(Wc),
+                 Wc.shape[0], nat.ptr(sp), 1 if trans else 0, nat.ptr(out), nat.stream_of(xc))
         return out
 
     @staticmethod

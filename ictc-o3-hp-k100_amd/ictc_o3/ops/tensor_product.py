@@ -321,7 +321,8 @@ class Topology:
         self._rows_from = (positions.detach(), spacing) if positions is not None and nodes > 0 else None
         self._src_rows = self._dst_rows = None
         self._gate_rows = None    # int32 [E]: row of the shared radial gates each edge reads (pair_edges)
-        self._gate_reps = None    # int64 [rows]: the edge whose length fills each gate row
+        self._gate_reps = None    # int32 [rows]: the edge whose length fills each gate row
+        self._gate_input = None   # (lengths, their version, those of the gate rows): every layer reads them
         self._pending = None      # pairing launched, row count on its way to the host
         self._pairs_of = None
 
@@ -363,7 +364,7 @@ class Topology:
         event.synchronize()
         n = int(host[0])
         if n < E:
-            self._gate_rows, self._gate_reps = rows, reps[:n].long()
+            self._gate_rows, self._gate_reps = rows, reps[:n]
         if src_order is not None and int(host[1]) == 1 and self._by_src is None:
             # every edge paired one-to-one with its reverse: the source CSR shares the receiver CSR's ptr
             self._by_src = Csr.prebuilt(self.by_dst.ptr, src_order, self.nodes)
@@ -407,6 +408,7 @@ class Topology:
         E = self.src.numel()
         self._pending = None
         self._gate_rows = self._gate_reps = None
+        self._gate_input = None
         ws_bytes = int(nat.lib().ictc_edge_pairs_workspace_bytes(E))
         # pairing is an optimisation: graphs past its index range keep one gate row per edge
         if E > 0 and ws_bytes >= 0 and self.nodes < (1 << 31) - 2:
@@ -438,8 +440,22 @@ class Topology:
         self._pairs_of = (None if shifts is None else weakref.ref(shifts), key)
 
     def gate_input(self, r: torch.Tensor) -> torch.Tensor:
-        """The edge lengths of the gate rows (r itself when the rows are per edge)."""
-        return r if self.gate_reps is None else r.index_select(0, self.gate_reps)
+        """The edge lengths of the gate rows (r itself when the rows are per edge); the gather is kept for the
+        same lengths (the same storage at an unchanged version), which every layer of a step reads."""
+        if self.gate_reps is None:
+            return r
+        graph = torch.is_grad_enabled() and r.requires_grad
+        memo = self._gate_input
+        if not graph and memo is not None:
+            held, version, out = memo   # held keeps the storage alive, so its address is not reused
+            if (held.data_ptr() == r.data_ptr() and held.shape == r.shape and held.stride() == r.stride()
+                    and held.dtype == r.dtype and held.device == r.device and held._version == version):
+                return out
+        out = r.index_select(0, self.gate_reps)
+        if not graph:
+            held = r.detach()   # shares r's version counter: an in-place change invalidates the memo
+            self._gate_input = (held, held._version, out)
+        return out
 
     @property
     def by_src(self):

@@ -114,7 +114,17 @@ def test_pairing_matches_brute_force(device, case):
         assert topo.gate_rows is None
         return
     assert torch.equal(topo.gate_rows.long().cpu(), rows)
-    assert torch.equal(topo.gate_reps.cpu(), reps)
+    assert torch.equal(topo.gate_reps.long().cpu(), reps)
+    # gate_input: the lengths of the gate rows, the gather kept for the same (unchanged) lengths
+    r = torch.rand(src.numel(), device=device)
+    g1 = topo.gate_input(r)
+    assert torch.equal(g1.cpu(), r.cpu()[reps])
+    assert topo.gate_input(r.view_as(r)) is g1
+    r.mul_(2.0)                                   # an in-place change is seen
+    g2 = topo.gate_input(r)
+    assert g2 is not g1 and torch.equal(g2.cpu(), r.cpu()[reps])
+    other_r = torch.rand(src.numel(), device=device)
+    assert torch.equal(topo.gate_input(other_r).cpu(), other_r.cpu()[reps])
     # each row is its owner's; an edge reading another edge's row reads its reverse's
     assert torch.equal(rows[reps], torch.arange(reps.numel()))
     owner = reps[rows]
