@@ -229,6 +229,87 @@ __global__ __launch_bounds__(kBlock) void geometry_sh_bwd_kernel(const float* __
   for (int c = 0; c < 3; ++c) dvec[3 * e + c] = t[c];
 }
 
+// Unit vectors of given edge vectors (the second-order route, where vec is an autograd input):
+// r = |v|, n = v / max(r, eps); the first adjoint gv(v, gr, gn) as edge_adjoint_values; and that
+// adjoint's derivative for a cotangent h on gv: with P x = (x - (x . n) n) / r (r > eps)
+//   d gr = n . h,   d gn = P h,
+//   d v  = gr P h - ((h . n) P gn + (gn . n) P h) / r - (gn . h - (gn . n)(h . n)) n / r^2.
+// Below eps n = v / eps and gv = gr v / r + gn / eps: d gr = (v / r) . h, d gn = h / eps,
+// d v = gr (h - (h . u) u) / r with u = v / r (zero at r = 0).
+__global__ __launch_bounds__(kBlock) void unit_fwd_kernel(const float* __restrict__ v, int64_t E,
+                                                          float* __restrict__ r, float* __restrict__ n) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  const float x = v[3 * e], y = v[3 * e + 1], z = v[3 * e + 2];
+  const float len = sqrtf(x * x + y * y + z * z), den = fmaxf(len, kClamp);
+  r[e] = len;
+  n[3 * e] = x / den;
+  n[3 * e + 1] = y / den;
+  n[3 * e + 2] = z / den;
+}
+
+__global__ __launch_bounds__(kBlock) void unit_bwd_kernel(const float* __restrict__ r, const float* __restrict__ n,
+                                                          const float* __restrict__ gr, const float* __restrict__ gn,
+                                                          int64_t E, float* __restrict__ gv) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  const float a[3] = {gn ? gn[3 * e] : 0.f, gn ? gn[3 * e + 1] : 0.f, gn ? gn[3 * e + 2] : 0.f};
+  float out[3];
+  edge_adjoint_values(r[e], n[3 * e], n[3 * e + 1], n[3 * e + 2], gr ? gr[e] : 0.f, a, out);
+#pragma unroll
+  for (int c = 0; c < 3; ++c) gv[3 * e + c] = out[c];
+}
+
+__global__ __launch_bounds__(kBlock) void unit_bwd2_kernel(const float* __restrict__ r, const float* __restrict__ n,
+                                                           const float* __restrict__ gr, const float* __restrict__ gn,
+                                                           const float* __restrict__ h, int64_t E,
+                                                           float* __restrict__ dv, float* __restrict__ dgr,
+                                                           float* __restrict__ dgn) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= E) return;
+  const float len = r[e], g = gr ? gr[e] : 0.f;
+  const float nn[3] = {n[3 * e], n[3 * e + 1], n[3 * e + 2]};
+  const float hv[3] = {h[3 * e], h[3 * e + 1], h[3 * e + 2]};
+  const float a[3] = {gn ? gn[3 * e] : 0.f, gn ? gn[3 * e + 1] : 0.f, gn ? gn[3 * e + 2] : 0.f};
+  float o[3], ogn[3], ogr;
+  if (len > kClamp) {
+    const float inv = 1.f / len;
+    const float hn = hv[0] * nn[0] + hv[1] * nn[1] + hv[2] * nn[2];
+    const float an = a[0] * nn[0] + a[1] * nn[1] + a[2] * nn[2];
+    const float ah = a[0] * hv[0] + a[1] * hv[1] + a[2] * hv[2];
+    ogr = hn;
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+      const float ph = (hv[c] - hn * nn[c]) * inv;   // P h
+      const float pa = (a[c] - an * nn[c]) * inv;    // P gn
+      ogn[c] = ph;
+      o[c] = g * ph - (hn * pa + an * ph) * inv - (ah - an * hn) * nn[c] * inv * inv;
+    }
+  } else {
+    const float inv = 1.f / kClamp;
+    if (len > 0.f) {
+      // u = v / r = n * eps / r
+      const float s = kClamp / len, u[3] = {nn[0] * s, nn[1] * s, nn[2] * s};
+      const float hu = hv[0] * u[0] + hv[1] * u[1] + hv[2] * u[2];
+      ogr = hu;
+#pragma unroll
+      for (int c = 0; c < 3; ++c) o[c] = g * (hv[c] - hu * u[c]) / len;
+    } else {
+      ogr = 0.f;
+#pragma unroll
+      for (int c = 0; c < 3; ++c) o[c] = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) ogn[c] = hv[c] * inv;
+  }
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    if (dv) dv[3 * e + c] = o[c];
+    if (dgn) dgn[3 * e + c] = ogn[c];
+  }
+  if (dgr) dgr[e] = ogr;
+}
+
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
 
 int launch_status(const char* what) {
@@ -352,6 +433,25 @@ int ictc_edge_vector_bwd(const float* dvec, int64_t nodes, int64_t edges, const 
                      dim3(kBlock), 0, (hipStream_t)stream, nullptr, nullptr, nullptr, dvec, nodes, dst_ptr, dst_order,
                      src_ptr, src_order, nullptr, dpos);
   return launch_status("ictc_edge_vector_bwd launch");
+}
+
+int ictc_edge_unit(int order, const float* v, const float* r, const float* n, const float* gr, const float* gn,
+                   const float* h, int64_t edges, float* out0, float* out1, float* out2, void* stream) {
+  if (edges < 0 || order < 0 || order > 2) return fail(ICTC_ERR_ARGUMENT, "edge_unit: order 0..2, edges >= 0");
+  if (edges == 0) return ICTC_OK;
+  const dim3 grid((unsigned)((edges + kBlock - 1) / kBlock));
+  hipStream_t st = (hipStream_t)stream;
+  if (order == 0) {
+    if (!v || !out0 || !out1) return fail(ICTC_ERR_ARGUMENT, "edge_unit: null operand");
+    hipLaunchKernelGGL(unit_fwd_kernel, grid, dim3(kBlock), 0, st, v, edges, out0, out1);
+  } else if (order == 1) {
+    if (!r || !n || !out0) return fail(ICTC_ERR_ARGUMENT, "edge_unit: null operand");
+    hipLaunchKernelGGL(unit_bwd_kernel, grid, dim3(kBlock), 0, st, r, n, gr, gn, edges, out0);
+  } else {
+    if (!r || !n || !h) return fail(ICTC_ERR_ARGUMENT, "edge_unit: null operand");
+    hipLaunchKernelGGL(unit_bwd2_kernel, grid, dim3(kBlock), 0, st, r, n, gr, gn, h, edges, out0, out1, out2);
+  }
+  return launch_status("ictc_edge_unit launch");
 }
 
 }  // extern "C"

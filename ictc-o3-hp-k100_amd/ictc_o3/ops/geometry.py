@@ -193,3 +193,85 @@ def shift_vectors(shifts: torch.Tensor, cell: torch.Tensor, batch: torch.Tensor 
     nat.call("ictc_shift_vectors", nat.ptr(shifts), E, nat.ptr(cells), G, nat.ptr(batch) if G > 1 else None,
              nat.ptr(src) if G > 1 else None, nodes, nat.ptr(out), nat.stream_of(shifts))
     return out
+
+
+def _unit(order, v=None, r=None, n=None, gr=None, gn=None, h=None, outs=()):
+    E = (v if v is not None else r).shape[0]
+    nat.call("ictc_edge_unit", order, nat.ptr(v), nat.ptr(r), nat.ptr(n), nat.ptr(gr), nat.ptr(gn), nat.ptr(h), E,
+             *[nat.ptr(t) for t in outs], *([None] * (3 - len(outs))), nat.stream_of(v if v is not None else r))
+
+
+def _edge_unit_torch(vec):
+    r = vec.norm(dim=1)
+    return r, vec / r.clamp(min=1e-8).unsqueeze(-1)
+
+
+class _EdgeUnit(torch.autograd.Function):
+    """(r, n) = (|v|, v / max(|v|, 1e-8)) of edge vectors; the adjoint is _EdgeUnitAdjoint."""
+
+    @staticmethod
+    def forward(ctx, vec):
+        v = _c(vec.detach())
+        r, n = v.new_empty(v.shape[0]), torch.empty_like(v)
+        _unit(0, v=v, outs=(r, n))
+        ctx.save_for_backward(vec, r, n)
+        return r, n
+
+    @staticmethod
+    def backward(ctx, gr, gn):
+        vec, r, n = ctx.saved_tensors
+        if gr is None and gn is None:
+            return None
+        return _EdgeUnitAdjoint.apply(vec, r, n, gr, gn)
+
+
+class _EdgeUnitAdjoint(torch.autograd.Function):
+    """gv(v, gr, gn) = gr n + (gn - (gn . n) n) / r, differentiable once more on ictc_edge_unit (order 2) and
+    to higher orders through the composed torch form."""
+
+    @staticmethod
+    def forward(ctx, vec, r, n, gr, gn):
+        grc = None if gr is None else _c(gr.detach())
+        gnc = None if gn is None else _c(gn.detach())
+        gv = torch.empty_like(n)
+        _unit(1, r=r, n=n, gr=grc, gn=gnc, outs=(gv,))
+        ctx.save_for_backward(vec, r, n, gr, gn)
+        return gv
+
+    @staticmethod
+    def backward(ctx, h):
+        vec, r, n, gr, gn = ctx.saved_tensors
+        need_v, _, _, need_gr, need_gn = ctx.needs_input_grad
+        if h is None:
+            return None, None, None, None, None
+        if torch.is_grad_enabled():
+            return _edge_unit_adjoint_torch(vec, gr, gn, h, (need_v, need_gr, need_gn))
+        dv = torch.empty_like(n) if need_v else None
+        dgr = r.new_empty(r.shape[0]) if need_gr and gr is not None else None
+        dgn = torch.empty_like(n) if need_gn and gn is not None else None
+        _unit(2, r=r, n=n, gr=None if gr is None else _c(gr.detach()), gn=None if gn is None else _c(gn.detach()),
+              h=_c(h), outs=(dv, dgr, dgn))
+        return dv, None, None, dgr, dgn
+
+
+def _edge_unit_adjoint_torch(vec, gr, gn, h, needs):
+    """Derivative of the adjoint on the composed form, keeping the graph (third and higher orders)."""
+    inputs = [t if t is not None and t.requires_grad else (None if t is None else t.detach().requires_grad_(True))
+              for t in (vec, gr, gn)]
+    v, g1, g2 = inputs
+    with torch.enable_grad():
+        r, n = _edge_unit_torch(v)
+        outs = [(o, c) for o, c in ((r, g1), (n, g2)) if c is not None]
+        (gv,) = torch.autograd.grad([o for o, _ in outs], v, [c for _, c in outs], create_graph=True)
+        wanted = [t for t, need in zip(inputs, needs) if need and t is not None]
+        got = iter(torch.autograd.grad(gv, wanted, h, create_graph=True, allow_unused=True))
+    dv, dgr, dgn = (next(got) if need and t is not None else None for t, need in zip(inputs, needs))
+    return dv, None, None, dgr, dgn
+
+
+def edge_unit(vec: torch.Tensor):
+    """(r [E], n [E, 3]) = (|vec|, vec / max(|vec|, 1e-8)) with first and second derivatives on ictc_edge_unit
+    (float32 on the device); other inputs, and a third derivative, through the composed torch form."""
+    if not (vec.is_cuda and vec.dtype == torch.float32 and vec.dim() == 2 and vec.shape[1] == 3):
+        return _edge_unit_torch(vec)
+    return _EdgeUnit.apply(vec)

@@ -377,8 +377,8 @@ class PureCartesianICTDFix(nn.Module):
                 vec = edge_vectors(pos, shift_vec, topology)
             else:
                 vec = pos[edge_dst] - pos[edge_src] + shift_vec
-            r = vec.norm(dim=1)
-            n = vec / r.clamp(min=1e-8).unsqueeze(-1)
+            from ictc_o3.ops.geometry import edge_unit
+            r, n = edge_unit(vec)   # r = |vec|, n = vec / max(r, 1e-8), derivatives to any order
             mask = (r <= self.max_radius).to(pos.dtype)
             Y = harmonics_packed(n, self.ictd_fix_edge_lmax)
         else:

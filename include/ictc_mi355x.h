@@ -512,6 +512,15 @@ int ictc_edge_harmonics_fwd(const float* pos, const float* shift, const int64_t*
 int ictc_edge_harmonics_bwd(const float* r, const float* n, const float* dr, const float* dY, const float* dr2,
                             const float* dY2, int64_t edges, int lmax, float* dvec, void* stream);
 
+/* Unit vectors of edge vectors that are themselves autograd inputs (the
+ * second-order route of pure_cartesian_ictd_layers.py:1288-1297, where the
+ * reference composes norm and division): order 0: v [E, 3] -> out0 = r [E],
+ * out1 = n [E, 3] (n = v / max(r, 1e-8)); order 1: the adjoint out0 = gv
+ * [E, 3] from r, n and the cotangents gr [E], gn [E, 3] (either nullable);
+ * order 2: that adjoint's derivative for a cotangent h [E, 3] on gv:
+ * out0 = d v, out1 = d gr, out2 = d gn (each nullable).                      */
+int ictc_edge_unit(int order, const float* v, const float* r, const float* n, const float* gr, const float* gn,
+                   const float* h, int64_t edges, float* out0, float* out1, float* out2, void* stream);
 /* Cartesian image shifts of the edges, replacing `edge_shifts @ cell[batch[src]]`
  * (backbone.py:940-944, the shift term of vec): out [E,3] = shifts [E,3] (lattice
  * coordinates) times the 3x3 cell (rows = lattice vectors) of the edge's graph,

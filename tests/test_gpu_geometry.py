@@ -210,3 +210,48 @@ def test_edge_harmonics_two_consumers(device, lmax, cot):
 
     a, b = run(True), run(False)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_edge_unit_derivatives(device):
+    """edge_unit (r, n of edge vectors that are autograd inputs, ictc_edge_unit): values, the adjoint, its
+    derivative (the force-loss second order) and a third derivative (composed form) against float64 autograd of
+    norm and clamped division, 1e-5; vectors below the clamp and a zero vector included."""
+    from ictc_o3.ops.geometry import edge_unit
+    g = torch.Generator().manual_seed(11)
+    v64 = torch.randn(3000, 3, generator=g, dtype=torch.float64) * 2
+    v64[:5] *= 1e-9          # below the 1e-8 clamp
+    v64[5] = 0.0
+    gr = torch.randn(3000, generator=g, dtype=torch.float64)
+    gn = torch.randn(3000, 3, generator=g, dtype=torch.float64)
+    h = torch.randn(3000, 3, generator=g, dtype=torch.float64)
+    w = torch.randn(3000, 3, generator=g, dtype=torch.float64)
+
+    def ref_unit(v):
+        r = v.norm(dim=1)
+        return r, v / r.clamp(min=1e-8).unsqueeze(-1)
+
+    def run(f, v, gr, gn, h, w, third):
+        v = v.clone().requires_grad_(True)
+        gr = gr.clone().requires_grad_(True)
+        gn = gn.clone().requires_grad_(True)
+        r, n = f(v)
+        (gv,) = torch.autograd.grad((r, n), v, (gr, gn), create_graph=True)
+        # without a graph the second derivative runs on the kernel (order 2); with one, on the composed form
+        d2 = torch.autograd.grad(gv, (v, gr, gn), h, create_graph=third)
+        if not third:
+            return [r, n, gv, *d2]
+        (d3,) = torch.autograd.grad(d2[0], v, w)
+        return [d3]
+
+    ok = slice(6, None)   # derivatives of the clamped branch are compared on the regular edges only
+    for third in (False, True):
+        ref = run(ref_unit, v64, gr, gn, h, w, third)
+        got = run(edge_unit, *[t.float().to(device) for t in (v64, gr, gn, h, w)], third)
+        for k, (a, b) in enumerate(zip(got, ref)):
+            assert rel_err(a[ok], b[ok]) < 1e-5, (third, k)
+        if not third:
+            # below the clamp: r and n exact forms, and finite first and second derivatives on the kernel
+            assert torch.equal(got[0][5].cpu(), torch.tensor(0.0))
+            assert torch.equal(got[1][5].cpu(), torch.zeros(3))
+            for t in got:
+                assert bool(torch.isfinite(t).all())
