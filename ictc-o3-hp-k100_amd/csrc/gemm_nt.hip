@@ -264,89 +264,6 @@ __global__ __launch_bounds__(kSumThreads) void graph_sum_kernel(const float* __r
   if (threadIdx.x == 0) out[b] = part[0];
 }
 
-// Element-conditioned self connection (layers.py:21-87): out[n, a] = sum_b M_s[a][b] x[n, b] with s =
-// species[n] and M_s = W[s] ([C, C], output by input) or its transpose (TRANS: the input adjoint).  A wave
-// takes 16 nodes; for each species present among them (wave-uniform loop, a ballot skips the others) it runs
-// the C x C product on FP32 MFMA with the other species' rows masked to zero, so the [N, S C] products of
-// every species and their gather are never formed.  Reduction index b = (l / 16) * C / 4 + ks: each lane
-// reads one contiguous run of its node's row and of its weight row.  Species outside [0, S) give zero rows.
-template <int C, bool TRANS>
-__global__ __launch_bounds__(256) void species_linear_kernel(const float* __restrict__ x, int64_t ldx, int64_t N,
-                                                             const float* __restrict__ W, int S,
-                                                             const int64_t* __restrict__ species,
-                                                             float* __restrict__ out) {
-  constexpr int KR = C / 4;    // reduction terms per lane
-  constexpr int NB = C / 16;   // 16-column output blocks
-  const int l = threadIdx.x & 63, li = l & 15, g = l >> 4;
-  const int64_t n0 = 16 * ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6));
-  if (n0 >= N) return;
-  const int64_t n = n0 + li;
-  const bool ok = n < N;
-  const int64_t spv = ok ? species[n] : -1;
-  const int sp = (spv >= 0 && spv < S) ? (int)spv : -1;
-  float xa[KR];
-  const float* xp = x + (ok ? n : 0) * ldx + g * KR;
-#pragma unroll
-  for (int q = 0; q < KR / 4; ++q) {
-    const float4 v = ok ? *reinterpret_cast<const float4*>(xp + 4 * q) : make_float4(0.f, 0.f, 0.f, 0.f);
-    xa[4 * q] = v.x;
-    xa[4 * q + 1] = v.y;
-    xa[4 * q + 2] = v.z;
-    xa[4 * q + 3] = v.w;
-  }
-  v4f acc[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) acc[nb] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < S; ++s) {
-    if (!__any(sp == s)) continue;
-    float xm[KR];
-#pragma unroll
-    for (int ks = 0; ks < KR; ++ks) xm[ks] = sp == s ? xa[ks] : 0.f;
-    const float* Ws = W + (int64_t)s * C * C;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int a = 16 * nb + li;
-      float wb[KR];
-      if (!TRANS) {
-        const float* wp = Ws + a * C + g * KR;
-#pragma unroll
-        for (int q = 0; q < KR / 4; ++q) {
-          const float4 v = *reinterpret_cast<const float4*>(wp + 4 * q);
-          wb[4 * q] = v.x;
-          wb[4 * q + 1] = v.y;
-          wb[4 * q + 2] = v.z;
-          wb[4 * q + 3] = v.w;
-        }
-      } else {
-#pragma unroll
-        for (int ks = 0; ks < KR; ++ks) wb[ks] = Ws[(g * KR + ks) * C + a];
-      }
-#pragma unroll
-      for (int ks = 0; ks < KR; ++ks) acc[nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xm[ks], wb[ks], acc[nb], 0, 0, 0);
-    }
-  }
-  // lane holds rows (nodes) 4 g + r, column 16 nb + li of each block
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t node = n0 + 4 * g + r;
-    if (node < N) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) out[node * C + 16 * nb + li] = acc[nb][r];
-    }
-  }
-}
-
-template <int C>
-void species_linear_launch(const float* x, int64_t ldx, int64_t N, const float* W, int S, const int64_t* species,
-                           int trans, float* out, hipStream_t st) {
-  const unsigned grid = (unsigned)((N + 63) / 64);
-  if (trans)
-    hipLaunchKernelGGL((species_linear_kernel<C, true>), dim3(grid), dim3(256), 0, st, x, ldx, N, W, S, species, out);
-  else
-    hipLaunchKernelGGL((species_linear_kernel<C, false>), dim3(grid), dim3(256), 0, st, x, ldx, N, W, S, species,
-                       out);
-}
-
 int launch_status(const char* what) {
   const hipError_t e = hipGetLastError();
   if (e == hipSuccess) return ICTC_OK;
@@ -414,26 +331,6 @@ int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t
     hipLaunchKernelGGL(graph_sum_kernel<false>, dim3((unsigned)graphs), dim3(kSumThreads), 0, (hipStream_t)stream,
                        values, batch, n, out);
   return launch_status("ictc_graph_sum launch");
-}
-
-int ictc_species_linear(const float* x, int64_t ldx, int64_t nodes, int channels, const float* W, int species_count,
-                        const int64_t* species, int transpose, float* out, void* stream) {
-  if (nodes < 0 || species_count <= 0 || ldx < channels || ldx % 4)
-    return fail(ICTC_ERR_ARGUMENT, "species_linear: invalid sizes (row pitch >= channels, a multiple of 4)");
-  if (channels != 16 && channels != 32 && channels != 64 && channels != 128)
-    return fail(ICTC_ERR_UNSUPPORTED, "species_linear: compiled for 16, 32, 64 and 128 channels");
-  if (nodes == 0) return ICTC_OK;
-  if (!x || !W || !species || !out) return fail(ICTC_ERR_ARGUMENT, "species_linear: null operand");
-  if (((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W)) & 15) != 0)
-    return fail(ICTC_ERR_ARGUMENT, "species_linear: x and W must be 16-byte aligned");
-  hipStream_t st = (hipStream_t)stream;
-  switch (channels) {
-    case 16: species_linear_launch<16>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
-    case 32: species_linear_launch<32>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
-    case 64: species_linear_launch<64>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
-    default: species_linear_launch<128>(x, ldx, nodes, W, species_count, species, transpose, out, st); break;
-  }
-  return launch_status("ictc_species_linear launch");
 }
 
 }  // extern "C"

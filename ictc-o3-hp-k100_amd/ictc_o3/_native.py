@@ -85,7 +85,6 @@ _SIGNATURES = {
     "ictc_graph_sum": (_i, [_p, _p, _i64, _i64, _i, _p, _p]),
     "ictc_gemm_tn": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p]),
     "ictc_edge_unit": (_i, [_i, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p]),
-    "ictc_species_linear": (_i, [_p, _i64, _i64, _i, _p, _i, _p, _i, _p, _p]),
     "ictc_gemm_tn_grouped": (_i, [_p, _i64, _i64, _i, _i64, _p, _i64, _i64, _i, _i64, _i64, _i, _i64, _i64, _p, _p,
                                   _i64, _p]),
     "ictc_edge_geometry_fwd": (_i, [_p, _p, _p, _p, _i64, _i64, ctypes.c_float, _p, _p, _p, _p]),

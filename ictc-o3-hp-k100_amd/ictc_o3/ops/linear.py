@@ -49,56 +49,10 @@ def path_linear(m: torch.Tensor, weights: List[torch.Tensor], counts: Dict[int, 
 
 
 def species_linear(x: torch.Tensor, weight: torch.Tensor, species: torch.Tensor):
-    """out[n] = weight[species[n]] @ x[n], weight [S, Cout, Cin] (species in [0, S)).
-
-    Square float32 maps of 16, 32, 64 or 128 channels on the device run on ictc_species_linear (each node's
-    product only; differentiable to any order); otherwise all species products in one GEMM, then a select."""
+    """weight [S, Cout, Cin]: all species products in one GEMM, then select per node."""
     S, Co, Ci = weight.shape
-    if (x.is_cuda and x.dtype == torch.float32 and weight.dtype == torch.float32 and Co == Ci
-            and Ci in (16, 32, 64, 128) and x.dim() == 2 and x.shape[1] == Ci and species.dtype == torch.int64):
-        return _SpeciesLinear.apply(x, weight, species, False)
     allp = edge_linear(x, weight.reshape(S * Co, Ci)).reshape(x.shape[0], S, Co)
     return allp.gather(1, species.view(-1, 1, 1).expand(-1, 1, Co)).squeeze(1)
-
-
-def _species_outer(a: torch.Tensor, b: torch.Tensor, species: torch.Tensor, S: int) -> torch.Tensor:
-    """[S, Ca, Cb]: sum over the nodes of species s of a[n] b[n]^T (differentiable)."""
-    from ictc_o3.ops.radial_mlp import _WeightGrad
-    N, Ca = a.shape
-    scat = a.new_zeros(N, S, Ca).scatter(1, species.view(-1, 1, 1).expand(-1, 1, Ca), a.unsqueeze(1))
-    return _WeightGrad.apply(scat.reshape(N, S * Ca), b).reshape(S, Ca, b.shape[1])
-
-
-class _SpeciesLinear(torch.autograd.Function):
-    """y[n] = W[s_n] x[n] (trans: W[s_n]^T x[n]) on ictc_species_linear; the input adjoint is the other map,
-    the weight gradient the per-species outer products (_species_outer)."""
-
-    @staticmethod
-    def forward(ctx, x, W, species, trans):
-        ctx.trans = trans
-        ctx.save_for_backward(x, W, species)
-        xc = x.detach()
-        if xc.stride(1) != 1 or xc.stride(0) % 4 or xc.data_ptr() % 16:
-            xc = xc.contiguous()   # the kernel reads rows with a pitch (a column slice stays in place)
-        Wc = W.detach().contiguous()
-        sp = species.contiguous()
-        out = xc.new_empty(xc.shape[0], xc.shape[1])
-        nat.call("ictc_species_linear", nat.ptr(xc), xc.stride(0), xc.shape[0], xc.shape[1], nat.ptr(Wc),
-                 Wc.shape[0], nat.ptr(sp), 1 if trans else 0, nat.ptr(out), nat.stream_of(xc))
-        return out
-
-    @staticmethod
-    def backward(ctx, g):
-        from ictc_o3.autograd import required_gradients
-        x, W, species = ctx.saved_tensors
-        needs = required_gradients((x, W), ctx.needs_input_grad[:2])
-        if g is None or not any(needs):
-            return None, None, None, None
-        dx = _SpeciesLinear.apply(g, W, species, not ctx.trans) if needs[0] else None
-        dW = None
-        if needs[1]:
-            dW = _species_outer(x, g, species, W.shape[0]) if ctx.trans else _species_outer(g, x, species, W.shape[0])
-        return dx, dW, None, None
 
 
 class _SpeciesRows(torch.autograd.Function):

@@ -434,14 +434,6 @@ int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t
 int64_t ictc_gemm_tn_workspace_bytes(int64_t k, int64_t m, int64_t n);
 int ictc_gemm_tn(const float* a, int64_t k, int64_t m, int64_t lda, const float* b, int64_t n, int64_t ldb,
                  float* out, void* workspace, int64_t workspace_bytes, void* stream);
-/* Element-conditioned self connection (replaces the species-selected
- * product of ElementConditionedLinearSO3, layers.py:21-87):
- * out[n, a] = sum_b W[species[n], a, b] x[n, b] (transpose = 1: W[s]^T, the
- * input adjoint), W [S, C, C] row-major, x [nodes, C] with row pitch ldx (a
- * multiple of 4), out [nodes, C] contiguous, FP32 MFMA; channels 16, 32, 64
- * or 128; species outside [0, S) give zero rows; x and W 16-byte aligned.    */
-int ictc_species_linear(const float* x, int64_t ldx, int64_t nodes, int channels, const float* W, int species_count,
-                        const int64_t* species, int transpose, float* out, void* stream);
 /* ictc_gemm_tn over grouped rows and blocked columns, for the weight
  * gradient of one degree of a packed channel linear (the per-degree
  * dW_l = dout_l^T x_l of EquivariantChannelLinearSO3 / the path-preserving

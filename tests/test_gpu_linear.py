@@ -168,7 +168,7 @@ def test_packed_linear_any_order(device, kind, C, lmax, N):
 
 @pytest.mark.parametrize("C,S,N", [(64, 3, 1000), (128, 10, 517), (16, 1, 33), (32, 4, 4096)])
 def test_species_linear(device, C, S, N):
-    """ictc_species_linear (out[n] = W[species[n]] x[n]): values, first derivatives (input and weights) and the
+    """species_linear (out[n] = W[species[n]] x[n]): values, first derivatives (input and weights) and the
     derivative of a first-derivative quantity against float64 autograd of the indexed product, 1e-5."""
     from ictc_o3.ops.linear import species_linear
     g = torch.Generator().manual_seed(C + S + N)
