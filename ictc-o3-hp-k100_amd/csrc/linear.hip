@@ -21,6 +21,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "../../include/ictc_mi355x.h"
 #include "split_bf16.h"
 
@@ -40,8 +42,10 @@ struct LinearDesc {
   int64_t in_off[kMaxDeg];   // column offset of the degree block in an input row
   int64_t out_off[kMaxDeg];
   int pin[kMaxDeg], pout[kMaxDeg];
+  int wld[kMaxDeg];          // weight row length (paths_in * Cin of the whole map; a launch may take a slice)
   float scale[kMaxDeg];
   int lmax;
+  int accumulate;            // add to the output rows instead of writing them
 };
 
 __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
@@ -182,8 +186,8 @@ __global__ __launch_bounds__(lin_waves<NZ>() * 64, 1) void packed_linear_bf16_ke
     const int col = col0 + 16 * cb + (lane & 15), k = 32 * ks + 8 * (lane >> 4);
     float v[8];
     if (col < ncols && k < K) {
-      const float4 a = *reinterpret_cast<const float4*>(W + (int64_t)col * K + k);
-      const float4 b = *reinterpret_cast<const float4*>(W + (int64_t)col * K + k + 4);
+      const float4 a = *reinterpret_cast<const float4*>(W + (int64_t)col * d.wld[l] + k);
+      const float4 b = *reinterpret_cast<const float4*>(W + (int64_t)col * d.wld[l] + k + 4);
       v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
     } else {
 #pragma unroll
@@ -237,13 +241,61 @@ __global__ __launch_bounds__(lin_waves<NZ>() * 64, 1) void packed_linear_bf16_ke
         const int col = col0 + 16 * cb + 4 * g;
         if (col >= ncols) continue;
         const int p = col / Co, c = col % Co;
-        *reinterpret_cast<v4f*>(out + n * out_stride + d.out_off[l] + ((int64_t)p * w + m) * Co + c) = sc * acc[cb];
+        v4f* dst = reinterpret_cast<v4f*>(out + n * out_stride + d.out_off[l] + ((int64_t)p * w + m) * Co + c);
+        *dst = d.accumulate ? *dst + sc * acc[cb] : sc * acc[cb];
       }
     }
   }
 }
 
 int fail(int code, const char* msg) { return ictc::set_error(code, msg); }
+
+// The split-bf16 kernel over every (component, column block) pair: one 16-wave block per CU.
+int launch_bf16(const float* in, int64_t in_stride, float* out, int64_t out_stride, int channels_in,
+                int channels_out, int64_t nodes, const LinearDesc& d, int maxk, int maxcols, unsigned gy, unsigned gz,
+                hipStream_t stream) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                               hipSuccess || cus <= 0)
+    cus = 256;
+  const int64_t node_tiles = (nodes + 15) / 16;
+  // a narrow linear with up to 256 output columns covers them all in one workgroup (inputs read once)
+  const bool wide4 = maxk <= 64 && maxcols > 64 && maxcols <= 256;
+  const unsigned gzw = wide4 ? 1u : gz;
+  const int nw = wide4 ? lin_waves<4>() : lin_waves<1>();
+  const int64_t most = (node_tiles + nw - 1) / nw;
+  // Blocks per (component, column block): one block per CU over all pairs; where that leaves more than a fifth
+  // of the CUs idle (many pairs), the fewest whose estimated makespan (rounds of one block per CU times node
+  // tiles per wave) is least.  cfg5's message-linear adjoint (16 components x 10 column blocks): 249 us with
+  // one block per pair, 160 us with eight.
+  const int64_t pairs = (int64_t)gy * gzw;
+  int64_t gx = (int64_t)cus / pairs;
+  gx = gx < 1 ? 1 : (gx > most ? most : gx);
+  if (5 * gx * pairs < 4 * (int64_t)cus) {
+    int64_t best = INT64_MAX;
+    for (int64_t x = 1; x <= most && x <= 4 * cus; ++x) {
+      const int64_t rounds = (x * pairs + cus - 1) / cus, per_wave = (node_tiles + x * nw - 1) / (x * nw);
+      if (rounds * per_wave < best) {
+        best = rounds * per_wave;
+        gx = x;
+      }
+    }
+  }
+  const size_t lds = (size_t)(maxk / 32) * 4 * (wide4 ? 4 : 1) * 3 * 64 * sizeof(bf16x8);
+  if (wide4)
+    hipLaunchKernelGGL(packed_linear_bf16_kernel<4>, dim3((unsigned)gx, gy, 1), dim3(lin_waves<4>() * 64), lds, stream,
+                       in, in_stride, out, out_stride, channels_in, channels_out, nodes, d, node_tiles);
+  else
+    hipLaunchKernelGGL(packed_linear_bf16_kernel<1>, dim3((unsigned)gx, gy, gz), dim3(lin_waves<1>() * 64), lds,
+                       stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d, node_tiles);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "ictc_packed_linear launch: %s", hipGetErrorString(e));
+    return fail(ICTC_ERR_RUNTIME, buf);
+  }
+  return ICTC_OK;
+}
 
 }  // namespace
 
@@ -274,6 +326,7 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
     d.out_off[l] = out_offsets[l];
     d.pin[l] = in_paths[l];
     d.pout[l] = out_paths[l];
+    d.wld[l] = in_paths[l] * channels_in;
     d.scale[l] = scales[l];
     if (out_paths[l] * channels_out > maxcols) maxcols = out_paths[l] * channels_out;
   }
@@ -286,29 +339,33 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
   }
   const int64_t node_blocks = (nodes + 63) / 64;
   const unsigned gy = (unsigned)((lmax + 1) * (lmax + 1)), gz = (unsigned)((maxcols + 63) / 64);
+  // Panels wider than the LDS holds run as consecutive launches over slices of the input paths (at most
+  // kWholeK / Cin paths each), the later ones adding to the output rows.
+  const int slice = channels_in <= kWholeK ? kWholeK / channels_in : 0;
+  if (maxk > kWholeK && slice > 0) {
+    int slices = 1;
+    for (int l = 0; l <= lmax; ++l) slices = std::max(slices, (in_paths[l] + slice - 1) / slice);
+    for (int j = 0; j < slices; ++j) {
+      LinearDesc dj = d;
+      dj.accumulate = j > 0;
+      int kj = 0;
+      for (int l = 0; l <= lmax; ++l) {
+        const int p0 = std::min(j * slice, in_paths[l]), p1 = std::min((j + 1) * slice, in_paths[l]);
+        dj.pin[l] = p1 - p0;
+        dj.w[l] = weights[l] + (int64_t)p0 * channels_in;
+        dj.in_off[l] = in_offsets[l] + (int64_t)p0 * (2 * l + 1) * channels_in;
+        kj = std::max(kj, (dj.pin[l] * channels_in + 63) / 64 * 64);
+      }
+      if (int rc = launch_bf16(in, in_stride, out, out_stride, channels_in, channels_out, nodes, dj, kj, maxcols,
+                               gy, gz, (hipStream_t)stream))
+        return rc;
+    }
+    return ICTC_OK;
+  }
   if (maxk <= kWholeK) {
-    // one 16-wave block per CU over all (component, column block) pairs
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                 hipSuccess || cus <= 0)
-      cus = 256;
-    const int64_t node_tiles = (nodes + 15) / 16;
-    // a narrow linear with up to 256 output columns covers them all in one workgroup (inputs read once)
-    const bool wide4 = maxk <= 64 && maxcols > 64 && maxcols <= 256;
-    const unsigned gzw = wide4 ? 1u : gz;
-    int64_t gx = (int64_t)cus / (gy * gzw);
-    const int nw = wide4 ? lin_waves<4>() : lin_waves<1>();
-    const int64_t most = (node_tiles + nw - 1) / nw;
-    gx = gx < 1 ? 1 : (gx > most ? most : gx);
-    const size_t lds = (size_t)(maxk / 32) * 4 * (wide4 ? 4 : 1) * 3 * 64 * sizeof(bf16x8);
-    if (wide4)
-      hipLaunchKernelGGL(packed_linear_bf16_kernel<4>, dim3((unsigned)gx, gy, 1), dim3(lin_waves<4>() * 64), lds,
-                         (hipStream_t)stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d,
-                         node_tiles);
-    else
-      hipLaunchKernelGGL(packed_linear_bf16_kernel<1>, dim3((unsigned)gx, gy, gz), dim3(lin_waves<1>() * 64), lds,
-                         (hipStream_t)stream, in, in_stride, out, out_stride, channels_in, channels_out, nodes, d,
-                         node_tiles);
+    if (int rc = launch_bf16(in, in_stride, out, out_stride, channels_in, channels_out, nodes, d, maxk, maxcols, gy,
+                             gz, (hipStream_t)stream))
+      return rc;
   } else {
     hipLaunchKernelGGL(packed_linear_kernel<false>, dim3((unsigned)node_blocks, gy, gz), dim3(256),
                        (size_t)64 * kPanel * sizeof(float), (hipStream_t)stream, in, in_stride, out, out_stride,
