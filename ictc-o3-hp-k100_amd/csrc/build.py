@@ -19,7 +19,7 @@ PKG = os.path.dirname(HERE)
 OUT_DIR = os.path.join(PKG, "ictc_o3", "_lib")
 LIB = os.path.join(OUT_DIR, "libictc_mi355x.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["capi.hip", "misc.hip", "radial_mlp.hip", "gate_gemm.hip", "gemm_tn.hip", "gemm_nt.hip", "linear.hip", "geometry.hip", "neighbors.hip", "sc.hip", "tp_edge.hip", "msg_fwd.hip", "pairs.hip",
+SOURCES = ["capi.hip", "misc.hip", "radial_mlp.hip", "gate_gemm.hip", "gemm_tn.hip", "gemm_nt.hip", "species.hip", "linear.hip", "geometry.hip", "neighbors.hip", "sc.hip", "tp_edge.hip", "msg_fwd.hip", "pairs.hip",
            "msg_bwd.hip", "msg_bwd_tan.hip", "msg_fused.hip", "tp_second.hip", "msg_second_rcv.hip", "msg_second_src.hip", "sc_part_low.hip", "sc_part_l3_t0.hip", "sc_part_l3_t1.hip", "sc_part_l3_t2.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",

@@ -83,6 +83,9 @@ _SIGNATURES = {
     "ictc_gemm_tn_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "ictc_gemm_nt": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i, _p]),
     "ictc_graph_sum": (_i, [_p, _p, _i64, _i64, _i, _p, _p]),
+    "ictc_species_linear": (_i, [_p, _i64, _i64, _i, _p, _i, _p, _p, _i, _p, _i64, _p]),
+    "ictc_species_outer_workspace_bytes": (_i64, [_i64, _i, _i, _i]),
+    "ictc_species_outer": (_i, [_p, _i64, _p, _i64, _i64, _i, _i, _p, _p, _i, _p, _p, _i64, _p]),
     "ictc_gemm_tn": (_i, [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p]),
     "ictc_edge_unit": (_i, [_i, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p]),
     "ictc_gemm_tn_grouped": (_i, [_p, _i64, _i64, _i, _i64, _p, _i64, _i64, _i, _i64, _i64, _i, _i64, _i64, _p, _p,

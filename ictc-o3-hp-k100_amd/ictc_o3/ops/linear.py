@@ -49,10 +49,115 @@ def path_linear(m: torch.Tensor, weights: List[torch.Tensor], counts: Dict[int, 
 
 
 def species_linear(x: torch.Tensor, weight: torch.Tensor, species: torch.Tensor):
-    """weight [S, Cout, Cin]: all species products in one GEMM, then select per node."""
+    """out[n] = weight[species[n]] @ x[n], weight [S, Cout, Cin] (layers.py:21-87).
+
+    Square float32 maps of 64 or 128 channels on the device run on ictc_species_linear over species-sorted
+    node tiles (each node's product only, differentiable to any order; nodes whose species is outside
+    [0, S) get zero rows); otherwise all species products in one GEMM, then a select."""
     S, Co, Ci = weight.shape
+    if (x.is_cuda and x.dtype == torch.float32 and weight.dtype == torch.float32 and Co == Ci and Ci in (64, 128)
+            and x.dim() == 2 and x.shape[1] == Ci and species.dtype == torch.int64 and x.shape[0] < 2 ** 31):
+        order = species_order(species, S)
+        return _SpeciesLinear.apply(x, weight, order, False)
     allp = edge_linear(x, weight.reshape(S * Co, Ci)).reshape(x.shape[0], S, Co)
     return allp.gather(1, species.view(-1, 1, 1).expand(-1, 1, Co)).squeeze(1)
+
+
+class SpeciesOrder:
+    """Nodes in species order: perm [N] int32 node ids sorted by species (stable), off [S + 2] int32 with
+    species s at sorted rows off[s] .. off[s + 1] and the nodes of species outside [0, S) last."""
+
+    def __init__(self, species: torch.Tensor, S: int):
+        from ictc_o3.ops.tensor_product import Csr
+        csr = Csr(species.contiguous(), S)   # ictc_csr_build: stable radix sort over the species bits
+        self.perm, self.off = csr.order, csr.ptr
+        self.S, self.N = S, species.shape[0]
+
+
+_order_memo = None
+
+
+def species_order(species: torch.Tensor, S: int) -> SpeciesOrder:
+    """SpeciesOrder of this species tensor, kept while the same unmodified tensor is passed again (both
+    layers of a step and their backward share one sort)."""
+    global _order_memo
+    key = (species.data_ptr(), species._version, species.shape[0], S, species.device)
+    if _order_memo is not None and _order_memo[0] == key and _order_memo[1] is species:
+        return _order_memo[2]
+    order = SpeciesOrder(species, S)
+    _order_memo = (key, species, order)
+    return order
+
+
+def _rows_ok(t: torch.Tensor) -> torch.Tensor:
+    """t with unit column stride and a row pitch and base the kernels read as 16-byte runs."""
+    if t.stride(1) != 1 or t.stride(0) % 4 or t.data_ptr() % 16:
+        return t.contiguous()
+    return t
+
+
+def _species_apply(x: torch.Tensor, W: torch.Tensor, order: SpeciesOrder, trans: bool) -> torch.Tensor:
+    x, W = _rows_ok(x.detach()), W.detach().contiguous()
+    out = x.new_empty(x.shape[0], W.shape[1])
+    nat.call("ictc_species_linear", nat.ptr(x), x.stride(0), x.shape[0], x.shape[1], nat.ptr(W), order.S,
+             nat.ptr(order.perm), nat.ptr(order.off), 1 if trans else 0, nat.ptr(out), out.stride(0),
+             nat.stream_of(x))
+    return out
+
+
+def _species_outer_raw(a: torch.Tensor, b: torch.Tensor, order: SpeciesOrder) -> torch.Tensor:
+    a, b = _rows_ok(a.detach()), _rows_ok(b.detach())
+    N, C, S = a.shape[0], a.shape[1], order.S
+    rows = max(128, ((N + 255) // 256 + 31) // 32 * 32)   # about 256 row tiles per species set
+    ws_bytes = int(nat.lib().ictc_species_outer_workspace_bytes(N, C, S, rows))
+    ws = torch.empty(max(ws_bytes, 16) // 4, dtype=torch.float32, device=a.device)
+    out = a.new_empty(S, C, C)
+    nat.call("ictc_species_outer", nat.ptr(a), a.stride(0), nat.ptr(b), b.stride(0), N, C, S, nat.ptr(order.perm),
+             nat.ptr(order.off), rows, nat.ptr(out), nat.ptr(ws), ws_bytes, nat.stream_of(a))
+    return out
+
+
+class _SpeciesLinear(torch.autograd.Function):
+    """y[n] = W[s_n] x[n] (trans: W[s_n]^T x[n]); the input adjoint is the other map, the weight gradient
+    the per-species outer products (_SpeciesOuter)."""
+
+    @staticmethod
+    def forward(ctx, x, W, order, trans):
+        ctx.order, ctx.trans = order, trans
+        ctx.save_for_backward(x, W)
+        return _species_apply(x, W, order, trans)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, W = ctx.saved_tensors
+        needs = ctx.needs_input_grad
+        if g is None or not (needs[0] or needs[1]):
+            return None, None, None, None
+        dx = _SpeciesLinear.apply(g, W, ctx.order, not ctx.trans) if needs[0] else None
+        dW = None
+        if needs[1]:
+            dW = _SpeciesOuter.apply(x, g, ctx.order) if ctx.trans else _SpeciesOuter.apply(g, x, ctx.order)
+        return dx, dW, None, None
+
+
+class _SpeciesOuter(torch.autograd.Function):
+    """out[s] = sum over the nodes n of species s of a[n] b[n]^T; adjoints a[n] <- H[s] b[n] and
+    b[n] <- H[s]^T a[n] (the species linear and its transpose)."""
+
+    @staticmethod
+    def forward(ctx, a, b, order):
+        ctx.order = order
+        ctx.save_for_backward(a, b)
+        return _species_outer_raw(a, b, order)
+
+    @staticmethod
+    def backward(ctx, H):
+        a, b = ctx.saved_tensors
+        if H is None:
+            return None, None, None
+        da = _SpeciesLinear.apply(b, H, ctx.order, False) if ctx.needs_input_grad[0] else None
+        db = _SpeciesLinear.apply(a, H, ctx.order, True) if ctx.needs_input_grad[1] else None
+        return da, db, None
 
 
 class _SpeciesRows(torch.autograd.Function):

@@ -423,6 +423,31 @@ int ictc_gemm_nt(const float* a, int64_t m, int64_t k, int64_t lda, const float*
 int ictc_graph_sum(const float* values, const int64_t* batch, int64_t n, int64_t graphs, int batch_sorted,
                    double* out, void* stream);
 
+/* Element-conditioned self connection (ElementConditionedLinearSO3,
+ * layers.py:21-87, applied at layers.py:1042-1100 as the model's sc =
+ * self_connection[species](h)): out[n] = M_s x[n] with s = species[n], M_s =
+ * W[s] ([S, C, C], output by input) or, transpose != 0, W[s]^T (the input
+ * adjoint).  The nodes come in species order: perm [nodes] int32 node ids
+ * sorted by species (stable), offsets [S + 2] int32 with species s at sorted
+ * rows offsets[s] .. offsets[s + 1] and group S (rows offsets[S] .. nodes)
+ * the nodes whose species is outside [0, S), which get zero rows.  Each
+ * 64-row tile of one species stages its weights once; FP32 MFMA.  C = 64 or
+ * 128; x row pitch ldx (a multiple of 4, 16-byte aligned), out pitch ldo.     */
+int ictc_species_linear(const float* x, int64_t ldx, int64_t nodes, int channels, const float* W, int species_count,
+                        const int32_t* perm, const int32_t* offsets, int transpose, float* out, int64_t ldo,
+                        void* stream);
+/* Weight gradient of ictc_species_linear: out[s] = sum over the nodes n of
+ * species s of a[n] b[n]^T ([S, C, C]; the autograd weight gradient of the
+ * same layer, layers.py:21-87).  Same perm / offsets; sorted rows are cut
+ * into tiles of rows_per_tile (a multiple of 32) within one species, whose
+ * partial products go to the workspace
+ * (ictc_species_outer_workspace_bytes) and are added per species in tile
+ * order (deterministic; zeros for a species with no nodes).                  */
+int64_t ictc_species_outer_workspace_bytes(int64_t nodes, int channels, int species_count, int rows_per_tile);
+int ictc_species_outer(const float* a, int64_t lda, const float* b, int64_t ldb, int64_t nodes, int channels,
+                       int species_count, const int32_t* perm, const int32_t* offsets, int rows_per_tile, float* out,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Weight gradient of a per-edge linear (replaces the library GEMM dW = dy^T x
  * that autograd runs for every Linear of the radial MLP fc in the force-loss
  * training step, mace_ictc/models/mace/layers.py:826-835 via
