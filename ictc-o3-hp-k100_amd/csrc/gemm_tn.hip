@@ -7,21 +7,19 @@
 // for 424k reduction rows); here the reduction rows are split instead.
 //
 // Grid: (output tile of 64 x 64) x (chunk of reduction rows).  A block of 4
-// waves stages 16-row slabs of A and B (64 columns each) through LDS with
+// waves stages 32-row slabs of A and B (64 columns each) through LDS with
 // 256-byte coalesced loads, prefetching the next slab into registers while
-// the MFMAs run on the current one.  Wave w owns output rows 16w .. 16w+15 of
-// the tile and all four 16-column blocks (v_mfma_f32_16x16x4_f32, FP32
-// products and sums).  Each block writes its partial tile to the workspace;
-// a second kernel adds the chunks of every output in a fixed order (chunks
-// interleaved over 16 waves, the 16 wave sums combined in wave order), so the
-// result does not depend on scheduling.
-//
-// Wide outputs (more than 16 tiles, e.g. the 2,176 x 64 gradient of a gate
-// projection) are MFMA-bound in FP32 (about 65 TFLOP/s measured); they run
-// the same tiling on bf16 MFMA with the three-way operand split (six
-// v_mfma_f32_16x16x32_bf16 per 16x16x32 step, FP32-level accuracy): each
-// 32-row slab is split once while it is staged, into hi / mid / lo planes
-// stored reduction-index-contiguous, so every operand is one 16-byte LDS read.
+// the MFMAs run on the current one.  The products run on bf16 MFMA with the
+// three-way operand split (six v_mfma_f32_16x16x32_bf16 per 16x16x32 step,
+// FP32-level accuracy): each slab is split once while it is staged, into
+// hi / mid / lo planes stored reduction-index-contiguous, so every operand is
+// one 16-byte LDS read.  Wave w owns output rows 16w .. 16w+15 of the tile and
+// all four 16-column blocks.  (An FP32-MFMA form, v_mfma_f32_16x16x4_f32,
+// measured 18-22 % slower even on single-tile 64 x 64 and 64 x 8 outputs over
+// 848k rows, and 65 TFLOP/s on the wide ones.)  Each block writes its partial
+// tile to the workspace; a second kernel adds the chunks of every output in a
+// fixed order (chunks interleaved over 16 waves, the 16 wave sums combined in
+// wave order), so the result does not depend on scheduling.
 //
 // Block order: the tiles of one chunk are consecutive logical blocks, and the
 // logical range is split contiguously over the 8 XCDs, so the chunk's rows of
@@ -42,8 +40,6 @@ namespace {
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 64;
-constexpr int kSlab = 16;        // reduction rows per LDS stage
-constexpr int kPitch = 80;       // LDS row pitch: rows r and r+1 fall in disjoint bank halves
 constexpr int kXcds = 8;
 constexpr int kSumWaves = 16;
 
@@ -82,7 +78,7 @@ Plan plan_for(int64_t K, int M, int N) {
   if (chunks > 1024) chunks = 1024;
   if (chunks < 1) chunks = 1;
   int64_t rows = (K + chunks - 1) / chunks;
-  rows = (rows + 31) / 32 * 32;   // whole slabs of both kernels (16 and 32 rows)
+  rows = (rows + 31) / 32 * 32;   // whole 32-row slabs
   if (rows < 32) rows = 32;
   chunks = K > 0 ? (K + rows - 1) / rows : 1;
   p.chunks = (int)chunks;
@@ -106,96 +102,8 @@ template <bool STRIDED>
 __device__ __forceinline__ int64_t col_offset(const Layout& L, int c) {
   return STRIDED ? (int64_t)(c / L.cg) * L.ldc + c % L.cg : c;
 }
-__device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
-template <bool STRIDED>
-__global__ __launch_bounds__(256) void gemm_tn_partial_kernel(const float* __restrict__ A, int64_t K, int M,
-    Layout la, const float* __restrict__ B, int N, Layout lb, float* __restrict__ part, int mt,
-                                                              int nt, int chunks, int64_t rows, int64_t blocks) {
-  // Physical block p runs on XCD p % 8; give XCD x the logical range [x * per, (x + 1) * per).
-  const int64_t per = blocks / kXcds;
-  const int64_t logical = (int64_t)(blockIdx.x % kXcds) * per + blockIdx.x / kXcds;
-  const int64_t tiles = (int64_t)mt * nt;
-  if (logical >= tiles * chunks) return;
-  const int tile = (int)(logical % tiles);
-  const int chunk = (int)(logical / tiles);
-  const int m0 = (tile % mt) * kTile, n0 = (tile / mt) * kTile;
-  const int64_t k0 = (int64_t)chunk * rows;
-  const int64_t k1 = k0 + rows < K ? k0 + rows : K;
-
-  __shared__ float sa[kSlab * kPitch];
-  __shared__ float sb[kSlab * kPitch];
-  const int t = threadIdx.x, col = t & 63, r0 = t >> 6;
-  const int lane = t & 63, wave = t >> 6;
-  const int li = lane & 15, lg = lane >> 4;
-  const bool a_col = m0 + col < M, b_col = n0 + col < N;
-  const float* __restrict__ Ap = A + (a_col ? col_offset<STRIDED>(la, m0 + col) : 0);
-  const float* __restrict__ Bp = B + (b_col ? col_offset<STRIDED>(lb, n0 + col) : 0);
-
-  float ra[4], rb[4];
-  auto load = [&](int64_t k) {
-    // grouped rows: one division for the first row, then (group, member) steps (both operands share rg)
-    uint32_t g = 0, i = 0;
-    if (STRIDED) {
-      const uint32_t u = (uint32_t)(k + r0);
-      g = u / (uint32_t)la.rg;
-      i = u - g * (uint32_t)la.rg;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t kr = k + r0 + 4 * j;
-      const bool in = kr < k1;
-      const int64_t oa = STRIDED ? (int64_t)g * la.ldg + (int64_t)i * la.ldr : kr * la.ldg;
-      const int64_t ob = STRIDED ? (int64_t)g * lb.ldg + (int64_t)i * lb.ldr : kr * lb.ldg;
-      ra[j] = (in && a_col) ? Ap[oa] : 0.f;
-      rb[j] = (in && b_col) ? Bp[ob] : 0.f;
-      if (STRIDED) {
-        i += 4;
-        while (i >= (uint32_t)la.rg) {
-          i -= (uint32_t)la.rg;
-          ++g;
-        }
-      }
-    }
-  };
-
-  v4f acc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
-  if (k0 < k1) load(k0);
-  for (int64_t k = k0; k < k1; k += kSlab) {
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      sa[(r0 + 4 * j) * kPitch + col] = ra[j];
-      sb[(r0 + 4 * j) * kPitch + col] = rb[j];
-    }
-    __syncthreads();
-    if (k + kSlab < k1) load(k + kSlab);
-#pragma unroll
-    for (int kk = 0; kk < kSlab / 4; ++kk) {
-      const int row = (4 * kk + lg) * kPitch;
-      const float a = sa[row + 16 * wave + li];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = mfma(a, sb[row + 16 * j + li], acc[j]);
-    }
-  }
-
-  float* __restrict__ P = part + (int64_t)chunk * M * N;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + 16 * j + li;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = m0 + 16 * wave + 4 * lg + r;
-      if (m < M && n < N) P[(int64_t)m * N + n] = acc[j][r];
-    }
-  }
-}
-
-constexpr int kSlabB = 32;     // reduction rows per stage of the bf16 kernel (one MFMA K)
+constexpr int kSlabB = 32;     // reduction rows per stage (one MFMA K)
 constexpr int kPlanePitch = 40;  // bf16 per plane row: 32 + 8 (80 bytes: 16-byte reads of 8 rows hit distinct banks)
 
 __device__ __forceinline__ v4f mfma16(bf16x8 a, bf16x8 b, v4f c) {
@@ -327,19 +235,12 @@ int gemm_tn_launch(const float* a, const Layout& la, int64_t k, int64_t m, const
   float* part = static_cast<float*>(workspace);
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)p.blocks), block(256);
-  const bool wide = (int64_t)p.mt * p.nt > 16;
-  if (wide && strided)
+  if (strided)
     hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel<true>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part,
                        p.mt, p.nt, p.chunks, p.rows, p.blocks);
-  else if (wide)
+  else
     hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel<false>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part,
                        p.mt, p.nt, p.chunks, p.rows, p.blocks);
-  else if (strided)
-    hipLaunchKernelGGL(gemm_tn_partial_kernel<true>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part, p.mt,
-                       p.nt, p.chunks, p.rows, p.blocks);
-  else
-    hipLaunchKernelGGL(gemm_tn_partial_kernel<false>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part, p.mt,
-                       p.nt, p.chunks, p.rows, p.blocks);
   const int64_t total = m * n;
   hipLaunchKernelGGL(gemm_tn_sum_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64 * kSumWaves), 0, st, part,
                      total, p.chunks, out);

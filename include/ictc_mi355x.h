@@ -452,7 +452,8 @@ int ictc_species_outer(const float* a, int64_t lda, const float* b, int64_t ldb,
  * that autograd runs for every Linear of the radial MLP fc in the force-loss
  * training step, mace_ictc/models/mace/layers.py:826-835 via
  * radial_checkpoint.py:133-164): out [m, n] = a^T b with a [k, m] (row pitch
- * lda) and b [k, n] (row pitch ldb), FP32 MFMA.  The k rows are split into
+ * lda) and b [k, n] (row pitch ldb), split-bf16 MFMA (each operand as three
+ * bf16 parts, six products kept: FP32-level accuracy).  The k rows are split into
  * chunks whose partial products go to the workspace
  * (ictc_gemm_tn_workspace_bytes(k, m, n) bytes) and are added in a fixed
  * order (deterministic).  k = 0 writes zeros.                                  */
