@@ -396,6 +396,64 @@ def add_scalars_(out, s):
     return _AddScalars.apply(out, s)
 
 
+class _AddScalarsAny(torch.autograd.Function):
+    """out[:, :C] += s in place on a fresh tensor, differentiable to any order: the gradient passes through
+    and s's is the contiguous take of its first C columns (_TakeScalars), where an in-place slice update
+    records a full-size clone and, differentiated again, a zero-filled as_strided gradient."""
+
+    @staticmethod
+    def forward(ctx, out, s):
+        C = s.shape[1]
+        out[:, :C] += s
+        ctx.mark_dirty(out)
+        ctx.C = C
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        if g is None:
+            return None, None
+        return g, _TakeScalars.apply(g, ctx.C)
+
+
+class _TakeScalars(torch.autograd.Function):
+    """x[:, :C] as a contiguous [N, C] tensor; the adjoint writes the (small) gradient into the first C
+    columns of a zero [N, W] tensor (_PadScalars), whose adjoint is this take again."""
+
+    @staticmethod
+    def forward(ctx, x, C):
+        ctx.W, ctx.C = x.shape[1], C
+        return x[:, :C].contiguous()
+
+    @staticmethod
+    def backward(ctx, g):
+        return (None if g is None else _PadScalars.apply(g, ctx.W)), None
+
+
+class _PadScalars(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, s, W):
+        ctx.C = s.shape[1]
+        out = s.new_zeros(s.shape[0], W)
+        out[:, :ctx.C] = s
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        return (None if g is None else _TakeScalars.apply(g, ctx.C)), None
+
+
+def add_scalars_any_(out, s):
+    """out[:, :C] += s (C = s.shape[1]) in place on a fresh tensor nothing else holds, any derivative order."""
+    return _AddScalarsAny.apply(out, s)
+
+
+def take_scalars(x, C):
+    """x[:, :C] as a contiguous copy with a single-node adjoint (any derivative order); x itself when it has
+    only C columns."""
+    return x if x.shape[1] == C else _TakeScalars.apply(x, C)
+
+
 def _fast_ok(x, weights, C):
     return (x.is_cuda and x.dtype == torch.float32 and C % 16 == 0 and len(weights) <= 4
             and all(w.numel() > 0 and w.dtype == torch.float32 for w in weights))

@@ -33,7 +33,7 @@ from ictc_o3.basis import tables
 from ictc_o3.basis.ictd_irreps import EdgeWeightedPathPreservingTensorProduct
 from ictc_o3.ops import tensor_product as tpo
 from ictc_o3.ops.harmonics import harmonics_packed
-from ictc_o3.ops.linear import species_rows
+from ictc_o3.ops.linear import species_rows, take_scalars
 from ictc_o3.ops.radial_mlp import EdgeLengths, edge_linear, hidden_supported, radial_mlp_lengths
 from ictc_o3.ops.symmetric_contraction import ICTDBridgeUSymmetricContractionSO3
 
@@ -180,10 +180,12 @@ class Interaction(nn.Module):
         input is the species embedding), which lets the message run in its species form."""
         C = self.channels
         first_order = radial is None
-        if entry is not None:
+        if entry is not None and entry[0] is not None:
             x, h0 = entry
         else:
-            x, h0 = self.linear_up(h, first_order), h[:, :C]
+            from ictc_o3.ops.linear import take_scalars
+            x = self.linear_up(h, first_order)
+            h0 = entry[1] if entry is not None else take_scalars(h, C)
         if radial is None and forces_only:
             m = tpo.radial_message(x, Y, r, self.fc, self.spec(), topo, mask, radial_cfg, basis_scale,
                                    species=None if species_table is None else (species_table, species))
@@ -220,8 +222,8 @@ class Product(nn.Module):
         if first_order:
             from ictc_o3.ops.linear import add_scalars_
             return add_scalars_(out, sc)
-        out[:, :C] += sc
-        return out
+        from ictc_o3.ops.linear import add_scalars_any_
+        return add_scalars_any_(out, sc)
 
 
 class ScalarReadout(nn.Module):
@@ -408,8 +410,10 @@ class PureCartesianICTDFix(nn.Module):
             # first-order route: the scalar columns come out of the next layer's entry op (one merged
             # adjoint instead of slice gradients), so layer i - 1's energy readout is taken here, in order
             entry = inter.entry(h) if radial is None else None
+            if entry is None:   # the scalar columns taken once for the readout and the self connection
+                entry = (None, take_scalars(h, self.channels))
             if i > 0:
-                e = self.layer_energy_readouts[i - 1](entry[1] if entry is not None else h[:, :self.channels])
+                e = self.layer_energy_readouts[i - 1](entry[1])
                 energy = e if energy is None else energy + e
             table = None
             if i == 0 and radial is None and forces_only and inter.input_lmax == 0:
