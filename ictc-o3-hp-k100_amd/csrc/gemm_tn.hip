@@ -212,9 +212,22 @@ __global__ __launch_bounds__(64 * kSumWaves) void gemm_tn_sum_kernel(const float
   __shared__ float red[kSumWaves][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+  // four independent partial sums (chunks w + 64 q + 16 j go to sum j), added in a fixed order, so four
+  // loads are in flight per lane instead of one
   float v = 0.f;
-  if (i < n)
-    for (int c = wave; c < chunks; c += kSumWaves) v += part[(int64_t)c * n + i];
+  if (i < n) {
+    float v0 = 0.f, v1 = 0.f, v2 = 0.f, v3 = 0.f;
+    const float* __restrict__ p = part + i;
+    int c = wave;
+    for (; c + 3 * kSumWaves < chunks; c += 4 * kSumWaves) {
+      v0 += p[(int64_t)c * n];
+      v1 += p[(int64_t)(c + kSumWaves) * n];
+      v2 += p[(int64_t)(c + 2 * kSumWaves) * n];
+      v3 += p[(int64_t)(c + 3 * kSumWaves) * n];
+    }
+    for (; c < chunks; c += kSumWaves) v0 += p[(int64_t)c * n];
+    v = (v0 + v1) + (v2 + v3);
+  }
   red[wave][lane] = v;
   __syncthreads();
   if (wave == 0 && i < n) {
