@@ -110,7 +110,9 @@ __device__ __forceinline__ v4f mfma16(bf16x8 a, bf16x8 b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <bool STRIDED>
+// NJ: 16-column blocks of the tile computed (1 for outputs at most 16 wide, such as the 64 x 8 gradient of a
+// radial MLP's first layer: the other three blocks would multiply zero columns).
+template <bool STRIDED, int NJ>
 __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* __restrict__ A, int64_t K, int M,
     Layout la, const float* __restrict__ B, int N, Layout lb, float* __restrict__ part, int mt,
                                                                    int nt, int chunks, int64_t rows, int64_t blocks) {
@@ -157,9 +159,9 @@ __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* 
     }
   };
 
-  v4f acc[4];
+  v4f acc[NJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NJ; ++j) acc[j] = v4f{0.f, 0.f, 0.f, 0.f};
   if (k0 < k1) load(k0);
   for (int64_t k = k0; k < k1; k += kSlabB) {
     const Split sa = split8(ra), sb = split8(rb);
@@ -178,7 +180,7 @@ __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* 
     const bf16x8 amid = *reinterpret_cast<const bf16x8*>(&planes[0][1][am][8 * lg]);
     const bf16x8 alo = *reinterpret_cast<const bf16x8*>(&planes[0][2][am][8 * lg]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < NJ; ++j) {
       const int bn = 16 * j + li;
       const bf16x8 bhi = *reinterpret_cast<const bf16x8*>(&planes[1][0][bn][8 * lg]);
       const bf16x8 bmid = *reinterpret_cast<const bf16x8*>(&planes[1][1][bn][8 * lg]);
@@ -194,7 +196,7 @@ __global__ __launch_bounds__(256) void gemm_tn_bf16_partial_kernel(const float* 
 
   float* __restrict__ P = part + (int64_t)chunk * M * N;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < NJ; ++j) {
     const int n = n0 + 16 * j + li;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -248,12 +250,18 @@ int gemm_tn_launch(const float* a, const Layout& la, int64_t k, int64_t m, const
   float* part = static_cast<float*>(workspace);
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)p.blocks), block(256);
-  if (strided)
-    hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel<true>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part,
-                       p.mt, p.nt, p.chunks, p.rows, p.blocks);
+#define ICTC_TN_LAUNCH(S, NJ)                                                                                \
+  hipLaunchKernelGGL((gemm_tn_bf16_partial_kernel<S, NJ>), grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part, \
+                     p.mt, p.nt, p.chunks, p.rows, p.blocks)
+  if (strided && n <= 16)
+    ICTC_TN_LAUNCH(true, 1);
+  else if (strided)
+    ICTC_TN_LAUNCH(true, 4);
+  else if (n <= 16)
+    ICTC_TN_LAUNCH(false, 1);
   else
-    hipLaunchKernelGGL(gemm_tn_bf16_partial_kernel<false>, grid, block, 0, st, a, k, (int)m, la, b, (int)n, lb, part,
-                       p.mt, p.nt, p.chunks, p.rows, p.blocks);
+    ICTC_TN_LAUNCH(false, 4);
+#undef ICTC_TN_LAUNCH
   const int64_t total = m * n;
   hipLaunchKernelGGL(gemm_tn_sum_kernel, dim3((unsigned)((total + 63) / 64)), dim3(64 * kSumWaves), 0, st, part,
                      total, p.chunks, out);

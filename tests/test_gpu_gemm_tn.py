@@ -20,7 +20,7 @@ def _tn(device, a, b):
 
 
 @pytest.mark.parametrize("K,M,N", [(100003, 64, 64), (50001, 70, 8), (20000, 2176, 64), (17, 5, 3), (424000, 64, 64),
-                                   (1000, 512, 130)])
+                                   (1000, 512, 130), (300001, 64, 16), (40000, 130, 1)])
 def test_gemm_tn_accuracy(device, K, M, N):
     g = torch.Generator().manual_seed(K + M + N)
     a = torch.randn(K, M, generator=g)
@@ -118,7 +118,7 @@ def _blocks(x, groups, rg, cg, blocks, off):
 
 
 @pytest.mark.parametrize("groups,rg,pa,pb,C", [(5000, 3, 1, 1, 64), (777, 5, 3, 1, 48), (3001, 1, 2, 5, 32),
-                                               (1200, 7, 1, 3, 128), (0, 3, 2, 2, 16)])
+                                               (1200, 7, 1, 3, 128), (0, 3, 2, 2, 16), (900, 2, 2, 1, 16)])
 def test_gemm_tn_grouped(device, groups, rg, pa, pb, C):
     """ictc_gemm_tn_grouped against a float64 product of the rearranged blocks (the per-degree weight
     gradient of a packed linear), elementwise bound 1e-5 * (|a|^T |b|); no groups writes zeros."""
