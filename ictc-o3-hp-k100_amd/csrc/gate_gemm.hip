@@ -149,8 +149,9 @@ __global__ __launch_bounds__(64 * kNtWaves, 1) void gate_gemm_nt_kernel(const fl
 // of dg per 16-edge tile (B operand: lane l reads 32 contiguous bytes of edge
 // l % 16), so dg streams from HBM exactly once.  The slices' partial sums meet
 // in LDS and are added in slice order (deterministic); the LDS tile is double
-// buffered so one barrier per tile suffices.  The next tile's dg block is
-// loaded while the current one is multiplied.
+// buffered so one barrier per tile suffices.  The next D tiles' dg blocks
+// are loaded while the current one is multiplied (D = 1 at up to 12 waves,
+// D = 3 at up to 8, whose register budget holds the deeper ring).
 constexpr int kMaxSlices = 12;  // up to 768 gates: 12 waves per block leave 170 VGPRs per lane
 constexpr int kRedRow = 68;  // LDS row pitch (floats) of a partial 16 x 64 tile
 
@@ -167,9 +168,11 @@ __device__ __forceinline__ void load_dg(const float* __restrict__ dg, int64_t e,
 }
 
 // dg rows have pitch ldg (a column block of a wider gradient); accumulate != 0 adds to dh.
-__global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const float* __restrict__ dg, int64_t ldg,
-                                                                       int64_t E, const float* __restrict__ W, int M,
-                                                                       float* __restrict__ dh, int accumulate) {
+// D: tiles of dg in flight per wave (a ring of register buffers); MAXS: waves per block at most.
+template <int D, int MAXS>
+__global__ __launch_bounds__(64 * MAXS) void gate_gemm_nn_kernel(const float* __restrict__ dg, int64_t ldg,
+                                                                 int64_t E, const float* __restrict__ W, int M,
+                                                                 float* __restrict__ dh, int accumulate) {
   extern __shared__ float red[];  // [2][S][16][kRedRow]
   const int l = threadIdx.x & 63, s = threadIdx.x >> 6, S = blockDim.x >> 6;
   const int i = l & 15, g = l >> 4;
@@ -185,14 +188,21 @@ __global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const flo
       A[kb][ks] = split8(v);
     }
   const int64_t tiles = (E + 15) / 16;
-  float next[16];
-  int64_t t = blockIdx.x;
-  if (t < tiles) load_dg(dg, 16 * t + i, E, ldg, s, next);
-  for (int buf = 0; t < tiles; t += gridDim.x, buf ^= 1) {
+  const int64_t G = gridDim.x;
+  float ring[D][16];
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    if (blockIdx.x + j * G < tiles) load_dg(dg, 16 * (blockIdx.x + j * G) + i, E, ldg, s, ring[j]);
+  int buf = 0;
+  for (int64_t t0 = blockIdx.x; t0 < tiles; t0 += D * G) {
+#pragma unroll
+  for (int j = 0; j < D; ++j, buf ^= 1) {
+    const int64_t t = t0 + j * G;
+    if (t >= tiles) break;
     float cur[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) cur[q] = next[q];
-    if (t + gridDim.x < tiles) load_dg(dg, 16 * (t + gridDim.x) + i, E, ldg, s, next);
+    for (int q = 0; q < 16; ++q) cur[q] = ring[j][q];
+    if (t + D * G < tiles) load_dg(dg, 16 * (t + D * G) + i, E, ldg, s, ring[j]);
     const Split B0 = split8(cur), B1 = split8(cur + 8);
     v4f acc[4];
 #pragma unroll
@@ -220,6 +230,7 @@ __global__ __launch_bounds__(64 * kMaxSlices) void gate_gemm_nn_kernel(const flo
         *o = accumulate ? *o + sum : sum;
       }
     }
+  }
   }
 }
 
@@ -282,15 +293,22 @@ int ictc_gate_gemm_bwd_strided(const float* grad, int64_t grad_pitch, int64_t ed
   const int64_t tiles = (edges + 15) / 16;
   const size_t lds = sizeof(float) * 2 * S * 16 * kRedRow;
   // persistent blocks: as many as are resident at once (LDS and registers), so none waits for a second round
+  // up to 512 gates: 8 waves with three tiles of dg in flight each (242 -> 214 us for 424k edges x 512);
+  // wider blocks keep 12 waves with one tile in flight (the register budget of 3 waves per SIMD)
+  const bool use_deep = S <= 8;
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_gemm_nn_kernel, 64 * S, lds) != hipSuccess ||
-      per_cu <= 0)
-    per_cu = 1;
+  const hipError_t oe = use_deep ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_gemm_nn_kernel<3, 8>, 64 * S, lds)
+                                 : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gate_gemm_nn_kernel<1, kMaxSlices>, 64 * S, lds);
+  if (oe != hipSuccess || per_cu <= 0) per_cu = 1;
   if (per_cu > 4) per_cu = 4;
   const int64_t want = (int64_t)cu_count() * per_cu;
   const unsigned blocks = (unsigned)(tiles < want ? tiles : want);
-  hipLaunchKernelGGL(gate_gemm_nn_kernel, dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream, grad, grad_pitch,
-                     edges, weight, gates, dhidden, accumulate);
+  if (use_deep)
+    hipLaunchKernelGGL((gate_gemm_nn_kernel<3, 8>), dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream, grad,
+                       grad_pitch, edges, weight, gates, dhidden, accumulate);
+  else
+    hipLaunchKernelGGL((gate_gemm_nn_kernel<1, kMaxSlices>), dim3(blocks), dim3(64 * S), lds, (hipStream_t)stream,
+                       grad, grad_pitch, edges, weight, gates, dhidden, accumulate);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     char buf[256];

@@ -62,7 +62,7 @@ def _check_adjoint(device, E, M, scale=None, seed=0):
     return got
 
 
-@pytest.mark.parametrize("E,M", [(1000, 704), (77, 192), (4099, 64), (16, 768), (1, 320), (70001, 704),
+@pytest.mark.parametrize("E,M", [(1000, 704), (77, 192), (4099, 64), (16, 768), (1, 320), (70001, 704), (90001, 512), (33, 448),
                                  (300, 2176), (50, 48)])
 def test_gate_adjoint_accuracy(device, E, M):
     """Kernel for M a multiple of 64 up to 768 (ragged tiles included); library GEMM beyond."""
