@@ -20,7 +20,7 @@ namespace sc {
 
 constexpr int kWave = 64;
 constexpr int kWaves = 4;
-constexpr int kChunk = 32;    // nodes per weight-gradient partial
+constexpr int kChunk = 16;    // nodes per weight-gradient partial
 constexpr int kDwBlock = 32;  // weights per weight-gradient wave (DW_BLOCK in gen_sc.py)
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
