@@ -52,12 +52,15 @@ __device__ __forceinline__ v4f mfma(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// FP32 MFMA form for panels too wide for LDS (K > kWholeK; K <= kWholeK runs the split-bf16 kernel
+// FP32 MFMA form for panels too wide for LDS (K > kBf16MaxK with more channels than a slice holds; K <= kBf16MaxK runs the split-bf16 kernel
 // below).  WHOLE: the block's whole weight panel (64 output columns x K) is staged in LDS once, and the
 // block loops over 64-node tiles (grid.x persistent blocks); otherwise the panel is staged per 64-wide
 // k-chunk.  MFMA operands: A = weights (M = 16 output columns), B = inputs (N = 16 nodes),
 // so each lane ends with 4 consecutive output columns of one node and stores them as one 16-byte write.
 constexpr int kWholeK = 256;
+// Widest panel of the split-bf16 kernel: its three bf16 parts of 64 columns x 384 take 147 KB of LDS (one
+// 16-wave block per CU either way, as at 256).
+constexpr int kBf16MaxK = 384;
 
 template <bool WHOLE>
 __global__ __launch_bounds__(256) void packed_linear_kernel(const float* __restrict__ in, int64_t in_stride,
@@ -147,7 +150,7 @@ __global__ __launch_bounds__(256) void packed_linear_kernel(const float* __restr
   }
 }
 
-// Split-bf16 form of the whole-panel path (K <= kWholeK): the weight panel is split once into three bf16
+// Split-bf16 form of the whole-panel path (K <= kBf16MaxK): the weight panel is split once into three bf16
 // parts in LDS (the A operand of v_mfma_f32_16x16x32_bf16, lane l: output column 16 cb + l % 16,
 // k = 32 ks + 8 (l / 16) .. + 7), each 16-node tile's inputs are split once per 32-wide k-step (B
 // operand: node l % 16, the same k), and each 16 x 16 x 32 block keeps the six products whose size is at
@@ -340,9 +343,9 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
   const int64_t node_blocks = (nodes + 63) / 64;
   const unsigned gy = (unsigned)((lmax + 1) * (lmax + 1)), gz = (unsigned)((maxcols + 63) / 64);
   // Panels wider than the LDS holds run as consecutive launches over slices of the input paths (at most
-  // kWholeK / Cin paths each), the later ones adding to the output rows.
-  const int slice = channels_in <= kWholeK ? kWholeK / channels_in : 0;
-  if (maxk > kWholeK && slice > 0) {
+  // kBf16MaxK / Cin paths each), the later ones adding to the output rows.
+  const int slice = channels_in <= kBf16MaxK ? kBf16MaxK / channels_in : 0;
+  if (maxk > kBf16MaxK && slice > 0) {
     int slices = 1;
     for (int l = 0; l <= lmax; ++l) slices = std::max(slices, (in_paths[l] + slice - 1) / slice);
     for (int j = 0; j < slices; ++j) {
@@ -362,7 +365,7 @@ int ictc_packed_linear(int lmax, int channels_in, int channels_out, const float*
     }
     return ICTC_OK;
   }
-  if (maxk <= kWholeK) {
+  if (maxk <= kBf16MaxK) {
     if (int rc = launch_bf16(in, in_stride, out, out_stride, channels_in, channels_out, nodes, d, maxk, maxcols, gy,
                              gz, (hipStream_t)stream))
       return rc;
