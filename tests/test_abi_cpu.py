@@ -175,3 +175,26 @@ def test_weight_operand_cache_follows_versions():
     assert b is not a and torch.equal(b, blk)
     c = torch.randn(16, 16)
     assert _weight_operand(c) is not None and _weight_operand(c).data_ptr() == c.data_ptr()
+
+
+def test_species_entry_points_host_checks():
+    """Argument checks of the species-sorted self connection and its weight gradient (no device work)."""
+    from ictc_o3 import _native
+    if not os.path.exists(_native.library_path()):
+        pytest.skip("library not built")
+    lib = _native.lib()
+    assert lib.ictc_species_outer_workspace_bytes(1000, 128, 10, 128) == (8 + 10) * 128 * 128 * 4
+    assert lib.ictc_species_outer_workspace_bytes(1000, 128, 10, 100) < 0      # tile rows not a multiple of 32
+    assert lib.ictc_species_outer_workspace_bytes(1000, 64, 0, 128) < 0        # no species
+    # zero nodes: nothing to do, no operand is touched
+    _native.call("ictc_species_linear", None, 64, 0, 64, None, 3, None, None, 0, None, 64, None)
+    with pytest.raises(ValueError, match="64 and 128"):
+        _native.call("ictc_species_linear", None, 32, 10, 32, None, 3, None, None, 0, None, 32, None)
+    with pytest.raises(ValueError, match="pitch"):
+        _native.call("ictc_species_linear", None, 66, 10, 64, None, 3, None, None, 0, None, 64, None)
+    with pytest.raises(ValueError, match="null operand"):
+        _native.call("ictc_species_linear", None, 64, 10, 64, None, 3, None, None, 0, None, 64, None)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        _native.call("ictc_species_outer", None, 64, None, 64, 10, 64, 3, None, None, 48, None, None, 0, None)
+    with pytest.raises(ValueError, match="64 and 128"):
+        _native.call("ictc_species_outer", None, 96, None, 96, 10, 96, 3, None, None, 128, None, None, 0, None)
