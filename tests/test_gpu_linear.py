@@ -228,3 +228,37 @@ def test_species_linear_column_slice(device):
     assert torch.equal(a, b)
     ref = _species_ref(xs.double().cpu(), W.double().cpu(), sp.cpu())
     assert rel_err(a, ref) < 1e-5
+
+
+def test_species_linear_edge_cases(device):
+    """No nodes; every species id outside [0, S) (zero rows, zero weight gradient); and the weight gradient
+    through the C ABI with 256-row tiles (eight LDS stages per tile) against the float64 per-species sums."""
+    import ctypes
+    from ictc_o3 import _native as nat
+    from ictc_o3.ops import linear as lin
+    C, S = 64, 4
+    W = (torch.randn(S, C, C) / C ** 0.5).to(device).requires_grad_(True)
+    x0 = torch.zeros(0, C, device=device, requires_grad=True)
+    y0 = lin.species_linear(x0, W, torch.zeros(0, dtype=torch.int64, device=device))
+    assert y0.shape == (0, C)
+    x = torch.randn(50, C, device=device, requires_grad=True)
+    bad = torch.tensor([S, -1, S + 7] * 16 + [S, -2], device=device)
+    y = lin.species_linear(x, W, bad)
+    assert torch.equal(y, torch.zeros_like(y))
+    dx, dW = torch.autograd.grad(y.sum(), (x, W))
+    assert torch.equal(dx, torch.zeros_like(dx)) and torch.equal(dW, torch.zeros_like(dW))
+    g = torch.Generator().manual_seed(11)
+    N, C, S = 3000, 128, 3
+    a64 = torch.randn(N, C, generator=g, dtype=torch.float64)
+    b64 = torch.randn(N, C, generator=g, dtype=torch.float64)
+    sp = torch.randint(0, S, (N,), generator=g)
+    order = lin.species_order(sp.to(device), S)
+    a, b = a64.float().to(device), b64.float().to(device)
+    rows = 256
+    nb = int(nat.lib().ictc_species_outer_workspace_bytes(N, C, S, rows))
+    ws = torch.empty(nb // 4, device=device)
+    out = torch.empty(S, C, C, device=device)
+    nat.call("ictc_species_outer", nat.ptr(a), C, nat.ptr(b), C, N, C, S, nat.ptr(order.perm), nat.ptr(order.off),
+             rows, nat.ptr(out), nat.ptr(ws), nb, nat.stream_of(a))
+    ref = torch.stack([a64[sp == s].t() @ b64[sp == s] for s in range(S)])
+    assert rel_err(out, ref) < 1e-5
